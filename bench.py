@@ -1,0 +1,303 @@
+#!/usr/bin/env python3
+"""Benchmark: CosyVoice3 Flow DiT Euler-step mel frames/s at T=500, B=2 (CFG pair).
+
+One "step" is one device-resident CFG Euler step of the full 22-block DiT
+estimator (time MLP + stacked AdaLN GEMV + input embedding + 22 blocks +
+norm_out/proj_out + CFG combine/x update), inputs resident in HBM.
+value = T * steps / wall time of the timed region (mel frames per second).
+
+Also reported on the same JSON line:
+  roofline      the dominant kernel's achieved FLOP/s (HIP events on the stream
+                the library launches on) vs the 157.3 TFLOP/s fp32 MFMA peak;
+  kernels       per-kernel-class HIP-event timings of one step's launches;
+  fused_ops     achieved HBM GB/s of every fused op at the configs' shapes, with
+                each launch on a distinct buffer set (> 256 MB rotation, so the
+                MALL does not serve the reads);
+  cpu_baseline  the CPU oracle's Euler step on this host's cores (bounded sample).
+
+Usage: python bench.py [--steps K] [--warmup W] [--T 500] [--no-cpu]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+MFMA_F32_PEAK_TFLOPS = 157.3
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--T", type=int, default=500)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-fused", action="store_true", help="skip the fused-op GB/s sweep")
+    return ap.parse_args()
+
+
+def event_time_ms(fn, n, torch):
+    """Average ms per call of fn over n calls, HIP events on torch's current
+    stream (the stream every liblxops call of this script is enqueued on)."""
+    s = torch.cuda.current_stream()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    fn()
+    torch.cuda.synchronize()
+    a.record(s)
+    for _ in range(n):
+        fn()
+    b.record(s)
+    b.synchronize()
+    return a.elapsed_time(b) / n
+
+
+def gemm_kernels(torch, ops, T, dev):
+    """Per-class timings of the estimator's projection GEMMs and attention at
+    the step's shapes (each class is one kernel instantiation)."""
+    D, F, B = 1024, 2048, 2
+    M = B * T
+    g = torch.Generator(device=dev).manual_seed(3)
+    x = torch.randn(M, F, device=dev, generator=g)
+    wq = torch.randn(3 * D, D, device=dev, generator=g) * 0.02
+    w1 = torch.randn(F, D, device=dev, generator=g) * 0.02
+    w2 = torch.randn(D, F, device=dev, generator=g) * 0.02
+    wo = torch.randn(D, D, device=dev, generator=g) * 0.02
+    bq = torch.zeros(3 * D, device=dev)
+    b1 = torch.zeros(F, device=dev)
+    bd = torch.zeros(D, device=dev)
+    h = torch.randn(M, D, device=dev, generator=g)
+    gate = torch.randn(B, D, device=dev, generator=g)
+    pos = torch.arange(T, dtype=torch.int32, device=dev)
+    qkv = torch.empty(M, 3 * D, device=dev)
+    ff = torch.empty(M, F, device=dev)
+    rope = ops.Epilogue(kind=ops.LX_EPI_ROPE_PARTIAL, rows_per_batch=T, pos=pos.data_ptr(),
+                        rot_dim=64, rope_section=D, rope_sections=2, rope_base=10000.0)
+    gelu = ops.Epilogue(kind=ops.LX_EPI_GELU_TANH)
+    gated = ops.Epilogue(kind=ops.LX_EPI_GATED_RESID, rows_per_batch=T, gate=gate.data_ptr(),
+                         gate_stride=D)
+    xd = x[:, :D]
+    out = {}
+    n = 50
+    cases = {
+        "gemm_qkv_rope": (lambda: ops.linear(xd, wq, bq, rope, out=qkv), 2 * M * 3 * D * D, 1),
+        "gemm_out_gated": (lambda: ops.linear(xd, wo, bd, gated, out=h), 2 * M * D * D, 1),
+        "gemm_ff0_gelu": (lambda: ops.linear(xd, w1, b1, gelu, out=ff), 2 * M * F * D, 1),
+        "gemm_ff2_gated": (lambda: ops.linear(x, w2, bd, gated, out=h), 2 * M * D * F, 1),
+        "attention": (lambda: ops.attention(qkv[:, :D].view(B, T, D),
+                                            qkv[:, D:2 * D].view(B, T, D),
+                                            qkv[:, 2 * D:].view(B, T, D), 16,
+                                            out=ff[:, :D].view(B, T, D)),
+                      4 * B * 16 * T * T * 64, 1),
+    }
+    for name, (fn, flops, per_block) in cases.items():
+        ms = event_time_ms(fn, n, torch)
+        out[name] = {"avg_us": ms * 1e3, "flop": flops, "tflops": flops / (ms * 1e-3) / 1e12,
+                     "per_block": per_block}
+    return out
+
+
+def fused_ops_gbs(torch, ops, dev):
+    """Achieved HBM GB/s per fused op: algorithmic bytes (each tensor read once,
+    output written once) / HIP-event time per launch, each launch on its own
+    buffer set so the working set (> 256 MB) streams from HBM."""
+    res = {}
+    g = torch.Generator(device=dev).manual_seed(9)
+    ROT = 320 * 2**20  # bytes cycled through per op
+
+    def run(name, make, call, algo_bytes, set_bytes, shape_note):
+        nset = max(2, int(ROT // set_bytes))
+        sets = [make() for _ in range(nset)]
+        it = [0]
+
+        def fn():
+            call(*sets[it[0] % nset])
+            it[0] += 1
+        ms = event_time_ms(fn, nset, torch)
+        res[name] = {"shape": shape_note, "bytes": int(algo_bytes), "avg_us": ms * 1e3,
+                     "gbs": algo_bytes / (ms * 1e-3) / 1e9,
+                     "frac": algo_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+        del sets
+
+    for T in (500, 3000):
+        B, D = 2, 1024
+        N = B * T
+        emb = torch.randn(B, 6 * D, device=dev, generator=g) * 0.1
+        run(f"adaln_T{T}",
+            lambda: (torch.randn(B, T, D, device=dev, generator=g), torch.empty(B, T, D, device=dev)),
+            lambda x, y: ops.ada_ln(x, emb[:, D:2 * D], emb[:, :D], out=y),
+            2 * N * D * 4 + 2 * B * D * 4, 2 * N * D * 4, f"B={B} T={T} D={D}")
+        run(f"gelu_T{T}",
+            lambda: (torch.randn(N * 2048, device=dev, generator=g), torch.empty(N * 2048, device=dev)),
+            lambda h, y: ops.gelu_tanh(h, out=y),
+            2 * N * 2048 * 4, 2 * N * 2048 * 4, f"N={N} F=2048")
+        run(f"gated_residual_T{T}",
+            lambda: (torch.randn(B, T, D, device=dev, generator=g), torch.randn(B, T, D, device=dev, generator=g)),
+            lambda x, y: ops.gated_residual(x, y, emb[:, 2 * D:3 * D]),
+            3 * N * D * 4 + B * D * 4, 2 * N * D * 4, f"B={B} T={T} D={D}")
+        pos = torch.arange(T, dtype=torch.int32, device=dev)
+        run(f"rope_partial_T{T}",
+            lambda: (torch.randn(B, T, D, device=dev, generator=g), torch.randn(B, T, D, device=dev, generator=g)),
+            lambda q, k: ops.rope_partial(q, k, pos),
+            2 * (2 * N * 64 * 4), 2 * N * D * 4, f"q,k B={B} T={T}, 64 of {D} channels")
+    L, H, I = 256, 896, 4864
+    wn = torch.randn(H, device=dev, generator=g)
+    run("rmsnorm_L256",
+        lambda: (torch.randn(L, H, device=dev, generator=g), torch.empty(L, H, device=dev)),
+        lambda x, y: ops.rms_norm(x, wn, out=y), 2 * L * H * 4 + H * 4, 2 * L * H * 4, "L=256 H=896")
+    posl = torch.arange(L, dtype=torch.int32, device=dev)
+    run("rope_neox_L256",
+        lambda: (torch.randn(L, 1152, device=dev, generator=g),),
+        lambda qkv: (ops.rope_full(qkv[:, :896], posl, 14), ops.rope_full(qkv[:, 896:1024], posl, 2)),
+        2 * L * 1024 * 4, L * 1152 * 4, "q 14 + k 2 heads x 64, L=256")
+    run("swiglu_L256",
+        lambda: (torch.randn(L * I, device=dev, generator=g), torch.randn(L * I, device=dev, generator=g),
+                 torch.empty(L * I, device=dev)),
+        lambda a, b, c: ops.swiglu(a, b, out=c), 3 * L * I * 4, 3 * L * I * 4, "L=256 I=4864")
+    table = torch.randn(151936, 896, device=dev, generator=g)
+    ids = list(range(0, 151936, 151936 // 256))[:256]
+    run("embed_gather_n256",
+        lambda: (torch.empty(256, 896, device=dev),),
+        lambda y: ops.embed_gather(table, ids, out=y), 2 * 256 * 896 * 4 + 256 * 4,
+        256 * 896 * 4, "256 rows of the 151936x896 text table")
+    return res
+
+
+def cpu_baseline(T, seconds):
+    """The CPU oracle's CFG Euler step (22-block DiT, B=2, T) on this host."""
+    import numpy as np
+    from oracle import oracle as orc
+    from larynx_amd.flow import DiTConfig, dit_param_shapes
+    params = orc.make_params(dit_param_shapes(DiTConfig()), 1)
+    dit = orc.Dit(params)
+    x = orc.normal((80, T), 2, 1)
+    mu = orc.normal((80, T), 2, 2)
+    cond = orc.normal((80, T), 2, 3)
+    spks = orc.normal((80,), 2, 4, 1.0 / np.sqrt(80.0))
+    dit.cfm_step(x, mu, cond, spks, 0.0, 0.0123)  # warm-up (page in weights, threads)
+    times = []
+    t_start = time.perf_counter()
+    while True:
+        t0 = time.perf_counter()
+        x = dit.cfm_step(x, mu, cond, spks, 0.0123, 0.05)
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_start > seconds or len(times) >= 20:
+            break
+    t_step = float(np.median(times))
+    return {"value": T / t_step, "unit": "mel frames/s", "cores": orc.lib.orc_get_threads(),
+            "kind": "port",
+            "sample": f"{len(times)} CFG Euler step(s) of the 22-block DiT at B=2, T={T} "
+                      f"(median {t_step:.2f} s/step), fp32 storage / fp64 accumulation"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (requested --gpus {args.gpus}); the DiT path "
+              "shards by CFG row / heads across GPUs by design but no multi-GPU figure is "
+              "produced by this build.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        sys.exit(1)
+    from larynx_amd import ops
+    from larynx_amd.flow import DiTConfig, DiTEstimator, cfm_t_span, dit_param_shapes
+
+    dev = torch.device("cuda:0")
+    T = args.T
+    cfg = DiTConfig()
+    g = torch.Generator(device=dev).manual_seed(0)
+    params = {}
+    for name, shape in dit_param_shapes(cfg):
+        params[name] = torch.randn(*shape, device=dev, generator=g) * 0.02
+    est = DiTEstimator(params, cfg, B=2, max_T=max(T, 3000))
+    del params
+    x = torch.randn(80, T, device=dev, generator=g)
+    mu = torch.randn(80, T, device=dev, generator=g)
+    cond = torch.randn(80, T, device=dev, generator=g)
+    spks = torch.randn(80, device=dev, generator=g) / 80 ** 0.5
+    ts = cfm_t_span(cfg.n_timesteps)
+    sched = [(float(ts[i]), float(ts[i + 1] - ts[i])) for i in range(cfg.n_timesteps)]
+
+    def step(i):
+        t, dt = sched[i % len(sched)]
+        est.cfm_step(x, mu, cond, spks, t, dt)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    s = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(s)
+    for i in range(args.steps):
+        step(i)
+    e1.record(s)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ev_ms = e0.elapsed_time(e1)
+    ms_per_step = wall * 1e3 / args.steps
+    value = T * args.steps / wall
+
+    # 10-step solve (the reference's whole CFM loop) at the same shape
+    z = torch.randn(80, T, device=dev, generator=g)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    est.cfm_solve(z, mu, cond, spks)
+    torch.cuda.synchronize()
+    solve_ms = (time.perf_counter() - t1) * 1e3
+
+    kernels = gemm_kernels(torch, ops, T, dev)
+    # dominant kernel: largest share of a step (22 blocks, one launch each)
+    dom_name, dom = max(kernels.items(), key=lambda kv: kv[1]["avg_us"] * kv[1]["per_block"])
+    roofline = {"kernel": dom_name, "bound": "mfma", "achieved": round(dom["tflops"], 3),
+                "peak": MFMA_F32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(dom["tflops"] / MFMA_F32_PEAK_TFLOPS, 4), "traffic": None,
+                "avg_us": round(dom["avg_us"], 2), "flop_per_launch": dom["flop"]}
+    gemm_flop_step = 22 * sum(k["flop"] for k in kernels.values())
+    fused = {} if args.no_fused else fused_ops_gbs(torch, ops, dev)
+    est.close()
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(T, args.cpu_seconds)
+
+    line = {
+        "metric": "DiT Euler-step mel frames/s at T=500 B=2",
+        "value": round(value, 1),
+        "unit": "mel frames/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (random ~N(0,0.02) weights, N(0,1) mel inputs)",
+        "config": {"workload": "CosyVoice3 Flow DiT estimator, one CFG Euler step "
+                               "(22 blocks, dim 1024, 16x64 heads, ff 2048, mel 80)",
+                   "B": 2, "T": T, "blocks": 22, "cfg_rate": 0.7},
+        "event_ms_per_step": round(ev_ms / args.steps, 4),
+        "euler_10step_ms": round(solve_ms, 3),
+        "step_tflops": round(gemm_flop_step / (ms_per_step * 1e-3) / 1e12, 2),
+        "roofline": roofline,
+        "kernels": {k: {"avg_us": round(v["avg_us"], 2), "tflops": round(v["tflops"], 2)}
+                    for k, v in kernels.items()},
+        "fused_ops": {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv)
+                          for kk, vv in v.items()} for k, v in fused.items()},
+        "cpu_baseline": cpu,
+    }
+    if cpu:
+        line["gpu_over_cpu"] = round(value / cpu["value"], 1)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

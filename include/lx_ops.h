@@ -1,0 +1,356 @@
+/*
+ * lx_ops.h — C-ABI of the MI355X (gfx950) op library `liblxops.so`.
+ *
+ * Every entry point replaces one group of ggml graph nodes on the hot path of
+ * Larynx's CosyVoice3 Flow DiT estimator and Qwen2 LM. The citation on each
+ * declaration names the reference node(s) it stands in for (paths relative to
+ * the Larynx source tree).
+ *
+ * Conventions (shared by every function):
+ *   - All tensor pointers are DEVICE pointers (hipMalloc'd or torch CUDA
+ *     tensors), fp32, contiguous row-major in the PyTorch sense.  A PyTorch
+ *     (B, T, C) tensor is byte-identical to ggml's [C, T, B] ("Space B" of the
+ *     reference, docs/FLOW.md §2).  Exceptions are marked HOST.
+ *   - Return value: LX_OK (0) on success, a negative LX_ERR_* code otherwise.
+ *     Bad arguments are rejected before any work is enqueued.  Errors are never
+ *     silently clamped: a bad token id is an error, not a zero row.
+ *   - Work is enqueued on `stream` (0 = the default stream); no call
+ *     synchronises unless documented.  No per-op call allocates device memory;
+ *     the composite objects (lx_dit, lx_qwen2) allocate at create time only.
+ *   - Reentrant per stream: calls on different streams touching disjoint
+ *     buffers may overlap.
+ */
+#ifndef LX_OPS_H
+#define LX_OPS_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  LX_OK = 0,
+  LX_ERR_ARG = -1,     /* null pointer, bad shape, unsupported size */
+  LX_ERR_LAUNCH = -2,  /* hipLaunch / hipGetLastError failure */
+  LX_ERR_RANGE = -3,   /* token id outside its embedding table */
+  LX_ERR_ALLOC = -4,   /* device allocation failed (create calls only) */
+  LX_ERR_STATE = -5    /* call out of order (e.g. decode before prefill) */
+};
+
+/* Library identity: returns a static string naming the build and target. */
+const char* lx_version(void);
+/* Last error string of the calling thread (static storage, never NULL). */
+const char* lx_last_error(void);
+
+/* ------------------------------------------------------------------------ */
+/* Flow DiT fused row / pointwise ops                                        */
+/* ------------------------------------------------------------------------ */
+
+/* a1/a2 — AdaLayerNorm modulation:
+ *   y[b,t,:] = LN_eps(x[b,t,:]) * (1 + scale[b,:]) + shift[b,:]
+ * LN: biased variance, no affine.  x, y: (B, T, D).  shift/scale rows are
+ * `mod_stride` floats apart, so they may point straight into the chunked AdaLN
+ * embedding (B, 6*D) with mod_stride = 6*D (no chunk copies).  y may alias x.
+ * Replaces ada_ln (src/flow/ops.cpp:94-104: ggml_norm + add(scale,1) + mul +
+ * add) and the view_chunk conts (src/flow/dit.cpp:26-31, 57-62, 134-135).
+ * D % 4 == 0, D <= 4096. */
+int lx_adaln_modulate_f32(const float* x, const float* shift, const float* scale,
+                          long mod_stride, float* y, int B, int T, int D, float eps,
+                          hipStream_t stream);
+
+/* AdaLN modulation embedding (GEMV over the batch rows):
+ *   emb[b, :] = W @ silu(c[b, :]) + bias,   W: (n_out, D) row-major.
+ * Replaces linear(attn_norm_w, attn_norm_b, ggml_silu(t)) (src/flow/dit.cpp:56)
+ * and the norm_out linear (src/flow/dit.cpp:133).  B <= 8. */
+int lx_adaln_emb_f32(const float* c, const float* W, const float* bias, float* emb,
+                     int B, int D, int n_out, hipStream_t stream);
+
+/* a3 — partial interleaved (GPT-J) rotary, in place on q and k (k may be NULL):
+ * for channels c < rot_dim, pairs (2i, 2i+1) of every row (b, t) rotate by
+ * angle = fp32(pos[t]) * inv_freq[i], inv_freq[i] = 1/base^(2i/rot_dim) in fp32.
+ * Channels >= rot_dim are untouched.  q, k: (B, T, ld) with the row stride `ld`
+ * in floats; pos: device int32[T].
+ * Replaces rope_partial (src/flow/ops.cpp:85-92: permute + ggml_rope_ext
+ * NORMAL n_dims=64 base 1e4 + permute + cont).  rot_dim even, <= 128. */
+int lx_rope_partial_interleaved_f32(float* q, float* k, const int* pos, int B, int T,
+                                    int ld, int rot_dim, float base, hipStream_t stream);
+
+/* a4 — tanh-GELU: y = 0.5 x (1 + tanh(0.7978845608028654 (x + 0.044715 x^3))).
+ * y may alias h.  Replaces gelu_tanh (src/flow/ops.cpp:73-83, 9 ggml nodes). */
+int lx_gelu_tanh_f32(const float* h, float* y, long n, hipStream_t stream);
+
+/* a5 — gated residual, in place: x[b,t,:] += gate[b,:] * y[b,t,:].
+ * gate rows are `gate_stride` floats apart (may point into the AdaLN emb).
+ * Replaces ggml_add(x, ggml_mul(y, gate)) (src/flow/dit.cpp:71, 77). */
+int lx_gated_residual_f32(float* x, const float* y, const float* gate, long gate_stride,
+                          int B, int T, int D, hipStream_t stream);
+
+/* a6 — sinusoidal timestep embedding:
+ *   out[b, j]          = sin(scale * t[b] * e^(-j ln(1e4)/(half_dim-1)))
+ *   out[b, half_dim+j] = cos(...),                 j < half_dim.
+ * t: device float[B]; out: (B, 2*half_dim).  Replaces the sinusoid half of
+ * time_embed_host (src/flow/flow_matching.cpp:13-20). */
+int lx_timestep_embed_f32(const float* t, int B, int half_dim, float scale, float* out,
+                          hipStream_t stream);
+
+/* a6 — full TimestepEmbedding: sinusoid(256, scale 1000) -> Linear(256->D) ->
+ * SiLU -> Linear(D->D).  w0: (D, 256), w2: (D, D).  work: device scratch of at
+ * least B*(256 + D) floats.  Replaces time_embed_host
+ * (src/flow/flow_matching.cpp:10-42) on the device. */
+int lx_time_mlp_f32(const float* t, int B, const float* w0, const float* b0,
+                    const float* w2, const float* b2, int D, float* work, float* out,
+                    hipStream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* Qwen2 fused ops                                                           */
+/* ------------------------------------------------------------------------ */
+
+/* a10 — RMSNorm: y = x / sqrt(mean(x^2) + eps) * w.  x, y: (rows, D).
+ * Replaces rms_norm (src/llm/ops.cpp:7-11: ggml_rms_norm + mul). */
+int lx_rmsnorm_f32(const float* x, const float* w, float* y, int rows, int D, float eps,
+                   hipStream_t stream);
+
+/* a11 — NEOX rotary, in place: row r holds n_heads heads of head_dim; within a
+ * head pairs (i, i + head_dim/2) rotate by fp32(pos[r]) * theta^(-2i/head_dim).
+ * qk: (rows, ld) floats with the heads packed from column 0; pos: device
+ * int32[rows].  Replaces rope_full (src/llm/ops.cpp:21-30, GGML_ROPE_TYPE_NEOX). */
+int lx_rope_neox_f32(float* qk, const int* pos, int rows, int n_heads, int head_dim,
+                     int ld, float theta, hipStream_t stream);
+
+/* a12 — SwiGLU gate: out = silu(gate) * up, elementwise over n.
+ * Replaces ggml_mul(ggml_silu(gate), up) (src/llm/llm.cpp:167-169, 285-287). */
+int lx_swiglu_f32(const float* gate, const float* up, float* out, long n,
+                  hipStream_t stream);
+
+/* a13 — embedding gather: out[i, :] = table[ids[i], :], bit-exact copy.
+ * ids is a HOST int32 array (the reference holds token ids on the host); every
+ * id is checked against [0, n_rows) before any work is enqueued and a bad id
+ * returns LX_ERR_RANGE with nothing written.  table: (n_rows, D); out: (n, D).
+ * Replaces the per-row ggml_backend_tensor_get copies of build_lm_input
+ * (src/llm/llm.cpp:63-100), decode (src/llm/llm.cpp:226-230) and the flow
+ * token ggml_get_rows (src/flow/flow.cpp:150-151). */
+int lx_embed_gather_f32(const float* table, long n_rows, int D, const int* ids, int n,
+                        float* out, hipStream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* Dense parts (MFMA fp32)                                                   */
+/* ------------------------------------------------------------------------ */
+
+/* Epilogues fused into the projection GEMM  acc = x @ W^T (+ bias). */
+enum {
+  LX_EPI_NONE = 0,          /* y = acc + bias                                   */
+  LX_EPI_GELU_TANH = 1,     /* y = gelu_tanh(acc + bias)                        */
+  LX_EPI_GATED_RESID = 2,   /* y[m,:] += gate[m / rows_per_batch, :] * (acc+bias) */
+  LX_EPI_ROPE_PARTIAL = 3,  /* y = acc + bias, then partial interleaved rotary on
+                               columns c with (c % rope_section) < rot_dim and
+                               c < rope_sections * rope_section; position of row
+                               m is pos[m % rows_per_batch]                       */
+  LX_EPI_RESID = 4,         /* y[m,:] += acc (+ bias)                           */
+  LX_EPI_SWIGLU_PAIRED = 5  /* W rows interleave gate/up: y[m, j] =
+                               silu(acc[2j]) * acc[2j+1]; y has N/2 columns      */
+};
+
+typedef struct lx_epilogue {
+  int kind;                 /* LX_EPI_* */
+  int rows_per_batch;       /* T: row m belongs to batch m / T (GATED_RESID, ROPE) */
+  const float* gate;        /* GATED_RESID: gate rows, gate_stride floats apart  */
+  long gate_stride;
+  const int* pos;           /* ROPE_PARTIAL: device int32[rows_per_batch]        */
+  int rot_dim;              /* ROPE_PARTIAL: rotated channels per section (even) */
+  int rope_section;         /* ROPE_PARTIAL: columns per rotated section         */
+  int rope_sections;        /* ROPE_PARTIAL: number of leading sections rotated  */
+  float rope_base;          /* ROPE_PARTIAL: frequency base                      */
+} lx_epilogue;
+
+/* Linear: y = epi(x @ W^T + bias).  x: (M, K) with row stride ldx; W: (N, K)
+ * row-major (torch nn.Linear weight == ggml [K, N]); bias: (N) or NULL;
+ * y: (M, N) with row stride ldy (N/2 columns for SWIGLU_PAIRED).  K % 4 == 0.
+ * Replaces linear() = ggml_mul_mat + ggml_add (src/flow/ops.cpp:20-26,
+ * src/llm/ops.cpp:13-19) plus whatever node the epilogue absorbs.
+ * epi may be NULL (== LX_EPI_NONE). */
+int lx_linear_f32(const float* x, int ldx, const float* W, const float* bias, float* y,
+                  int ldy, int M, int N, int K, const lx_epilogue* epi,
+                  hipStream_t stream);
+
+/* Scaled-dot-product attention (flash-style, fp32 MFMA, scores never stored):
+ *   o[b, t, h*hd:(h+1)*hd] = softmax(scale * q_h k_g^T [+ causal mask]) v_g
+ * with g = h / (n_heads / n_kv_heads) (GQA, consecutive like HF repeat_kv).
+ * q: (B, Tq, *) row stride ldq, head h at column h*hd; k, v: (B, Tk, *) row
+ * strides ldk/ldv, kv head g at column g*hd; o: (B, Tq, *) row stride ldo.
+ * causal != 0: query i (absolute position q_offset + i) sees keys <= that
+ * position.  head_dim must be 64.
+ * Replaces attention() (src/flow/dit.cpp:34-51; src/llm/ops.cpp:49-65) and
+ * repeat_kv (src/llm/ops.cpp:32-47). */
+int lx_attention_f32(const float* q, int ldq, const float* k, int ldk, const float* v,
+                     int ldv, float* o, int ldo, int B, int Tq, int Tk, int n_heads,
+                     int n_kv_heads, int head_dim, float scale, int causal, int q_offset,
+                     hipStream_t stream);
+
+/* Causal grouped conv1d + Mish (one CausalConvPositionEmbedding half):
+ *   y[b,t,oc] = mish(bias[oc] + sum_{k<K, ic<C/G} w[oc, ic, k] *
+ *                                 x[b, t-(K-1)+k, g*(C/G)+ic]) (+ resid[b,t,oc])
+ * with g = oc / (C/G) and x = 0 for negative time (left pad K-1).  x, y, resid:
+ * (B, T, C); resid may be NULL; y must not alias x.  `wp` is the weight in the
+ * tap-major layout written by lx_conv_pack_weight_f32.  C/G must be 64,
+ * K <= 32.  Replaces ggml_pad_ext + grouped_conv1d + mish (+ add)
+ * (src/flow/dit.cpp:113-122; src/flow/ops.cpp:28-71). */
+int lx_conv_pos_mish_f32(const float* x, const float* wp, const float* bias,
+                         const float* resid, float* y, int B, int T, int C, int G, int K,
+                         hipStream_t stream);
+
+/* Packs a torch Conv1d weight w (C, C/G, K) into the tap-major layout
+ * wp (G, K, C/G, C/G) used above (same element count; done once at load,
+ * like the reference's GGUF conversion). */
+int lx_conv_pack_weight_f32(const float* w, float* wp, int C, int G, int K,
+                            hipStream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* DiT estimator and CFM Euler loop (host C++ over the ops above)            */
+/* ------------------------------------------------------------------------ */
+
+/* Per-block weights, torch nn.Linear layout (out, in); device pointers.
+ * Mirrors FlowWeights::Block (src/flow/internal.h:72-87). */
+typedef struct lx_dit_block_weights {
+  const float* attn_norm_w; const float* attn_norm_b;   /* (6D, D), (6D) */
+  const float* to_q_w; const float* to_q_b;              /* (D, D), (D)   */
+  const float* to_k_w; const float* to_k_b;
+  const float* to_v_w; const float* to_v_b;
+  const float* to_out_w; const float* to_out_b;          /* (D, D), (D)   */
+  const float* ff0_w; const float* ff0_b;                /* (F, D), (F)   */
+  const float* ff2_w; const float* ff2_b;                /* (D, F), (D)   */
+} lx_dit_block_weights;
+
+/* Whole-estimator weights.  Mirrors FlowWeights (src/flow/internal.h:46-94)
+ * minus the frontend tensors. */
+typedef struct lx_dit_weights {
+  int dim, depth, heads, head_dim, ff_inner, mel_dim;    /* 1024,22,16,64,2048,80 */
+  const float* time_mlp_0_w; const float* time_mlp_0_b;  /* (D, 256), (D)        */
+  const float* time_mlp_2_w; const float* time_mlp_2_b;  /* (D, D), (D)          */
+  const float* input_proj_w; const float* input_proj_b;  /* (D, 4*mel), (D)      */
+  const float* conv_pos_1_w; const float* conv_pos_1_b;  /* (D, 64, 31), (D)    */
+  const float* conv_pos_2_w; const float* conv_pos_2_b;
+  const lx_dit_block_weights* blocks;                    /* HOST array [depth]   */
+  const float* norm_out_w; const float* norm_out_b;      /* (2D, D), (2D)        */
+  const float* proj_out_w; const float* proj_out_b;      /* (mel, D), (mel)      */
+} lx_dit_weights;
+
+typedef struct lx_dit lx_dit;
+
+/* Builds an estimator for batches of B rows and up to max_T frames.  Weights
+ * are re-packed into library-owned device memory (QKV fused, conv taps
+ * transposed, all AdaLN linears stacked), so the caller's buffers may be freed
+ * afterwards.  Replaces build_dit + ggml_backend_alloc_ctx_tensors
+ * (src/flow/dit.cpp:83-145; src/flow/flow.cpp:184-200). */
+int lx_dit_create(const lx_dit_weights* w, int B, int max_T, lx_dit** out);
+void lx_dit_destroy(lx_dit* dit);
+
+/* One estimator forward (DiT.forward):
+ *   x, mu, cond: (B, mel, T) ("Space A", torch (B, C, T)); spks: (B, mel);
+ *   t: device float[B] timesteps in [0, 1]; dphi out: (B, mel, T).
+ * The time embedding is computed on the device from t.
+ * Replaces one ggml_backend_graph_compute of the DiT graph
+ * (src/flow/flow.cpp:244-254) with its host time_embed_host. */
+int lx_dit_forward(lx_dit* dit, const float* x, const float* mu, const float* cond,
+                   const float* spks, const float* t, float* dphi, int T,
+                   hipStream_t stream);
+
+/* Stage capture for parity tests (FlowDebug, include/larynx/flow/flow.h:15-34).
+ * When non-NULL, the next lx_dit_forward calls write: time_embed (B, D),
+ * input_proj / conv_pos / input_embed (B, T, D), blocks (depth, B, T, D),
+ * norm_out (B, T, D).  Pass NULL pointers to disable each. */
+typedef struct lx_dit_capture {
+  float* time_embed; float* input_proj; float* conv_pos; float* input_embed;
+  float* blocks; float* norm_out;
+} lx_dit_capture;
+int lx_dit_set_capture(lx_dit* dit, const lx_dit_capture* cap);
+
+/* Full CFM Euler solve with classifier-free guidance, device resident
+ * (CausalConditionalCFM.solve_euler; src/flow/flow.cpp:202-274):
+ *   t_span = 1 - cos(linspace(0,1,n_steps+1) * pi/2)
+ *   per step: dphi = est([x;x], [mu;0], [spks;0], [cond;0], [t;t])
+ *             x += dt * ((1+cfg) dphi[0] - cfg dphi[1])
+ * x: in/out (mel, T) — the initial noise z on entry, the solution on return;
+ * mu, cond: (mel, T); spks: (mel).  The estimator must have B == 2. */
+int lx_cfm_solve(lx_dit* dit, float* x, const float* mu, const float* cond,
+                 const float* spks, int T, int n_steps, float cfg_rate,
+                 hipStream_t stream);
+
+/* One Euler step of the above, for timing and resumable loops:
+ * t and dt are host scalars. */
+int lx_cfm_step(lx_dit* dit, float* x, const float* mu, const float* cond,
+                const float* spks, int T, float t, float dt, float cfg_rate,
+                hipStream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* Qwen2 LM (host C++ over the ops above; device-resident KV cache)          */
+/* ------------------------------------------------------------------------ */
+
+/* Mirrors LLMWeights::Layer (src/llm/internal.h:48-61), torch layout. */
+typedef struct lx_qwen2_layer_weights {
+  const float* q_w; const float* q_b;        /* (H, H), (H)          */
+  const float* k_w; const float* k_b;        /* (KV, H), (KV)        */
+  const float* v_w; const float* v_b;        /* (KV, H), (KV)        */
+  const float* o_w;                          /* (H, H)               */
+  const float* gate_w; const float* up_w;    /* (I, H)               */
+  const float* down_w;                       /* (H, I)               */
+  const float* in_norm; const float* post_norm; /* (H)               */
+} lx_qwen2_layer_weights;
+
+typedef struct lx_qwen2_weights {
+  int hidden, intermediate, n_heads, n_kv_heads, head_dim, n_layers;
+  int text_vocab, speech_vocab;
+  float rms_eps, rope_theta;
+  const float* embed_tokens;                 /* (text_vocab, H)      */
+  const float* speech_embedding;             /* (speech_vocab, H)    */
+  const float* final_norm;                   /* (H)                  */
+  const float* llm_decoder;                  /* (speech_vocab, H)    */
+  const lx_qwen2_layer_weights* layers;      /* HOST array [n_layers]*/
+} lx_qwen2_weights;
+
+typedef struct lx_qwen2 lx_qwen2;
+
+/* Replaces LLM::load's weight upload (src/llm/llm.cpp:50-61); the tables are
+ * referenced, the layer weights re-packed (QKV fused, gate/up interleaved).
+ * max_ctx bounds prompt + generated tokens (KV cache capacity). */
+int lx_qwen2_create(const lx_qwen2_weights* w, int max_ctx, lx_qwen2** out);
+void lx_qwen2_destroy(lx_qwen2* m);
+
+/* LLM::build_lm_input (src/llm/llm.cpp:63-100): lm_input (L, H) =
+ * [speech_emb[6561]; embed_tokens[text...]; speech_emb[6563];
+ *  speech_emb[prompt_speech...]].  Ids are HOST arrays, all validated first
+ * (LX_ERR_RANGE on any bad id).  L_out receives L.  out: device (L, H). */
+int lx_qwen2_build_lm_input(lx_qwen2* m, const int* text_tokens, int n_text,
+                            const int* prompt_speech, int n_speech, float* out, int* L_out,
+                            hipStream_t stream);
+
+/* LLM::prefill (src/llm/llm.cpp:102-216): causal 24-layer pass over lm_input
+ * (L, H) (device), resets and fills the KV cache.  logits (L, speech_vocab)
+ * device, may be NULL; hidden (n_layers, L, H) and final_norm (L, H) capture
+ * buffers may be NULL. */
+int lx_qwen2_prefill(lx_qwen2* m, const float* lm_input, int L, float* logits,
+                     float* hidden, float* final_norm, hipStream_t stream);
+
+/* LLM::decode (src/llm/llm.cpp:218-327): one token (HOST id in
+ * [0, speech_vocab)) at position cache_len, appends to the device KV cache.
+ * logits: device (speech_vocab); final_norm: device (H) or NULL. */
+int lx_qwen2_decode(lx_qwen2* m, int token, float* logits, float* final_norm,
+                    hipStream_t stream);
+
+/* LLM::cache_len / cache_key / cache_value (include/larynx/llm/llm.h:77-84).
+ * The cache of layer l is (cache_len, n_kv_heads * head_dim) roped keys /
+ * raw values on the device; pointers stay valid until destroy. */
+int lx_qwen2_cache_len(const lx_qwen2* m);
+const float* lx_qwen2_cache_key(const lx_qwen2* m, int layer);
+const float* lx_qwen2_cache_value(const lx_qwen2* m, int layer);
+/* Sets cache_len (<= max_ctx) without touching the contents, so a caller can
+ * load a synthetic cache through the pointers above (benchmarks, tests). */
+int lx_qwen2_set_cache_len(lx_qwen2* m, int len);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LX_OPS_H */

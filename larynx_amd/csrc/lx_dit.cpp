@@ -1,0 +1,395 @@
+// CosyVoice3 Flow DiT estimator and CFM Euler/CFG loop, device resident.
+//
+// Host-side counterpart of build_dit / dit_block (src/flow/dit.cpp:34-145) and
+// of the CFM loop of FlowDecoder::infer (src/flow/flow.cpp:202-274).  Instead
+// of a ~8000-node ggml graph the forward is ~10 launches per block:
+//
+//   adaln(x) -> QKV GEMM (+bias, +partial rotary epilogue) -> flash attention
+//   -> out GEMM (+bias, gated-residual epilogue into x) -> adaln(x)
+//   -> FF0 GEMM (+bias, tanh-GELU epilogue) -> FF2 GEMM (+bias, gated residual)
+//
+// and per Euler step the 22 AdaLN modulation linears plus norm_out's are one
+// stacked weight-streaming GEMV (t is shared by both CFG rows and all frames).
+// Nothing crosses PCIe inside the loop: the timestep is written by a fill
+// kernel and the CFG combine + Euler update reads the proj_out rows directly.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstring>
+#include <new>
+#include <vector>
+
+#include "lx_common.hpp"
+#include "lx_internal.hpp"
+
+using namespace lx;
+
+namespace {
+
+constexpr int kFreqDim = 256;      // SinusPositionEmbedding(256)
+constexpr int kConvK = 31;         // CONV_POS_KERNEL (src/flow/internal.h:32)
+constexpr int kConvG = 16;         // CONV_POS_GROUPS (src/flow/internal.h:33)
+constexpr float kLnEps = 1e-6f;    // LN_EPS (src/flow/internal.h:34)
+constexpr float kRopeBase = 10000.0f;  // ROPE_FREQ_BASE (src/flow/internal.h:35)
+constexpr int kRotDim = 64;        // ROT_DIM (src/flow/internal.h:25)
+
+#define LX_TRY(expr)         \
+  do {                       \
+    int _rc = (expr);        \
+    if (_rc != LX_OK) return _rc; \
+  } while (0)
+
+struct Arena {
+  std::vector<void*> ptrs;
+  ~Arena() {
+    for (void* p : ptrs) (void)hipFree(p);
+  }
+  template <typename T>
+  T* alloc(size_t n) {
+    void* p = nullptr;
+    if (n == 0) n = 1;
+    if (hipMalloc(&p, n * sizeof(T)) != hipSuccess) return nullptr;
+    ptrs.push_back(p);
+    return static_cast<T*>(p);
+  }
+};
+
+}  // namespace
+
+struct lx_dit {
+  Arena arena;
+  int B = 0, max_T = 0;
+  int D = 0, depth = 0, heads = 0, hd = 0, F = 0, mel = 0;
+  long NA = 0;  // stacked AdaLN rows: depth * 6D + 2D
+
+  // packed weights
+  float *tm0_w, *tm0_b, *tm2_w, *tm2_b;
+  float *in_w, *in_b;
+  float *conv1_wp, *conv1_b, *conv2_wp, *conv2_b;
+  float *ada_w, *ada_b;                 // (NA, D), (NA)
+  std::vector<float*> qkv_w, qkv_b;     // (3D, D), (3D)
+  std::vector<float*> out_w, out_b, ff0_w, ff0_b, ff2_w, ff2_b;
+  float *proj_w, *proj_b;
+
+  // activations (sized for B x max_T)
+  float *t_dev, *temb, *tmlp_work, *emb;
+  float *A0, *xe, *c1, *h, *xn, *qkv, *att, *ff, *P;
+  int* pos;
+  // CFM (B == 2) inputs
+  float *x_in, *mu_in, *cond_in, *spks_in;
+
+  lx_dit_capture cap{};
+  hipStream_t create_stream = nullptr;
+};
+
+namespace {
+
+int copy_d2d(float* dst, const float* src, size_t n, hipStream_t s) {
+  if (!src) {
+    set_error("dit_create: missing weight tensor");
+    return LX_ERR_ARG;
+  }
+  if (hipMemcpyAsync(dst, src, n * sizeof(float), hipMemcpyDeviceToDevice, s) != hipSuccess) {
+    set_error("dit_create: device copy failed");
+    return LX_ERR_LAUNCH;
+  }
+  return LX_OK;
+}
+
+// Everything up to the proj_out rows P (B*T, mel).
+int forward_core(lx_dit* m, const float* x, const float* mu, const float* cond, const float* spks,
+                 const float* t, int T, hipStream_t s) {
+  const int B = m->B, D = m->D, mel = m->mel;
+  const int rows = B * T;
+  // Time embedding (a6) and every AdaLN modulation of this step in one GEMV.
+  LX_TRY(lx_time_mlp_f32(t, B, m->tm0_w, m->tm0_b, m->tm2_w, m->tm2_b, D, m->tmlp_work,
+                         m->temb, s));
+  LX_TRY(gemv(m->temb, B, D, m->ada_w, m->ada_b, m->emb, m->NA, m->NA, /*silu in*/ 1, 0, s));
+  if (m->cap.time_embed)
+    (void)hipMemcpyAsync(m->cap.time_embed, m->temb, sizeof(float) * B * D,
+                         hipMemcpyDeviceToDevice, s);
+
+  // InputEmbedding: proj(concat[x, cond, mu, spks]) + conv_pos_embed.
+  LX_TRY(dit_pack_input(x, cond, mu, spks, m->A0, B, T, mel, s));
+  LX_TRY(lx_linear_f32(m->A0, 4 * mel, m->in_w, m->in_b, m->xe, D, rows, D, 4 * mel, nullptr, s));
+  LX_TRY(conv_pos_mish_packed(m->xe, m->conv1_wp, m->conv1_b, nullptr, m->c1, B, T, D, kConvG,
+                              kConvK, s));
+  // h = xe + mish(conv2(c1)); c1 doubles as the conv_pos capture source below.
+  LX_TRY(conv_pos_mish_packed(m->c1, m->conv2_wp, m->conv2_b, m->xe, m->h, B, T, D, kConvG, kConvK,
+                              s));
+  if (m->cap.input_proj)
+    (void)hipMemcpyAsync(m->cap.input_proj, m->xe, sizeof(float) * rows * D,
+                         hipMemcpyDeviceToDevice, s);
+  if (m->cap.conv_pos) {
+    // conv_pos = h - xe is not recomputed; re-run conv2 without the residual.
+    LX_TRY(conv_pos_mish_packed(m->c1, m->conv2_wp, m->conv2_b, nullptr, m->xn, B, T, D, kConvG,
+                                kConvK, s));
+    (void)hipMemcpyAsync(m->cap.conv_pos, m->xn, sizeof(float) * rows * D,
+                         hipMemcpyDeviceToDevice, s);
+  }
+  if (m->cap.input_embed)
+    (void)hipMemcpyAsync(m->cap.input_embed, m->h, sizeof(float) * rows * D,
+                         hipMemcpyDeviceToDevice, s);
+
+  const long NA = m->NA;
+  for (int i = 0; i < m->depth; ++i) {
+    const float* e = m->emb + (long)i * 6 * D;  // chunk order: shift, scale, gate (msa), (mlp)
+    const float* shift_msa = e;
+    const float* scale_msa = e + D;
+    const float* gate_msa = e + 2 * D;
+    const float* shift_mlp = e + 3 * D;
+    const float* scale_mlp = e + 4 * D;
+    const float* gate_mlp = e + 5 * D;
+
+    LX_TRY(lx_adaln_modulate_f32(m->h, shift_msa, scale_msa, NA, m->xn, B, T, D, kLnEps, s));
+    lx_epilogue rope{};
+    rope.kind = LX_EPI_ROPE_PARTIAL;
+    rope.rows_per_batch = T;
+    rope.pos = m->pos;
+    rope.rot_dim = kRotDim;
+    rope.rope_section = D;   // q occupies columns [0, D), k [D, 2D)
+    rope.rope_sections = 2;
+    rope.rope_base = kRopeBase;
+    LX_TRY(lx_linear_f32(m->xn, D, m->qkv_w[i], m->qkv_b[i], m->qkv, 3 * D, rows, 3 * D, D, &rope,
+                         s));
+    LX_TRY(lx_attention_f32(m->qkv, 3 * D, m->qkv + D, 3 * D, m->qkv + 2 * D, 3 * D, m->att, D, B,
+                            T, T, m->heads, m->heads, m->hd, 1.0f / std::sqrt((float)m->hd), 0, 0,
+                            s));
+    lx_epilogue gated{};
+    gated.kind = LX_EPI_GATED_RESID;
+    gated.rows_per_batch = T;
+    gated.gate = gate_msa;
+    gated.gate_stride = NA;
+    LX_TRY(lx_linear_f32(m->att, D, m->out_w[i], m->out_b[i], m->h, D, rows, D, D, &gated, s));
+
+    LX_TRY(lx_adaln_modulate_f32(m->h, shift_mlp, scale_mlp, NA, m->xn, B, T, D, kLnEps, s));
+    lx_epilogue gelu{};
+    gelu.kind = LX_EPI_GELU_TANH;
+    LX_TRY(lx_linear_f32(m->xn, D, m->ff0_w[i], m->ff0_b[i], m->ff, m->F, rows, m->F, D, &gelu, s));
+    gated.gate = gate_mlp;
+    LX_TRY(lx_linear_f32(m->ff, m->F, m->ff2_w[i], m->ff2_b[i], m->h, D, rows, D, m->F, &gated, s));
+    if (m->cap.blocks)
+      (void)hipMemcpyAsync(m->cap.blocks + (long)i * rows * D, m->h, sizeof(float) * rows * D,
+                           hipMemcpyDeviceToDevice, s);
+  }
+  // norm_out (AdaLayerNormZero_Final): chunk order scale, shift (src/flow/dit.cpp:134-135).
+  const float* ef = m->emb + (long)m->depth * 6 * D;
+  LX_TRY(lx_adaln_modulate_f32(m->h, /*shift*/ ef + D, /*scale*/ ef, NA, m->xn, B, T, D, kLnEps, s));
+  if (m->cap.norm_out)
+    (void)hipMemcpyAsync(m->cap.norm_out, m->xn, sizeof(float) * rows * D, hipMemcpyDeviceToDevice,
+                         s);
+  LX_TRY(lx_linear_f32(m->xn, D, m->proj_w, m->proj_b, m->P, mel, rows, mel, D, nullptr, s));
+  return check_launch("dit forward");
+}
+
+}  // namespace
+
+extern "C" int lx_dit_create(const lx_dit_weights* w, int B, int max_T, lx_dit** out) {
+  LX_REQUIRE(w && out, "dit_create: null argument");
+  *out = nullptr;
+  LX_REQUIRE(B >= 1 && B <= 8 && max_T >= 1, "dit_create: B=%d max_T=%d", B, max_T);
+  LX_REQUIRE(w->dim > 0 && w->dim % 64 == 0 && w->depth >= 1 && w->heads >= 1 &&
+                 w->head_dim == 64 && w->heads * w->head_dim == w->dim && w->ff_inner > 0 &&
+                 w->ff_inner % 4 == 0 && w->mel_dim > 0 && w->mel_dim % 4 == 0,
+             "dit_create: unsupported geometry dim=%d heads=%d head_dim=%d ff=%d mel=%d",
+             w->dim, w->heads, w->head_dim, w->ff_inner, w->mel_dim);
+  LX_REQUIRE(w->dim / kConvG == 64, "dit_create: conv_pos needs dim/16 == 64");
+  LX_REQUIRE(w->blocks, "dit_create: blocks array is NULL");
+  lx_dit* m = new (std::nothrow) lx_dit();
+  if (!m) return LX_ERR_ALLOC;
+  m->B = B;
+  m->max_T = max_T;
+  m->D = w->dim;
+  m->depth = w->depth;
+  m->heads = w->heads;
+  m->hd = w->head_dim;
+  m->F = w->ff_inner;
+  m->mel = w->mel_dim;
+  const int D = m->D, F = m->F, mel = m->mel, depth = m->depth;
+  m->NA = (long)depth * 6 * D + 2 * D;
+  Arena& a = m->arena;
+  bool ok = true;
+  auto A = [&](size_t n) {
+    float* p = a.alloc<float>(n);
+    ok = ok && p;
+    return p;
+  };
+  m->tm0_w = A((size_t)D * kFreqDim);
+  m->tm0_b = A(D);
+  m->tm2_w = A((size_t)D * D);
+  m->tm2_b = A(D);
+  m->in_w = A((size_t)D * 4 * mel);
+  m->in_b = A(D);
+  m->conv1_wp = A((size_t)D * 64 * kConvK);
+  m->conv1_b = A(D);
+  m->conv2_wp = A((size_t)D * 64 * kConvK);
+  m->conv2_b = A(D);
+  m->ada_w = A((size_t)m->NA * D);
+  m->ada_b = A(m->NA);
+  for (int i = 0; i < depth; ++i) {
+    m->qkv_w.push_back(A((size_t)3 * D * D));
+    m->qkv_b.push_back(A((size_t)3 * D));
+    m->out_w.push_back(A((size_t)D * D));
+    m->out_b.push_back(A(D));
+    m->ff0_w.push_back(A((size_t)F * D));
+    m->ff0_b.push_back(A(F));
+    m->ff2_w.push_back(A((size_t)D * F));
+    m->ff2_b.push_back(A(D));
+  }
+  m->proj_w = A((size_t)mel * D);
+  m->proj_b = A(mel);
+  const size_t rows = (size_t)B * max_T;
+  m->t_dev = A(B);
+  m->temb = A((size_t)B * D);
+  m->tmlp_work = A((size_t)B * (kFreqDim + D));
+  m->emb = A((size_t)B * m->NA);
+  m->A0 = A(rows * 4 * mel);
+  m->xe = A(rows * D);
+  m->c1 = A(rows * D);
+  m->h = A(rows * D);
+  m->xn = A(rows * D);
+  m->qkv = A(rows * 3 * D);
+  m->att = A(rows * D);
+  m->ff = A(rows * F);
+  m->P = A(rows * mel);
+  m->pos = a.alloc<int>(max_T);
+  ok = ok && m->pos;
+  m->x_in = A((size_t)2 * mel * max_T);
+  m->mu_in = A((size_t)2 * mel * max_T);
+  m->cond_in = A((size_t)2 * mel * max_T);
+  m->spks_in = A((size_t)2 * mel);
+  if (!ok) {
+    delete m;
+    set_error("dit_create: device allocation failed");
+    return LX_ERR_ALLOC;
+  }
+
+  hipStream_t s = nullptr;
+  if (hipStreamCreate(&s) != hipSuccess) {
+    delete m;
+    set_error("dit_create: stream creation failed");
+    return LX_ERR_LAUNCH;
+  }
+  int rc = LX_OK;
+  auto C = [&](float* dst, const float* src, size_t n) {
+    if (rc == LX_OK) rc = copy_d2d(dst, src, n, s);
+  };
+  C(m->tm0_w, w->time_mlp_0_w, (size_t)D * kFreqDim);
+  C(m->tm0_b, w->time_mlp_0_b, D);
+  C(m->tm2_w, w->time_mlp_2_w, (size_t)D * D);
+  C(m->tm2_b, w->time_mlp_2_b, D);
+  C(m->in_w, w->input_proj_w, (size_t)D * 4 * mel);
+  C(m->in_b, w->input_proj_b, D);
+  C(m->conv1_b, w->conv_pos_1_b, D);
+  C(m->conv2_b, w->conv_pos_2_b, D);
+  if (rc == LX_OK) rc = (w->conv_pos_1_w && w->conv_pos_2_w) ? LX_OK : LX_ERR_ARG;
+  if (rc == LX_OK) rc = conv_weight_pack(w->conv_pos_1_w, m->conv1_wp, D, kConvG, kConvK, s);
+  if (rc == LX_OK) rc = conv_weight_pack(w->conv_pos_2_w, m->conv2_wp, D, kConvG, kConvK, s);
+  for (int i = 0; i < depth && rc == LX_OK; ++i) {
+    const lx_dit_block_weights& bw = w->blocks[i];
+    C(m->ada_w + (size_t)i * 6 * D * D, bw.attn_norm_w, (size_t)6 * D * D);
+    C(m->ada_b + (size_t)i * 6 * D, bw.attn_norm_b, (size_t)6 * D);
+    C(m->qkv_w[i], bw.to_q_w, (size_t)D * D);
+    C(m->qkv_w[i] + (size_t)D * D, bw.to_k_w, (size_t)D * D);
+    C(m->qkv_w[i] + (size_t)2 * D * D, bw.to_v_w, (size_t)D * D);
+    C(m->qkv_b[i], bw.to_q_b, D);
+    C(m->qkv_b[i] + D, bw.to_k_b, D);
+    C(m->qkv_b[i] + 2 * D, bw.to_v_b, D);
+    C(m->out_w[i], bw.to_out_w, (size_t)D * D);
+    C(m->out_b[i], bw.to_out_b, D);
+    C(m->ff0_w[i], bw.ff0_w, (size_t)F * D);
+    C(m->ff0_b[i], bw.ff0_b, F);
+    C(m->ff2_w[i], bw.ff2_w, (size_t)D * F);
+    C(m->ff2_b[i], bw.ff2_b, D);
+  }
+  C(m->ada_w + (size_t)depth * 6 * D * D, w->norm_out_w, (size_t)2 * D * D);
+  C(m->ada_b + (size_t)depth * 6 * D, w->norm_out_b, (size_t)2 * D);
+  C(m->proj_w, w->proj_out_w, (size_t)mel * D);
+  C(m->proj_b, w->proj_out_b, mel);
+  if (rc == LX_OK) rc = iota_i32(m->pos, max_T, s);
+  if (rc == LX_OK && hipStreamSynchronize(s) != hipSuccess) {
+    set_error("dit_create: weight packing failed");
+    rc = LX_ERR_LAUNCH;
+  }
+  (void)hipStreamDestroy(s);
+  if (rc != LX_OK) {
+    if (rc == LX_ERR_ARG) set_error("dit_create: missing weight tensor");
+    delete m;
+    return rc;
+  }
+  *out = m;
+  return LX_OK;
+}
+
+extern "C" void lx_dit_destroy(lx_dit* dit) {
+  if (!dit) return;
+  (void)hipDeviceSynchronize();
+  delete dit;
+}
+
+extern "C" int lx_dit_set_capture(lx_dit* dit, const lx_dit_capture* cap) {
+  LX_REQUIRE(dit, "dit_set_capture: null estimator");
+  if (cap)
+    dit->cap = *cap;
+  else
+    dit->cap = lx_dit_capture{};
+  return LX_OK;
+}
+
+extern "C" int lx_dit_forward(lx_dit* m, const float* x, const float* mu, const float* cond,
+                              const float* spks, const float* t, float* dphi, int T,
+                              hipStream_t s) {
+  LX_REQUIRE(m && x && mu && cond && spks && t && dphi, "dit_forward: null argument");
+  LX_REQUIRE(T >= 1 && T <= m->max_T, "dit_forward: T=%d outside [1, %d]", T, m->max_T);
+  LX_TRY(forward_core(m, x, mu, cond, spks, t, T, s));
+  return dit_unpack_output(m->P, dphi, m->B, T, m->mel, s);
+}
+
+extern "C" int lx_cfm_step(lx_dit* m, float* x, const float* mu, const float* cond,
+                           const float* spks, int T, float t, float dt, float cfg_rate,
+                           hipStream_t s) {
+  LX_REQUIRE(m && x && mu && cond && spks, "cfm_step: null argument");
+  LX_REQUIRE(m->B == 2, "cfm_step: the estimator must be built with B == 2 (CFG pair)");
+  LX_REQUIRE(T >= 1 && T <= m->max_T, "cfm_step: T=%d outside [1, %d]", T, m->max_T);
+  const long n = (long)m->mel * T;
+  // Batch-2 inputs: conditional row 0, unconditional row 1 (= 0) (src/flow/flow.cpp:215-224).
+  LX_TRY(fill_batch(m->x_in, x, n, 2, 0, s));
+  LX_TRY(fill_batch(m->mu_in, mu, n, 2, 1, s));
+  LX_TRY(fill_batch(m->cond_in, cond, n, 2, 1, s));
+  LX_TRY(fill_batch(m->spks_in, spks, m->mel, 2, 1, s));
+  LX_TRY(fill_f32(m->t_dev, 2, t, s));
+  LX_TRY(forward_core(m, m->x_in, m->mu_in, m->cond_in, m->spks_in, m->t_dev, T, s));
+  // combined = (1+cfg) dphi_cond - cfg dphi_uncond; x += dt * combined (flow.cpp:256-259)
+  return cfm_euler_update(x, m->P, T, m->mel, dt, 1.0f + cfg_rate, cfg_rate, s);
+}
+
+extern "C" int lx_cfm_solve(lx_dit* m, float* x, const float* mu, const float* cond,
+                            const float* spks, int T, int n_steps, float cfg_rate,
+                            hipStream_t s) {
+  LX_REQUIRE(m && x && mu && cond && spks, "cfm_solve: null argument");
+  LX_REQUIRE(n_steps >= 1 && n_steps <= 1000, "cfm_solve: n_steps=%d", n_steps);
+  LX_REQUIRE(m->B == 2, "cfm_solve: the estimator must be built with B == 2 (CFG pair)");
+  LX_REQUIRE(T >= 1 && T <= m->max_T, "cfm_solve: T=%d outside [1, %d]", T, m->max_T);
+  // t_span = 1 - cos(linspace(0, 1, n+1) * pi/2), evaluated as src/flow/flow.cpp:203-207.
+  const float PI = 3.14159265358979323846f;
+  std::vector<float> t_span(n_steps + 1);
+  for (int i = 0; i <= n_steps; ++i) {
+    float tt = (float)i / (float)n_steps;
+    t_span[i] = 1.0f - cosf(tt * 0.5f * PI);
+  }
+  const long n = (long)m->mel * T;
+  LX_TRY(fill_batch(m->mu_in, mu, n, 2, 1, s));
+  LX_TRY(fill_batch(m->cond_in, cond, n, 2, 1, s));
+  LX_TRY(fill_batch(m->spks_in, spks, m->mel, 2, 1, s));
+  float t = t_span[0];
+  float dt = t_span[1] - t_span[0];
+  for (int step = 1; step <= n_steps; ++step) {
+    LX_TRY(fill_batch(m->x_in, x, n, 2, 0, s));
+    LX_TRY(fill_f32(m->t_dev, 2, t, s));
+    LX_TRY(forward_core(m, m->x_in, m->mu_in, m->cond_in, m->spks_in, m->t_dev, T, s));
+    LX_TRY(cfm_euler_update(x, m->P, T, m->mel, dt, 1.0f + cfg_rate, cfg_rate, s));
+    t += dt;
+    if (step < n_steps) dt = t_span[step + 1] - t;
+  }
+  return LX_OK;
+}

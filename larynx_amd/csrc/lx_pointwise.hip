@@ -1,0 +1,284 @@
+// Pointwise / gather ops of the DiT block and the Qwen2 layer.  Each kernel
+// is a single HBM pass: float4 loads and stores, grid-stride loops sized to
+// keep every CU busy, tables (rotary inverse frequencies, sinusoid
+// coefficients, token ids) passed by value in the kernel arguments.
+#include <cmath>
+#include <cstring>
+
+#include "lx_common.hpp"
+
+namespace lx {
+
+void rope_inv_freq(float base, int dim, float* out) {
+  for (int i = 0; i < dim / 2; ++i) {
+    float e = (float)(2 * i) / (float)dim;
+    float p = (float)std::pow((double)base, (double)e);
+    out[i] = 1.0f / p;
+  }
+}
+
+namespace {
+
+template <int N>
+struct Table {
+  float v[N];
+};
+
+constexpr int kGatherChunk = 240;  // ids per launch: 960 bytes of kernel arguments
+struct IdChunk {
+  int id[kGatherChunk];
+};
+
+inline int grid_for(long work, int block) {
+  long g = (work + block - 1) / block;
+  // 256 CUs x 8 resident blocks is plenty to saturate HBM; beyond that the
+  // grid-stride loop takes over.
+  if (g > 2048) g = 2048;
+  if (g < 1) g = 1;
+  return (int)g;
+}
+
+__global__ void gelu_kernel(const float* h, float* y, long n4, long n) {
+  const long stride = (long)gridDim.x * blockDim.x;
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride) {
+    float4 v = reinterpret_cast<const float4*>(h)[i];
+    v.x = gelu_tanh(v.x);
+    v.y = gelu_tanh(v.y);
+    v.z = gelu_tanh(v.z);
+    v.w = gelu_tanh(v.w);
+    reinterpret_cast<float4*>(y)[i] = v;
+  }
+  // scalar tail (n not a multiple of 4)
+  long t = n4 * 4 + (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t < n) y[t] = gelu_tanh(h[t]);
+}
+
+__global__ void gated_residual_kernel(float* x, const float* __restrict__ y,
+                                      const float* __restrict__ gate, long gate_stride,
+                                      long rows, int T, int D4) {
+  const long n4 = rows * D4;
+  const long stride = (long)gridDim.x * blockDim.x;
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride) {
+    long row = i / D4;
+    int c4 = (int)(i - row * D4);
+    int b = (int)(row / T);
+    float4 g = reinterpret_cast<const float4*>(gate + (long)b * gate_stride)[c4];
+    float4 a = reinterpret_cast<float4*>(x)[i];
+    float4 v = reinterpret_cast<const float4*>(y)[i];
+    a.x += v.x * g.x;
+    a.y += v.y * g.y;
+    a.z += v.z * g.z;
+    a.w += v.w * g.w;
+    reinterpret_cast<float4*>(x)[i] = a;
+  }
+}
+
+__device__ __forceinline__ float silu_mul(float g, float u) { return (g / (1.0f + expf(-g))) * u; }
+
+__global__ void swiglu_kernel(const float* __restrict__ gate, const float* __restrict__ up,
+                              float* out, long n4, long n) {
+  const long stride = (long)gridDim.x * blockDim.x;
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride) {
+    float4 g = reinterpret_cast<const float4*>(gate)[i];
+    float4 u = reinterpret_cast<const float4*>(up)[i];
+    float4 o;
+    o.x = silu_mul(g.x, u.x);
+    o.y = silu_mul(g.y, u.y);
+    o.z = silu_mul(g.z, u.z);
+    o.w = silu_mul(g.w, u.w);
+    reinterpret_cast<float4*>(out)[i] = o;
+  }
+  long t = n4 * 4 + (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t < n) out[t] = silu_mul(gate[t], up[t]);
+}
+
+// Partial interleaved rotary: thread = (row, pair).  blockIdx.y selects q / k.
+__global__ void rope_partial_kernel(float* q, float* k, const int* __restrict__ pos,
+                                    long rows, int T, int ld, int half, Table<64> inv) {
+  float* base = blockIdx.y == 0 ? q : k;
+  const long n = rows * half;
+  const long stride = (long)gridDim.x * blockDim.x;
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    long row = i / half;
+    int p = (int)(i - row * half);
+    int t = (int)(row % T);
+    float ang = (float)pos[t] * inv.v[p];
+    float s, c;
+    sincosf(ang, &s, &c);
+    float2* ptr = reinterpret_cast<float2*>(base + row * ld) + p;
+    float2 x = *ptr;
+    float2 o;
+    o.x = x.x * c - x.y * s;
+    o.y = x.y * c + x.x * s;
+    *ptr = o;
+  }
+}
+
+// NEOX rotary: thread = (row, head, pair); pair (i, i + hd/2).
+__global__ void rope_neox_kernel(float* qk, const int* __restrict__ pos, long rows,
+                                 int n_heads, int hd, int ld, Table<64> inv) {
+  const int half = hd / 2;
+  const long n = rows * n_heads * half;
+  const long stride = (long)gridDim.x * blockDim.x;
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    long row = i / (n_heads * half);
+    int rem = (int)(i - row * (n_heads * half));
+    int h = rem / half;
+    int p = rem - h * half;
+    float ang = (float)pos[row] * inv.v[p];
+    float s, c;
+    sincosf(ang, &s, &c);
+    float* ptr = qk + row * ld + h * hd + p;
+    float x0 = ptr[0], x1 = ptr[half];
+    ptr[0] = x0 * c - x1 * s;
+    ptr[half] = x1 * c + x0 * s;
+  }
+}
+
+__global__ void timestep_kernel(const float* __restrict__ t, int B, int half, float scale,
+                                float* out, Table<256> coeff) {
+  int b = blockIdx.x;
+  float ts = scale * t[b];
+  for (int j = threadIdx.x; j < half; j += blockDim.x) {
+    float ang = ts * coeff.v[j];
+    float s, c;
+    sincosf(ang, &s, &c);
+    out[(long)b * 2 * half + j] = s;
+    out[(long)b * 2 * half + half + j] = c;
+  }
+}
+
+// Gather: block per output row; bit-exact float copies.
+__global__ void gather_kernel4(const float4* __restrict__ table, int D4, IdChunk ids,
+                               float4* out) {
+  const float4* src = table + (long)ids.id[blockIdx.x] * D4;
+  float4* dst = out + (long)blockIdx.x * D4;
+  for (int i = threadIdx.x; i < D4; i += blockDim.x) dst[i] = src[i];
+}
+
+__global__ void gather_kernel1(const float* __restrict__ table, int D, IdChunk ids,
+                               float* out) {
+  const float* src = table + (long)ids.id[blockIdx.x] * D;
+  float* dst = out + (long)blockIdx.x * D;
+  for (int i = threadIdx.x; i < D; i += blockDim.x) dst[i] = src[i];
+}
+
+}  // namespace
+}  // namespace lx
+
+using namespace lx;
+
+extern "C" int lx_gelu_tanh_f32(const float* h, float* y, long n, hipStream_t stream) {
+  LX_REQUIRE(h && y && n >= 0, "gelu: bad args");
+  LX_REQUIRE(((uintptr_t)h | (uintptr_t)y) % 16 == 0, "gelu: pointers must be 16-byte aligned");
+  if (n == 0) return LX_OK;
+  long n4 = n / 4;
+  hipLaunchKernelGGL(gelu_kernel, dim3(grid_for(n4 > 0 ? n4 : 1, 256)), dim3(256), 0, stream, h,
+                     y, n4, n);
+  return check_launch("gelu_kernel");
+}
+
+extern "C" int lx_gated_residual_f32(float* x, const float* y, const float* gate,
+                                     long gate_stride, int B, int T, int D,
+                                     hipStream_t stream) {
+  LX_REQUIRE(x && y && gate, "gated_residual: null pointer");
+  LX_REQUIRE(B > 0 && T > 0 && D > 0 && D % 4 == 0, "gated_residual: bad shape");
+  LX_REQUIRE(gate_stride >= D && gate_stride % 4 == 0, "gated_residual: bad gate_stride");
+  LX_REQUIRE(((uintptr_t)x | (uintptr_t)y | (uintptr_t)gate) % 16 == 0,
+             "gated_residual: pointers must be 16-byte aligned");
+  long rows = (long)B * T;
+  hipLaunchKernelGGL(gated_residual_kernel, dim3(grid_for(rows * D / 4, 256)), dim3(256), 0,
+                     stream, x, y, gate, gate_stride, rows, T, D / 4);
+  return check_launch("gated_residual_kernel");
+}
+
+extern "C" int lx_swiglu_f32(const float* gate, const float* up, float* out, long n,
+                             hipStream_t stream) {
+  LX_REQUIRE(gate && up && out && n >= 0, "swiglu: bad args");
+  LX_REQUIRE(((uintptr_t)gate | (uintptr_t)up | (uintptr_t)out) % 16 == 0,
+             "swiglu: pointers must be 16-byte aligned");
+  if (n == 0) return LX_OK;
+  long n4 = n / 4;
+  hipLaunchKernelGGL(swiglu_kernel, dim3(grid_for(n4 > 0 ? n4 : 1, 256)), dim3(256), 0, stream,
+                     gate, up, out, n4, n);
+  return check_launch("swiglu_kernel");
+}
+
+extern "C" int lx_rope_partial_interleaved_f32(float* q, float* k, const int* pos, int B,
+                                               int T, int ld, int rot_dim, float base,
+                                               hipStream_t stream) {
+  LX_REQUIRE(q && pos, "rope_partial: null pointer");
+  LX_REQUIRE(B > 0 && T > 0, "rope_partial: bad shape");
+  LX_REQUIRE(rot_dim > 0 && rot_dim % 2 == 0 && rot_dim <= 128 && rot_dim <= ld,
+             "rope_partial: rot_dim=%d must be even, <= 128 and <= ld=%d", rot_dim, ld);
+  LX_REQUIRE(((uintptr_t)q % 8 == 0) && (k == nullptr || (uintptr_t)k % 8 == 0) && ld % 2 == 0,
+             "rope_partial: pairs must be 8-byte aligned");
+  Table<64> inv;
+  std::memset(&inv, 0, sizeof(inv));
+  rope_inv_freq(base, rot_dim, inv.v);
+  long rows = (long)B * T;
+  int half = rot_dim / 2;
+  dim3 grid(grid_for(rows * half, 256), k ? 2 : 1);
+  hipLaunchKernelGGL(rope_partial_kernel, grid, dim3(256), 0, stream, q, k, pos, rows, T, ld,
+                     half, inv);
+  return check_launch("rope_partial_kernel");
+}
+
+extern "C" int lx_rope_neox_f32(float* qk, const int* pos, int rows, int n_heads,
+                                int head_dim, int ld, float theta, hipStream_t stream) {
+  LX_REQUIRE(qk && pos, "rope_neox: null pointer");
+  LX_REQUIRE(rows > 0 && n_heads > 0 && head_dim > 0 && head_dim % 2 == 0 && head_dim <= 128,
+             "rope_neox: bad shape");
+  LX_REQUIRE(ld >= n_heads * head_dim, "rope_neox: ld=%d < n_heads*head_dim", ld);
+  Table<64> inv;
+  std::memset(&inv, 0, sizeof(inv));
+  rope_inv_freq(theta, head_dim, inv.v);
+  long n = (long)rows * n_heads * (head_dim / 2);
+  hipLaunchKernelGGL(rope_neox_kernel, dim3(grid_for(n, 256)), dim3(256), 0, stream, qk, pos,
+                     (long)rows, n_heads, head_dim, ld, inv);
+  return check_launch("rope_neox_kernel");
+}
+
+extern "C" int lx_timestep_embed_f32(const float* t, int B, int half_dim, float scale,
+                                     float* out, hipStream_t stream) {
+  LX_REQUIRE(t && out, "timestep_embed: null pointer");
+  LX_REQUIRE(B > 0 && half_dim > 1 && half_dim <= 256, "timestep_embed: bad shape");
+  // Coefficients exactly as the reference host loop forms them
+  // (src/flow/flow_matching.cpp:161-163): fp32 product then expf.
+  Table<256> coeff;
+  std::memset(&coeff, 0, sizeof(coeff));
+  const float step = (float)(std::log(10000.0) / (double)(half_dim - 1));
+  for (int j = 0; j < half_dim; ++j) coeff.v[j] = expf(-(float)j * step);
+  hipLaunchKernelGGL(timestep_kernel, dim3(B), dim3(128), 0, stream, t, B, half_dim, scale, out,
+                     coeff);
+  return check_launch("timestep_kernel");
+}
+
+extern "C" int lx_embed_gather_f32(const float* table, long n_rows, int D, const int* ids,
+                                   int n, float* out, hipStream_t stream) {
+  LX_REQUIRE(table && out && (ids || n == 0), "embed_gather: null pointer");
+  LX_REQUIRE(n_rows > 0 && D > 0 && n >= 0, "embed_gather: bad shape");
+  for (int i = 0; i < n; ++i) {
+    if (ids[i] < 0 || (long)ids[i] >= n_rows) {
+      set_error("embed_gather: id %d at position %d outside [0, %ld)", ids[i], i, n_rows);
+      return LX_ERR_RANGE;
+    }
+  }
+  const bool vec = D % 4 == 0 && ((uintptr_t)table | (uintptr_t)out) % 16 == 0;
+  for (int base = 0; base < n; base += kGatherChunk) {
+    int cnt = n - base < kGatherChunk ? n - base : kGatherChunk;
+    IdChunk chunk;
+    std::memset(&chunk, 0, sizeof(chunk));
+    std::memcpy(chunk.id, ids + base, sizeof(int) * cnt);
+    if (vec)
+      hipLaunchKernelGGL(gather_kernel4, dim3(cnt), dim3(256), 0, stream,
+                         reinterpret_cast<const float4*>(table), D / 4, chunk,
+                         reinterpret_cast<float4*>(out + (long)base * D));
+    else
+      hipLaunchKernelGGL(gather_kernel1, dim3(cnt), dim3(256), 0, stream, table, D, chunk,
+                         out + (long)base * D);
+    int rc = check_launch("gather_kernel");
+    if (rc != LX_OK) return rc;
+  }
+  return LX_OK;
+}

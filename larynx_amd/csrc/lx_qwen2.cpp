@@ -1,0 +1,344 @@
+// Qwen2 backbone of CosyVoice3LM, device resident.
+//
+// Host-side counterpart of LLM::build_lm_input / prefill / decode
+// (src/llm/llm.cpp:63-327).  Differences from the reference by design:
+//   - the KV cache lives on the device (the reference reads it back to host
+//     vectors after prefill and re-uploads the whole cache as graph constants
+//     on every decode step, src/llm/llm.cpp:200-204, 269-275);
+//   - q/k/v are one fused GEMM, gate/up one GEMM with interleaved rows whose
+//     epilogue applies silu(gate)*up, and o_proj / down_proj add into the
+//     residual stream in their epilogues;
+//   - GQA never materialises repeated K/V (the attention kernel maps query
+//     head h to kv head h / 7, as HF repeat_kv's consecutive layout).
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <new>
+#include <vector>
+
+#include "lx_common.hpp"
+#include "lx_internal.hpp"
+
+using namespace lx;
+
+namespace {
+
+constexpr int kSosToken = 6561;     // SOS_TOKEN (src/llm/internal.h:33)
+constexpr int kTaskIdToken = 6563;  // TASK_ID_TOKEN (src/llm/internal.h:34)
+
+#define LX_TRY(expr)              \
+  do {                            \
+    int _rc = (expr);             \
+    if (_rc != LX_OK) return _rc; \
+  } while (0)
+
+struct Arena {
+  std::vector<void*> ptrs;
+  ~Arena() {
+    for (void* p : ptrs) (void)hipFree(p);
+  }
+  template <typename T>
+  T* alloc(size_t n) {
+    void* p = nullptr;
+    if (n == 0) n = 1;
+    if (hipMalloc(&p, n * sizeof(T)) != hipSuccess) return nullptr;
+    ptrs.push_back(p);
+    return static_cast<T*>(p);
+  }
+};
+
+struct Layer {
+  float *qkv_w, *qkv_b, *o_w, *gu_w, *down_w, *in_norm, *post_norm;
+  float *k_cache, *v_cache;  // (max_ctx, KV)
+};
+
+}  // namespace
+
+struct lx_qwen2 {
+  Arena arena;
+  int H = 0, I = 0, NH = 0, NKV = 0, HD = 0, NL = 0, text_vocab = 0, speech_vocab = 0;
+  int KV = 0, QKV = 0;
+  float eps = 0.0f, theta = 0.0f;
+  int max_ctx = 0;
+  int cache_len = 0;
+  const float* embed_tokens = nullptr;
+  const float* speech_embedding = nullptr;
+  float *final_norm, *llm_decoder;
+  std::vector<Layer> layers;
+  // activations, sized for max_ctx rows
+  float *x, *hn, *qkv, *att, *act;
+  float* part;  // flash-decoding partials
+  int* pos;     // pos[i] = i
+};
+
+namespace {
+
+int layer_body(lx_qwen2* m, Layer& L, int rows, const int* pos, int row0, bool decode,
+               hipStream_t s) {
+  const int H = m->H, KV = m->KV, QKV = m->QKV;
+  // input_layernorm + q/k/v (+bias) + NEOX rotary on q and k (src/llm/llm.cpp:145-156)
+  LX_TRY(lx_rmsnorm_f32(m->x, L.in_norm, m->hn, rows, H, m->eps, s));
+  LX_TRY(lx_linear_f32(m->hn, H, L.qkv_w, L.qkv_b, m->qkv, QKV, rows, QKV, H, nullptr, s));
+  LX_TRY(lx_rope_neox_f32(m->qkv, pos, rows, m->NH, m->HD, QKV, m->theta, s));
+  LX_TRY(lx_rope_neox_f32(m->qkv + H, pos, rows, m->NKV, m->HD, QKV, m->theta, s));
+  // cache the roped key and raw value at rows [row0, row0 + rows)
+  LX_TRY(copy_rows(m->qkv + H, QKV, L.k_cache + (long)row0 * KV, KV, rows, KV, s));
+  LX_TRY(copy_rows(m->qkv + H + KV, QKV, L.v_cache + (long)row0 * KV, KV, rows, KV, s));
+  const int Tk = row0 + rows;
+  const float scale = 1.0f / std::sqrt((float)m->HD);
+  if (decode && rows == 1) {
+    LX_TRY(attention_decode_split(m->qkv, QKV, L.k_cache, KV, L.v_cache, KV, m->att, H, 1, Tk,
+                                  m->NH, m->NKV, scale, m->part, s));
+  } else {
+    LX_TRY(lx_attention_f32(m->qkv, QKV, L.k_cache, KV, L.v_cache, KV, m->att, H, 1, rows, Tk,
+                            m->NH, m->NKV, m->HD, scale, /*causal*/ 1, /*q_offset*/ row0, s));
+  }
+  lx_epilogue resid{};
+  resid.kind = LX_EPI_RESID;
+  LX_TRY(lx_linear_f32(m->att, H, L.o_w, nullptr, m->x, H, rows, H, H, &resid, s));
+  // post_attention_layernorm + SwiGLU MLP (src/llm/llm.cpp:165-170)
+  LX_TRY(lx_rmsnorm_f32(m->x, L.post_norm, m->hn, rows, H, m->eps, s));
+  lx_epilogue swiglu{};
+  swiglu.kind = LX_EPI_SWIGLU_PAIRED;
+  LX_TRY(lx_linear_f32(m->hn, H, L.gu_w, nullptr, m->act, m->I, rows, 2 * m->I, H, &swiglu, s));
+  LX_TRY(lx_linear_f32(m->act, m->I, L.down_w, nullptr, m->x, H, rows, H, m->I, &resid, s));
+  return LX_OK;
+}
+
+}  // namespace
+
+extern "C" int lx_qwen2_create(const lx_qwen2_weights* w, int max_ctx, lx_qwen2** out) {
+  LX_REQUIRE(w && out, "qwen2_create: null argument");
+  *out = nullptr;
+  LX_REQUIRE(w->hidden > 0 && w->hidden % 4 == 0 && w->head_dim == 64 && w->n_heads > 0 &&
+                 w->n_kv_heads > 0 && w->n_heads % w->n_kv_heads == 0 &&
+                 w->n_heads * w->head_dim == w->hidden && w->intermediate > 0 &&
+                 w->intermediate % 4 == 0 && w->n_layers > 0,
+             "qwen2_create: unsupported geometry");
+  LX_REQUIRE(max_ctx >= 1, "qwen2_create: max_ctx=%d", max_ctx);
+  LX_REQUIRE(w->embed_tokens && w->speech_embedding && w->final_norm && w->llm_decoder &&
+                 w->layers,
+             "qwen2_create: missing tables");
+  LX_REQUIRE(w->speech_vocab > kTaskIdToken, "qwen2_create: speech vocab too small");
+  lx_qwen2* m = new (std::nothrow) lx_qwen2();
+  if (!m) return LX_ERR_ALLOC;
+  m->H = w->hidden;
+  m->I = w->intermediate;
+  m->NH = w->n_heads;
+  m->NKV = w->n_kv_heads;
+  m->HD = w->head_dim;
+  m->NL = w->n_layers;
+  m->KV = m->NKV * m->HD;
+  m->QKV = m->H + 2 * m->KV;
+  m->text_vocab = w->text_vocab;
+  m->speech_vocab = w->speech_vocab;
+  m->eps = w->rms_eps;
+  m->theta = w->rope_theta;
+  m->max_ctx = max_ctx;
+  m->embed_tokens = w->embed_tokens;
+  m->speech_embedding = w->speech_embedding;
+  const int H = m->H, I = m->I, KV = m->KV, QKV = m->QKV;
+  Arena& a = m->arena;
+  bool ok = true;
+  auto A = [&](size_t n) {
+    float* p = a.alloc<float>(n);
+    ok = ok && p;
+    return p;
+  };
+  m->final_norm = A(H);
+  m->llm_decoder = A((size_t)m->speech_vocab * H);
+  m->layers.resize(m->NL);
+  for (auto& L : m->layers) {
+    L.qkv_w = A((size_t)QKV * H);
+    L.qkv_b = A(QKV);
+    L.o_w = A((size_t)H * H);
+    L.gu_w = A((size_t)2 * I * H);
+    L.down_w = A((size_t)H * I);
+    L.in_norm = A(H);
+    L.post_norm = A(H);
+    L.k_cache = A((size_t)max_ctx * KV);
+    L.v_cache = A((size_t)max_ctx * KV);
+  }
+  const size_t rows = max_ctx;
+  m->x = A(rows * H);
+  m->hn = A(rows * H);
+  m->qkv = A(rows * QKV);
+  m->att = A(rows * H);
+  m->act = A(rows * I);
+  m->part = A(attention_decode_part_floats(1, max_ctx, m->NH));
+  m->pos = a.alloc<int>(max_ctx);
+  ok = ok && m->pos;
+  if (!ok) {
+    delete m;
+    set_error("qwen2_create: device allocation failed");
+    return LX_ERR_ALLOC;
+  }
+  hipStream_t s = nullptr;
+  if (hipStreamCreate(&s) != hipSuccess) {
+    delete m;
+    set_error("qwen2_create: stream creation failed");
+    return LX_ERR_LAUNCH;
+  }
+  int rc = LX_OK;
+  auto C = [&](float* dst, const float* src, size_t n) {
+    if (rc != LX_OK) return;
+    if (!src) {
+      set_error("qwen2_create: missing weight tensor");
+      rc = LX_ERR_ARG;
+      return;
+    }
+    if (hipMemcpyAsync(dst, src, n * sizeof(float), hipMemcpyDeviceToDevice, s) != hipSuccess) {
+      set_error("qwen2_create: device copy failed");
+      rc = LX_ERR_LAUNCH;
+    }
+  };
+  C(m->final_norm, w->final_norm, H);
+  C(m->llm_decoder, w->llm_decoder, (size_t)m->speech_vocab * H);
+  for (int l = 0; l < m->NL && rc == LX_OK; ++l) {
+    const lx_qwen2_layer_weights& lw = w->layers[l];
+    Layer& L = m->layers[l];
+    C(L.qkv_w, lw.q_w, (size_t)H * H);
+    C(L.qkv_w + (size_t)H * H, lw.k_w, (size_t)KV * H);
+    C(L.qkv_w + (size_t)(H + KV) * H, lw.v_w, (size_t)KV * H);
+    C(L.qkv_b, lw.q_b, H);
+    C(L.qkv_b + H, lw.k_b, KV);
+    C(L.qkv_b + H + KV, lw.v_b, KV);
+    C(L.o_w, lw.o_w, (size_t)H * H);
+    C(L.down_w, lw.down_w, (size_t)H * I);
+    C(L.in_norm, lw.in_norm, H);
+    C(L.post_norm, lw.post_norm, H);
+    if (rc == LX_OK) rc = (lw.gate_w && lw.up_w) ? LX_OK : LX_ERR_ARG;
+    if (rc == LX_OK) rc = interleave_rows(lw.gate_w, lw.up_w, L.gu_w, I, H, s);
+  }
+  if (rc == LX_OK) rc = iota_i32(m->pos, max_ctx, s);
+  if (rc == LX_OK && hipStreamSynchronize(s) != hipSuccess) {
+    set_error("qwen2_create: weight packing failed");
+    rc = LX_ERR_LAUNCH;
+  }
+  (void)hipStreamDestroy(s);
+  if (rc != LX_OK) {
+    delete m;
+    return rc;
+  }
+  *out = m;
+  return LX_OK;
+}
+
+extern "C" void lx_qwen2_destroy(lx_qwen2* m) {
+  if (!m) return;
+  (void)hipDeviceSynchronize();
+  delete m;
+}
+
+extern "C" int lx_qwen2_build_lm_input(lx_qwen2* m, const int* text_tokens, int n_text,
+                                       const int* prompt_speech, int n_speech, float* out,
+                                       int* L_out, hipStream_t s) {
+  LX_REQUIRE(m && out, "qwen2_build_lm_input: null argument");
+  LX_REQUIRE(n_text >= 0 && n_speech >= 0 && (text_tokens || n_text == 0) &&
+                 (prompt_speech || n_speech == 0),
+             "qwen2_build_lm_input: bad token arrays");
+  if (L_out) *L_out = 0;
+  // Validate every id before writing anything (src/llm/llm.cpp:71-72).
+  for (int i = 0; i < n_text; ++i)
+    if (text_tokens[i] < 0 || text_tokens[i] >= m->text_vocab) {
+      set_error("qwen2_build_lm_input: text id %d at %d outside [0, %d)", text_tokens[i], i,
+                m->text_vocab);
+      return LX_ERR_RANGE;
+    }
+  for (int i = 0; i < n_speech; ++i)
+    if (prompt_speech[i] < 0 || prompt_speech[i] >= m->speech_vocab) {
+      set_error("qwen2_build_lm_input: speech id %d at %d outside [0, %d)", prompt_speech[i], i,
+                m->speech_vocab);
+      return LX_ERR_RANGE;
+    }
+  const int H = m->H;
+  float* p = out;
+  const int sos = kSosToken, task = kTaskIdToken;
+  LX_TRY(lx_embed_gather_f32(m->speech_embedding, m->speech_vocab, H, &sos, 1, p, s));
+  p += H;
+  if (n_text) LX_TRY(lx_embed_gather_f32(m->embed_tokens, m->text_vocab, H, text_tokens, n_text, p, s));
+  p += (long)n_text * H;
+  LX_TRY(lx_embed_gather_f32(m->speech_embedding, m->speech_vocab, H, &task, 1, p, s));
+  p += H;
+  if (n_speech)
+    LX_TRY(lx_embed_gather_f32(m->speech_embedding, m->speech_vocab, H, prompt_speech, n_speech, p,
+                               s));
+  if (L_out) *L_out = 1 + n_text + 1 + n_speech;
+  return LX_OK;
+}
+
+extern "C" int lx_qwen2_prefill(lx_qwen2* m, const float* lm_input, int L, float* logits,
+                                float* hidden, float* final_norm, hipStream_t s) {
+  LX_REQUIRE(m && lm_input, "qwen2_prefill: null argument");
+  LX_REQUIRE(L >= 1 && L <= m->max_ctx, "qwen2_prefill: L=%d outside [1, %d]", L, m->max_ctx);
+  const int H = m->H;
+  if (hipMemcpyAsync(m->x, lm_input, sizeof(float) * (size_t)L * H, hipMemcpyDeviceToDevice, s) !=
+      hipSuccess) {
+    set_error("qwen2_prefill: copy failed");
+    return LX_ERR_LAUNCH;
+  }
+  m->cache_len = 0;
+  for (int l = 0; l < m->NL; ++l) {
+    LX_TRY(layer_body(m, m->layers[l], L, m->pos, 0, false, s));
+    if (hidden)
+      (void)hipMemcpyAsync(hidden + (size_t)l * L * H, m->x, sizeof(float) * (size_t)L * H,
+                           hipMemcpyDeviceToDevice, s);
+  }
+  LX_TRY(lx_rmsnorm_f32(m->x, m->final_norm, m->hn, L, H, m->eps, s));
+  if (final_norm)
+    (void)hipMemcpyAsync(final_norm, m->hn, sizeof(float) * (size_t)L * H, hipMemcpyDeviceToDevice,
+                         s);
+  if (logits)
+    LX_TRY(lx_linear_f32(m->hn, H, m->llm_decoder, nullptr, logits, m->speech_vocab, L,
+                         m->speech_vocab, H, nullptr, s));
+  m->cache_len = L;
+  return check_launch("qwen2_prefill");
+}
+
+extern "C" int lx_qwen2_decode(lx_qwen2* m, int token, float* logits, float* final_norm,
+                               hipStream_t s) {
+  LX_REQUIRE(m && logits, "qwen2_decode: null argument");
+  if (token < 0 || token >= m->speech_vocab) {
+    set_error("qwen2_decode: token %d outside [0, %d)", token, m->speech_vocab);
+    return LX_ERR_RANGE;
+  }
+  if (m->cache_len <= 0) {
+    set_error("qwen2_decode: decode before prefill");
+    return LX_ERR_STATE;
+  }
+  if (m->cache_len >= m->max_ctx) {
+    set_error("qwen2_decode: KV cache full (%d)", m->max_ctx);
+    return LX_ERR_STATE;
+  }
+  const int H = m->H;
+  const int p = m->cache_len;
+  LX_TRY(lx_embed_gather_f32(m->speech_embedding, m->speech_vocab, H, &token, 1, m->x, s));
+  for (int l = 0; l < m->NL; ++l) LX_TRY(layer_body(m, m->layers[l], 1, m->pos + p, p, true, s));
+  LX_TRY(lx_rmsnorm_f32(m->x, m->final_norm, m->hn, 1, H, m->eps, s));
+  if (final_norm)
+    (void)hipMemcpyAsync(final_norm, m->hn, sizeof(float) * H, hipMemcpyDeviceToDevice, s);
+  LX_TRY(lx_linear_f32(m->hn, H, m->llm_decoder, nullptr, logits, m->speech_vocab, 1,
+                       m->speech_vocab, H, nullptr, s));
+  m->cache_len += 1;
+  return LX_OK;
+}
+
+extern "C" int lx_qwen2_cache_len(const lx_qwen2* m) { return m ? m->cache_len : 0; }
+
+extern "C" const float* lx_qwen2_cache_key(const lx_qwen2* m, int layer) {
+  if (!m || layer < 0 || layer >= m->NL) return nullptr;
+  return m->layers[layer].k_cache;
+}
+
+extern "C" const float* lx_qwen2_cache_value(const lx_qwen2* m, int layer) {
+  if (!m || layer < 0 || layer >= m->NL) return nullptr;
+  return m->layers[layer].v_cache;
+}
+
+extern "C" int lx_qwen2_set_cache_len(lx_qwen2* m, int len) {
+  LX_REQUIRE(m, "qwen2_set_cache_len: null model");
+  LX_REQUIRE(len >= 0 && len <= m->max_ctx, "qwen2_set_cache_len: %d outside [0, %d]", len,
+             m->max_ctx);
+  m->cache_len = len;
+  return LX_OK;
+}

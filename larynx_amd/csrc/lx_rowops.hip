@@ -1,0 +1,176 @@
+// Row-reduction ops: AdaLN-modulated LayerNorm (DiT) and RMSNorm (Qwen2).
+//
+// One wave64 owns one row.  The row is read once into registers (float4 per
+// lane per 256 channels), mean and centred variance are two shuffle
+// reductions over those registers, and the output is written once: one HBM
+// read + one HBM write per element.  The (1 + scale) / shift vectors of the
+// block's batch are staged in LDS once per workgroup.
+#include "lx_common.hpp"
+
+namespace lx {
+namespace {
+
+constexpr int kRowsPerBlock = 8;           // 8 waves, 512 threads
+
+template <int NV>
+__global__ __launch_bounds__(kRowsPerBlock * kWave) void adaln_kernel(
+    const float* x, const float* __restrict__ shift,
+    const float* __restrict__ scale, long mod_stride, float* y, int rows,
+    int T, int D, float eps) {
+  // LDS: (1 + scale) and shift for up to two batches touched by this block.
+  extern __shared__ float smem[];
+  const int D4 = D >> 2;
+  const int row0 = blockIdx.x * kRowsPerBlock;
+  const int b_first = row0 / T;
+  const int last_row = min(row0 + kRowsPerBlock, rows) - 1;
+  const int nb = last_row / T - b_first + 1;  // 1 or 2 when T >= kRowsPerBlock
+  for (int bi = 0; bi < nb; ++bi) {
+    const float4* sc = reinterpret_cast<const float4*>(scale + (long)(b_first + bi) * mod_stride);
+    const float4* sh = reinterpret_cast<const float4*>(shift + (long)(b_first + bi) * mod_stride);
+    float4* s1 = reinterpret_cast<float4*>(smem + (2 * bi) * D);
+    float4* s2 = reinterpret_cast<float4*>(smem + (2 * bi + 1) * D);
+    for (int i = threadIdx.x; i < D4; i += blockDim.x) {
+      float4 a = sc[i];
+      s1[i] = make_float4(1.0f + a.x, 1.0f + a.y, 1.0f + a.z, 1.0f + a.w);
+      s2[i] = sh[i];
+    }
+  }
+  __syncthreads();
+
+  const int wave = threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave;
+  const int row = row0 + wave;
+  if (row >= rows) return;
+  const int bi = row / T - b_first;
+  const float4* xr = reinterpret_cast<const float4*>(x + (long)row * D);
+  float4 v[NV];
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    int i = lane + j * kWave;
+    v[j] = i < D4 ? xr[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
+  }
+  const float mean = wave_sum(s) / (float)D;
+  float q = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    int i = lane + j * kWave;
+    if (i < D4) {
+      float a = v[j].x - mean, b = v[j].y - mean, c = v[j].z - mean, d = v[j].w - mean;
+      q += (a * a + b * b) + (c * c + d * d);
+    }
+  }
+  const float var = wave_sum(q) / (float)D;  // biased, as ggml_norm / nn.LayerNorm
+  const float rstd = 1.0f / sqrtf(var + eps);
+  const float4* s1 = reinterpret_cast<const float4*>(smem + (2 * bi) * D);
+  const float4* s2 = reinterpret_cast<const float4*>(smem + (2 * bi + 1) * D);
+  float4* yr = reinterpret_cast<float4*>(y + (long)row * D);
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    int i = lane + j * kWave;
+    if (i < D4) {
+      float4 m = s1[i], h = s2[i], o;
+      o.x = ((v[j].x - mean) * rstd) * m.x + h.x;
+      o.y = ((v[j].y - mean) * rstd) * m.y + h.y;
+      o.z = ((v[j].z - mean) * rstd) * m.z + h.z;
+      o.w = ((v[j].w - mean) * rstd) * m.w + h.w;
+      yr[i] = o;
+    }
+  }
+}
+
+template <int NV>
+__global__ __launch_bounds__(kRowsPerBlock * kWave) void rmsnorm_kernel(
+    const float* x, const float* __restrict__ w, float* y, int rows, int D, float eps) {
+  extern __shared__ float smem[];
+  const int D4 = D >> 2;
+  for (int i = threadIdx.x; i < D4; i += blockDim.x)
+    reinterpret_cast<float4*>(smem)[i] = reinterpret_cast<const float4*>(w)[i];
+  __syncthreads();
+  const int wave = threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave;
+  const int row = blockIdx.x * kRowsPerBlock + wave;
+  if (row >= rows) return;
+  const float4* xr = reinterpret_cast<const float4*>(x + (long)row * D);
+  float4 v[NV];
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    int i = lane + j * kWave;
+    v[j] = i < D4 ? xr[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    s += (v[j].x * v[j].x + v[j].y * v[j].y) + (v[j].z * v[j].z + v[j].w * v[j].w);
+  }
+  const float ms = wave_sum(s) / (float)D;
+  const float r = 1.0f / sqrtf(ms + eps);
+  float4* yr = reinterpret_cast<float4*>(y + (long)row * D);
+  const float4* ws = reinterpret_cast<const float4*>(smem);
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    int i = lane + j * kWave;
+    if (i < D4) {
+      float4 g = ws[i], o;
+      o.x = (v[j].x * r) * g.x;
+      o.y = (v[j].y * r) * g.y;
+      o.z = (v[j].z * r) * g.z;
+      o.w = (v[j].w * r) * g.w;
+      yr[i] = o;
+    }
+  }
+}
+
+}  // namespace
+}  // namespace lx
+
+using namespace lx;
+
+extern "C" int lx_adaln_modulate_f32(const float* x, const float* shift, const float* scale,
+                                     long mod_stride, float* y, int B, int T, int D,
+                                     float eps, hipStream_t stream) {
+  LX_REQUIRE(x && shift && scale && y, "adaln: null pointer");
+  LX_REQUIRE(B > 0 && T > 0 && D > 0, "adaln: bad shape B=%d T=%d D=%d", B, T, D);
+  LX_REQUIRE(D % 4 == 0 && D <= 16 * 256, "adaln: D=%d must be a multiple of 4 and <= 4096", D);
+  LX_REQUIRE(mod_stride >= D && mod_stride % 4 == 0, "adaln: bad mod_stride %ld", mod_stride);
+  LX_REQUIRE(((uintptr_t)x | (uintptr_t)y | (uintptr_t)shift | (uintptr_t)scale) % 16 == 0,
+             "adaln: pointers must be 16-byte aligned");
+  const int rows = B * T;
+  const int nblk = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
+  // A block touches at most ceil(kRowsPerBlock / T) + 1 batches.
+  const int span = (T >= kRowsPerBlock) ? 2 : (kRowsPerBlock / T + 2);
+  const int max_b = span < B ? span : B;
+  const size_t lds = (size_t)2 * max_b * D * sizeof(float);
+  LX_REQUIRE(lds <= 64 * 1024, "adaln: T=%d too small for D=%d", T, D);
+  const int nv = (D / 4 + kWave - 1) / kWave;
+  if (nv <= 4)
+    hipLaunchKernelGGL(adaln_kernel<4>, dim3(nblk), dim3(kRowsPerBlock * kWave), lds, stream,
+                       x, shift, scale, mod_stride, y, rows, T, D, eps);
+  else if (nv <= 8)
+    hipLaunchKernelGGL(adaln_kernel<8>, dim3(nblk), dim3(kRowsPerBlock * kWave), lds, stream,
+                       x, shift, scale, mod_stride, y, rows, T, D, eps);
+  else
+    hipLaunchKernelGGL(adaln_kernel<16>, dim3(nblk), dim3(kRowsPerBlock * kWave), lds, stream,
+                       x, shift, scale, mod_stride, y, rows, T, D, eps);
+  return check_launch("adaln_kernel");
+}
+
+extern "C" int lx_rmsnorm_f32(const float* x, const float* w, float* y, int rows, int D,
+                              float eps, hipStream_t stream) {
+  LX_REQUIRE(x && w && y, "rmsnorm: null pointer");
+  LX_REQUIRE(rows > 0 && D > 0 && D % 4 == 0 && D <= 16 * 256, "rmsnorm: bad shape rows=%d D=%d",
+             rows, D);
+  LX_REQUIRE(((uintptr_t)x | (uintptr_t)y | (uintptr_t)w) % 16 == 0,
+             "rmsnorm: pointers must be 16-byte aligned");
+  const int nblk = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
+  const size_t lds = (size_t)D * sizeof(float);
+  const int nv = (D / 4 + kWave - 1) / kWave;
+  if (nv <= 4)
+    hipLaunchKernelGGL(rmsnorm_kernel<4>, dim3(nblk), dim3(kRowsPerBlock * kWave), lds, stream,
+                       x, w, y, rows, D, eps);
+  else if (nv <= 8)
+    hipLaunchKernelGGL(rmsnorm_kernel<8>, dim3(nblk), dim3(kRowsPerBlock * kWave), lds, stream,
+                       x, w, y, rows, D, eps);
+  else
+    hipLaunchKernelGGL(rmsnorm_kernel<16>, dim3(nblk), dim3(kRowsPerBlock * kWave), lds, stream,
+                       x, w, y, rows, D, eps);
+  return check_launch("rmsnorm_kernel");
+}

@@ -1,0 +1,192 @@
+"""Torch-tensor front end of the liblxops C-ABI.
+
+Function names follow the reference's op builders (src/flow/ops.cpp,
+src/llm/ops.cpp): ada_ln, rope_partial, gelu_tanh, linear, attention,
+rms_norm, rope_full, ...  Tensors are CUDA (HIP) fp32 tensors in PyTorch row-major
+layout; work is enqueued on torch's current stream.  Every call goes through
+liblxops.so; a failing call raises LxError (no fallback path exists).
+"""
+import ctypes as C
+
+import torch
+
+from ._lib import (LX_EPI_GATED_RESID, LX_EPI_GELU_TANH, LX_EPI_NONE, LX_EPI_RESID,
+                   LX_EPI_ROPE_PARTIAL, LX_EPI_SWIGLU_PAIRED, Epilogue, check, lib)
+
+__all__ = [
+    "stream", "ada_ln", "adaln_emb", "rope_partial", "gelu_tanh", "gated_residual",
+    "timestep_embed", "time_mlp", "rms_norm", "rope_full", "swiglu", "embed_gather", "linear",
+    "attention", "conv_pos_mish", "conv_pack_weight", "Epilogue",
+    "LX_EPI_NONE", "LX_EPI_GELU_TANH", "LX_EPI_GATED_RESID", "LX_EPI_ROPE_PARTIAL",
+    "LX_EPI_RESID", "LX_EPI_SWIGLU_PAIRED",
+]
+
+
+def stream():
+    """hipStream_t handle of torch's current stream."""
+    return C.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _p(t):
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise ValueError("liblxops ops take device tensors")
+    return C.c_void_p(t.data_ptr())
+
+
+def _f32(t, name):
+    if t.dtype != torch.float32 or not t.is_cuda:
+        raise ValueError(f"{name} must be a CUDA float32 tensor")
+
+
+def ada_ln(x, scale, shift, eps=1e-6, out=None):
+    """LN(x) * (1 + scale[b]) + shift[b]; x (B, T, D), scale/shift (B, D) possibly strided
+    rows (views into the chunked AdaLN embedding).  src/flow/ops.cpp:94-104."""
+    _f32(x, "x")
+    B, T, D = x.shape
+    if scale.stride(-1) != 1 or shift.stride(-1) != 1 or scale.stride(0) != shift.stride(0):
+        raise ValueError("scale/shift rows must be contiguous with a common row stride")
+    y = torch.empty_like(x) if out is None else out
+    check(lib.lx_adaln_modulate_f32(_p(x), _p(shift), _p(scale), scale.stride(0), _p(y), B, T, D,
+                                    eps, stream()))
+    return y
+
+
+def adaln_emb(c, W, b):
+    """W @ silu(c[b]) + bias, c (B, D), W (n_out, D).  src/flow/dit.cpp:56."""
+    B, D = c.shape
+    n_out = W.shape[0]
+    emb = torch.empty(B, n_out, device=c.device, dtype=torch.float32)
+    check(lib.lx_adaln_emb_f32(_p(c), _p(W), _p(b), _p(emb), B, D, n_out, stream()))
+    return emb
+
+
+def rope_partial(q, k, pos, rot_dim=64, base=10000.0):
+    """In-place partial interleaved rotary on q and k (B, T, ld).  src/flow/ops.cpp:85-92."""
+    B, T, ld = q.shape
+    if k is not None and k.shape != q.shape:
+        raise ValueError("q and k shapes differ")
+    check(lib.lx_rope_partial_interleaved_f32(_p(q), _p(k), _p(pos), B, T, q.stride(1), rot_dim,
+                                              base, stream()))
+    return q, k
+
+
+def gelu_tanh(h, out=None):
+    """tanh-GELU.  src/flow/ops.cpp:73-83."""
+    y = torch.empty_like(h) if out is None else out
+    check(lib.lx_gelu_tanh_f32(_p(h), _p(y), h.numel(), stream()))
+    return y
+
+
+def gated_residual(x, y, gate):
+    """x += gate[b] * y in place; gate (B, D) rows may be strided.  src/flow/dit.cpp:71, 77."""
+    B, T, D = x.shape
+    check(lib.lx_gated_residual_f32(_p(x), _p(y), _p(gate), gate.stride(0), B, T, D, stream()))
+    return x
+
+
+def timestep_embed(t, half_dim=128, scale=1000.0):
+    """Sinusoid of SinusPositionEmbedding.  src/flow/flow_matching.cpp:13-20."""
+    B = t.shape[0]
+    out = torch.empty(B, 2 * half_dim, device=t.device, dtype=torch.float32)
+    check(lib.lx_timestep_embed_f32(_p(t), B, half_dim, scale, _p(out), stream()))
+    return out
+
+
+def time_mlp(t, w0, b0, w2, b2):
+    """TimestepEmbedding (sinusoid -> Linear -> SiLU -> Linear).
+    src/flow/flow_matching.cpp:10-42."""
+    B = t.shape[0]
+    D = w0.shape[0]
+    work = torch.empty(B * (256 + D), device=t.device, dtype=torch.float32)
+    out = torch.empty(B, D, device=t.device, dtype=torch.float32)
+    check(lib.lx_time_mlp_f32(_p(t), B, _p(w0), _p(b0), _p(w2), _p(b2), D, _p(work), _p(out),
+                              stream()))
+    return out
+
+
+def rms_norm(x, w, eps=1e-6, out=None):
+    """x / sqrt(mean(x^2) + eps) * w.  src/llm/ops.cpp:7-11."""
+    D = x.shape[-1]
+    rows = x.numel() // D
+    y = torch.empty_like(x) if out is None else out
+    check(lib.lx_rmsnorm_f32(_p(x), _p(w), _p(y), rows, D, eps, stream()))
+    return y
+
+
+def rope_full(qk, pos, n_heads, head_dim=64, theta=1e6):
+    """In-place NEOX rotary on (rows, ld) with heads packed from column 0.
+    src/llm/ops.cpp:21-30."""
+    rows = qk.shape[0]
+    check(lib.lx_rope_neox_f32(_p(qk), _p(pos), rows, n_heads, head_dim, qk.stride(0), theta,
+                               stream()))
+    return qk
+
+
+def swiglu(gate, up, out=None):
+    """silu(gate) * up.  src/llm/llm.cpp:167-169."""
+    y = torch.empty_like(gate) if out is None else out
+    check(lib.lx_swiglu_f32(_p(gate), _p(up), _p(y), gate.numel(), stream()))
+    return y
+
+
+def embed_gather(table, ids, out=None):
+    """table[ids] (bit-exact).  ids: host int sequence.  src/llm/llm.cpp:63-100."""
+    ids = [int(i) for i in ids]
+    n_rows, D = table.shape
+    arr = (C.c_int * max(1, len(ids)))(*ids)
+    y = torch.empty(len(ids), D, device=table.device, dtype=table.dtype) if out is None else out
+    check(lib.lx_embed_gather_f32(_p(table), n_rows, D, arr, len(ids), _p(y), stream()))
+    return y
+
+
+def linear(x, W, b=None, epilogue=None, out=None):
+    """epi(x @ W^T + b) on the matrix cores; x (M, K) (row stride may exceed K),
+    W (N, K).  `epilogue` is an Epilogue (kind LX_EPI_*) or None.
+    src/flow/ops.cpp:20-26."""
+    M, K = x.shape
+    N = W.shape[0]
+    kind = epilogue.kind if epilogue is not None else LX_EPI_NONE
+    if out is None:
+        if kind in (LX_EPI_GATED_RESID, LX_EPI_RESID):
+            raise ValueError("residual epilogues need out= (the residual stream)")
+        ncol = N // 2 if kind == LX_EPI_SWIGLU_PAIRED else N
+        out = torch.empty(M, ncol, device=x.device, dtype=torch.float32)
+    check(lib.lx_linear_f32(_p(x), x.stride(0), _p(W), _p(b), _p(out), out.stride(0), M, N, K,
+                            C.byref(epilogue) if epilogue is not None else None, stream()))
+    return out
+
+
+def attention(q, k, v, n_heads, n_kv_heads=None, scale=None, causal=False, q_offset=0,
+              out=None, head_dim=64):
+    """softmax(scale q k^T) v per head; q (B, Tq, *), k/v (B, Tk, *) with heads packed from
+    column 0 (row strides may exceed the head span).  src/flow/dit.cpp:34-51."""
+    n_kv_heads = n_kv_heads or n_heads
+    B, Tq = q.shape[0], q.shape[1]
+    Tk = k.shape[1]
+    scale = scale if scale is not None else head_dim ** -0.5
+    if out is None:
+        out = torch.empty(B, Tq, n_heads * head_dim, device=q.device, dtype=torch.float32)
+    check(lib.lx_attention_f32(_p(q), q.stride(1), _p(k), k.stride(1), _p(v), v.stride(1),
+                               _p(out), out.stride(1), B, Tq, Tk, n_heads, n_kv_heads, head_dim,
+                               scale, int(causal), q_offset, stream()))
+    return out
+
+
+def conv_pack_weight(w, groups=16):
+    """torch Conv1d weight (C, C/G, K) -> tap-major packed copy."""
+    Cc, cg, K = w.shape
+    wp = torch.empty_like(w)
+    check(lib.lx_conv_pack_weight_f32(_p(w), _p(wp), Cc, groups, K, stream()))
+    return wp
+
+
+def conv_pos_mish(x, wp, bias, resid=None, groups=16, kernel=31):
+    """mish(causal grouped conv1d(x)) (+ resid); x (B, T, C), wp packed weight.
+    src/flow/dit.cpp:113-122."""
+    B, T, Cc = x.shape
+    y = torch.empty_like(x)
+    check(lib.lx_conv_pos_mish_f32(_p(x), _p(wp), _p(bias), _p(resid), _p(y), B, T, Cc, groups,
+                                   kernel, stream()))
+    return y

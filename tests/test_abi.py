@@ -1,0 +1,111 @@
+"""C-ABI boundary checks that need no GPU: the library loads, exports every
+function include/lx_ops.h declares, and rejects bad arguments before any
+device work is enqueued."""
+import ctypes as C
+import os
+import re
+
+import pytest
+
+from conftest import ROOT
+
+HEADER = os.path.join(ROOT, "include", "lx_ops.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    names = re.findall(r"\b(lx_[a-z0-9_]+)\s*\(", text)
+    return sorted(set(names))
+
+
+def test_header_declares_the_path():
+    names = declared_functions()
+    for must in ["lx_adaln_modulate_f32", "lx_rope_partial_interleaved_f32", "lx_gelu_tanh_f32",
+                 "lx_gated_residual_f32", "lx_timestep_embed_f32", "lx_rmsnorm_f32",
+                 "lx_rope_neox_f32", "lx_swiglu_f32", "lx_embed_gather_f32", "lx_linear_f32",
+                 "lx_attention_f32", "lx_dit_forward", "lx_cfm_solve", "lx_qwen2_prefill",
+                 "lx_qwen2_decode"]:
+        assert must in names
+
+
+def test_library_exports_every_declared_symbol():
+    from larynx_amd._lib import LIB_PATH, SIGNATURES
+    lib = C.CDLL(LIB_PATH)
+    names = declared_functions()
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+    bound = {s[0] for s in SIGNATURES}
+    assert set(names) == bound, (set(names) ^ bound)
+
+
+def test_version_string():
+    import larynx_amd
+    assert "gfx950" in larynx_amd.version()
+
+
+def test_argument_errors_need_no_device():
+    from larynx_amd._lib import LX_ERR_ARG, LX_ERR_RANGE, lib
+    # null pointers
+    assert lib.lx_adaln_modulate_f32(None, None, None, 1024, None, 2, 500, 1024, 1e-6,
+                                     None) == LX_ERR_ARG
+    assert b"null" in lib.lx_last_error()
+    assert lib.lx_linear_f32(None, 4, None, None, None, 4, 1, 1, 4, None, None) == LX_ERR_ARG
+    # a bad token id is rejected on the host before any launch
+    fake = C.c_void_p(16)
+    ids = (C.c_int * 3)(1, 7000, 2)
+    assert lib.lx_embed_gather_f32(fake, 6761, 896, ids, 3, fake, None) == LX_ERR_RANGE
+    assert b"7000" in lib.lx_last_error()
+    ids = (C.c_int * 1)(-1)
+    assert lib.lx_embed_gather_f32(fake, 6761, 896, ids, 1, fake, None) == LX_ERR_RANGE
+    # unsupported head dim / misaligned shapes
+    assert lib.lx_attention_f32(fake, 1024, fake, 1024, fake, 1024, fake, 1024, 1, 4, 4, 8, 8, 128,
+                                0.1, 0, 0, None) == LX_ERR_ARG
+    assert lib.lx_linear_f32(fake, 6, fake, None, fake, 6, 8, 8, 6, None, None) == LX_ERR_ARG
+    assert lib.lx_conv_pos_mish_f32(fake, fake, fake, None, fake, 1, 8, 1024, 8, 31,
+                                    None) == LX_ERR_ARG  # 128 channels per group
+
+
+def _c_layout(struct, fields):
+    """sizeof / offsetof of a header struct, as the C compiler lays it out."""
+    import shutil
+    import subprocess
+    import tempfile
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if not cc:
+        pytest.skip("no C compiler")
+    prints = "".join(f'printf("%zu\\n", offsetof({struct}, {f}));' for f in fields)
+    src = (f'#include <stddef.h>\n#include <stdio.h>\n#include "lx_ops.h"\n'
+           f'int main(void){{printf("%zu\\n", sizeof({struct})); {prints} return 0;}}\n')
+    with tempfile.TemporaryDirectory() as d:
+        c_file, exe = os.path.join(d, "l.c"), os.path.join(d, "l")
+        open(c_file, "w").write(src)
+        subprocess.run([cc, "-D__HIP_PLATFORM_AMD__", "-I", os.path.join(ROOT, "include"),
+                        "-I", "/opt/rocm/include", c_file, "-o", exe], check=True,
+                       capture_output=True)
+        out = subprocess.run([exe], check=True, capture_output=True, text=True).stdout.split()
+    return [int(v) for v in out]
+
+
+@pytest.mark.parametrize("struct,cls", [
+    ("lx_epilogue", "Epilogue"), ("lx_dit_block_weights", "DitBlockWeights"),
+    ("lx_dit_weights", "DitWeights"), ("lx_dit_capture", "DitCapture"),
+    ("lx_qwen2_layer_weights", "Qwen2LayerWeights"), ("lx_qwen2_weights", "Qwen2Weights")])
+def test_struct_layouts_match_header(struct, cls):
+    import larynx_amd._lib as L
+    py = getattr(L, cls)
+    fields = [f[0] for f in py._fields_]
+    got = _c_layout(struct, fields)
+    assert got[0] == C.sizeof(py)
+    assert got[1:] == [getattr(py, f).offset for f in fields]
+
+
+def test_product_path_does_not_reference_the_oracle():
+    """The shipped package and library never load or name the oracle."""
+    pkg = os.path.join(ROOT, "larynx_amd")
+    for dirpath, _, files in os.walk(pkg):
+        for f in files:
+            if f.endswith((".py", ".hip", ".cpp", ".hpp", ".h")):
+                text = open(os.path.join(dirpath, f), errors="ignore").read()
+                assert "lxoracle" not in text and "import oracle" not in text, f
+                assert "from oracle" not in text, f

@@ -1,0 +1,113 @@
+"""Qwen2 LM parity on the GPU against the oracle (which is itself pinned to
+transformers' Qwen2Model in test_oracle_golden.py).
+
+Full hidden size / heads / intermediate, fewer layers (4) and a reduced text
+vocabulary to keep the oracle fast; the full-size tables are exercised by the
+gather tests.  Prefill at L=256 (160 text + 96 speech-prompt rows, the config's
+mix), decode steps through the device KV cache, and decode against synthetic
+caches of length 1 / 256 / 1024 / 2048.
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import announce
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-4
+
+
+@pytest.fixture(scope="module")
+def qwen(gpu):
+    from larynx_amd.llm import Qwen2Config, Qwen2LM, qwen2_param_shapes
+    cfg = Qwen2Config(n_layers=4, text_vocab=2000)
+    params = orc.make_params(qwen2_param_shapes(cfg), 77)
+    for k in params:
+        if k.endswith("layernorm.weight") or k == "norm.weight":
+            params[k] = (params[k] + 1.0).astype(np.float32)
+    dparams = {k: torch.from_numpy(v).to(gpu) for k, v in params.items()}
+    lm = Qwen2LM(dparams, cfg, max_ctx=2304)
+    yield cfg, params, dparams, lm
+    lm.close()
+
+
+def test_prefill_then_decode(gpu, qwen):
+    cfg, params, _, lm = qwen
+    rng = np.random.default_rng(5)
+    text = rng.integers(0, cfg.text_vocab, 160)
+    speech = rng.integers(0, 6564, 94)
+    announce("qwen2 build_lm_input + prefill L=256")
+    lm_in = lm.build_lm_input(text, speech)
+    o = orc.Qwen2(params, cfg, cap=2304)
+    ref_in = o.build_lm_input(text, speech)
+    assert lm_in.shape[0] == 256
+    assert np.array_equal(lm_in.cpu().numpy().view(np.uint32), ref_in.view(np.uint32))
+    logits, hidden, final = lm.prefill(lm_in, capture=True)
+    torch.cuda.synchronize()
+    rl, rh, rf = o.prefill(ref_in, capture=True)
+    for layer in range(cfg.n_layers):
+        assert orc.rel_err(hidden[layer].cpu().numpy(), rh[layer]) < TOL, layer
+    assert orc.rel_err(final.cpu().numpy(), rf) < TOL
+    assert orc.rel_err(logits.cpu().numpy(), rl) < TOL
+    assert lm.cache_len == 256
+    k0, v0 = lm.cache_views(0)
+    assert orc.rel_err(k0[:256].cpu().numpy(), o.k_cache[0, :256]) < TOL
+    assert orc.rel_err(v0[:256].cpu().numpy(), o.v_cache[0, :256]) < TOL
+    for step, tok in enumerate([17, 6560, 3000]):
+        announce(f"qwen2 decode step {step}")
+        lg, fn = lm.decode(tok, final_norm=True)
+        torch.cuda.synchronize()
+        rlg, rfn = o.decode(tok)
+        assert orc.rel_err(fn.cpu().numpy(), rfn) < TOL
+        assert orc.rel_err(lg.cpu().numpy(), rlg) < TOL
+        assert int(lg.argmax()) == int(np.argmax(rlg))
+    assert lm.cache_len == 259
+
+
+@pytest.mark.parametrize("cache_len", [1, 256, 1024, 2048])
+def test_decode_against_synthetic_cache(gpu, qwen, cache_len):
+    """The decode config: KV cache lengths 1..2048 with random ~N(0, 0.02) contents."""
+    cfg, params, _, lm = qwen
+    announce(f"qwen2 decode cache_len={cache_len}")
+    o = orc.Qwen2(params, cfg, cap=2304)
+    for layer in range(cfg.n_layers):
+        kc = orc.normal((cache_len, 128), 60 + layer, 1, 0.02)
+        vc = orc.normal((cache_len, 128), 60 + layer, 2, 0.02)
+        o.k_cache[layer, :cache_len] = kc
+        o.v_cache[layer, :cache_len] = vc
+        kd, vd = lm.cache_views(layer)
+        kd[:cache_len].copy_(torch.from_numpy(kc))
+        vd[:cache_len].copy_(torch.from_numpy(vc))
+    o.cache_len = cache_len
+    lm.set_cache_len(cache_len)
+    torch.cuda.synchronize()
+    lg, fn = lm.decode(4321, final_norm=True)
+    torch.cuda.synchronize()
+    rlg, rfn = o.decode(4321)
+    assert orc.rel_err(fn.cpu().numpy(), rfn) < TOL
+    assert orc.rel_err(lg.cpu().numpy(), rlg) < TOL
+
+
+def test_errors(gpu, qwen):
+    from larynx_amd import LxError
+    from larynx_amd._lib import LX_ERR_RANGE, LX_ERR_STATE
+    cfg, params, dparams, _ = qwen
+    from larynx_amd.llm import Qwen2LM
+    announce("qwen2 error paths")
+    lm = Qwen2LM(dparams, cfg, max_ctx=64)
+    with pytest.raises(LxError) as e:
+        lm.decode(5)  # before prefill
+    assert e.value.code == LX_ERR_STATE
+    with pytest.raises(LxError) as e:
+        lm.build_lm_input([0, cfg.text_vocab], [])
+    assert e.value.code == LX_ERR_RANGE
+    with pytest.raises(LxError) as e:
+        lm.build_lm_input([0], [6761])
+    assert e.value.code == LX_ERR_RANGE
+    x = lm.build_lm_input([1, 2], [3])
+    lm.prefill(x, want_logits=False)
+    with pytest.raises(LxError) as e:
+        lm.decode(6761)
+    assert e.value.code == LX_ERR_RANGE
+    lm.close()

@@ -1,0 +1,313 @@
+"""Per-op parity of the HIP library against the CPU oracle on the same seeded
+inputs, at the configs' shapes (B=2, T=500 / 3000, D=1024; Qwen2 L=256 / 1).
+
+Bars: embedding gather bit-exact; fp32 ops max|gpu - oracle| / max|oracle| below
+1e-4 (the per-op tolerance of the target); GEMMs and attention below 1e-4 as
+well (fp32 MFMA, no reduced precision).
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import announce
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-4
+
+
+def rnd(shape, stream, std=1.0, seed=21):
+    return orc.normal(shape, seed, stream, std)
+
+
+def dev(a, gpu):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(gpu)
+
+
+@pytest.fixture(scope="module")
+def ops(gpu):
+    from larynx_amd import ops as o
+    return o
+
+
+# --- a1 / a2 ---------------------------------------------------------------------
+@pytest.mark.parametrize("B,T", [(2, 500), (2, 3000), (2, 24), (2, 3), (1, 1), (4, 7)])
+def test_adaln(gpu, ops, B, T):
+    announce(f"adaln B={B} T={T}")
+    D = 1024
+    x = rnd((B, T, D), 1) * 2 + 0.3
+    emb = rnd((B, 6 * D), 2, 0.2)  # chunks viewed in place (row stride 6D)
+    ed = dev(emb, gpu)
+    y = ops.ada_ln(dev(x, gpu), ed[:, D:2 * D], ed[:, 0:D]).cpu().numpy()
+    ref = orc.adaln(x, emb[:, D:2 * D], emb[:, :D])
+    assert orc.rel_err(y, ref) < TOL
+
+
+def test_adaln_final_chunk_order(gpu, ops):
+    """norm_out uses chunk order (scale, shift) (src/flow/dit.cpp:134-135)."""
+    announce("adaln final order")
+    B, T, D = 2, 500, 1024
+    x = rnd((B, T, D), 3)
+    emb = rnd((B, 2 * D), 4, 0.3)
+    ed = dev(emb, gpu)
+    y = ops.ada_ln(dev(x, gpu), ed[:, 0:D], ed[:, D:]).cpu().numpy()
+    assert orc.rel_err(y, orc.adaln(x, emb[:, :D], emb[:, D:])) < TOL
+
+
+def test_adaln_emb_gemv(gpu, ops):
+    announce("adaln_emb gemv")
+    B, D, N = 2, 1024, 6144
+    c = rnd((B, D), 1)
+    W, b = rnd((N, D), 2, 0.02), rnd((N,), 3, 0.02)
+    e = ops.adaln_emb(dev(c, gpu), dev(W, gpu), dev(b, gpu)).cpu().numpy()
+    sc = (c.astype(np.float64) / (1 + np.exp(-c.astype(np.float64)))).astype(np.float32)
+    assert orc.rel_err(e, orc.linear(sc, W, b)) < TOL
+
+
+# --- a3 ------------------------------------------------------------------------
+@pytest.mark.parametrize("T", [500, 3000, 17])
+def test_rope_partial(gpu, ops, T):
+    announce(f"rope_partial T={T}")
+    B, D = 2, 1024
+    q, k = rnd((B, T, D), 1), rnd((B, T, D), 2)
+    qd, kd = dev(q, gpu), dev(k, gpu)
+    pos = torch.arange(T, dtype=torch.int32, device=gpu)
+    ops.rope_partial(qd, kd, pos)
+    p = np.arange(T, dtype=np.int32)
+    qo, ko = qd.cpu().numpy(), kd.cpu().numpy()
+    assert np.array_equal(qo[..., 64:], q[..., 64:])
+    assert orc.rel_err(qo, orc.rope_partial(q, p)) < TOL
+    assert orc.rel_err(ko, orc.rope_partial(k, p)) < TOL
+
+
+def test_rope_partial_golden_T3000(gpu, ops):
+    import os
+    from conftest import GOLDEN
+    r = np.load(os.path.join(GOLDEN, "flow_rope_T3000.npz"))
+    T = int(r["T"])
+    announce("rope_partial golden T=3000")
+    q = orc.normal((1, T, 64), int(r["q_seed"]), int(r["q_stream"]))
+    qd = dev(q, gpu)
+    ops.rope_partial(qd, None, torch.arange(T, dtype=torch.int32, device=gpu))
+    out = qd.cpu().numpy()[0, r["sel"]]
+    assert np.abs(out - r["out"]).max() < 1e-5
+
+
+# --- a4 / a5 --------------------------------------------------------------------
+@pytest.mark.parametrize("n", [2 * 500 * 2048, 2 * 3000 * 2048, 4095, 1])
+def test_gelu(gpu, ops, n):
+    announce(f"gelu n={n}")
+    h = rnd((n,), 1) * 3
+    y = ops.gelu_tanh(dev(h, gpu)).cpu().numpy()
+    assert orc.rel_err(y, orc.gelu_tanh(h)) < TOL
+
+
+@pytest.mark.parametrize("T", [500, 3000, 5])
+def test_gated_residual(gpu, ops, T):
+    announce(f"gated_residual T={T}")
+    B, D = 2, 1024
+    x, y = rnd((B, T, D), 1), rnd((B, T, D), 2)
+    emb = rnd((B, 6 * D), 3, 0.2)
+    xd, ed = dev(x, gpu), dev(emb, gpu)
+    ops.gated_residual(xd, dev(y, gpu), ed[:, 2 * D:3 * D])
+    ref = orc.gated_residual(x, y, emb[:, 2 * D:3 * D])
+    assert orc.rel_err(xd.cpu().numpy(), ref) < TOL
+
+
+# --- a6 ----------------------------------------------------------------------------
+def test_timestep_golden(gpu, ops):
+    import os
+    from conftest import GOLDEN
+    announce("timestep sinusoid golden")
+    s = np.load(os.path.join(GOLDEN, "flow_sinus.npz"))
+    out = ops.timestep_embed(dev(s["t"], gpu)).cpu().numpy()
+    assert np.abs(out - s["out"]).max() < 2e-5
+    assert np.abs(out - orc.timestep_embed(s["t"])).max() < 2e-6
+
+
+def test_time_mlp(gpu, ops):
+    announce("time_mlp")
+    D = 1024
+    w0, b0 = rnd((D, 256), 1, 0.02), rnd((D,), 2, 0.02)
+    w2, b2 = rnd((D, D), 3, 0.02), rnd((D,), 4, 0.02)
+    t = np.array([0.0, 0.31, 0.99], np.float32)
+    out = ops.time_mlp(*(dev(a, gpu) for a in (t, w0, b0, w2, b2))).cpu().numpy()
+    assert orc.rel_err(out, orc.time_mlp(t, w0, b0, w2, b2)) < TOL
+
+
+# --- a10 - a13 ------------------------------------------------------------------------
+@pytest.mark.parametrize("rows", [256, 1, 7])
+def test_rmsnorm(gpu, ops, rows):
+    announce(f"rmsnorm rows={rows}")
+    x, w = rnd((rows, 896), 1) * 2, rnd((896,), 2) + 1
+    y = ops.rms_norm(dev(x, gpu), dev(w, gpu)).cpu().numpy()
+    assert orc.rel_err(y, orc.rmsnorm(x, w)) < TOL
+
+
+@pytest.mark.parametrize("rows,start", [(256, 0), (1, 2047), (3, 1023)])
+def test_rope_neox(gpu, ops, rows, start):
+    announce(f"rope_neox rows={rows} start={start}")
+    qkv = rnd((rows, 1152), 1)
+    pos = np.arange(start, start + rows, dtype=np.int32)
+    qd = dev(qkv, gpu)
+    pd = dev(pos, gpu)
+    ops.rope_full(qd[:, :896], pd, 14)
+    ops.rope_full(qd[:, 896:1024], pd, 2)
+    out = qd.cpu().numpy()
+    ref = qkv.copy()
+    ref[:, :896] = orc.rope_neox(qkv[:, :896], pos, 14)
+    ref[:, 896:1024] = orc.rope_neox(qkv[:, 896:1024], pos, 2)
+    assert np.array_equal(out[:, 1024:], qkv[:, 1024:])
+    assert orc.rel_err(out, ref) < TOL
+
+
+@pytest.mark.parametrize("n", [256 * 4864, 4864, 4863])
+def test_swiglu(gpu, ops, n):
+    announce(f"swiglu n={n}")
+    g, u = rnd((n,), 1) * 3, rnd((n,), 2)
+    y = ops.swiglu(dev(g, gpu), dev(u, gpu)).cpu().numpy()
+    assert orc.rel_err(y, orc.swiglu(g, u)) < TOL
+
+
+def test_embed_gather_bitexact(gpu, ops):
+    announce("embed_gather")
+    table = rnd((6761, 896), 1)
+    td = dev(table, gpu)
+    rng = np.random.default_rng(0)
+    for ids in ([6561], [0, 6760, 6563], rng.integers(0, 6564, 256).tolist(),
+                rng.integers(0, 6761, 1000).tolist()):
+        out = ops.embed_gather(td, ids).cpu().numpy()
+        assert np.array_equal(out.view(np.uint32), table[ids].view(np.uint32))
+    # odd width falls back to the scalar copy kernel, still bit-exact
+    t2 = rnd((100, 81), 2)
+    out = ops.embed_gather(dev(t2, gpu), [99, 0, 5]).cpu().numpy()
+    assert np.array_equal(out, t2[[99, 0, 5]])
+
+
+def test_embed_gather_rejects_bad_ids(gpu, ops):
+    from larynx_amd import LxError
+    announce("embed_gather bad ids")
+    td = dev(rnd((10, 896), 1), gpu)
+    out = torch.zeros(3, 896, device=gpu)
+    with pytest.raises(LxError):
+        ops.embed_gather(td, [0, 10, 1], out=out)
+    with pytest.raises(LxError):
+        ops.embed_gather(td, [-1], out=out[:1])
+    torch.cuda.synchronize()
+    assert float(out.abs().sum()) == 0.0  # nothing written
+
+
+def test_embed_gather_text_table(gpu, ops):
+    announce("embed_gather text table 151936x896")
+    table = torch.randn(151936, 896, device=gpu)
+    ids = [0, 151935, 12345, 151935, 7]
+    out = ops.embed_gather(table, ids)
+    assert torch.equal(out, table[torch.tensor(ids, device=gpu)])
+
+
+# --- dense ---------------------------------------------------------------------------
+@pytest.mark.parametrize("M,N,K", [(1000, 1024, 1024), (1000, 80, 1024), (1000, 1024, 320),
+                                   (37, 67, 96), (256, 1152, 896), (256, 6761, 896),
+                                   (3, 9728, 896), (1, 6761, 896), (6000, 1024, 2048)])
+def test_linear_plain(gpu, ops, M, N, K):
+    announce(f"linear M={M} N={N} K={K}")
+    x, W, b = rnd((M, K), 1), rnd((N, K), 2, 0.03), rnd((N,), 3)
+    y = ops.linear(dev(x, gpu), dev(W, gpu), dev(b, gpu)).cpu().numpy()
+    assert orc.rel_err(y, orc.linear(x, W, b)) < TOL
+
+
+@pytest.mark.parametrize("M", [1000, 6000, 5])
+def test_linear_gelu_epilogue(gpu, ops, M):
+    announce(f"linear+gelu M={M}")
+    x, W, b = rnd((M, 1024), 1), rnd((2048, 1024), 2, 0.03), rnd((2048,), 3)
+    ep = ops.Epilogue(kind=ops.LX_EPI_GELU_TANH)
+    y = ops.linear(dev(x, gpu), dev(W, gpu), dev(b, gpu), epilogue=ep).cpu().numpy()
+    assert orc.rel_err(y, orc.gelu_tanh(orc.linear(x, W, b))) < TOL
+
+
+@pytest.mark.parametrize("T,K", [(500, 1024), (500, 2048), (3, 1024)])
+def test_linear_gated_residual_epilogue(gpu, ops, T, K):
+    announce(f"linear+gated T={T} K={K}")
+    B, D = 2, 1024
+    x, W, b = rnd((B * T, K), 1), rnd((D, K), 2, 0.03), rnd((D,), 3)
+    h = rnd((B, T, D), 4)
+    emb = rnd((B, 6 * D), 5, 0.3)
+    hd, ed = dev(h, gpu), dev(emb, gpu)
+    gate = ed[:, 5 * D:]
+    ep = ops.Epilogue(kind=ops.LX_EPI_GATED_RESID, rows_per_batch=T, gate=gate.data_ptr(),
+                      gate_stride=6 * D)
+    ops.linear(dev(x, gpu), dev(W, gpu), dev(b, gpu), epilogue=ep, out=hd.view(B * T, D))
+    ref = orc.gated_residual(h, orc.linear(x, W, b).reshape(B, T, D), emb[:, 5 * D:])
+    assert orc.rel_err(hd.cpu().numpy(), ref) < TOL
+
+
+@pytest.mark.parametrize("T", [500, 24, 3])
+def test_linear_qkv_rope_epilogue(gpu, ops, T):
+    announce(f"linear+qkv rope T={T}")
+    B, D = 2, 1024
+    x, W, b = rnd((B * T, D), 1), rnd((3 * D, D), 2, 0.03), rnd((3 * D,), 3)
+    pos = torch.arange(T, dtype=torch.int32, device=gpu)
+    ep = ops.Epilogue(kind=ops.LX_EPI_ROPE_PARTIAL, rows_per_batch=T, pos=pos.data_ptr(),
+                      rot_dim=64, rope_section=D, rope_sections=2, rope_base=10000.0)
+    y = ops.linear(dev(x, gpu), dev(W, gpu), dev(b, gpu), epilogue=ep).cpu().numpy()
+    ref = orc.linear(x, W, b).reshape(B, T, 3 * D)
+    p = np.arange(T, dtype=np.int32)
+    q = orc.rope_partial(np.ascontiguousarray(ref[..., :D]), p)
+    k = orc.rope_partial(np.ascontiguousarray(ref[..., D:2 * D]), p)
+    ref = np.concatenate([q, k, ref[..., 2 * D:]], -1).reshape(B * T, 3 * D)
+    assert orc.rel_err(y, ref) < TOL
+
+
+@pytest.mark.parametrize("M", [256, 1, 9])
+def test_linear_swiglu_and_resid_epilogues(gpu, ops, M):
+    announce(f"linear swiglu/resid M={M}")
+    H, I = 896, 4864
+    x = rnd((M, H), 1)
+    Wg, Wu = rnd((I, H), 2, 0.03), rnd((I, H), 3, 0.03)
+    Wgu = np.empty((2 * I, H), np.float32)
+    Wgu[0::2], Wgu[1::2] = Wg, Wu
+    ep = ops.Epilogue(kind=ops.LX_EPI_SWIGLU_PAIRED)
+    act = ops.linear(dev(x, gpu), dev(Wgu, gpu), None, epilogue=ep)
+    ref_act = orc.swiglu(orc.linear(x, Wg), orc.linear(x, Wu))
+    assert orc.rel_err(act.cpu().numpy(), ref_act) < TOL
+    Wd = rnd((H, I), 4, 0.02)
+    res = rnd((M, H), 5)
+    rd = dev(res, gpu)
+    ops.linear(act, dev(Wd, gpu), None, epilogue=ops.Epilogue(kind=ops.LX_EPI_RESID), out=rd)
+    ref = res.astype(np.float64) + orc.linear(ref_act, Wd)
+    assert orc.rel_err(rd.cpu().numpy(), ref) < TOL
+
+
+@pytest.mark.parametrize("B,T", [(2, 500), (2, 45), (1, 1), (2, 3000)])
+def test_attention_dit(gpu, ops, B, T):
+    announce(f"attention dit B={B} T={T}")
+    D = 1024
+    qkv = rnd((B, T, 3 * D), 1)
+    qd = dev(qkv, gpu)
+    o = ops.attention(qd[..., :D], qd[..., D:2 * D], qd[..., 2 * D:], 16).cpu().numpy()
+    ref = orc.attention(qkv[..., :D], qkv[..., D:2 * D], qkv[..., 2 * D:], 16)
+    assert orc.rel_err(o, ref) < TOL
+
+
+@pytest.mark.parametrize("Tq,Tk,off", [(256, 256, 0), (37, 37, 0), (5, 300, 295), (1, 2048, 2047)])
+def test_attention_qwen_causal_gqa(gpu, ops, Tq, Tk, off):
+    announce(f"attention qwen Tq={Tq} Tk={Tk}")
+    q = rnd((1, Tq, 896), 1)
+    k, v = rnd((1, Tk, 128), 2), rnd((1, Tk, 128), 3)
+    o = ops.attention(dev(q, gpu), dev(k, gpu), dev(v, gpu), 14, 2, causal=True,
+                      q_offset=off).cpu().numpy()
+    ref = orc.attention(q, k, v, 14, 2, causal=True, q_offset=off)
+    assert orc.rel_err(o, ref) < TOL
+
+
+@pytest.mark.parametrize("B,T", [(2, 500), (2, 50), (1, 1), (2, 3000)])
+def test_conv_pos_mish(gpu, ops, B, T):
+    announce(f"conv_pos B={B} T={T}")
+    Cc = 1024
+    x, r = rnd((B, T, Cc), 1), rnd((B, T, Cc), 4)
+    w, b = rnd((Cc, 64, 31), 2, 0.03), rnd((Cc,), 3, 0.03)
+    wp = ops.conv_pack_weight(dev(w, gpu))
+    y = ops.conv_pos_mish(dev(x, gpu), wp, dev(b, gpu), dev(r, gpu)).cpu().numpy()
+    assert orc.rel_err(y, orc.conv_pos_mish(x, w, b, r)) < TOL
+    y0 = ops.conv_pos_mish(dev(x, gpu), wp, dev(b, gpu)).cpu().numpy()
+    assert orc.rel_err(y0, orc.conv_pos_mish(x, w, b)) < TOL
