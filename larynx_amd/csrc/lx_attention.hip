@@ -1,6 +1,6 @@
 // Scaled-dot-product attention, fp32 on the CDNA4 matrix cores.
 //
-// Prefill / DiT path (Tq > 1): one wave64 per (batch, head, 32-query tile).
+// Prefill / DiT path: per (batch, head, query tile), see attn_flash_kernel.
 // Scores are formed transposed, S^T = K Q^T, with v_mfma_f32_32x32x2f32 so
 // that in the accumulator layout every lane owns ONE query column (lane & 31)
 // and 16 keys of the 32-key block.  Row statistics of the online softmax are
@@ -11,9 +11,10 @@
 // contributes at MFMA step i.  Scores are never written to memory (the
 // reference materialises KQ [T, T, heads, B]).
 //
-// Decode path (Tq == 1): flash-decoding.  Keys are split across workgroups
-// (256 keys each, one thread per key for the scores, one lane per channel for
-// P V), then a second kernel merges the per-split (max, sum, o) triples.
+// Decode path (one query row, internal to the Qwen2 decode step):
+// flash-decoding.  Keys are split across workgroups (256 keys each, one thread
+// per key for the scores, one lane per channel for P V), then a second kernel
+// merges the per-split (max, sum, o) triples.
 #include <cmath>
 
 #include "lx_common.hpp"
@@ -23,34 +24,67 @@ namespace {
 
 constexpr int kHD = 64;  // head dim handled by these kernels
 
-__global__ __launch_bounds__(64) void attn_mfma_kernel(
+// Flash attention, 4 waves per workgroup: a 64-query tile of one (batch, head)
+// split as 2 query sub-tiles (32 queries each) x 2 key halves.  Every 64-key
+// tile of K and V is loaded once into LDS (coalesced, double buffered) and
+// read by all four waves; wave (qs, ks) scores its 32 queries against keys
+// [ks*32, ks*32 + 32) of each tile.  The two key halves of a query sub-tile
+// are merged through LDS at the end in a fixed order (deterministic).
+// Softmax runs in base 2: q is pre-scaled by scale * log2(e), so p = exp2(s - m).
+constexpr int kQT = 64;          // queries per workgroup
+constexpr int kKT = 64;          // keys per LDS tile
+constexpr int kLD = kHD + 4;     // LDS row stride (floats)
+constexpr size_t kFlashLds = (size_t)2 * 2 * kKT * kLD * sizeof(float);  // K,V x 2 buffers
+
+__global__ __launch_bounds__(256) void attn_flash_kernel(
     const float* __restrict__ q, int ldq, const float* __restrict__ k, int ldk,
     const float* __restrict__ v, int ldv, float* __restrict__ o, int ldo, int Tq, int Tk,
-    int H, int rep, float scale, int causal, int q_offset) {
-  __shared__ __attribute__((aligned(16))) float Os[32 * (kHD + 4)];
-  const int lane = threadIdx.x;
-  const int r = lane & 31, h = lane >> 5;
-  const int q0 = blockIdx.x * 32;
-  const int head = blockIdx.y;
-  const int b = blockIdx.z;
-  const int g = head / rep;
+    int rep, float qscale, int causal, int q_offset) {
+  extern __shared__ __attribute__((aligned(16))) float lds[];
+  float* Ks = lds;                       // [2][kKT][kLD]
+  float* Vs = lds + 2 * kKT * kLD;       // [2][kKT][kLD]
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int qs = wave & 1, ks = wave >> 1;
+  const int lane = tid & 63, r = lane & 31, h = lane >> 5;
+  const int head = blockIdx.y, b = blockIdx.z, g = head / rep;
+  const int qt0 = blockIdx.x * kQT;
+  const int q0 = qt0 + qs * 32;
 
-  // Q^T operand: lane holds Q[q0 + r][h*32 + s] * scale, s = 0..31.
-  float qf[32];
+  // Q^T operand: lane holds Q[q0 + r][h*32 + s] * scale * log2(e), s = 0..31.
+  floatx4 qf[8];
   {
     const float* qrow = q + ((long)b * Tq + min(q0 + r, Tq - 1)) * ldq + head * kHD + h * 32;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      float4 t = reinterpret_cast<const float4*>(qrow)[j];
-      qf[4 * j + 0] = t.x * scale;
-      qf[4 * j + 1] = t.y * scale;
-      qf[4 * j + 2] = t.z * scale;
-      qf[4 * j + 3] = t.w * scale;
-    }
+    for (int j = 0; j < 8; ++j) qf[j] = *reinterpret_cast<const floatx4*>(qrow + 4 * j) * qscale;
   }
-  const int my_q = q_offset + q0 + r;  // absolute position of this lane's query
-  int kend = Tk;
-  if (causal) kend = min(Tk, q_offset + min(q0 + 31, Tq - 1) + 1);
+  const int my_q = q_offset + q0 + r;
+  const int kend = causal ? min(Tk, q_offset + min(qt0 + kQT - 1, Tq - 1) + 1) : Tk;
+  const int ntiles = (kend + kKT - 1) / kKT;
+
+  // K/V tile loader: 2 x 1024 float4 per tile, 8 per thread.
+  const float* kbase = k + (long)b * Tk * ldk + g * kHD;
+  const float* vbase = v + (long)b * Tk * ldv + g * kHD;
+  floatx4 rk[4], rv[4];
+  auto gload = [&](int t) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int idx = tid + 256 * j;
+      const int row = idx >> 4, c = (idx & 15) * 4;
+      const int key = min(t * kKT + row, Tk - 1);
+      rk[j] = *reinterpret_cast<const floatx4*>(kbase + (long)key * ldk + c);
+      rv[j] = *reinterpret_cast<const floatx4*>(vbase + (long)key * ldv + c);
+    }
+  };
+  auto sstore = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int idx = tid + 256 * j;
+      const int row = idx >> 4, c = (idx & 15) * 4;
+      *reinterpret_cast<floatx4*>(Ks + (buf * kKT + row) * kLD + c) = rk[j];
+      *reinterpret_cast<floatx4*>(Vs + (buf * kKT + row) * kLD + c) = rv[j];
+    }
+  };
 
   floatx16 o0, o1;
 #pragma unroll
@@ -60,74 +94,104 @@ __global__ __launch_bounds__(64) void attn_mfma_kernel(
   }
   float m_run = -INFINITY, l_run = 0.0f;
 
-  const float* kbase = k + (long)b * Tk * ldk + g * kHD;
-  const float* vbase = v + (long)b * Tk * ldv + g * kHD;
-  for (int kb = 0; kb < kend; kb += 32) {
-    float kf[32];
-    const float* krow = kbase + (long)min(kb + r, Tk - 1) * ldk + h * 32;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      float4 t = reinterpret_cast<const float4*>(krow)[j];
-      kf[4 * j + 0] = t.x;
-      kf[4 * j + 1] = t.y;
-      kf[4 * j + 2] = t.z;
-      kf[4 * j + 3] = t.w;
-    }
-    floatx16 s;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) s[i] = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 32; ++j) s = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[j], qf[j], s, 0, 0, 0);
-
-    float mloc = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int key = kb + (i >> 2) * 8 + h * 4 + (i & 3);
-      const bool ok = key < Tk && (!causal || key <= my_q);
-      s[i] = ok ? s[i] : -INFINITY;
-      mloc = fmaxf(mloc, s[i]);
-    }
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-    const float m_new = fmaxf(m_run, mloc);
-    const float alpha = expf(m_run - m_new);  // 0 on the first block
-    float psum = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      s[i] = expf(s[i] - m_new);
-      psum += s[i];
-    }
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      o0[i] *= alpha;
-      o1[i] *= alpha;
-    }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int key = min(kb + (i >> 2) * 8 + h * 4 + (i & 3), Tk - 1);
-      const float* vrow = vbase + (long)key * ldv;
-      o0 = __builtin_amdgcn_mfma_f32_32x32x2f32(vrow[r], s[i], o0, 0, 0, 0);
-      o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(vrow[32 + r], s[i], o1, 0, 0, 0);
-    }
-  }
-  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
-  const float inv = 1.0f / l_tot;
-  // O^T accumulator: register i of tile t is channel t*32 + (i/4)*8 + h*4 + i%4.
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int d = (i >> 2) * 8 + h * 4 + (i & 3);
-    Os[r * (kHD + 4) + d] = o0[i] * inv;
-    Os[r * (kHD + 4) + 32 + d] = o1[i] * inv;
+  if (ntiles > 0) {
+    gload(0);
+    sstore(0);
   }
   __syncthreads();
+  for (int t = 0; t < ntiles; ++t) {
+    const int buf = t & 1;
+    if (t + 1 < ntiles) gload(t + 1);
+    const int kb = t * kKT + ks * 32;  // first key of this wave's half tile
+    if (kb < kend) {
+      const float* krow = Ks + (buf * kKT + ks * 32 + r) * kLD + h * 32;
+      floatx16 s;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int idx = lane + j * 64;  // 512 float4 = 32 rows x 16
-    const int row = idx >> 4, c = (idx & 15) * 4;
-    if (q0 + row < Tq) {
-      float4 t = *reinterpret_cast<const float4*>(Os + row * (kHD + 4) + c);
-      *reinterpret_cast<float4*>(o + ((long)b * Tq + q0 + row) * ldo + head * kHD + c) = t;
+      for (int i = 0; i < 16; ++i) s[i] = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const floatx4 kv = *reinterpret_cast<const floatx4*>(krow + 4 * j);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv[e], qf[j][e], s, 0, 0, 0);
+      }
+      // S^T register i of lane half h is key kb + (i/4)*8 + h*4 + i%4 for query r.
+      float mloc = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int key = kb + (i >> 2) * 8 + h * 4 + (i & 3);
+        const bool ok = key < Tk && (!causal || key <= my_q);
+        s[i] = ok ? s[i] : -INFINITY;
+        mloc = fmaxf(mloc, s[i]);
+      }
+      mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+      const float m_new = fmaxf(m_run, mloc);
+      const float m_use = m_new == -INFINITY ? 0.0f : m_new;  // fully masked so far
+      const float alpha = exp2f(m_run - m_use);
+      float psum = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        s[i] = exp2f(s[i] - m_use);
+        psum += s[i];
+      }
+      l_run = l_run * alpha + psum;
+      m_run = m_new;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        o0[i] *= alpha;
+        o1[i] *= alpha;
+      }
+      // O^T += V^T P^T: register i supplies k index key_h(i) for lane half h.
+      const float* vt = Vs + (buf * kKT + ks * 32) * kLD;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const float* vrow = vt + ((i >> 2) * 8 + h * 4 + (i & 3)) * kLD;
+        o0 = __builtin_amdgcn_mfma_f32_32x32x2f32(vrow[r], s[i], o0, 0, 0, 0);
+        o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(vrow[32 + r], s[i], o1, 0, 0, 0);
+      }
+    }
+    if (t + 1 < ntiles) sstore(buf ^ 1);
+    __syncthreads();
+  }
+
+  // Merge the key halves: ks = 1 publishes (m, l, O^T) per lane, ks = 0 combines.
+  float* xch = lds + qs * (64 * 34);  // per query sub-tile: 64 lanes x (32 O + m + l)
+  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+  if (ks == 1) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      xch[i * 64 + lane] = o0[i];
+      xch[(16 + i) * 64 + lane] = o1[i];
+    }
+    xch[32 * 64 + lane] = m_run;
+    xch[33 * 64 + lane] = l_tot;
+  }
+  __syncthreads();
+  float* ot = lds + 2 * (64 * 34) + qs * (32 * kLD);  // transposed output tile [32 q][kLD]
+  if (ks == 0) {
+    const float m1 = xch[32 * 64 + lane], l1 = xch[33 * 64 + lane];
+    const float m = fmaxf(m_run, m1);
+    const float a0 = exp2f(m_run - m), a1 = exp2f(m1 - m);
+    const float inv = 1.0f / (l_tot * a0 + l1 * a1);
+    // register i of tile t is channel t*32 + (i/4)*8 + h*4 + i%4 of query r
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int d = (i >> 2) * 8 + h * 4 + (i & 3);
+      ot[r * kLD + d] = (o0[i] * a0 + xch[i * 64 + lane] * a1) * inv;
+      ot[r * kLD + 32 + d] = (o1[i] * a0 + xch[(16 + i) * 64 + lane] * a1) * inv;
+    }
+  }
+  __syncthreads();
+  // coalesced store of both sub-tiles: 64 queries x 16 float4
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int idx = tid + 256 * j;
+    const int row = idx >> 4, c = (idx & 15) * 4;  // row 0..63 = qs*32 + local row
+    const int qi = qt0 + row;
+    if (qi < Tq) {
+      const float* src = lds + 2 * (64 * 34) + (row >> 5) * (32 * kLD) + (row & 31) * kLD + c;
+      *reinterpret_cast<floatx4*>(o + ((long)b * Tq + qi) * ldo + head * kHD + c) =
+          *reinterpret_cast<const floatx4*>(src);
     }
   }
 }
@@ -241,11 +305,23 @@ extern "C" int lx_attention_f32(const float* q, int ldq, const float* k, int ldk
   LX_REQUIRE(ldq % 4 == 0 && ldk % 4 == 0 && ldo % 4 == 0 &&
                  ((uintptr_t)q | (uintptr_t)k | (uintptr_t)o) % 16 == 0,
              "attention: q/k/o rows must be 16-byte aligned");
+  LX_REQUIRE(ldv % 4 == 0 && (uintptr_t)v % 16 == 0, "attention: v rows must be 16-byte aligned");
   LX_REQUIRE(q_offset >= 0, "attention: q_offset < 0");
   if (causal) LX_REQUIRE(q_offset + Tq <= Tk, "attention: causal needs q_offset + Tq <= Tk");
   const int rep = n_heads / n_kv_heads;
-  dim3 grid((Tq + 31) / 32, n_heads, B);
-  hipLaunchKernelGGL(attn_mfma_kernel, grid, dim3(64), 0, stream, q, ldq, k, ldk, v, ldv, o, ldo,
-                     Tq, Tk, n_heads, rep, scale, causal, q_offset);
-  return check_launch("attn_mfma_kernel");
+  static bool attr_set = false;
+  if (!attr_set) {
+    if (hipFuncSetAttribute((const void*)attn_flash_kernel,
+                            hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)kFlashLds) != hipSuccess) {
+      set_error("attention: cannot raise the LDS limit to %zu bytes", kFlashLds);
+      return LX_ERR_LAUNCH;
+    }
+    attr_set = true;
+  }
+  dim3 grid((Tq + kQT - 1) / kQT, n_heads, B);
+  const float log2e = 1.4426950408889634f;
+  hipLaunchKernelGGL(attn_flash_kernel, grid, dim3(256), kFlashLds, stream, q, ldq, k, ldk, v,
+                     ldv, o, ldo, Tq, Tk, rep, scale * log2e, causal, q_offset);
+  return check_launch("attn_flash_kernel");
 }

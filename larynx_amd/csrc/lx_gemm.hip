@@ -2,9 +2,13 @@
 //
 //   - v_mfma_f32_32x32x2f32, fp32 in / fp32 accumulate (no reduced-precision
 //     shortcut: the reference pins fp32 GEMMs, cf. its TF32 ADR).
-//   - 64x64 output tile per 256-thread workgroup, one 32x32 accumulator per
-//     wave64; K staged through LDS in 32-wide slabs, double buffered, with the
-//     next slab's global loads in flight during the current slab's MFMAs.
+//   - Output tiles of BM x BN per workgroup, 32x32 accumulators per wave64; K
+//     staged through LDS in BK-wide slabs, double buffered, the next slab's
+//     global loads in flight during the current slab's MFMAs.
+//   - Intra-workgroup split-K (KS groups of waves on disjoint K slabs, reduced
+//     through LDS in a fixed order) raises the waves per SIMD for the small-M
+//     DiT shapes (M = 2 x 500 rows gives only 256 tiles of 64 x 64 for N = 1024,
+//     one per CU) without atomics, so results stay bit-reproducible.
 //   - Within a slab, lane half h consumes k = h*16 + s at MFMA step s, so each
 //     lane's operands are 16 contiguous floats (four ds_read_b128).
 //   - Workgroup ids are remapped so the tiles resident on one XCD are a
@@ -20,10 +24,6 @@
 
 namespace lx {
 namespace {
-
-constexpr int BM = 64, BN = 64, BK = 32, PAD = 4;
-constexpr int LDA = BK + PAD;  // LDS row stride (floats) of the A / W slabs
-constexpr int LDC = BN + 4;    // LDS row stride of the epilogue tile
 
 struct EpiArgs {
   int kind;
@@ -44,15 +44,78 @@ __device__ __forceinline__ void rotate_pair(float& x0, float& x1, float ang) {
   x1 = b;
 }
 
+// Shared epilogue of the tiled kernels: 4 consecutive columns n..n+3 of row m.
 template <int EPI>
-__global__ __launch_bounds__(256) void gemm_nt_kernel(const float* __restrict__ X, int ldx,
-                                                      const float* __restrict__ W,
-                                                      const float* __restrict__ bias, float* Y,
-                                                      int ldy, int M, int N, int K,
-                                                      EpiArgs ep) {
-  __shared__ __attribute__((aligned(16))) float smem[2 * (BM + BN) * LDA];
-  float* As = smem;                    // [2][BM][LDA]
-  float* Ws = smem + 2 * BM * LDA;     // [2][BN][LDA]
+__device__ __forceinline__ void epilogue4(float* Y, int ldy, int m, int n, int N,
+                                          const float* __restrict__ bias, float4 v,
+                                          const EpiArgs& ep) {
+  float vv[4] = {v.x, v.y, v.z, v.w};
+  const int nv = min(4, N - n);
+  if (bias) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (e < nv) vv[e] += bias[n + e];
+  }
+  if (EPI == LX_EPI_SWIGLU_PAIRED) {
+    // columns (n, n+1) and (n+2, n+3) are (gate, up) pairs of outputs n/2, n/2+1
+    float* yr = Y + (long)m * ldy + (n >> 1);
+    if (nv >= 2) yr[0] = (vv[0] / (1.0f + expf(-vv[0]))) * vv[1];
+    if (nv >= 4) yr[1] = (vv[2] / (1.0f + expf(-vv[2]))) * vv[3];
+    return;
+  }
+  if (EPI == LX_EPI_GELU_TANH) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) vv[e] = gelu_tanh(vv[e]);
+  }
+  if (EPI == LX_EPI_ROPE_PARTIAL) {
+    const int cs = n % ep.section;
+    if (n < ep.sections * ep.section && cs < ep.rot_dim) {
+      const float p = (float)ep.pos[m % ep.rows_per_batch];
+      const int i0 = cs >> 1;
+      rotate_pair(vv[0], vv[1], p * ep.inv_freq[i0]);
+      rotate_pair(vv[2], vv[3], p * ep.inv_freq[i0 + 1]);
+    }
+  }
+  float* yp = Y + (long)m * ldy + n;
+  if (EPI == LX_EPI_GATED_RESID) {
+    const float* g = ep.gate + (long)(m / ep.rows_per_batch) * ep.gate_stride + n;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (e < nv) yp[e] = yp[e] + vv[e] * g[e];
+  } else if (EPI == LX_EPI_RESID) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (e < nv) yp[e] = yp[e] + vv[e];
+  } else if (nv == 4 && ((ldy & 3) == 0)) {
+    *reinterpret_cast<float4*>(yp) = make_float4(vv[0], vv[1], vv[2], vv[3]);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (e < nv) yp[e] = vv[e];
+  }
+}
+
+// Tiled NT GEMM.  BM x BN output tile per workgroup; WM x WN waves per k-group,
+// each owning (BM/WM) x (BN/WN) as 32x32 MFMA tiles; KS k-groups split the K
+// slabs of one tile between them (KS * WM * WN waves per workgroup, reduced
+// through LDS in a fixed order, so results are deterministic).  Each k-group
+// double-buffers its BK-wide slabs in LDS with the next slab's global loads in
+// flight during the current slab's MFMAs.  Loads always hit valid addresses
+// (rows / k clamped into range) and out-of-range values are zeroed by a
+// select on the data, so they stay plain global_load_dwordx4.
+template <int EPI, int BM, int BN, int BK, int WM, int WN, int KS>
+__global__ __launch_bounds__(64 * WM * WN * KS) void gemm_tile_kernel(
+    const float* __restrict__ X, int ldx, const float* __restrict__ W,
+    const float* __restrict__ bias, float* Y, int ldy, int M, int N, int K, EpiArgs ep) {
+  constexpr int GT = 64 * WM * WN;             // threads per k-group
+  constexpr int NT = GT * KS;
+  constexpr int LDA = BK + 4;
+  constexpr int TM = BM / WM / 32, TN = BN / WN / 32;
+  constexpr int A4 = BM * BK / 4, W4 = BN * BK / 4;
+  constexpr int LA = A4 / GT, LW = W4 / GT;
+  static_assert(A4 % GT == 0 && W4 % GT == 0, "slab must split evenly over the k-group");
+  static_assert(TM >= 1 && TN >= 1 && BK % 32 == 0, "bad tile");
+  extern __shared__ __attribute__((aligned(16))) float smem[];
 
   const int tiles_m = (M + BM - 1) / BM;
   const int tiles_n = (N + BN - 1) / BN;
@@ -60,137 +123,190 @@ __global__ __launch_bounds__(256) void gemm_nt_kernel(const float* __restrict__ 
   int id = blockIdx.x;
   const int full = (nwg / 8) * 8;
   if (id < full) id = (id % 8) * (full / 8) + id / 8;  // XCD-contiguous runs
-  const int tm = id % tiles_m;
-  const int tn = id / tiles_m;
-  const int m0 = tm * BM, n0 = tn * BN;
+  const int m0 = (id % tiles_m) * BM, n0 = (id / tiles_m) * BN;
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
-  const int wm = wave >> 1, wn = wave & 1;
+  // wave index through readfirstlane: the compiler then treats everything
+  // derived from it (k-group, slab index) as wave-uniform (scalar branches).
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int kg = wave / (WM * WN);
+  const int wl = wave % (WM * WN);
+  const int wm = wl / WN, wn = wl % WN;
   const int r = lane & 31, h = lane >> 5;
+  const int gtid = tid % GT;
+  float* As = smem + kg * 2 * (BM + BN) * LDA;
+  float* Ws = As + 2 * BM * LDA;
 
-  // Global -> LDS mapping: 2 float4 per thread per operand per slab.
-  const int lrow = tid >> 3;       // 0..31 (+32 for the second float4)
-  const int lc4 = (tid & 7) * 4;   // k offset within the slab
-  const float* xa0 = X + (long)min(m0 + lrow, M - 1) * ldx;
-  const float* xa1 = X + (long)min(m0 + lrow + 32, M - 1) * ldx;
-  const float* wb0 = W + (long)min(n0 + lrow, N - 1) * K;
-  const float* wb1 = W + (long)min(n0 + lrow + 32, N - 1) * K;
-  const bool va0 = m0 + lrow < M, va1 = m0 + lrow + 32 < M;
-  const bool vb0 = n0 + lrow < N, vb1 = n0 + lrow + 32 < N;
-
-  float4 ra0, ra1, rb0, rb1;
-  auto gload = [&](int k0) {
-    const int k = k0 + lc4;
-    const bool kin = k < K;  // K % 4 == 0, so a float4 is all-in or all-out
-    const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
-    ra0 = (va0 && kin) ? *reinterpret_cast<const float4*>(xa0 + k) : z;
-    ra1 = (va1 && kin) ? *reinterpret_cast<const float4*>(xa1 + k) : z;
-    rb0 = (vb0 && kin) ? *reinterpret_cast<const float4*>(wb0 + k) : z;
-    rb1 = (vb1 && kin) ? *reinterpret_cast<const float4*>(wb1 + k) : z;
-  };
-  auto sstore = [&](int buf) {
-    float* a = As + buf * BM * LDA;
-    float* w = Ws + buf * BN * LDA;
-    *reinterpret_cast<float4*>(a + lrow * LDA + lc4) = ra0;
-    *reinterpret_cast<float4*>(a + (lrow + 32) * LDA + lc4) = ra1;
-    *reinterpret_cast<float4*>(w + lrow * LDA + lc4) = rb0;
-    *reinterpret_cast<float4*>(w + (lrow + 32) * LDA + lc4) = rb1;
-  };
-
-  floatx16 acc;
+  // Per-thread load slots: clamped row pointers and validity.
+  const float* pa[LA];
+  const float* pw[LW];
+  int ca[LA], cw[LW];
+  bool oka[LA], okw[LW];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
+  for (int i = 0; i < LA; ++i) {
+    const int idx = gtid + i * GT;
+    const int row = idx / (BK / 4);
+    ca[i] = (idx % (BK / 4)) * 4;
+    oka[i] = m0 + row < M;
+    pa[i] = X + (long)min(m0 + row, M - 1) * ldx;
+  }
+#pragma unroll
+  for (int i = 0; i < LW; ++i) {
+    const int idx = gtid + i * GT;
+    const int row = idx / (BK / 4);
+    cw[i] = (idx % (BK / 4)) * 4;
+    okw[i] = n0 + row < N;
+    pw[i] = W + (long)min(n0 + row, N - 1) * K;
+  }
+  // Raw loads go to registers untouched; out-of-range lanes are zeroed when
+  // the slab is written to LDS, after the MFMAs, so no wait on the loads is
+  // forced at the top of the iteration.
+  floatx4 ra[LA], rb[LW];  // native vectors: selects stay in VGPRs (no stack copies)
+  auto gload = [&](int kt) {
+#pragma unroll
+    for (int i = 0; i < LA; ++i)
+      ra[i] = *reinterpret_cast<const floatx4*>(pa[i] + min(kt * BK + ca[i], K - 4));
+#pragma unroll
+    for (int i = 0; i < LW; ++i)
+      rb[i] = *reinterpret_cast<const floatx4*>(pw[i] + min(kt * BK + cw[i], K - 4));
+  };
+  auto sstore = [&](int buf, int kt) {
+#pragma unroll
+    for (int i = 0; i < LA; ++i) {
+      const int idx = gtid + i * GT;
+      const bool ok = oka[i] && kt * BK + ca[i] < K;
+      floatx4 v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = ok ? ra[i][e] : 0.0f;
+      *reinterpret_cast<floatx4*>(As + buf * BM * LDA + (idx / (BK / 4)) * LDA + ca[i]) = v;
+    }
+#pragma unroll
+    for (int i = 0; i < LW; ++i) {
+      const int idx = gtid + i * GT;
+      const bool ok = okw[i] && kt * BK + cw[i] < K;
+      floatx4 v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = ok ? rb[i][e] : 0.0f;
+      *reinterpret_cast<floatx4*>(Ws + buf * BN * LDA + (idx / (BK / 4)) * LDA + cw[i]) = v;
+    }
+  };
+
+  floatx16 acc[TM][TN];
+#pragma unroll
+  for (int a = 0; a < TM; ++a)
+#pragma unroll
+    for (int b = 0; b < TN; ++b)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[a][b][i] = 0.0f;
 
   const int nk = (K + BK - 1) / BK;
-  gload(0);
-  sstore(0);
-  __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < nk) gload((kt + 1) * BK);
-    const float* a = As + buf * BM * LDA + (wm * 32 + r) * LDA + h * 16;
-    const float* w = Ws + buf * BN * LDA + (wn * 32 + r) * LDA + h * 16;
-    float4 af[4], bf[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      af[j] = *reinterpret_cast<const float4*>(a + 4 * j);
-      bf[j] = *reinterpret_cast<const float4*>(w + 4 * j);
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(af[j].x, bf[j].x, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(af[j].y, bf[j].y, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(af[j].z, bf[j].z, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(af[j].w, bf[j].w, acc, 0, 0, 0);
-    }
-    if (kt + 1 < nk) sstore(buf ^ 1);
-    __syncthreads();
-  }
-
-  // Epilogue: accumulator tile -> LDS (reusing the slab buffers).
-  float* Cs = smem;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int row = wm * 32 + (i >> 2) * 8 + h * 4 + (i & 3);
-    Cs[row * LDC + wn * 32 + r] = acc[i];
+  const int iters = (nk + KS - 1) / KS;  // uniform trip count: barriers match across k-groups
+  if (kg < nk) {
+    gload(kg);
+    sstore(0, kg);
   }
   __syncthreads();
-
+  int buf = 0;
+  for (int it = 0; it < iters; ++it) {
+    const int kt = it * KS + kg;
+    const bool more = kt + KS < nk;
+    if (more) gload(kt + KS);
+    if (kt < nk) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int idx = tid + j * 256;
-    const int row = idx >> 4;
-    const int c = (idx & 15) * 4;
-    const int m = m0 + row, n = n0 + c;
-    if (m >= M || n >= N) continue;
-    float4 v = *reinterpret_cast<const float4*>(Cs + row * LDC + c);
-    float vv[4] = {v.x, v.y, v.z, v.w};
-    const int nv = min(4, N - n);
-    if (bias) {
+      for (int s32 = 0; s32 < BK / 32; ++s32) {
+        floatx4 af[TM][4], bf[TN][4];  // native vectors: component indexing stays in VGPRs
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (e < nv) vv[e] += bias[n + e];
-    }
-    if (EPI == LX_EPI_SWIGLU_PAIRED) {
-      // columns (n, n+1) and (n+2, n+3) are (gate, up) pairs of outputs n/2, n/2+1
-      float* yr = Y + (long)m * ldy + (n >> 1);
-      if (nv >= 2) yr[0] = (vv[0] / (1.0f + expf(-vv[0]))) * vv[1];
-      if (nv >= 4) yr[1] = (vv[2] / (1.0f + expf(-vv[2]))) * vv[3];
-      continue;
-    }
-    if (EPI == LX_EPI_GELU_TANH) {
+        for (int a = 0; a < TM; ++a) {
+          const float* p = As + buf * BM * LDA + ((wm * TM + a) * 32 + r) * LDA + s32 * 32 + h * 16;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) vv[e] = gelu_tanh(vv[e]);
-    }
-    if (EPI == LX_EPI_ROPE_PARTIAL) {
-      const int cs = n % ep.section;
-      if (n < ep.sections * ep.section && cs < ep.rot_dim) {
-        const int t = m % ep.rows_per_batch;
-        const float p = (float)ep.pos[t];
-        const int i0 = cs >> 1;
-        rotate_pair(vv[0], vv[1], p * ep.inv_freq[i0]);
-        if (cs + 2 < ep.rot_dim) rotate_pair(vv[2], vv[3], p * ep.inv_freq[i0 + 1]);
+          for (int j = 0; j < 4; ++j) af[a][j] = *reinterpret_cast<const floatx4*>(p + 4 * j);
+        }
+#pragma unroll
+        for (int b = 0; b < TN; ++b) {
+          const float* p = Ws + buf * BN * LDA + ((wn * TN + b) * 32 + r) * LDA + s32 * 32 + h * 16;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) bf[b][j] = *reinterpret_cast<const floatx4*>(p + 4 * j);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+#pragma unroll
+            for (int a = 0; a < TM; ++a)
+#pragma unroll
+              for (int b = 0; b < TN; ++b)
+                acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[a][j][e], bf[b][j][e],
+                                                                  acc[a][b], 0, 0, 0);
       }
     }
-    float* yp = Y + (long)m * ldy + n;
-    if (EPI == LX_EPI_GATED_RESID) {
-      const float* g = ep.gate + (long)(m / ep.rows_per_batch) * ep.gate_stride + n;
+    if (more) sstore(buf ^ 1, kt + KS);
+    __syncthreads();
+    buf ^= 1;
+  }
+
+  // k-group reduction into the LDS tile, highest group first (fixed order);
+  // accumulator register i of lane (r, h) is row (i/4)*8 + h*4 + i%4, col r.
+  constexpr int LDC = BN + 4;
+  float* Cs = smem;
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (e < nv) yp[e] = yp[e] + vv[e] * g[e];
-    } else if (EPI == LX_EPI_RESID) {
+  for (int g = KS - 1; g >= 0; --g) {
+    if (kg == g) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (e < nv) yp[e] = yp[e] + vv[e];
-    } else if (nv == 4 && ((ldy & 3) == 0)) {
-      *reinterpret_cast<float4*>(yp) = make_float4(vv[0], vv[1], vv[2], vv[3]);
-    } else {
+      for (int a = 0; a < TM; ++a)
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (e < nv) yp[e] = vv[e];
+        for (int b = 0; b < TN; ++b)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int row = (wm * TM + a) * 32 + (i >> 2) * 8 + h * 4 + (i & 3);
+            const int col = (wn * TN + b) * 32 + r;
+            float v = acc[a][b][i];
+            if (g < KS - 1) v += Cs[row * LDC + col];
+            Cs[row * LDC + col] = v;
+          }
+    }
+    __syncthreads();
+  }
+  for (int idx = tid; idx < BM * BN / 4; idx += NT) {
+    const int row = idx / (BN / 4), c = (idx % (BN / 4)) * 4;
+    const int m = m0 + row, n = n0 + c;
+    if (m < M && n < N)
+      epilogue4<EPI>(Y, ldy, m, n, N, bias,
+                     *reinterpret_cast<const float4*>(Cs + row * LDC + c), ep);
+  }
+}
+
+template <int BM, int BN, int BK, int WM, int WN, int KS>
+struct TileCfg {
+  static constexpr int bm = BM, bn = BN, bk = BK, wm = WM, wn = WN, ks = KS;
+  static constexpr int threads = 64 * WM * WN * KS;
+  static size_t lds() {
+    size_t a = (size_t)KS * 2 * (BM + BN) * (BK + 4) * sizeof(float);
+    size_t c = (size_t)BM * (BN + 4) * sizeof(float);
+    return a > c ? a : c;
+  }
+};
+
+template <int EPI, class CFG>
+int launch_tile(const float* x, int ldx, const float* W, const float* bias, float* y, int ldy,
+                int M, int N, int K, const EpiArgs& ep, hipStream_t stream) {
+  auto kern = gemm_tile_kernel<EPI, CFG::bm, CFG::bn, CFG::bk, CFG::wm, CFG::wn, CFG::ks>;
+  const size_t lds = CFG::lds();
+  if (lds > 64 * 1024) {
+    static bool attr_set = false;  // once per instantiation
+    if (!attr_set) {
+      if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)lds) != hipSuccess) {
+        set_error("linear: cannot raise the LDS limit to %zu bytes", lds);
+        return LX_ERR_LAUNCH;
+      }
+      attr_set = true;
     }
   }
+  const long tiles = (long)((M + CFG::bm - 1) / CFG::bm) * ((N + CFG::bn - 1) / CFG::bn);
+  hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(CFG::threads), lds, stream, x, ldx, W, bias,
+                     y, ldy, M, N, K, ep);
+  return check_launch("gemm_tile_kernel");
 }
 
 // Skinny-M variant: one wave per output column pair, the M (<= 8) rows of x
@@ -344,6 +460,61 @@ int gemv_epi(const float* x, int ldx, const float* W, const float* bias, float* 
   return check_launch("gemv_epi_kernel");
 }
 
+// Tile configurations (BM, BN, BK, waves M x N, split-K).
+using Cfg0 = TileCfg<64, 64, 32, 2, 2, 1>;
+using Cfg1 = TileCfg<64, 64, 32, 2, 2, 2>;
+using Cfg2 = TileCfg<64, 64, 32, 2, 2, 4>;
+using Cfg3 = TileCfg<64, 64, 64, 2, 2, 1>;
+using Cfg4 = TileCfg<64, 64, 64, 2, 2, 2>;
+using Cfg5 = TileCfg<128, 64, 32, 2, 2, 1>;
+using Cfg6 = TileCfg<64, 128, 32, 2, 2, 1>;
+constexpr int kNumCfg = 7;
+
+template <int EPI>
+int dispatch_cfg(int cfg, const float* x, int ldx, const float* W, const float* bias, float* y,
+                 int ldy, int M, int N, int K, const EpiArgs& ep, hipStream_t s) {
+  switch (cfg) {
+    case 0: return launch_tile<EPI, Cfg0>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
+    case 1: return launch_tile<EPI, Cfg1>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
+    case 2: return launch_tile<EPI, Cfg2>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
+    case 3: return launch_tile<EPI, Cfg3>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
+    case 4: return launch_tile<EPI, Cfg4>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
+    case 5: return launch_tile<EPI, Cfg5>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
+    case 6: return launch_tile<EPI, Cfg6>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
+  }
+  set_error("linear: unknown tile configuration %d", cfg);
+  return LX_ERR_ARG;
+}
+
+int dispatch_gemm(int kind, int cfg, const float* x, int ldx, const float* W, const float* bias,
+                  float* y, int ldy, int M, int N, int K, const EpiArgs& ep, hipStream_t s) {
+  switch (kind) {
+    case LX_EPI_NONE:
+      return dispatch_cfg<LX_EPI_NONE>(cfg, x, ldx, W, bias, y, ldy, M, N, K, ep, s);
+    case LX_EPI_GELU_TANH:
+      return dispatch_cfg<LX_EPI_GELU_TANH>(cfg, x, ldx, W, bias, y, ldy, M, N, K, ep, s);
+    case LX_EPI_GATED_RESID:
+      return dispatch_cfg<LX_EPI_GATED_RESID>(cfg, x, ldx, W, bias, y, ldy, M, N, K, ep, s);
+    case LX_EPI_ROPE_PARTIAL:
+      return dispatch_cfg<LX_EPI_ROPE_PARTIAL>(cfg, x, ldx, W, bias, y, ldy, M, N, K, ep, s);
+    case LX_EPI_RESID:
+      return dispatch_cfg<LX_EPI_RESID>(cfg, x, ldx, W, bias, y, ldy, M, N, K, ep, s);
+    case LX_EPI_SWIGLU_PAIRED:
+      return dispatch_cfg<LX_EPI_SWIGLU_PAIRED>(cfg, x, ldx, W, bias, y, ldy, M, N, K, ep, s);
+  }
+  set_error("linear: unknown epilogue kind %d", kind);
+  return LX_ERR_ARG;
+}
+
+// Tile configuration by shape, from a sweep of Cfg0..Cfg6 on MI355X over the
+// estimator's projections at B*T = 1000 and 6000 rows.
+int pick_config(int M, int N, int K) {
+  const long tiles = (long)((M + 63) / 64) * ((N + 63) / 64);
+  if (tiles >= 2048) return (N >= 2048 && K <= 1024) ? 6 : 1;  // long utterances
+  if (N >= 3072) return 4;  // fused QKV at T = 500: split-K 2 with 64-wide slabs
+  return 1;                 // split-K 2: two waves per SIMD on 256-512 tiles
+}
+
 }  // namespace lx
 
 using namespace lx;
@@ -365,22 +536,19 @@ extern "C" int lx_linear_f32(const float* x, int ldx, const float* W, const floa
   if (rc) return rc;
   if (kind == LX_EPI_SWIGLU_PAIRED)
     LX_REQUIRE(ldy % 2 == 0, "linear: SWIGLU_PAIRED needs even ldy");
-  const long tiles = (long)((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+  const long tiles = (long)((M + 63) / 64) * ((N + 63) / 64);
   LX_REQUIRE(tiles < (1L << 31), "linear: too many tiles");
-  dim3 grid((unsigned)tiles), block(256);
-#define LX_GEMM_CASE(E)                                                                       \
-  case E:                                                                                     \
-    hipLaunchKernelGGL(gemm_nt_kernel<E>, grid, block, 0, stream, x, ldx, W, bias, y, ldy, M, \
-                       N, K, ep);                                                             \
-    break;
-  switch (kind) {
-    LX_GEMM_CASE(LX_EPI_NONE)
-    LX_GEMM_CASE(LX_EPI_GELU_TANH)
-    LX_GEMM_CASE(LX_EPI_GATED_RESID)
-    LX_GEMM_CASE(LX_EPI_ROPE_PARTIAL)
-    LX_GEMM_CASE(LX_EPI_RESID)
-    LX_GEMM_CASE(LX_EPI_SWIGLU_PAIRED)
-  }
-#undef LX_GEMM_CASE
-  return check_launch("gemm_nt_kernel");
+  return dispatch_gemm(kind, pick_config(M, N, K), x, ldx, W, bias, y, ldy, M, N, K, ep, stream);
 }
+
+#ifdef LX_GEMM_SWEEP
+// Tuning hook (built only into the sweep library, never into liblxops.so).
+extern "C" int lx_gemm_sweep(int cfg, int kind, const float* x, int ldx, const float* W,
+                             const float* bias, float* y, int ldy, int M, int N, int K,
+                             const lx_epilogue* epi, hipStream_t stream) {
+  EpiArgs ep;
+  int rc = make_epi(epi, N, &ep);
+  if (rc) return rc;
+  return dispatch_gemm(kind, cfg, x, ldx, W, bias, y, ldy, M, N, K, ep, stream);
+}
+#endif
