@@ -44,21 +44,27 @@ __global__ __launch_bounds__(256) void conv_mish_kernel(const float* __restrict_
     *reinterpret_cast<float4*>(xw + row * LDW + c4) = v;
   }
   const float* wg = wp + (long)g * K * CG * CG;
-  float4 wr[4];
-  auto wload = [&](int k) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) wr[j] = reinterpret_cast<const float4*>(wg + (long)k * CG * CG)[tid + 256 * j];
-  };
-  auto wstore = [&](int buf) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int idx = tid + 256 * j;
-      const int oc = idx >> 4, c4 = (idx & 15) * 4;
-      *reinterpret_cast<float4*>(wk + buf * CG * LDW + oc * LDW + c4) = wr[j];
-    }
-  };
-  wload(0);
-  wstore(0);
+  // Tap slabs: 64 oc x 64 ic = 1024 float4, four per thread, register staged
+  // (native vectors, no lambdas: keeps the staging in VGPRs).
+  floatx4 wr0, wr1, wr2, wr3;
+#define LX_WLOAD(k)                                                              \
+  do {                                                                           \
+    const floatx4* src = reinterpret_cast<const floatx4*>(wg + (long)(k) * CG * CG); \
+    wr0 = src[tid];                                                              \
+    wr1 = src[tid + 256];                                                        \
+    wr2 = src[tid + 512];                                                        \
+    wr3 = src[tid + 768];                                                        \
+  } while (0)
+#define LX_WSTORE(buf)                                                           \
+  do {                                                                           \
+    float* dst = wk + (buf) * CG * LDW;                                          \
+    *reinterpret_cast<floatx4*>(dst + ((tid) >> 4) * LDW + ((tid) & 15) * 4) = wr0; \
+    *reinterpret_cast<floatx4*>(dst + ((tid + 256) >> 4) * LDW + ((tid) & 15) * 4) = wr1; \
+    *reinterpret_cast<floatx4*>(dst + ((tid + 512) >> 4) * LDW + ((tid) & 15) * 4) = wr2; \
+    *reinterpret_cast<floatx4*>(dst + ((tid + 768) >> 4) * LDW + ((tid) & 15) * 4) = wr3; \
+  } while (0)
+  LX_WLOAD(0);
+  LX_WSTORE(0);
   __syncthreads();
 
   floatx16 acc;
@@ -66,21 +72,22 @@ __global__ __launch_bounds__(256) void conv_mish_kernel(const float* __restrict_
   for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
   for (int k = 0; k < K; ++k) {
     const int buf = k & 1;
-    if (k + 1 < K) wload(k + 1);
+    if (k + 1 < K) LX_WLOAD(k + 1);
     const float* a = xw + (wm * 32 + r + k) * LDW + h * 32;
     const float* w = wk + buf * CG * LDW + (wn * 32 + r) * LDW + h * 32;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      float4 av = *reinterpret_cast<const float4*>(a + 4 * j);
-      float4 bv = *reinterpret_cast<const float4*>(w + 4 * j);
-      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.x, bv.x, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.y, bv.y, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.z, bv.z, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.w, bv.w, acc, 0, 0, 0);
+      const floatx4 av = *reinterpret_cast<const floatx4*>(a + 4 * j);
+      const floatx4 bv = *reinterpret_cast<const floatx4*>(w + 4 * j);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[e], bv[e], acc, 0, 0, 0);
     }
-    if (k + 1 < K) wstore(buf ^ 1);
+    if (k + 1 < K) LX_WSTORE(buf ^ 1);
     __syncthreads();
   }
+#undef LX_WLOAD
+#undef LX_WSTORE
   // Epilogue through LDS (reuse the window region: TT x LDW floats).
   float* cs = smem;
 #pragma unroll

@@ -38,55 +38,102 @@ inline int grid_for(long work, int block) {
   return (int)g;
 }
 
-__global__ void gelu_kernel(const float* h, float* y, long n4, long n) {
-  const long stride = (long)gridDim.x * blockDim.x;
-  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride) {
-    float4 v = reinterpret_cast<const float4*>(h)[i];
-    v.x = gelu_tanh(v.x);
-    v.y = gelu_tanh(v.y);
-    v.z = gelu_tanh(v.z);
-    v.w = gelu_tanh(v.w);
-    reinterpret_cast<float4*>(y)[i] = v;
+// Elementwise kernels process kUnroll float4 per thread per pass, with all
+// loads issued before any arithmetic (memory-level parallelism on HBM).
+constexpr int kUnroll = 4;
+constexpr int kEwBlock = 256;
+
+inline unsigned ew_grid(long n4) {
+  long g = (n4 + (long)kEwBlock * kUnroll - 1) / ((long)kEwBlock * kUnroll);
+  if (g > 8192) g = 8192;
+  if (g < 1) g = 1;
+  return (unsigned)g;
+}
+
+__global__ __launch_bounds__(kEwBlock) void gelu_kernel(const float* h, float* y, long n4, long n) {
+  const long stride = (long)gridDim.x * kEwBlock * kUnroll;
+  for (long i0 = (long)blockIdx.x * kEwBlock * kUnroll + threadIdx.x; i0 < n4; i0 += stride) {
+    float4 v[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const long i = min(i0 + (long)u * kEwBlock, n4 - 1);
+      v[u] = reinterpret_cast<const float4*>(h)[i];
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const long i = i0 + (long)u * kEwBlock;
+      if (i < n4) {
+        float4 o;
+        o.x = gelu_tanh(v[u].x);
+        o.y = gelu_tanh(v[u].y);
+        o.z = gelu_tanh(v[u].z);
+        o.w = gelu_tanh(v[u].w);
+        reinterpret_cast<float4*>(y)[i] = o;
+      }
+    }
   }
   // scalar tail (n not a multiple of 4)
   long t = n4 * 4 + (long)blockIdx.x * blockDim.x + threadIdx.x;
   if (t < n) y[t] = gelu_tanh(h[t]);
 }
 
-__global__ void gated_residual_kernel(float* x, const float* __restrict__ y,
-                                      const float* __restrict__ gate, long gate_stride,
-                                      long rows, int T, int D4) {
+__global__ __launch_bounds__(kEwBlock) void gated_residual_kernel(
+    float* x, const float* __restrict__ y, const float* __restrict__ gate, long gate_stride,
+    long rows, int T, int D4) {
   const long n4 = rows * D4;
-  const long stride = (long)gridDim.x * blockDim.x;
-  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride) {
-    long row = i / D4;
-    int c4 = (int)(i - row * D4);
-    int b = (int)(row / T);
-    float4 g = reinterpret_cast<const float4*>(gate + (long)b * gate_stride)[c4];
-    float4 a = reinterpret_cast<float4*>(x)[i];
-    float4 v = reinterpret_cast<const float4*>(y)[i];
-    a.x += v.x * g.x;
-    a.y += v.y * g.y;
-    a.z += v.z * g.z;
-    a.w += v.w * g.w;
-    reinterpret_cast<float4*>(x)[i] = a;
+  const long stride = (long)gridDim.x * kEwBlock * kUnroll;
+  for (long i0 = (long)blockIdx.x * kEwBlock * kUnroll + threadIdx.x; i0 < n4; i0 += stride) {
+    float4 a[kUnroll], v[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const long i = min(i0 + (long)u * kEwBlock, n4 - 1);
+      a[u] = reinterpret_cast<const float4*>(x)[i];
+      v[u] = reinterpret_cast<const float4*>(y)[i];
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const long i = i0 + (long)u * kEwBlock;
+      if (i < n4) {
+        const long row = i / D4;
+        const int c4 = (int)(i - row * D4);
+        const int b = (int)(row / T);
+        const float4 g = reinterpret_cast<const float4*>(gate + (long)b * gate_stride)[c4];
+        a[u].x += v[u].x * g.x;
+        a[u].y += v[u].y * g.y;
+        a[u].z += v[u].z * g.z;
+        a[u].w += v[u].w * g.w;
+        reinterpret_cast<float4*>(x)[i] = a[u];
+      }
+    }
   }
 }
 
 __device__ __forceinline__ float silu_mul(float g, float u) { return (g / (1.0f + expf(-g))) * u; }
 
-__global__ void swiglu_kernel(const float* __restrict__ gate, const float* __restrict__ up,
-                              float* out, long n4, long n) {
-  const long stride = (long)gridDim.x * blockDim.x;
-  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride) {
-    float4 g = reinterpret_cast<const float4*>(gate)[i];
-    float4 u = reinterpret_cast<const float4*>(up)[i];
-    float4 o;
-    o.x = silu_mul(g.x, u.x);
-    o.y = silu_mul(g.y, u.y);
-    o.z = silu_mul(g.z, u.z);
-    o.w = silu_mul(g.w, u.w);
-    reinterpret_cast<float4*>(out)[i] = o;
+__global__ __launch_bounds__(kEwBlock) void swiglu_kernel(const float* __restrict__ gate,
+                                                          const float* __restrict__ up,
+                                                          float* out, long n4, long n) {
+  const long stride = (long)gridDim.x * kEwBlock * kUnroll;
+  for (long i0 = (long)blockIdx.x * kEwBlock * kUnroll + threadIdx.x; i0 < n4; i0 += stride) {
+    float4 g[kUnroll], u4[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const long i = min(i0 + (long)u * kEwBlock, n4 - 1);
+      g[u] = reinterpret_cast<const float4*>(gate)[i];
+      u4[u] = reinterpret_cast<const float4*>(up)[i];
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const long i = i0 + (long)u * kEwBlock;
+      if (i < n4) {
+        float4 o;
+        o.x = silu_mul(g[u].x, u4[u].x);
+        o.y = silu_mul(g[u].y, u4[u].y);
+        o.z = silu_mul(g[u].z, u4[u].z);
+        o.w = silu_mul(g[u].w, u4[u].w);
+        reinterpret_cast<float4*>(out)[i] = o;
+      }
+    }
   }
   long t = n4 * 4 + (long)blockIdx.x * blockDim.x + threadIdx.x;
   if (t < n) out[t] = silu_mul(gate[t], up[t]);
@@ -173,8 +220,7 @@ extern "C" int lx_gelu_tanh_f32(const float* h, float* y, long n, hipStream_t st
   LX_REQUIRE(((uintptr_t)h | (uintptr_t)y) % 16 == 0, "gelu: pointers must be 16-byte aligned");
   if (n == 0) return LX_OK;
   long n4 = n / 4;
-  hipLaunchKernelGGL(gelu_kernel, dim3(grid_for(n4 > 0 ? n4 : 1, 256)), dim3(256), 0, stream, h,
-                     y, n4, n);
+  hipLaunchKernelGGL(gelu_kernel, dim3(ew_grid(n4)), dim3(kEwBlock), 0, stream, h, y, n4, n);
   return check_launch("gelu_kernel");
 }
 
@@ -187,7 +233,7 @@ extern "C" int lx_gated_residual_f32(float* x, const float* y, const float* gate
   LX_REQUIRE(((uintptr_t)x | (uintptr_t)y | (uintptr_t)gate) % 16 == 0,
              "gated_residual: pointers must be 16-byte aligned");
   long rows = (long)B * T;
-  hipLaunchKernelGGL(gated_residual_kernel, dim3(grid_for(rows * D / 4, 256)), dim3(256), 0,
+  hipLaunchKernelGGL(gated_residual_kernel, dim3(ew_grid(rows * D / 4)), dim3(kEwBlock), 0,
                      stream, x, y, gate, gate_stride, rows, T, D / 4);
   return check_launch("gated_residual_kernel");
 }
@@ -199,8 +245,8 @@ extern "C" int lx_swiglu_f32(const float* gate, const float* up, float* out, lon
              "swiglu: pointers must be 16-byte aligned");
   if (n == 0) return LX_OK;
   long n4 = n / 4;
-  hipLaunchKernelGGL(swiglu_kernel, dim3(grid_for(n4 > 0 ? n4 : 1, 256)), dim3(256), 0, stream,
-                     gate, up, out, n4, n);
+  hipLaunchKernelGGL(swiglu_kernel, dim3(ew_grid(n4)), dim3(kEwBlock), 0, stream, gate, up, out,
+                     n4, n);
   return check_launch("swiglu_kernel");
 }
 

@@ -10,20 +10,34 @@
 namespace lx {
 namespace {
 
-constexpr int kRowsPerBlock = 8;           // 8 waves, 512 threads
+constexpr int kRowsPerBlock = 4;  // 4 waves, 256 threads: 250 blocks at 1000 rows
 
 template <int NV>
 __global__ __launch_bounds__(kRowsPerBlock * kWave) void adaln_kernel(
     const float* x, const float* __restrict__ shift,
     const float* __restrict__ scale, long mod_stride, float* y, int rows,
     int T, int D, float eps) {
-  // LDS: (1 + scale) and shift for up to two batches touched by this block.
+  // LDS: (1 + scale) and shift for the (at most two, when T >= rows per block)
+  // batches this block touches.
   extern __shared__ float smem[];
   const int D4 = D >> 2;
   const int row0 = blockIdx.x * kRowsPerBlock;
+  const int wave = threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave;
+  const int row = row0 + wave;
+  const bool live = row < rows;
+  // Issue this wave's row loads first so their latency overlaps the
+  // modulation staging below.
+  const float4* xr = reinterpret_cast<const float4*>(x + (long)min(row, rows - 1) * D);
+  float4 v[NV];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    int i = lane + j * kWave;
+    v[j] = i < D4 ? xr[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
   const int b_first = row0 / T;
   const int last_row = min(row0 + kRowsPerBlock, rows) - 1;
-  const int nb = last_row / T - b_first + 1;  // 1 or 2 when T >= kRowsPerBlock
+  const int nb = last_row / T - b_first + 1;
   for (int bi = 0; bi < nb; ++bi) {
     const float4* sc = reinterpret_cast<const float4*>(scale + (long)(b_first + bi) * mod_stride);
     const float4* sh = reinterpret_cast<const float4*>(shift + (long)(b_first + bi) * mod_stride);
@@ -35,22 +49,9 @@ __global__ __launch_bounds__(kRowsPerBlock * kWave) void adaln_kernel(
       s2[i] = sh[i];
     }
   }
-  __syncthreads();
-
-  const int wave = threadIdx.x / kWave;
-  const int lane = threadIdx.x % kWave;
-  const int row = row0 + wave;
-  if (row >= rows) return;
-  const int bi = row / T - b_first;
-  const float4* xr = reinterpret_cast<const float4*>(x + (long)row * D);
-  float4 v[NV];
   float s = 0.0f;
 #pragma unroll
-  for (int j = 0; j < NV; ++j) {
-    int i = lane + j * kWave;
-    v[j] = i < D4 ? xr[i] : make_float4(0.f, 0.f, 0.f, 0.f);
-    s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
-  }
+  for (int j = 0; j < NV; ++j) s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
   const float mean = wave_sum(s) / (float)D;
   float q = 0.0f;
 #pragma unroll
@@ -63,6 +64,9 @@ __global__ __launch_bounds__(kRowsPerBlock * kWave) void adaln_kernel(
   }
   const float var = wave_sum(q) / (float)D;  // biased, as ggml_norm / nn.LayerNorm
   const float rstd = 1.0f / sqrtf(var + eps);
+  __syncthreads();
+  if (!live) return;
+  const int bi = row / T - b_first;
   const float4* s1 = reinterpret_cast<const float4*>(smem + (2 * bi) * D);
   const float4* s2 = reinterpret_cast<const float4*>(smem + (2 * bi + 1) * D);
   float4* yr = reinterpret_cast<float4*>(y + (long)row * D);
@@ -85,24 +89,27 @@ __global__ __launch_bounds__(kRowsPerBlock * kWave) void rmsnorm_kernel(
     const float* x, const float* __restrict__ w, float* y, int rows, int D, float eps) {
   extern __shared__ float smem[];
   const int D4 = D >> 2;
-  for (int i = threadIdx.x; i < D4; i += blockDim.x)
-    reinterpret_cast<float4*>(smem)[i] = reinterpret_cast<const float4*>(w)[i];
-  __syncthreads();
   const int wave = threadIdx.x / kWave;
   const int lane = threadIdx.x % kWave;
   const int row = blockIdx.x * kRowsPerBlock + wave;
-  if (row >= rows) return;
-  const float4* xr = reinterpret_cast<const float4*>(x + (long)row * D);
+  const bool live = row < rows;
+  const float4* xr = reinterpret_cast<const float4*>(x + (long)min(row, rows - 1) * D);
   float4 v[NV];
-  float s = 0.0f;
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
     int i = lane + j * kWave;
     v[j] = i < D4 ? xr[i] : make_float4(0.f, 0.f, 0.f, 0.f);
-    s += (v[j].x * v[j].x + v[j].y * v[j].y) + (v[j].z * v[j].z + v[j].w * v[j].w);
   }
+  for (int i = threadIdx.x; i < D4; i += blockDim.x)
+    reinterpret_cast<float4*>(smem)[i] = reinterpret_cast<const float4*>(w)[i];
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j)
+    s += (v[j].x * v[j].x + v[j].y * v[j].y) + (v[j].z * v[j].z + v[j].w * v[j].w);
   const float ms = wave_sum(s) / (float)D;
   const float r = 1.0f / sqrtf(ms + eps);
+  __syncthreads();
+  if (!live) return;
   float4* yr = reinterpret_cast<float4*>(y + (long)row * D);
   const float4* ws = reinterpret_cast<const float4*>(smem);
 #pragma unroll
