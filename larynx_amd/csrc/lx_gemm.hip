@@ -276,6 +276,193 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void gemm_tile_kernel(
   }
 }
 
+// Pipelined variant of the tiled kernel for 64 x 64 tiles, 4 waves (2 x 2) per
+// k-group: global loads run two slabs ahead of the MFMAs (two register
+// stages, statically indexed by unrolling the slab loop by 2), and within a
+// slab the LDS fragments of the next 32-wide sub-slab are read while the
+// current sub-slab's MFMAs issue.  One barrier per slab.
+template <int EPI, int BK, int KS>
+__global__ __launch_bounds__(256 * KS) void gemm_pipe_kernel(
+    const float* __restrict__ X, int ldx, const float* __restrict__ W,
+    const float* __restrict__ bias, float* Y, int ldy, int M, int N, int K, EpiArgs ep) {
+  constexpr int BM = 64, BN = 64, GT = 256, NT = GT * KS;
+  constexpr int LDA = BK + 4;
+  constexpr int A4 = BM * BK / 4;          // float4 per operand slab
+  constexpr int L = A4 / GT;               // float4 per thread per operand
+  constexpr int S32 = BK / 32;             // 32-wide sub-slabs
+  static_assert(A4 % GT == 0 && BK % 32 == 0, "bad slab");
+  extern __shared__ __attribute__((aligned(16))) float smem[];
+
+  const int tiles_m = (M + BM - 1) / BM;
+  const int tiles_n = (N + BN - 1) / BN;
+  const int nwg = tiles_m * tiles_n;
+  int id = blockIdx.x;
+  const int full = (nwg / 8) * 8;
+  if (id < full) id = (id % 8) * (full / 8) + id / 8;
+  const int m0 = (id % tiles_m) * BM, n0 = (id / tiles_m) * BN;
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int kg = wave >> 2;
+  const int wm = (wave >> 1) & 1, wn = wave & 1;
+  const int r = lane & 31, h = lane >> 5;
+  const int gtid = tid & (GT - 1);
+  float* As = smem + kg * 2 * (BM + BN) * LDA;
+  float* Ws = As + 2 * BM * LDA;
+
+  const float* pa[L];
+  const float* pw[L];
+  int cc[L], rr[L];
+  bool oka[L], okw[L];
+#pragma unroll
+  for (int i = 0; i < L; ++i) {
+    const int idx = gtid + i * GT;
+    rr[i] = idx / (BK / 4);
+    cc[i] = (idx % (BK / 4)) * 4;
+    oka[i] = m0 + rr[i] < M;
+    okw[i] = n0 + rr[i] < N;
+    pa[i] = X + (long)min(m0 + rr[i], M - 1) * ldx;
+    pw[i] = W + (long)min(n0 + rr[i], N - 1) * K;
+  }
+  floatx4 sa0[L], sw0[L], sa1[L], sw1[L];  // two register stages
+#define LX_GLOAD(SA, SW, KT)                                                         \
+  do {                                                                               \
+    _Pragma("unroll") for (int i = 0; i < L; ++i) {                                   \
+      SA[i] = *reinterpret_cast<const floatx4*>(pa[i] + min((KT) * BK + cc[i], K - 4)); \
+      SW[i] = *reinterpret_cast<const floatx4*>(pw[i] + min((KT) * BK + cc[i], K - 4)); \
+    }                                                                                \
+  } while (0)
+#define LX_SSTORE(SA, SW, BUF, KT)                                                   \
+  do {                                                                               \
+    _Pragma("unroll") for (int i = 0; i < L; ++i) {                                   \
+      const bool kin = (KT) * BK + cc[i] < K;                                        \
+      floatx4 va, vw;                                                                \
+      _Pragma("unroll") for (int e = 0; e < 4; ++e) {                                 \
+        va[e] = (oka[i] && kin) ? SA[i][e] : 0.0f;                                    \
+        vw[e] = (okw[i] && kin) ? SW[i][e] : 0.0f;                                    \
+      }                                                                              \
+      *reinterpret_cast<floatx4*>(As + (BUF) * BM * LDA + rr[i] * LDA + cc[i]) = va; \
+      *reinterpret_cast<floatx4*>(Ws + (BUF) * BN * LDA + rr[i] * LDA + cc[i]) = vw; \
+    }                                                                                \
+  } while (0)
+
+  floatx16 acc;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
+
+  const int nk = (K + BK - 1) / BK;
+  const int iters = (nk + KS - 1) / KS;
+  // slab of iteration it for this k-group
+#define LX_KT(IT) ((IT) * KS + kg)
+  // Loads and stores are unconditional (slab index clamped into range; the
+  // stored values are zero-masked by k), so the loop body is straight-line and
+  // the compiler's vmcnt waits count exactly the two stages in flight.
+#define LX_KC(IT) min(LX_KT(IT), nk - 1)
+  LX_GLOAD(sa0, sw0, LX_KC(0));
+  LX_SSTORE(sa0, sw0, 0, LX_KT(0));
+  LX_GLOAD(sa1, sw1, LX_KC(1));
+  LX_GLOAD(sa0, sw0, LX_KC(2));
+  __syncthreads();
+
+  // One slab: MFMAs on LDS buffer BUF, then the next slab (held in stage
+  // SNEXT) goes to the other buffer and stage SNEXT reloads three slabs ahead.
+#define LX_SLAB(IT, BUF, SNA, SNW)                                                     \
+  do {                                                                                 \
+    if (LX_KT(IT) < nk) {                                                              \
+      const float* ab = As + (BUF) * BM * LDA + (wm * 32 + r) * LDA + h * 16;         \
+      const float* wb = Ws + (BUF) * BN * LDA + (wn * 32 + r) * LDA + h * 16;         \
+      floatx4 af[2][4], bf[2][4];                                                      \
+      _Pragma("unroll") for (int j = 0; j < 4; ++j) {                                   \
+        af[0][j] = *reinterpret_cast<const floatx4*>(ab + 4 * j);                      \
+        bf[0][j] = *reinterpret_cast<const floatx4*>(wb + 4 * j);                      \
+      }                                                                                \
+      _Pragma("unroll") for (int s = 0; s < S32; ++s) {                                 \
+        if (s + 1 < S32) {                                                             \
+          _Pragma("unroll") for (int j = 0; j < 4; ++j) {                               \
+            af[(s + 1) & 1][j] = *reinterpret_cast<const floatx4*>(ab + (s + 1) * 32 + 4 * j); \
+            bf[(s + 1) & 1][j] = *reinterpret_cast<const floatx4*>(wb + (s + 1) * 32 + 4 * j); \
+          }                                                                            \
+        }                                                                              \
+        _Pragma("unroll") for (int j = 0; j < 4; ++j)                                   \
+          _Pragma("unroll") for (int e = 0; e < 4; ++e)                                 \
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(af[s & 1][j][e], bf[s & 1][j][e], acc, 0, 0, 0); \
+      }                                                                                \
+    }                                                                                  \
+    LX_SSTORE(SNA, SNW, (BUF) ^ 1, LX_KT((IT) + 1));                                   \
+    LX_GLOAD(SNA, SNW, LX_KC((IT) + 3));                                               \
+    __syncthreads();                                                                   \
+  } while (0)
+
+  // Both halves run unconditionally (a surplus half skips its MFMAs: its slab
+  // is past the end), so the loop has a single back-edge state for the waits.
+  for (int it = 0; it < iters; it += 2) {
+    LX_SLAB(it, 0, sa1, sw1);
+    LX_SLAB(it + 1, 1, sa0, sw0);
+  }
+#undef LX_SLAB
+#undef LX_KC
+#undef LX_KT
+#undef LX_GLOAD
+#undef LX_SSTORE
+
+  constexpr int LDC = BN + 4;
+  float* Cs = smem;
+#pragma unroll
+  for (int g = KS - 1; g >= 0; --g) {
+    if (kg == g) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int row = wm * 32 + (i >> 2) * 8 + h * 4 + (i & 3);
+        const int col = wn * 32 + r;
+        float v = acc[i];
+        if (g < KS - 1) v += Cs[row * LDC + col];
+        Cs[row * LDC + col] = v;
+      }
+    }
+    __syncthreads();
+  }
+  for (int idx = tid; idx < BM * BN / 4; idx += NT) {
+    const int row = idx / (BN / 4), c = (idx % (BN / 4)) * 4;
+    const int m = m0 + row, n = n0 + c;
+    if (m < M && n < N)
+      epilogue4<EPI>(Y, ldy, m, n, N, bias,
+                     *reinterpret_cast<const float4*>(Cs + row * LDC + c), ep);
+  }
+}
+
+template <int BK, int KS>
+struct PipeCfg {
+  static constexpr int threads = 256 * KS;
+  static size_t lds() {
+    size_t a = (size_t)KS * 2 * (64 + 64) * (BK + 4) * sizeof(float);
+    size_t c = (size_t)64 * (64 + 4) * sizeof(float);
+    return a > c ? a : c;
+  }
+};
+
+template <int EPI, int BK, int KS>
+int launch_pipe(const float* x, int ldx, const float* W, const float* bias, float* y, int ldy,
+                int M, int N, int K, const EpiArgs& ep, hipStream_t stream) {
+  auto kern = gemm_pipe_kernel<EPI, BK, KS>;
+  const size_t lds = PipeCfg<BK, KS>::lds();
+  if (lds > 64 * 1024) {
+    static bool attr_set = false;
+    if (!attr_set) {
+      if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)lds) != hipSuccess) {
+        set_error("linear: cannot raise the LDS limit to %zu bytes", lds);
+        return LX_ERR_LAUNCH;
+      }
+      attr_set = true;
+    }
+  }
+  const long tiles = (long)((M + 63) / 64) * ((N + 63) / 64);
+  hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(PipeCfg<BK, KS>::threads), lds, stream, x,
+                     ldx, W, bias, y, ldy, M, N, K, ep);
+  return check_launch("gemm_pipe_kernel");
+}
+
 template <int BM, int BN, int BK, int WM, int WN, int KS>
 struct TileCfg {
   static constexpr int bm = BM, bn = BN, bk = BK, wm = WM, wn = WN, ks = KS;
@@ -468,7 +655,7 @@ using Cfg3 = TileCfg<64, 64, 64, 2, 2, 1>;
 using Cfg4 = TileCfg<64, 64, 64, 2, 2, 2>;
 using Cfg5 = TileCfg<128, 64, 32, 2, 2, 1>;
 using Cfg6 = TileCfg<64, 128, 32, 2, 2, 1>;
-constexpr int kNumCfg = 7;
+constexpr int kNumCfg = 11;  // 7..10: pipelined 64x64 (BK, KS) = (32,1) (32,2) (64,1) (64,2)
 
 template <int EPI>
 int dispatch_cfg(int cfg, const float* x, int ldx, const float* W, const float* bias, float* y,
@@ -481,6 +668,10 @@ int dispatch_cfg(int cfg, const float* x, int ldx, const float* W, const float* 
     case 4: return launch_tile<EPI, Cfg4>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
     case 5: return launch_tile<EPI, Cfg5>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
     case 6: return launch_tile<EPI, Cfg6>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
+    case 7: return launch_pipe<EPI, 32, 1>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
+    case 8: return launch_pipe<EPI, 32, 2>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
+    case 9: return launch_pipe<EPI, 64, 1>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
+    case 10: return launch_pipe<EPI, 64, 2>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
   }
   set_error("linear: unknown tile configuration %d", cfg);
   return LX_ERR_ARG;
@@ -506,13 +697,16 @@ int dispatch_gemm(int kind, int cfg, const float* x, int ldx, const float* W, co
   return LX_ERR_ARG;
 }
 
-// Tile configuration by shape, from a sweep of Cfg0..Cfg6 on MI355X over the
-// estimator's projections at B*T = 1000 and 6000 rows.
+// Tile configuration by shape, from an on-device sweep of all configurations
+// over the estimator's projections at B*T = 1000 and 6000 rows (MI355X):
+//   >= 512 tiles of 64x64 (>= 2 per CU): the pipelined kernel, BK = 32, no
+//     split (QKV 62.6 us = 100 TFLOP/s, FF0 43.3 us at B*T = 1000);
+//   fewer tiles (N = 1024 at B*T = 1000, one tile per CU): the tiled kernel
+//     with intra-workgroup split-K 2 for two waves per SIMD (out 26.7 us).
 int pick_config(int M, int N, int K) {
+  (void)K;
   const long tiles = (long)((M + 63) / 64) * ((N + 63) / 64);
-  if (tiles >= 2048) return (N >= 2048 && K <= 1024) ? 6 : 1;  // long utterances
-  if (N >= 3072) return 4;  // fused QKV at T = 500: split-K 2 with 64-wide slabs
-  return 1;                 // split-K 2: two waves per SIMD on 256-512 tiles
+  return tiles >= 512 ? 7 : 1;
 }
 
 }  // namespace lx
