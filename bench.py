@@ -7,8 +7,9 @@ norm_out/proj_out + CFG combine/x update), inputs resident in HBM.
 value = T * steps / wall time of the timed region (mel frames per second).
 
 Also reported on the same JSON line:
-  roofline      the dominant kernel's achieved FLOP/s (HIP events on the stream
-                the library launches on) vs the 157.3 TFLOP/s fp32 MFMA peak;
+  roofline      the dominant kernel's achieved FLOP/s (a HIP event pair around each
+                launch, on the stream the library launches on) vs the 157.3 TFLOP/s
+                fp32 MFMA peak;
   kernels       per-kernel-class HIP-event timings of one step's launches;
   fused_ops     achieved HBM GB/s of every fused op at the configs' shapes, with
                 each launch on a distinct buffer set (> 256 MB rotation, so the
@@ -39,6 +40,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-fused", action="store_true", help="skip the fused-op GB/s sweep")
+    ap.add_argument("--no-llm", action="store_true", help="skip the Qwen2 prefill/decode timing")
     return ap.parse_args()
 
 
@@ -55,6 +57,24 @@ def event_time_ms(fn, n, torch):
     b.record(s)
     b.synchronize()
     return a.elapsed_time(b) / n
+
+
+def per_launch_ms(fn, n, torch):
+    """Average ms of one call of fn, each call bracketed by its own pair of HIP
+    events on torch's current stream (the library's launch stream): measures the
+    kernel itself, not the dispatch gaps between back-to-back launches."""
+    s = torch.cuda.current_stream()
+    fn()
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(n)]
+    for a, b in evs:
+        a.record(s)
+        fn()
+        b.record(s)
+    torch.cuda.synchronize()
+    t = sorted(a.elapsed_time(b) for a, b in evs)
+    return sum(t[: max(1, n - n // 10)]) / max(1, n - n // 10)  # drop the slowest 10%
 
 
 def graph_time_ms(fn, n, torch, reps=3):
@@ -125,10 +145,19 @@ def gemm_kernels(torch, ops, T, dev):
                                             out=att),
                       4 * B * 16 * T * T * 64, 1),
     }
+    # hipBLASLt (torch.mm, fp32) on the same plain-GEMM shapes, as a library reference point
+    lib_ref = {
+        "gemm_qkv_rope": lambda: torch.mm(xd, wq.T),
+        "gemm_out_gated": lambda: torch.mm(xd, wo.T),
+        "gemm_ff0_gelu": lambda: torch.mm(xd, w1.T),
+        "gemm_ff2_gated": lambda: torch.mm(xf, w2.T),
+    }
     for name, (fn, flops, per_block) in cases.items():
-        ms = event_time_ms(fn, n, torch)
+        ms = per_launch_ms(fn, n, torch)
         out[name] = {"avg_us": ms * 1e3, "flop": flops, "tflops": flops / (ms * 1e-3) / 1e12,
                      "per_block": per_block}
+        if name in lib_ref:
+            out[name]["hipblaslt_us"] = per_launch_ms(lib_ref[name], n, torch) * 1e3
     return out
 
 
@@ -200,6 +229,66 @@ def fused_ops_gbs(torch, ops, dev):
         lambda y: ops.embed_gather(table, ids, out=y), 2 * 256 * 896 * 4 + 256 * 4,
         256 * 896 * 4, "256 rows of the 151936x896 text table")
     return res
+
+
+def long_utterance(torch, est, dev, g, steps=3):
+    """ms per CFG Euler step at T=3000 (the long-utterance config), same estimator."""
+    from larynx_amd.flow import cfm_t_span
+    T = 3000
+    x = torch.randn(80, T, device=dev, generator=g)
+    mu = torch.randn(80, T, device=dev, generator=g)
+    cond = torch.randn(80, T, device=dev, generator=g)
+    spks = torch.randn(80, device=dev, generator=g) / 80 ** 0.5
+    ts = cfm_t_span(10)
+    est.cfm_step(x, mu, cond, spks, float(ts[0]), float(ts[1] - ts[0]))
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        est.cfm_step(x, mu, cond, spks, float(ts[i]), float(ts[i + 1] - ts[i]))
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    return {"T": T, "ms_per_step": round(ms, 3), "mel_frames_per_s": round(T / ms * 1e3, 1)}
+
+
+def qwen2_lm(torch, dev, g):
+    """Qwen2-0.5B (24 layers, full vocabularies): prefill at L=256 (160 text + 96
+    speech-prompt rows) and single-token decode against KV caches of 1 / 256 / 1024 /
+    2048 entries.  Decode is weight-streaming: 1.46 GB of weights per token."""
+    from larynx_amd.llm import Qwen2Config, Qwen2LM, qwen2_param_shapes
+    cfg = Qwen2Config()
+    params = {n: torch.randn(*sh, device=dev, generator=g) * 0.02
+              for n, sh in qwen2_param_shapes(cfg)}
+    lm = Qwen2LM(params, cfg, max_ctx=2304)
+    text = [int(v) for v in torch.randint(0, cfg.text_vocab, (160,), generator=g,
+                                          device=dev).cpu()]
+    speech = [int(v) for v in torch.randint(0, 6564, (94,), generator=g, device=dev).cpu()]
+    lm_in = lm.build_lm_input(text, speech)
+    lm.prefill(lm_in)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(3):
+        lm.prefill(lm_in)
+    torch.cuda.synchronize()
+    prefill_ms = (time.perf_counter() - t0) * 1e3 / 3
+    out = {"prefill_L256_ms": round(prefill_ms, 3), "decode_ms_per_token": {}}
+    weight_bytes = sum(t.numel() for n, t in params.items() if n != "embed_tokens.weight") * 4
+    for cache in (1, 256, 1024, 2048):
+        lm.set_cache_len(cache)
+        lm.decode(17)
+        torch.cuda.synchronize()
+        n = 20
+        t0 = time.perf_counter()
+        for i in range(n):
+            lm.set_cache_len(cache)
+            lm.decode(100 + i)
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / n
+        out["decode_ms_per_token"][str(cache)] = round(ms, 4)
+    ms1 = out["decode_ms_per_token"]["1"]
+    out["decode_weight_stream_gbs_at_cache1"] = round(weight_bytes / (ms1 * 1e-3) / 1e9, 1)
+    lm.close()
+    del params
+    return out
 
 
 def cpu_baseline(T, seconds):
@@ -295,8 +384,10 @@ def main():
                 "frac": round(dom["tflops"] / MFMA_F32_PEAK_TFLOPS, 4), "traffic": None,
                 "avg_us": round(dom["avg_us"], 2), "flop_per_launch": dom["flop"]}
     gemm_flop_step = 22 * sum(k["flop"] for k in kernels.values())
+    long_t = long_utterance(torch, est, dev, g)
     fused = {} if args.no_fused else fused_ops_gbs(torch, ops, dev)
     est.close()
+    qwen = None if args.no_llm else qwen2_lm(torch, dev, g)
 
     cpu = None
     if not args.no_cpu:
@@ -322,8 +413,10 @@ def main():
         "euler_10step_ms": round(solve_ms, 3),
         "step_tflops": round(gemm_flop_step / (ms_per_step * 1e-3) / 1e12, 2),
         "roofline": roofline,
-        "kernels": {k: {"avg_us": round(v["avg_us"], 2), "tflops": round(v["tflops"], 2)}
-                    for k, v in kernels.items()},
+        "kernels": {k: {kk: round(vv, 2) for kk, vv in v.items() if kk in
+                        ("avg_us", "tflops", "hipblaslt_us")} for k, v in kernels.items()},
+        "long_utterance": long_t,
+        "qwen2": qwen,
         "fused_ops": {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv)
                           for kk, vv in v.items()} for k, v in fused.items()},
         "cpu_baseline": cpu,

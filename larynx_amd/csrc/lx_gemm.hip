@@ -280,8 +280,11 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void gemm_tile_kernel(
 // k-group: global loads run two slabs ahead of the MFMAs (two register
 // stages, statically indexed by unrolling the slab loop by 2), and within a
 // slab the LDS fragments of the next 32-wide sub-slab are read while the
-// current sub-slab's MFMAs issue.  One barrier per slab.
-template <int EPI, int BK, int KS>
+// current sub-slab's MFMAs issue.  One barrier per slab.  With IL set, the
+// slab body (one basic block) carries scheduling-group barriers that spread the
+// DS reads, DS writes and global loads between the MFMAs of the wave's single
+// accumulator chain, so they issue in the MFMA shadow instead of in bursts.
+template <int EPI, int BK, int KS, bool IL>
 __global__ __launch_bounds__(256 * KS) void gemm_pipe_kernel(
     const float* __restrict__ X, int ldx, const float* __restrict__ W,
     const float* __restrict__ bias, float* Y, int ldy, int M, int N, int K, EpiArgs ep) {
@@ -369,33 +372,53 @@ __global__ __launch_bounds__(256 * KS) void gemm_pipe_kernel(
   // SNEXT) goes to the other buffer and stage SNEXT reloads three slabs ahead.
 #define LX_SLAB(IT, BUF, SNA, SNW)                                                     \
   do {                                                                                 \
-    if (LX_KT(IT) < nk) {                                                              \
-      const float* ab = As + (BUF) * BM * LDA + (wm * 32 + r) * LDA + h * 16;         \
-      const float* wb = Ws + (BUF) * BN * LDA + (wn * 32 + r) * LDA + h * 16;         \
-      floatx4 af[2][4], bf[2][4];                                                      \
-      _Pragma("unroll") for (int j = 0; j < 4; ++j) {                                   \
-        af[0][j] = *reinterpret_cast<const floatx4*>(ab + 4 * j);                      \
-        bf[0][j] = *reinterpret_cast<const floatx4*>(wb + 4 * j);                      \
-      }                                                                                \
-      _Pragma("unroll") for (int s = 0; s < S32; ++s) {                                 \
-        if (s + 1 < S32) {                                                             \
-          _Pragma("unroll") for (int j = 0; j < 4; ++j) {                               \
-            af[(s + 1) & 1][j] = *reinterpret_cast<const floatx4*>(ab + (s + 1) * 32 + 4 * j); \
-            bf[(s + 1) & 1][j] = *reinterpret_cast<const floatx4*>(wb + (s + 1) * 32 + 4 * j); \
-          }                                                                            \
+    /* No branch around the MFMAs: a surplus slab (past the end of K) holds zeros in \
+       LDS (SSTORE masks k >= K), so it adds exact zeros and the body stays one     \
+       scheduling region. */                                                         \
+    const float* ab = As + (BUF) * BM * LDA + (wm * 32 + r) * LDA + h * 16;           \
+    const float* wb = Ws + (BUF) * BN * LDA + (wn * 32 + r) * LDA + h * 16;           \
+    floatx4 af[2][4], bf[2][4];                                                        \
+    _Pragma("unroll") for (int j = 0; j < 4; ++j) {                                     \
+      af[0][j] = *reinterpret_cast<const floatx4*>(ab + 4 * j);                        \
+      bf[0][j] = *reinterpret_cast<const floatx4*>(wb + 4 * j);                        \
+    }                                                                                  \
+    _Pragma("unroll") for (int s = 0; s < S32; ++s) {                                   \
+      if (s + 1 < S32) {                                                               \
+        _Pragma("unroll") for (int j = 0; j < 4; ++j) {                                 \
+          af[(s + 1) & 1][j] = *reinterpret_cast<const floatx4*>(ab + (s + 1) * 32 + 4 * j); \
+          bf[(s + 1) & 1][j] = *reinterpret_cast<const floatx4*>(wb + (s + 1) * 32 + 4 * j); \
         }                                                                              \
-        _Pragma("unroll") for (int j = 0; j < 4; ++j)                                   \
-          _Pragma("unroll") for (int e = 0; e < 4; ++e)                                 \
-            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(af[s & 1][j][e], bf[s & 1][j][e], acc, 0, 0, 0); \
       }                                                                                \
+      _Pragma("unroll") for (int j = 0; j < 4; ++j)                                     \
+        _Pragma("unroll") for (int e = 0; e < 4; ++e)                                   \
+          acc = __builtin_amdgcn_mfma_f32_32x32x2f32(af[s & 1][j][e], bf[s & 1][j][e], acc, 0, 0, 0); \
     }                                                                                  \
     LX_SSTORE(SNA, SNW, (BUF) ^ 1, LX_KT((IT) + 1));                                   \
     LX_GLOAD(SNA, SNW, LX_KC((IT) + 3));                                               \
+    if (IL) {                                                                          \
+      /* interleave: two DS reads up front, then MFMAs alternating with the        \
+         remaining DS reads (8 per 32-wide sub-slab), the DS writes and the global  \
+         loads (2 L each), then the remaining MFMAs (16 per sub-slab) */            \
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);                               \
+      _Pragma("unroll") for (int q = 0; q < 8 * S32 - 2; ++q) {                         \
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                             \
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                             \
+      }                                                                                \
+      _Pragma("unroll") for (int q = 0; q < 2 * L; ++q) {                               \
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                             \
+        __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);                             \
+      }                                                                                \
+      _Pragma("unroll") for (int q = 0; q < 2 * L; ++q) {                               \
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                             \
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                             \
+      }                                                                                \
+      __builtin_amdgcn_sched_group_barrier(0x008, 16 * S32 - (8 * S32 - 2) - 4 * L, 0); \
+    }                                                                                  \
     __syncthreads();                                                                   \
   } while (0)
 
-  // Both halves run unconditionally (a surplus half skips its MFMAs: its slab
-  // is past the end), so the loop has a single back-edge state for the waits.
+  // Both halves run unconditionally (a surplus half multiplies the zeros its
+  // slab holds), so the loop has a single back-edge state for the waits.
   for (int it = 0; it < iters; it += 2) {
     LX_SLAB(it, 0, sa1, sw1);
     LX_SLAB(it + 1, 1, sa0, sw0);
@@ -441,10 +464,10 @@ struct PipeCfg {
   }
 };
 
-template <int EPI, int BK, int KS>
+template <int EPI, int BK, int KS, bool IL>
 int launch_pipe(const float* x, int ldx, const float* W, const float* bias, float* y, int ldy,
                 int M, int N, int K, const EpiArgs& ep, hipStream_t stream) {
-  auto kern = gemm_pipe_kernel<EPI, BK, KS>;
+  auto kern = gemm_pipe_kernel<EPI, BK, KS, IL>;
   const size_t lds = PipeCfg<BK, KS>::lds();
   if (lds > 64 * 1024) {
     static bool attr_set = false;
@@ -647,15 +670,13 @@ int gemv_epi(const float* x, int ldx, const float* W, const float* bias, float* 
   return check_launch("gemv_epi_kernel");
 }
 
-// Tile configurations (BM, BN, BK, waves M x N, split-K).
-using Cfg0 = TileCfg<64, 64, 32, 2, 2, 1>;
-using Cfg1 = TileCfg<64, 64, 32, 2, 2, 2>;
-using Cfg2 = TileCfg<64, 64, 32, 2, 2, 4>;
-using Cfg3 = TileCfg<64, 64, 64, 2, 2, 1>;
-using Cfg4 = TileCfg<64, 64, 64, 2, 2, 2>;
-using Cfg5 = TileCfg<128, 64, 32, 2, 2, 1>;
-using Cfg6 = TileCfg<64, 128, 32, 2, 2, 1>;
-constexpr int kNumCfg = 11;  // 7..10: pipelined 64x64 (BK, KS) = (32,1) (32,2) (64,1) (64,2)
+// Configurations the sweep hook can select:
+//   0: tiled 64 x 64, BK 32, split-K 2        1: tiled 128 x 64, BK 32
+//   2: pipelined BK 32                        3: pipelined BK 32, split-K 2
+//   4: pipelined BK 32, interleaved           5: pipelined BK 32, split-K 2, interleaved
+//   6: pipelined BK 64, interleaved
+using Cfg0 = TileCfg<64, 64, 32, 2, 2, 2>;
+using Cfg1 = TileCfg<128, 64, 32, 2, 2, 1>;
 
 template <int EPI>
 int dispatch_cfg(int cfg, const float* x, int ldx, const float* W, const float* bias, float* y,
@@ -663,15 +684,11 @@ int dispatch_cfg(int cfg, const float* x, int ldx, const float* W, const float* 
   switch (cfg) {
     case 0: return launch_tile<EPI, Cfg0>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
     case 1: return launch_tile<EPI, Cfg1>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
-    case 2: return launch_tile<EPI, Cfg2>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
-    case 3: return launch_tile<EPI, Cfg3>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
-    case 4: return launch_tile<EPI, Cfg4>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
-    case 5: return launch_tile<EPI, Cfg5>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
-    case 6: return launch_tile<EPI, Cfg6>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
-    case 7: return launch_pipe<EPI, 32, 1>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
-    case 8: return launch_pipe<EPI, 32, 2>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
-    case 9: return launch_pipe<EPI, 64, 1>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
-    case 10: return launch_pipe<EPI, 64, 2>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
+    case 2: return launch_pipe<EPI, 32, 1, false>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
+    case 3: return launch_pipe<EPI, 32, 2, false>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
+    case 4: return launch_pipe<EPI, 32, 1, true>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
+    case 5: return launch_pipe<EPI, 32, 2, true>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
+    case 6: return launch_pipe<EPI, 64, 1, true>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
   }
   set_error("linear: unknown tile configuration %d", cfg);
   return LX_ERR_ARG;
@@ -697,16 +714,17 @@ int dispatch_gemm(int kind, int cfg, const float* x, int ldx, const float* W, co
   return LX_ERR_ARG;
 }
 
-// Tile configuration by shape, from an on-device sweep of all configurations
-// over the estimator's projections at B*T = 1000 and 6000 rows (MI355X):
-//   >= 512 tiles of 64x64 (>= 2 per CU): the pipelined kernel, BK = 32, no
-//     split (QKV 62.6 us = 100 TFLOP/s, FF0 43.3 us at B*T = 1000);
-//   fewer tiles (N = 1024 at B*T = 1000, one tile per CU): the tiled kernel
-//     with intra-workgroup split-K 2 for two waves per SIMD (out 26.7 us).
+// Tile configuration by shape, from an on-device sweep over the estimator's
+// projections at B*T = 1000 and 6000 rows (MI355X, per-launch event timing):
+// the pipelined, interleaved kernel with intra-workgroup split-K 2 is within a
+// few percent of the best everywhere (QKV 62-67 us = 94-100 TFLOP/s, FF0 42 us,
+// out 26-27 us, FF2 44-45 us at B*T = 1000); with K <= 512 (the input
+// projection, K = 320) a split leaves too few slabs per k-group and the
+// unsplit variant wins (42 vs 51 us at B*T = 6000).
 int pick_config(int M, int N, int K) {
-  (void)K;
-  const long tiles = (long)((M + 63) / 64) * ((N + 63) / 64);
-  return tiles >= 512 ? 7 : 1;
+  (void)M;
+  (void)N;
+  return K <= 512 ? 4 : 5;
 }
 
 }  // namespace lx
