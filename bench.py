@@ -7,10 +7,11 @@ norm_out/proj_out + CFG combine/x update), inputs resident in HBM.
 value = T * steps / wall time of the timed region (mel frames per second).
 
 Also reported on the same JSON line:
-  roofline      the dominant kernel's achieved FLOP/s (a HIP event pair around each
-                launch, on the stream the library launches on) vs the 157.3 TFLOP/s
-                fp32 MFMA peak;
-  kernels       per-kernel-class HIP-event timings of one step's launches;
+  roofline      the dominant kernel's achieved FLOP/s (HIP events around graph
+                replays of its launches under continuous load, on the replay stream)
+                vs the 157.3 TFLOP/s fp32 MFMA peak, and its HBM traffic per launch
+                from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary;
+  kernels       per-kernel-class timings of one step's launches (same method);
   fused_ops     achieved HBM GB/s of every fused op at the configs' shapes, with
                 each launch on a distinct buffer set (> 256 MB rotation, so the
                 MALL does not serve the reads);
@@ -41,6 +42,9 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-fused", action="store_true", help="skip the fused-op GB/s sweep")
     ap.add_argument("--no-llm", action="store_true", help="skip the Qwen2 prefill/decode timing")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="only launch the dominant GEMM (QKV + rotary, T=500) and a plain "
+                         "device copy of known size, for rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE")
     return ap.parse_args()
 
 
@@ -59,22 +63,38 @@ def event_time_ms(fn, n, torch):
     return a.elapsed_time(b) / n
 
 
-def per_launch_ms(fn, n, torch):
-    """Average ms of one call of fn, each call bracketed by its own pair of HIP
-    events on torch's current stream (the library's launch stream): measures the
-    kernel itself, not the dispatch gaps between back-to-back launches."""
-    s = torch.cuda.current_stream()
-    fn()
-    torch.cuda.synchronize()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(n)]
-    for a, b in evs:
-        a.record(s)
+def steady_launch_ms(fn, torch, n=20, warm_ms=40.0, reps=10):
+    """Average ms of one call of fn under continuous load: n calls captured
+    into one HIP graph, replayed back to back for about warm_ms (the device's
+    clocks settle under load, as they do inside a run of Euler steps), then
+    `reps` more replays bracketed by a pair of HIP events on the replay stream.
+    The figure includes the device-side dispatch gap between consecutive graph
+    kernels (about 1 us)."""
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
         fn()
-        b.record(s)
     torch.cuda.synchronize()
-    t = sorted(a.elapsed_time(b) for a, b in evs)
-    return sum(t[: max(1, n - n // 10)]) / max(1, n - n // 10)  # drop the slowest 10%
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        for _ in range(n):
+            fn()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(s):
+        a.record(s)
+        g.replay()
+        b.record(s)
+        b.synchronize()
+        one = max(a.elapsed_time(b), 1e-3)
+        for _ in range(int(warm_ms / one) + 1):
+            g.replay()
+        a.record(s)
+        for _ in range(reps):
+            g.replay()
+        b.record(s)
+    b.synchronize()
+    ms = a.elapsed_time(b) / (reps * n)
+    del g
+    return ms
 
 
 def graph_time_ms(fn, n, torch, reps=3):
@@ -134,7 +154,6 @@ def gemm_kernels(torch, ops, T, dev):
     gated = ops.Epilogue(kind=ops.LX_EPI_GATED_RESID, rows_per_batch=T, gate=gate.data_ptr(),
                          gate_stride=D)
     out = {}
-    n = 50
     qv = qkv.view(B, T, 3 * D)
     cases = {
         "gemm_qkv_rope": (lambda: ops.linear(xd, wq, bq, rope, out=qkv), 2 * M * 3 * D * D, 1),
@@ -153,11 +172,14 @@ def gemm_kernels(torch, ops, T, dev):
         "gemm_ff2_gated": lambda: torch.mm(xf, w2.T),
     }
     for name, (fn, flops, per_block) in cases.items():
-        ms = per_launch_ms(fn, n, torch)
+        ms = steady_launch_ms(fn, torch)
         out[name] = {"avg_us": ms * 1e3, "flop": flops, "tflops": flops / (ms * 1e-3) / 1e12,
                      "per_block": per_block}
         if name in lib_ref:
-            out[name]["hipblaslt_us"] = per_launch_ms(lib_ref[name], n, torch) * 1e3
+            try:
+                out[name]["hipblaslt_us"] = steady_launch_ms(lib_ref[name], torch) * 1e3
+            except RuntimeError:  # library call not capturable: no reference figure
+                torch.cuda.synchronize()
     return out
 
 
@@ -318,6 +340,54 @@ def cpu_baseline(T, seconds):
                       f"(median {t_step:.2f} s/step), fp32 storage / fp64 accumulation"}
 
 
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemm_qkv_rope_T500_traffic.md")
+COPY_PROBE_BYTES = 256 << 20
+
+
+def traffic_probe(torch, ops, launches=20):
+    """Launch the QKV projection (B*T = 1000, N = 3072, K = 1024, rotary
+    epilogue) and a plain 256 MiB device-to-device copy, each `launches` times,
+    with nothing else on the device: the workload of the two rocprofv3 --pmc
+    runs (FETCH_SIZE, then WRITE_SIZE) whose per-dispatch readings give the
+    dominant kernel's HBM traffic, scaled by the copy's reading for its known
+    size."""
+    dev = torch.device("cuda:0")
+    D, T, B = 1024, 500, 2
+    M = B * T
+    g = torch.Generator(device=dev).manual_seed(3)
+    xd = torch.randn(M, D, device=dev, generator=g)
+    wq = torch.randn(3 * D, D, device=dev, generator=g) * 0.02
+    bq = torch.zeros(3 * D, device=dev)
+    pos = torch.arange(T, dtype=torch.int32, device=dev)
+    qkv = torch.empty(M, 3 * D, device=dev)
+    rope = ops.Epilogue(kind=ops.LX_EPI_ROPE_PARTIAL, rows_per_batch=T, pos=pos.data_ptr(),
+                        rot_dim=64, rope_section=D, rope_sections=2, rope_base=10000.0)
+    src = torch.randn(COPY_PROBE_BYTES // 4, device=dev, generator=g)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(launches):
+        ops.linear(xd, wq, bq, rope, out=qkv)
+    torch.cuda.synchronize()
+    for _ in range(launches):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(f"traffic probe: {launches} x QKV GEMM (M={M} N={3 * D} K={D}), "
+          f"{launches} x copy of {COPY_PROBE_BYTES} bytes", flush=True)
+
+
+def committed_traffic():
+    """HBM bytes per launch of the dominant kernel, from the committed summary
+    of the two --pmc runs over --traffic-probe (None when it is absent)."""
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            for ln in f:
+                if ln.startswith("traffic_bytes_per_launch:"):
+                    return int(ln.split(":", 1)[1].strip())
+    except OSError:
+        pass
+    return None
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -331,6 +401,9 @@ def main():
         sys.exit(1)
     from larynx_amd import ops
     from larynx_amd.flow import DiTConfig, DiTEstimator, cfm_t_span, dit_param_shapes
+    if args.traffic_probe:
+        traffic_probe(torch, ops)
+        return
 
     dev = torch.device("cuda:0")
     T = args.T
@@ -381,7 +454,9 @@ def main():
     dom_name, dom = max(kernels.items(), key=lambda kv: kv[1]["avg_us"] * kv[1]["per_block"])
     roofline = {"kernel": dom_name, "bound": "mfma", "achieved": round(dom["tflops"], 3),
                 "peak": MFMA_F32_PEAK_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(dom["tflops"] / MFMA_F32_PEAK_TFLOPS, 4), "traffic": None,
+                "frac": round(dom["tflops"] / MFMA_F32_PEAK_TFLOPS, 4),
+                "traffic": (committed_traffic()
+                            if dom_name == "gemm_qkv_rope" and T == 500 else None),
                 "avg_us": round(dom["avg_us"], 2), "flop_per_launch": dom["flop"]}
     gemm_flop_step = 22 * sum(k["flop"] for k in kernels.values())
     long_t = long_utterance(torch, est, dev, g)

@@ -284,9 +284,12 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void gemm_tile_kernel(
 // slab body (one basic block) carries scheduling-group barriers that spread the
 // DS reads, DS writes and global loads between the MFMAs of the wave's single
 // accumulator chain, so they issue in the MFMA shadow instead of in bursts.
-template <int EPI, int BK, int KS, bool IL>
+// Operand rows past M (or N) are read from the last valid row and only reach
+// output rows (columns) the epilogue never stores, so they need no mask; with
+// KMASK (K not a multiple of BK) the columns past K are stored to LDS as zeros.
+template <int EPI, int BK, int KS, bool IL, bool KMASK>
 __global__ __launch_bounds__(256 * KS) void gemm_pipe_kernel(
-    const float* __restrict__ X, int ldx, const float* __restrict__ W,
+    const float* X, int ldx, const float* W,
     const float* __restrict__ bias, float* Y, int ldy, int M, int N, int K, EpiArgs ep) {
   constexpr int BM = 64, BN = 64, GT = 256, NT = GT * KS;
   constexpr int LDA = BK + 4;
@@ -317,14 +320,11 @@ __global__ __launch_bounds__(256 * KS) void gemm_pipe_kernel(
   const float* pa[L];
   const float* pw[L];
   int cc[L], rr[L];
-  bool oka[L], okw[L];
 #pragma unroll
   for (int i = 0; i < L; ++i) {
     const int idx = gtid + i * GT;
     rr[i] = idx / (BK / 4);
     cc[i] = (idx % (BK / 4)) * 4;
-    oka[i] = m0 + rr[i] < M;
-    okw[i] = n0 + rr[i] < N;
     pa[i] = X + (long)min(m0 + rr[i], M - 1) * ldx;
     pw[i] = W + (long)min(n0 + rr[i], N - 1) * K;
   }
@@ -339,11 +339,13 @@ __global__ __launch_bounds__(256 * KS) void gemm_pipe_kernel(
 #define LX_SSTORE(SA, SW, BUF, KT)                                                   \
   do {                                                                               \
     _Pragma("unroll") for (int i = 0; i < L; ++i) {                                   \
-      const bool kin = (KT) * BK + cc[i] < K;                                        \
-      floatx4 va, vw;                                                                \
-      _Pragma("unroll") for (int e = 0; e < 4; ++e) {                                 \
-        va[e] = (oka[i] && kin) ? SA[i][e] : 0.0f;                                    \
-        vw[e] = (okw[i] && kin) ? SW[i][e] : 0.0f;                                    \
+      floatx4 va = SA[i], vw = SW[i];                                                \
+      if (KMASK) {                                                                   \
+        const bool kin = (KT) * BK + cc[i] < K;                                      \
+        _Pragma("unroll") for (int e = 0; e < 4; ++e) {                               \
+          va[e] = kin ? va[e] : 0.0f;                                                \
+          vw[e] = kin ? vw[e] : 0.0f;                                                \
+        }                                                                            \
       }                                                                              \
       *reinterpret_cast<floatx4*>(As + (BUF) * BM * LDA + rr[i] * LDA + cc[i]) = va; \
       *reinterpret_cast<floatx4*>(Ws + (BUF) * BN * LDA + rr[i] * LDA + cc[i]) = vw; \
@@ -362,18 +364,24 @@ __global__ __launch_bounds__(256 * KS) void gemm_pipe_kernel(
   // stored values are zero-masked by k), so the loop body is straight-line and
   // the compiler's vmcnt waits count exactly the two stages in flight.
 #define LX_KC(IT) min(LX_KT(IT), nk - 1)
+  // The empty asm statements keep the two stages' loads in order, so the
+  // outstanding-load order at the loop entry matches the one at the back edge
+  // and the loop's vmcnt waits count exactly one stage.
   LX_GLOAD(sa0, sw0, LX_KC(0));
   LX_SSTORE(sa0, sw0, 0, LX_KT(0));
+  asm volatile("" ::: "memory");
   LX_GLOAD(sa1, sw1, LX_KC(1));
+  asm volatile("" ::: "memory");
   LX_GLOAD(sa0, sw0, LX_KC(2));
+  asm volatile("" ::: "memory");
   __syncthreads();
 
   // One slab: MFMAs on LDS buffer BUF, then the next slab (held in stage
   // SNEXT) goes to the other buffer and stage SNEXT reloads three slabs ahead.
 #define LX_SLAB(IT, BUF, SNA, SNW)                                                     \
   do {                                                                                 \
-    /* No branch around the MFMAs: a surplus slab (past the end of K) holds zeros in \
-       LDS (SSTORE masks k >= K), so it adds exact zeros and the body stays one     \
+    /* No branch around the MFMAs: a surplus slab (past the end of K; only when   \
+       KMASK) holds zeros in LDS, so it adds exact zeros and the body stays one     \
        scheduling region. */                                                         \
     const float* ab = As + (BUF) * BM * LDA + (wm * 32 + r) * LDA + h * 16;           \
     const float* wb = Ws + (BUF) * BN * LDA + (wn * 32 + r) * LDA + h * 16;           \
@@ -418,7 +426,8 @@ __global__ __launch_bounds__(256 * KS) void gemm_pipe_kernel(
   } while (0)
 
   // Both halves run unconditionally (a surplus half multiplies the zeros its
-  // slab holds), so the loop has a single back-edge state for the waits.
+  // slab holds; the launcher sets KMASK whenever the slab count is not a
+  // multiple of 2 KS), so the loop has a single back-edge state for the waits.
   for (int it = 0; it < iters; it += 2) {
     LX_SLAB(it, 0, sa1, sw1);
     LX_SLAB(it + 1, 1, sa0, sw0);
@@ -464,10 +473,10 @@ struct PipeCfg {
   }
 };
 
-template <int EPI, int BK, int KS, bool IL>
-int launch_pipe(const float* x, int ldx, const float* W, const float* bias, float* y, int ldy,
-                int M, int N, int K, const EpiArgs& ep, hipStream_t stream) {
-  auto kern = gemm_pipe_kernel<EPI, BK, KS, IL>;
+template <int EPI, int BK, int KS, bool IL, bool KMASK>
+int launch_pipe_k(const float* x, int ldx, const float* W, const float* bias, float* y, int ldy,
+                  int M, int N, int K, const EpiArgs& ep, hipStream_t stream) {
+  auto kern = gemm_pipe_kernel<EPI, BK, KS, IL, KMASK>;
   const size_t lds = PipeCfg<BK, KS>::lds();
   if (lds > 64 * 1024) {
     static bool attr_set = false;
@@ -484,6 +493,16 @@ int launch_pipe(const float* x, int ldx, const float* W, const float* bias, floa
   hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(PipeCfg<BK, KS>::threads), lds, stream, x,
                      ldx, W, bias, y, ldy, M, N, K, ep);
   return check_launch("gemm_pipe_kernel");
+}
+
+// The unmasked kernel needs K to be whole slabs and the slab count a multiple
+// of 2 KS (the loop runs two slabs per k-group per iteration).
+template <int EPI, int BK, int KS, bool IL>
+int launch_pipe(const float* x, int ldx, const float* W, const float* bias, float* y, int ldy,
+                int M, int N, int K, const EpiArgs& ep, hipStream_t stream) {
+  const bool exact = K % BK == 0 && (K / BK) % (2 * KS) == 0;
+  return exact ? launch_pipe_k<EPI, BK, KS, IL, false>(x, ldx, W, bias, y, ldy, M, N, K, ep, stream)
+               : launch_pipe_k<EPI, BK, KS, IL, true>(x, ldx, W, bias, y, ldy, M, N, K, ep, stream);
 }
 
 template <int BM, int BN, int BK, int WM, int WN, int KS>
@@ -715,16 +734,15 @@ int dispatch_gemm(int kind, int cfg, const float* x, int ldx, const float* W, co
 }
 
 // Tile configuration by shape, from an on-device sweep over the estimator's
-// projections at B*T = 1000 and 6000 rows (MI355X, per-launch event timing):
-// the pipelined, interleaved kernel with intra-workgroup split-K 2 is within a
-// few percent of the best everywhere (QKV 62-67 us = 94-100 TFLOP/s, FF0 42 us,
-// out 26-27 us, FF2 44-45 us at B*T = 1000); with K <= 512 (the input
-// projection, K = 320) a split leaves too few slabs per k-group and the
-// unsplit variant wins (42 vs 51 us at B*T = 6000).
+// projections at B*T = 1000 and 6000 rows (MI355X, graph-replayed launches
+// under continuous load): with fewer than 2048 tiles (two workgroups or fewer
+// per CU at B*T = 1000) intra-workgroup split-K 2 gives each SIMD a second
+// wave (QKV 54.3 us = 116 TFLOP/s, out 23.3 us, FF0 38.4 us, FF2 39.8 us);
+// with many tiles, or K <= 512 (too few slabs to split), the unsplit kernel
+// wins (out 110.6 vs 112.7 us at B*T = 6000; input projection 8.9 vs 10.7 us).
 int pick_config(int M, int N, int K) {
-  (void)M;
-  (void)N;
-  return K <= 512 ? 4 : 5;
+  const long tiles = (long)((M + 63) / 64) * ((N + 63) / 64);
+  return (K <= 512 || tiles >= 2048) ? 4 : 5;
 }
 
 }  // namespace lx

@@ -208,7 +208,9 @@ def test_embed_gather_text_table(gpu, ops):
 # --- dense ---------------------------------------------------------------------------
 @pytest.mark.parametrize("M,N,K", [(1000, 1024, 1024), (1000, 80, 1024), (1000, 1024, 320),
                                    (37, 67, 96), (256, 1152, 896), (256, 6761, 896),
-                                   (3, 9728, 896), (1, 6761, 896), (6000, 1024, 2048)])
+                                   (3, 9728, 896), (1, 6761, 896), (6000, 1024, 2048),
+                                   # K not whole 32-wide slabs / odd slab counts: masked path
+                                   (61, 131, 100), (64, 64, 36), (70, 50, 4), (200, 96, 480)])
 def test_linear_plain(gpu, ops, M, N, K):
     announce(f"linear M={M} N={N} K={K}")
     x, W, b = rnd((M, K), 1), rnd((N, K), 2, 0.03), rnd((N,), 3)
