@@ -116,22 +116,30 @@ __global__ __launch_bounds__(256) void attn_flash_kernel(
           s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv[e], qf[j][e], s, 0, 0, 0);
       }
       // S^T register i of lane half h is key kb + (i/4)*8 + h*4 + i%4 for query r.
-      float mloc = -INFINITY;
+      // Only a block that crosses Tk or (causal) the wave's first query needs
+      // masking; the test is uniform across the wave.
+      if (kb + 32 > Tk || (causal && kb + 31 > q_offset + q0)) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int key = kb + (i >> 2) * 8 + h * 4 + (i & 3);
-        const bool ok = key < Tk && (!causal || key <= my_q);
-        s[i] = ok ? s[i] : -INFINITY;
-        mloc = fmaxf(mloc, s[i]);
+        for (int i = 0; i < 16; ++i) {
+          const int key = kb + (i >> 2) * 8 + h * 4 + (i & 3);
+          const bool ok = key < Tk && (!causal || key <= my_q);
+          s[i] = ok ? s[i] : -INFINITY;
+        }
       }
+      float mloc = s[0];
+#pragma unroll
+      for (int i = 1; i < 16; ++i) mloc = fmaxf(mloc, s[i]);
       mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
       const float m_new = fmaxf(m_run, mloc);
       const float m_use = m_new == -INFINITY ? 0.0f : m_new;  // fully masked so far
-      const float alpha = exp2f(m_run - m_use);
+      // v_exp_f32 directly: every argument is <= 0 (or -inf -> 0), where the
+      // hardware exp2 is accurate to about 1 ulp; results below 2^-126 flush
+      // to zero, far under the weight of any unmasked key.
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
       float psum = 0.0f;
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        s[i] = exp2f(s[i] - m_use);
+        s[i] = __builtin_amdgcn_exp2f(s[i] - m_use);
         psum += s[i];
       }
       l_run = l_run * alpha + psum;
