@@ -11,10 +11,8 @@
 // contributes at MFMA step i.  Scores are never written to memory (the
 // reference materialises KQ [T, T, heads, B]).
 //
-// Decode path (one query row, internal to the Qwen2 decode step):
-// flash-decoding.  Keys are split across workgroups (256 keys each, one thread
-// per key for the scores, one lane per channel for P V), then a second kernel
-// merges the per-split (max, sum, o) triples.
+// The single-token Qwen2 decode attention lives with the other decode
+// kernels (lx_decode.hip).
 #include <cmath>
 
 #include "lx_common.hpp"
@@ -204,96 +202,7 @@ __global__ __launch_bounds__(256) void attn_flash_kernel(
   }
 }
 
-constexpr int kSplit = 256;  // keys per decode workgroup
-
-// Partial pass: grid (H, n_split, B); 256 threads; thread = key for scores.
-__global__ __launch_bounds__(256) void attn_decode_partial(
-    const float* __restrict__ q, const float* __restrict__ k, int ldk,
-    const float* __restrict__ v, int ldv, int Tk, int rep, float scale,
-    float* __restrict__ part, int n_split, int ldq, int H) {
-  __shared__ float qs[kHD];
-  __shared__ float ps[kSplit];
-  __shared__ float red[8];
-  __shared__ float osum[4][kHD];
-  const int head = blockIdx.x, sp = blockIdx.y, b = blockIdx.z;
-  const int g = head / rep;
-  const int tid = threadIdx.x;
-  if (tid < kHD) qs[tid] = q[(long)b * ldq + head * kHD + tid] * scale;
-  __syncthreads();
-  const int key = sp * kSplit + tid;
-  float sc = -INFINITY;
-  if (key < Tk) {
-    const float4* kr = reinterpret_cast<const float4*>(k + ((long)b * Tk + key) * ldk + g * kHD);
-    float acc = 0.0f;
-#pragma unroll
-    for (int j = 0; j < kHD / 4; ++j) {
-      float4 t = kr[j];
-      acc += (t.x * qs[4 * j] + t.y * qs[4 * j + 1]) + (t.z * qs[4 * j + 2] + t.w * qs[4 * j + 3]);
-    }
-    sc = acc;
-  }
-  // block max
-  float m = wave_max(sc);
-  if ((tid & 63) == 0) red[tid >> 6] = m;
-  __syncthreads();
-  m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  const float p = key < Tk ? expf(sc - m) : 0.0f;
-  ps[tid] = p;
-  float l = wave_sum(p);
-  __syncthreads();
-  if ((tid & 63) == 0) red[4 + (tid >> 6)] = l;
-  // P V: wave w sums keys w, w+4, ...; lane = channel.
-  const int wave = tid >> 6, lane = tid & 63;
-  float acc = 0.0f;
-  const int nk = min(kSplit, Tk - sp * kSplit);
-  for (int j = wave; j < nk; j += 4)
-    acc += ps[j] * v[((long)b * Tk + sp * kSplit + j) * ldv + g * kHD + lane];
-  osum[wave][lane] = acc;
-  __syncthreads();
-  float* out = part + (((long)b * H + head) * n_split + sp) * (kHD + 2);
-  if (tid < kHD) out[tid] = (osum[0][tid] + osum[1][tid]) + (osum[2][tid] + osum[3][tid]);
-  if (tid == 0) {
-    out[kHD] = m;
-    out[kHD + 1] = (red[4] + red[5]) + (red[6] + red[7]);
-  }
-}
-
-__global__ __launch_bounds__(64) void attn_decode_merge(const float* __restrict__ part,
-                                                        int n_split, float* __restrict__ o,
-                                                        int ldo, int H) {
-  const int head = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
-  const float* p = part + ((long)b * H + head) * n_split * (kHD + 2);
-  float m = -INFINITY;
-  for (int s = 0; s < n_split; ++s) m = fmaxf(m, p[s * (kHD + 2) + kHD]);
-  float l = 0.0f, acc = 0.0f;
-  for (int s = 0; s < n_split; ++s) {
-    const float w = expf(p[s * (kHD + 2) + kHD] - m);
-    l += w * p[s * (kHD + 2) + kHD + 1];
-    acc += w * p[s * (kHD + 2) + lane];
-  }
-  o[(long)b * ldo + head * kHD + lane] = acc / l;
-}
-
 }  // namespace
-
-int attention_decode_split(const float* q, int ldq, const float* k, int ldk, const float* v,
-                           int ldv, float* o, int ldo, int B, int Tk, int n_heads,
-                           int n_kv_heads, float scale, float* part, hipStream_t stream) {
-  const int rep = n_heads / n_kv_heads;
-  const int n_split = (Tk + kSplit - 1) / kSplit;
-  hipLaunchKernelGGL(attn_decode_partial, dim3(n_heads, n_split, B), dim3(256), 0, stream, q, k,
-                     ldk, v, ldv, Tk, rep, scale, part, n_split, ldq, n_heads);
-  int rc = check_launch("attn_decode_partial");
-  if (rc) return rc;
-  hipLaunchKernelGGL(attn_decode_merge, dim3(n_heads, B), dim3(64), 0, stream, part, n_split, o,
-                     ldo, n_heads);
-  return check_launch("attn_decode_merge");
-}
-
-size_t attention_decode_part_floats(int B, int Tk, int n_heads) {
-  return (size_t)B * n_heads * ((Tk + kSplit - 1) / kSplit) * (kHD + 2);
-}
-
 }  // namespace lx
 
 using namespace lx;

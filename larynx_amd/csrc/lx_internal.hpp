@@ -48,12 +48,58 @@ int interleave_rows(const float* a, const float* b, float* out, int rows, int K,
 int copy_rows(const float* src, int lds, float* dst, int ldd, int rows, int cols,
               hipStream_t stream);
 
-// Flash-decoding for one query row per batch (Tq == 1); `part` holds
-// attention_decode_part_floats(B, Tk, n_heads) floats.
-int attention_decode_split(const float* q, int ldq, const float* k, int ldk, const float* v,
-                           int ldv, float* o, int ldo, int B, int Tk, int n_heads,
-                           int n_kv_heads, float scale, float* part, hipStream_t stream);
-size_t attention_decode_part_floats(int B, int Tk, int n_heads);
+// ---- single-token decode (lx_decode.hip) ----
+enum { DEC_QKV_ROPE = 0, DEC_SWIGLU = 1, DEC_RESID = 2, DEC_HEAD = 3 };
+
+// y = epi(W @ norm(x) + bias) for one activation row x (K), W (N, K).
+//   DEC_QKV_ROPE: x RMSNorm'ed with norm_w; columns [0, q_cols) -> y (q),
+//     [q_cols, q_cols + kv_cols) -> k_cache[pos], the rest -> v_cache[pos];
+//     NEOX rotary (head_dim 64, device table inv_freq) on the first rope_heads heads.
+//   DEC_SWIGLU: x RMSNorm'ed; W rows interleaved (gate_i, up_i);
+//     y[i] = silu(gate_i) * up_i.
+//   DEC_RESID: y[n] += (W x)[n] (no norm).
+//   DEC_HEAD: x RMSNorm'ed; y[n] = (W x)[n]; y2 (K), if set, receives norm(x).
+struct DecGemvArgs {
+  const float* x = nullptr;
+  const float* norm_w = nullptr;
+  float eps = 0.0f;
+  const float* W = nullptr;
+  const float* bias = nullptr;
+  float* y = nullptr;
+  float* y2 = nullptr;
+  long N = 0;
+  int K = 0;
+  const int* pos = nullptr;  // device: position of the token
+  int q_cols = 0, kv_cols = 0, rope_heads = 0;
+  float* k_cache = nullptr;
+  float* v_cache = nullptr;
+  const float* inv_freq = nullptr;  // device: 32 rotary inverse frequencies
+};
+int dec_gemv(int epi, const DecGemvArgs& a, hipStream_t stream);
+// True when the decode kernels cover this geometry (K = hidden <= 2048,
+// K = intermediate <= 6144).
+bool dec_supported(int hidden, int intermediate);
+
+// Split-key GQA attention of one query row over keys [0, *pos] of the cache.
+struct DecAttnArgs {
+  const float* q = nullptr;  // (n_heads * 64), roped
+  const float* k_cache = nullptr;
+  const float* v_cache = nullptr;
+  int ld = 0;                // cache row stride (n_kv_heads * 64)
+  const int* pos = nullptr;  // device
+  float scale = 0.0f;
+  int rep = 0;               // n_heads / n_kv_heads
+  int max_rows = 0;          // cache capacity (rows)
+  float* part = nullptr;     // n_kv_heads * part_group_stride floats
+  long part_group_stride = 0;
+  float* out = nullptr;      // (n_heads * 64)
+};
+int dec_attention(const DecAttnArgs& a, int n_kv_heads, hipStream_t stream);
+int dec_attention_splits(int max_ctx);
+int dec_attention_max_ctx();  // largest cache the merge pass covers
+// x = table[row]; *d_pos = pos.
+int dec_begin(const float* table, long row, int D, float* x, int* d_pos, int pos,
+              hipStream_t stream);
 
 // Grouped conv + Mish with tap-major packed weights (lx_conv_pos_mish_f32).
 int conv_pos_mish_packed(const float* x, const float* wp, const float* bias, const float* resid,

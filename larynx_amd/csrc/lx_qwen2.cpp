@@ -13,6 +13,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cmath>
+#include <cstdlib>
 #include <new>
 #include <vector>
 
@@ -67,14 +68,27 @@ struct lx_qwen2 {
   std::vector<Layer> layers;
   // activations, sized for max_ctx rows
   float *x, *hn, *qkv, *att, *act;
-  float* part;  // flash-decoding partials
   int* pos;     // pos[i] = i
+  // single-token decode state (lx_decode.hip kernels)
+  int* d_pos = nullptr;       // position of the token being decoded
+  float* part = nullptr;      // attention split partials
+  long part_stride = 0;       // floats per kv head in `part`
+  int max_splits = 0;
+  float* rope_tab = nullptr;  // device copy of the rotary inverse frequencies
+  bool use_graph = true;      // replay the layer stack as one HIP graph
+  hipStream_t cap_stream = nullptr;
+  hipGraphExec_t graph = nullptr;
+  ~lx_qwen2() {
+    if (graph) (void)hipGraphExecDestroy(graph);
+    if (cap_stream) (void)hipStreamDestroy(cap_stream);
+  }
 };
 
 namespace {
 
-int layer_body(lx_qwen2* m, Layer& L, int rows, const int* pos, int row0, bool decode,
-               hipStream_t s) {
+// Prefill layer (rows >= 1 query rows at positions pos[0..rows), appended to
+// the cache at row0).
+int layer_body(lx_qwen2* m, Layer& L, int rows, const int* pos, int row0, hipStream_t s) {
   const int H = m->H, KV = m->KV, QKV = m->QKV;
   // input_layernorm + q/k/v (+bias) + NEOX rotary on q and k (src/llm/llm.cpp:145-156)
   LX_TRY(lx_rmsnorm_f32(m->x, L.in_norm, m->hn, rows, H, m->eps, s));
@@ -86,13 +100,8 @@ int layer_body(lx_qwen2* m, Layer& L, int rows, const int* pos, int row0, bool d
   LX_TRY(copy_rows(m->qkv + H + KV, QKV, L.v_cache + (long)row0 * KV, KV, rows, KV, s));
   const int Tk = row0 + rows;
   const float scale = 1.0f / std::sqrt((float)m->HD);
-  if (decode && rows == 1) {
-    LX_TRY(attention_decode_split(m->qkv, QKV, L.k_cache, KV, L.v_cache, KV, m->att, H, 1, Tk,
-                                  m->NH, m->NKV, scale, m->part, s));
-  } else {
-    LX_TRY(lx_attention_f32(m->qkv, QKV, L.k_cache, KV, L.v_cache, KV, m->att, H, 1, rows, Tk,
-                            m->NH, m->NKV, m->HD, scale, /*causal*/ 1, /*q_offset*/ row0, s));
-  }
+  LX_TRY(lx_attention_f32(m->qkv, QKV, L.k_cache, KV, L.v_cache, KV, m->att, H, 1, rows, Tk,
+                          m->NH, m->NKV, m->HD, scale, /*causal*/ 1, /*q_offset*/ row0, s));
   lx_epilogue resid{};
   resid.kind = LX_EPI_RESID;
   LX_TRY(lx_linear_f32(m->att, H, L.o_w, nullptr, m->x, H, rows, H, H, &resid, s));
@@ -105,6 +114,99 @@ int layer_body(lx_qwen2* m, Layer& L, int rows, const int* pos, int row0, bool d
   return LX_OK;
 }
 
+// One decode layer (src/llm/llm.cpp:254-289) as five launches: RMSNorm + QKV
+// + rotary + cache append; split-key attention; o_proj + residual; RMSNorm +
+// gate/up + SwiGLU; down_proj + residual.  The position is read from m->d_pos.
+int decode_layer(lx_qwen2* m, Layer& L, hipStream_t s) {
+  const int H = m->H, KV = m->KV;
+  DecGemvArgs q;
+  q.x = m->x;
+  q.norm_w = L.in_norm;
+  q.eps = m->eps;
+  q.W = L.qkv_w;
+  q.bias = L.qkv_b;
+  q.y = m->hn;  // roped q row
+  q.N = m->QKV;
+  q.K = H;
+  q.pos = m->d_pos;
+  q.q_cols = H;
+  q.kv_cols = KV;
+  q.rope_heads = m->NH + m->NKV;
+  q.k_cache = L.k_cache;
+  q.v_cache = L.v_cache;
+  q.inv_freq = m->rope_tab;
+  LX_TRY(dec_gemv(DEC_QKV_ROPE, q, s));
+  DecAttnArgs at;
+  at.q = m->hn;
+  at.k_cache = L.k_cache;
+  at.v_cache = L.v_cache;
+  at.ld = KV;
+  at.pos = m->d_pos;
+  at.scale = 1.0f / std::sqrt((float)m->HD);
+  at.rep = m->NH / m->NKV;
+  at.max_rows = m->max_ctx;
+  at.part = m->part;
+  at.part_group_stride = m->part_stride;
+  at.out = m->att;
+  LX_TRY(dec_attention(at, m->NKV, s));
+  DecGemvArgs o;
+  o.x = m->att;
+  o.W = L.o_w;
+  o.y = m->x;
+  o.N = H;
+  o.K = H;
+  LX_TRY(dec_gemv(DEC_RESID, o, s));
+  DecGemvArgs gu;
+  gu.x = m->x;
+  gu.norm_w = L.post_norm;
+  gu.eps = m->eps;
+  gu.W = L.gu_w;
+  gu.y = m->act;
+  gu.N = 2L * m->I;
+  gu.K = H;
+  LX_TRY(dec_gemv(DEC_SWIGLU, gu, s));
+  DecGemvArgs d;
+  d.x = m->act;
+  d.W = L.down_w;
+  d.y = m->x;
+  d.N = H;
+  d.K = m->I;
+  return dec_gemv(DEC_RESID, d, s);
+}
+
+int decode_stack(lx_qwen2* m, hipStream_t s) {
+  for (auto& L : m->layers) LX_TRY(decode_layer(m, L, s));
+  return LX_OK;
+}
+
+// Captures the decode layer stack into a HIP graph on the library's own
+// stream (capture needs a stream other than the legacy default stream).
+int capture_decode(lx_qwen2* m) {
+  if (!m->cap_stream &&
+      hipStreamCreateWithFlags(&m->cap_stream, hipStreamNonBlocking) != hipSuccess) {
+    set_error("qwen2_decode: stream creation failed");
+    return LX_ERR_LAUNCH;
+  }
+  if (hipStreamBeginCapture(m->cap_stream, hipStreamCaptureModeRelaxed) != hipSuccess) {
+    set_error("qwen2_decode: hipStreamBeginCapture failed");
+    return LX_ERR_LAUNCH;
+  }
+  int rc = decode_stack(m, m->cap_stream);
+  hipGraph_t g = nullptr;
+  const hipError_t e = hipStreamEndCapture(m->cap_stream, &g);
+  if (rc == LX_OK && (e != hipSuccess || !g)) {
+    set_error("qwen2_decode: hipStreamEndCapture failed");
+    rc = LX_ERR_LAUNCH;
+  }
+  if (rc == LX_OK && hipGraphInstantiate(&m->graph, g, nullptr, nullptr, 0) != hipSuccess) {
+    set_error("qwen2_decode: hipGraphInstantiate failed");
+    m->graph = nullptr;
+    rc = LX_ERR_LAUNCH;
+  }
+  if (g) (void)hipGraphDestroy(g);
+  return rc;
+}
+
 }  // namespace
 
 extern "C" int lx_qwen2_create(const lx_qwen2_weights* w, int max_ctx, lx_qwen2** out) {
@@ -115,7 +217,11 @@ extern "C" int lx_qwen2_create(const lx_qwen2_weights* w, int max_ctx, lx_qwen2*
                  w->n_heads * w->head_dim == w->hidden && w->intermediate > 0 &&
                  w->intermediate % 4 == 0 && w->n_layers > 0,
              "qwen2_create: unsupported geometry");
-  LX_REQUIRE(max_ctx >= 1, "qwen2_create: max_ctx=%d", max_ctx);
+  LX_REQUIRE(max_ctx >= 1 && max_ctx <= dec_attention_max_ctx(),
+             "qwen2_create: max_ctx=%d outside [1, %d]", max_ctx, dec_attention_max_ctx());
+  LX_REQUIRE(dec_supported(w->hidden, w->intermediate) && w->n_heads / w->n_kv_heads <= 8,
+             "qwen2_create: decode kernels need hidden <= 2048, intermediate <= 6144 and "
+             "at most 8 query heads per kv head");
   LX_REQUIRE(w->embed_tokens && w->speech_embedding && w->final_norm && w->llm_decoder &&
                  w->layers,
              "qwen2_create: missing tables");
@@ -165,9 +271,15 @@ extern "C" int lx_qwen2_create(const lx_qwen2_weights* w, int max_ctx, lx_qwen2*
   m->qkv = A(rows * QKV);
   m->att = A(rows * H);
   m->act = A(rows * I);
-  m->part = A(attention_decode_part_floats(1, max_ctx, m->NH));
+  m->max_splits = dec_attention_splits(max_ctx);
+  m->part_stride = ((long)m->max_splits * (m->NH / m->NKV) * (m->HD + 2) + 31) / 32 * 32;
+  m->part = A((size_t)m->part_stride * m->NKV);
   m->pos = a.alloc<int>(max_ctx);
-  ok = ok && m->pos;
+  m->d_pos = a.alloc<int>(1);
+  m->rope_tab = A(m->HD / 2);
+  ok = ok && m->pos && m->d_pos;
+  const char* env = std::getenv("LX_DECODE_GRAPH");
+  m->use_graph = !(env && env[0] == '0');
   if (!ok) {
     delete m;
     set_error("qwen2_create: device allocation failed");
@@ -211,6 +323,13 @@ extern "C" int lx_qwen2_create(const lx_qwen2_weights* w, int max_ctx, lx_qwen2*
     if (rc == LX_OK) rc = interleave_rows(lw.gate_w, lw.up_w, L.gu_w, I, H, s);
   }
   if (rc == LX_OK) rc = iota_i32(m->pos, max_ctx, s);
+  FreqTable inv{};
+  rope_inv_freq(m->theta, m->HD, inv.v);
+  if (rc == LX_OK && hipMemcpyAsync(m->rope_tab, inv.v, sizeof(float) * (m->HD / 2),
+                                    hipMemcpyHostToDevice, s) != hipSuccess) {
+    set_error("qwen2_create: rotary table upload failed");
+    rc = LX_ERR_LAUNCH;
+  }
   if (rc == LX_OK && hipStreamSynchronize(s) != hipSuccess) {
     set_error("qwen2_create: weight packing failed");
     rc = LX_ERR_LAUNCH;
@@ -279,7 +398,7 @@ extern "C" int lx_qwen2_prefill(lx_qwen2* m, const float* lm_input, int L, float
   }
   m->cache_len = 0;
   for (int l = 0; l < m->NL; ++l) {
-    LX_TRY(layer_body(m, m->layers[l], L, m->pos, 0, false, s));
+    LX_TRY(layer_body(m, m->layers[l], L, m->pos, 0, s));
     if (hidden)
       (void)hipMemcpyAsync(hidden + (size_t)l * L * H, m->x, sizeof(float) * (size_t)L * H,
                            hipMemcpyDeviceToDevice, s);
@@ -311,14 +430,28 @@ extern "C" int lx_qwen2_decode(lx_qwen2* m, int token, float* logits, float* fin
     return LX_ERR_STATE;
   }
   const int H = m->H;
-  const int p = m->cache_len;
-  LX_TRY(lx_embed_gather_f32(m->speech_embedding, m->speech_vocab, H, &token, 1, m->x, s));
-  for (int l = 0; l < m->NL; ++l) LX_TRY(layer_body(m, m->layers[l], 1, m->pos + p, p, true, s));
-  LX_TRY(lx_rmsnorm_f32(m->x, m->final_norm, m->hn, 1, H, m->eps, s));
-  if (final_norm)
-    (void)hipMemcpyAsync(final_norm, m->hn, sizeof(float) * H, hipMemcpyDeviceToDevice, s);
-  LX_TRY(lx_linear_f32(m->hn, H, m->llm_decoder, nullptr, logits, m->speech_vocab, 1,
-                       m->speech_vocab, H, nullptr, s));
+  // speech_embedding row of the token (src/llm/llm.cpp:226-230) and its position
+  LX_TRY(dec_begin(m->speech_embedding, token, H, m->x, m->d_pos, m->cache_len, s));
+  if (m->use_graph) {
+    if (!m->graph) LX_TRY(capture_decode(m));
+    if (hipGraphLaunch(m->graph, s) != hipSuccess) {
+      set_error("qwen2_decode: hipGraphLaunch failed");
+      return LX_ERR_LAUNCH;
+    }
+  } else {
+    LX_TRY(decode_stack(m, s));
+  }
+  // final norm + llm_decoder head (src/llm/llm.cpp:291-300)
+  DecGemvArgs h;
+  h.x = m->x;
+  h.norm_w = m->final_norm;
+  h.eps = m->eps;
+  h.W = m->llm_decoder;
+  h.y = logits;
+  h.y2 = final_norm;
+  h.N = m->speech_vocab;
+  h.K = H;
+  LX_TRY(dec_gemv(DEC_HEAD, h, s));
   m->cache_len += 1;
   return LX_OK;
 }

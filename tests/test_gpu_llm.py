@@ -111,3 +111,51 @@ def test_errors(gpu, qwen):
         lm.decode(6761)
     assert e.value.code == LX_ERR_RANGE
     lm.close()
+
+
+def test_decode_graph_matches_eager_and_crosses_splits(gpu, qwen):
+    """The decode layer stack replayed as a HIP graph and launched eagerly
+    (LX_DECODE_GRAPH=0) give bit-identical logits; sequential decode steps
+    across the 64-key attention split boundary (cache 62 -> 67) track the
+    oracle, including its device-side position and split counters."""
+    import os
+    from larynx_amd.llm import Qwen2LM
+    cfg, params, dparams, _ = qwen
+    announce("qwen2 decode graph vs eager, cache 62..67")
+    os.environ["LX_DECODE_GRAPH"] = "0"
+    try:
+        eager = Qwen2LM(dparams, cfg, max_ctx=128)
+    finally:
+        del os.environ["LX_DECODE_GRAPH"]
+    graph = Qwen2LM(dparams, cfg, max_ctx=128)
+    o = orc.Qwen2(params, cfg, cap=128)
+    n0 = 62
+    for layer in range(cfg.n_layers):
+        kc = orc.normal((n0, 128), 90 + layer, 1, 0.02)
+        vc = orc.normal((n0, 128), 90 + layer, 2, 0.02)
+        o.k_cache[layer, :n0] = kc
+        o.v_cache[layer, :n0] = vc
+        for lm in (eager, graph):
+            kd, vd = lm.cache_views(layer)
+            kd[:n0].copy_(torch.from_numpy(kc))
+            vd[:n0].copy_(torch.from_numpy(vc))
+    o.cache_len = n0
+    eager.set_cache_len(n0)
+    graph.set_cache_len(n0)
+    torch.cuda.synchronize()
+    for step, tok in enumerate([5, 6561, 77, 6000, 1234]):
+        announce(f"qwen2 decode step {step} at position {n0 + step}")
+        lg_e, fn_e = eager.decode(tok, final_norm=True)
+        lg_g, fn_g = graph.decode(tok, final_norm=True)
+        torch.cuda.synchronize()
+        assert torch.equal(lg_e, lg_g) and torch.equal(fn_e, fn_g), step
+        rlg, rfn = o.decode(tok)
+        assert orc.rel_err(fn_g.cpu().numpy(), rfn) < TOL, step
+        assert orc.rel_err(lg_g.cpu().numpy(), rlg) < TOL, step
+    assert graph.cache_len == n0 + 5
+    for layer in range(cfg.n_layers):
+        kd, vd = graph.cache_views(layer)
+        assert orc.rel_err(kd[:n0 + 5].cpu().numpy(), o.k_cache[layer, :n0 + 5]) < TOL
+        assert orc.rel_err(vd[:n0 + 5].cpu().numpy(), o.v_cache[layer, :n0 + 5]) < TOL
+    eager.close()
+    graph.close()
