@@ -105,8 +105,9 @@ __device__ __forceinline__ void epilogue4(float* Y, int ldy, int m, int n, int N
 // select on the data, so they stay plain global_load_dwordx4.
 template <int EPI, int BM, int BN, int BK, int WM, int WN, int KS>
 __global__ __launch_bounds__(64 * WM * WN * KS) void gemm_tile_kernel(
-    const float* __restrict__ X, int ldx, const float* __restrict__ W,
-    const float* __restrict__ bias, float* Y, int ldy, int M, int N, int K, EpiArgs ep) {
+    const float* __restrict__ X, int ldx, const float* __restrict__ W, int ldw,
+    const float* __restrict__ bias, float* Y, int ldy, int M, int N, int K, int ksplit,
+    EpiArgs ep) {
   constexpr int GT = 64 * WM * WN;             // threads per k-group
   constexpr int NT = GT * KS;
   constexpr int LDA = BK + 4;
@@ -137,6 +138,11 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void gemm_tile_kernel(
   const int gtid = tid % GT;
   float* As = smem + kg * 2 * (BM + BN) * LDA;
   float* Ws = As + 2 * BM * LDA;
+  // K slice of this workgroup (blockIdx.y; one slice unless split-K partials)
+  X += (long)blockIdx.y * ksplit;
+  W += (long)blockIdx.y * ksplit;
+  Y += (long)blockIdx.y * M * ldy;
+  K = min(ksplit, K - (int)blockIdx.y * ksplit);
 
   // Per-thread load slots: clamped row pointers and validity.
   const float* pa[LA];
@@ -157,7 +163,7 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void gemm_tile_kernel(
     const int row = idx / (BK / 4);
     cw[i] = (idx % (BK / 4)) * 4;
     okw[i] = n0 + row < N;
-    pw[i] = W + (long)min(n0 + row, N - 1) * K;
+    pw[i] = W + (long)min(n0 + row, N - 1) * ldw;
   }
   // Raw loads go to registers untouched; out-of-range lanes are zeroed when
   // the slab is written to LDS, after the MFMAs, so no wait on the loads is
@@ -289,8 +295,9 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void gemm_tile_kernel(
 // KMASK (K not a multiple of BK) the columns past K are stored to LDS as zeros.
 template <int EPI, int BK, int KS, bool IL, bool KMASK>
 __global__ __launch_bounds__(256 * KS) void gemm_pipe_kernel(
-    const float* X, int ldx, const float* W,
-    const float* __restrict__ bias, float* Y, int ldy, int M, int N, int K, EpiArgs ep) {
+    const float* X, int ldx, const float* W, int ldw,
+    const float* __restrict__ bias, float* Y, int ldy, int M, int N, int K, int ksplit,
+    EpiArgs ep) {
   constexpr int BM = 64, BN = 64, GT = 256, NT = GT * KS;
   constexpr int LDA = BK + 4;
   constexpr int A4 = BM * BK / 4;          // float4 per operand slab
@@ -316,6 +323,11 @@ __global__ __launch_bounds__(256 * KS) void gemm_pipe_kernel(
   const int gtid = tid & (GT - 1);
   float* As = smem + kg * 2 * (BM + BN) * LDA;
   float* Ws = As + 2 * BM * LDA;
+  // K slice of this workgroup (blockIdx.y; one slice unless split-K partials)
+  X += (long)blockIdx.y * ksplit;
+  W += (long)blockIdx.y * ksplit;
+  Y += (long)blockIdx.y * M * ldy;
+  K = min(ksplit, K - (int)blockIdx.y * ksplit);
 
   const float* pa[L];
   const float* pw[L];
@@ -326,7 +338,7 @@ __global__ __launch_bounds__(256 * KS) void gemm_pipe_kernel(
     rr[i] = idx / (BK / 4);
     cc[i] = (idx % (BK / 4)) * 4;
     pa[i] = X + (long)min(m0 + rr[i], M - 1) * ldx;
-    pw[i] = W + (long)min(n0 + rr[i], N - 1) * K;
+    pw[i] = W + (long)min(n0 + rr[i], N - 1) * ldw;
   }
   floatx4 sa0[L], sw0[L], sa1[L], sw1[L];  // two register stages
 #define LX_GLOAD(SA, SW, KT)                                                         \
@@ -473,9 +485,18 @@ struct PipeCfg {
   }
 };
 
+// Launch geometry shared by the launchers: `splits` K slices of `ksplit`
+// columns each (blockIdx.y); a single slice covers all of K.
+struct Split {
+  int splits = 1;
+  int ksplit = 0;
+  int ldw = 0;
+};
+
 template <int EPI, int BK, int KS, bool IL, bool KMASK>
 int launch_pipe_k(const float* x, int ldx, const float* W, const float* bias, float* y, int ldy,
-                  int M, int N, int K, const EpiArgs& ep, hipStream_t stream) {
+                  int M, int N, int K, const EpiArgs& ep, hipStream_t stream,
+                  const Split& sp) {
   auto kern = gemm_pipe_kernel<EPI, BK, KS, IL, KMASK>;
   const size_t lds = PipeCfg<BK, KS>::lds();
   if (lds > 64 * 1024) {
@@ -490,19 +511,24 @@ int launch_pipe_k(const float* x, int ldx, const float* W, const float* bias, fl
     }
   }
   const long tiles = (long)((M + 63) / 64) * ((N + 63) / 64);
-  hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(PipeCfg<BK, KS>::threads), lds, stream, x,
-                     ldx, W, bias, y, ldy, M, N, K, ep);
+  hipLaunchKernelGGL(kern, dim3((unsigned)tiles, sp.splits), dim3(PipeCfg<BK, KS>::threads), lds,
+                     stream, x, ldx, W, sp.ldw, bias, y, ldy, M, N, K, sp.ksplit, ep);
   return check_launch("gemm_pipe_kernel");
 }
 
-// The unmasked kernel needs K to be whole slabs and the slab count a multiple
-// of 2 KS (the loop runs two slabs per k-group per iteration).
+// The unmasked kernel needs every K slice to be whole slabs and its slab
+// count a multiple of 2 KS (the loop runs two slabs per k-group per iteration).
 template <int EPI, int BK, int KS, bool IL>
 int launch_pipe(const float* x, int ldx, const float* W, const float* bias, float* y, int ldy,
-                int M, int N, int K, const EpiArgs& ep, hipStream_t stream) {
-  const bool exact = K % BK == 0 && (K / BK) % (2 * KS) == 0;
-  return exact ? launch_pipe_k<EPI, BK, KS, IL, false>(x, ldx, W, bias, y, ldy, M, N, K, ep, stream)
-               : launch_pipe_k<EPI, BK, KS, IL, true>(x, ldx, W, bias, y, ldy, M, N, K, ep, stream);
+                int M, int N, int K, const EpiArgs& ep, hipStream_t stream, Split sp = Split()) {
+  if (sp.ksplit <= 0) sp.ksplit = K;
+  if (sp.ldw <= 0) sp.ldw = K;
+  const int step = 2 * KS * BK;
+  const bool exact = sp.ksplit % step == 0 && (K % sp.ksplit) % step == 0;
+  return exact ? launch_pipe_k<EPI, BK, KS, IL, false>(x, ldx, W, bias, y, ldy, M, N, K, ep,
+                                                       stream, sp)
+               : launch_pipe_k<EPI, BK, KS, IL, true>(x, ldx, W, bias, y, ldy, M, N, K, ep,
+                                                      stream, sp);
 }
 
 template <int BM, int BN, int BK, int WM, int WN, int KS>
@@ -533,8 +559,8 @@ int launch_tile(const float* x, int ldx, const float* W, const float* bias, floa
     }
   }
   const long tiles = (long)((M + CFG::bm - 1) / CFG::bm) * ((N + CFG::bn - 1) / CFG::bn);
-  hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(CFG::threads), lds, stream, x, ldx, W, bias,
-                     y, ldy, M, N, K, ep);
+  hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(CFG::threads), lds, stream, x, ldx, W, K,
+                     bias, y, ldy, M, N, K, K, ep);
   return check_launch("gemm_tile_kernel");
 }
 
@@ -740,9 +766,44 @@ int dispatch_gemm(int kind, int cfg, const float* x, int ldx, const float* W, co
 // wave (QKV 54.3 us = 116 TFLOP/s, out 23.3 us, FF0 38.4 us, FF2 39.8 us);
 // with many tiles, or K <= 512 (too few slabs to split), the unsplit kernel
 // wins (out 110.6 vs 112.7 us at B*T = 6000; input projection 8.9 vs 10.7 us).
+// Split-K partial GEMMs aim for this many workgroups (two per CU).
+constexpr long kSplitTargetWgs = 512;
+
 int pick_config(int M, int N, int K) {
   const long tiles = (long)((M + 63) / 64) * ((N + 63) / 64);
   return (K <= 512 || tiles >= 2048) ? 4 : 5;
+}
+
+int gemm_splitk_partials(const float* x, int ldx, const float* W, int ldw, float* ws, int M,
+                         int N, int K, int splits, int ksplit, hipStream_t stream) {
+  LX_REQUIRE(x && W && ws && M > 0 && N > 0 && K > 0 && splits >= 1 && ksplit > 0 &&
+                 ksplit % 4 == 0 && (long)(splits - 1) * ksplit < K && (long)splits * ksplit >= K &&
+                 ldx % 4 == 0 && ldw % 4 == 0 && ldx >= K && ldw >= K,
+             "gemm_splitk_partials: bad shape M=%d N=%d K=%d splits=%d ksplit=%d", M, N, K,
+             splits, ksplit);
+  LX_REQUIRE(((uintptr_t)x | (uintptr_t)W) % 16 == 0, "gemm_splitk_partials: misaligned operand");
+  EpiArgs ep;
+  int rc = make_epi(nullptr, N, &ep);
+  if (rc) return rc;
+  Split sp;
+  sp.splits = splits;
+  sp.ksplit = ksplit;
+  sp.ldw = ldw;
+  return launch_pipe<LX_EPI_NONE, 32, 1, true>(x, ldx, W, nullptr, ws, N, M, N, K, ep, stream, sp);
+}
+
+int gemm_splitk_plan(int M, int N, int K, int* ksplit) {
+  const long tiles = (long)((M + 63) / 64) * ((N + 63) / 64);
+  int s = (int)((kSplitTargetWgs + tiles - 1) / tiles);
+  int max_s = K / 128 > 0 ? K / 128 : 1;  // at least four 32-wide slabs per slice
+  if (max_s > 8) max_s = 8;                   // the reduce passes sum at most 8 slices
+  if (s > max_s) s = max_s;
+  if (s < 1) s = 1;
+  int ks = (K + s - 1) / s;
+  ks = (ks + 63) / 64 * 64;  // whole slab pairs
+  s = (K + ks - 1) / ks;
+  *ksplit = ks;
+  return s;
 }
 
 }  // namespace lx

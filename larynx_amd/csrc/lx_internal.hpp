@@ -44,9 +44,24 @@ int fill_f32(float* p, long n, float value, hipStream_t stream);
 int interleave_rows(const float* a, const float* b, float* out, int rows, int K,
                     hipStream_t stream);
 
-// Strided 2-D copy: dst[r, c] = src[r, c] for r < rows, c < cols.
-int copy_rows(const float* src, int lds, float* dst, int ldd, int rows, int cols,
-              hipStream_t stream);
+// ---- split-K GEMM (lx_gemm.hip) and its reduce / epilogue kernels (lx_splitk.hip) ----
+// ws[s] (M, N) = x[:, s*ksplit : (s+1)*ksplit] @ W[:, same]^T, s < splits (no bias).
+int gemm_splitk_partials(const float* x, int ldx, const float* W, int ldw, float* ws, int M,
+                         int N, int K, int splits, int ksplit, hipStream_t stream);
+// Number of K slices (and slice width, a multiple of 64) that gives the
+// (M, N) tile grid about two workgroups per CU.
+int gemm_splitk_plan(int M, int N, int K, int* ksplit);
+// x[m, :] += sum_s ws[s][m, :] (+ bias); then, if norm_w, hn[m, :] =
+// RMSNorm(x[m, :]) * norm_w (the next sub-layer's input norm).  Rows of N floats.
+int splitk_resid_rmsnorm(const float* ws, int splits, int M, int N, const float* bias, float* x,
+                         const float* norm_w, float eps, float* hn, hipStream_t stream);
+// v = sum_s ws[s][m, :] + bias over the fused q|k|v row (n_heads + 2 n_kv_heads
+// heads of 64); NEOX rotary at position pos[m] on the q and k heads; q ->
+// q_out[m, 0:n_heads*64] (row stride ldq), k / v -> k_cache / v_cache row
+// row0 + m (row stride n_kv_heads*64).
+int splitk_qkv_rope_cache(const float* ws, int splits, int M, const float* bias, int n_heads,
+                          int n_kv_heads, const int* pos, const float* inv_freq, float* q_out,
+                          int ldq, float* k_cache, float* v_cache, int row0, hipStream_t stream);
 
 // ---- single-token decode (lx_decode.hip) ----
 enum { DEC_QKV_ROPE = 0, DEC_SWIGLU = 1, DEC_RESID = 2, DEC_HEAD = 3 };

@@ -115,16 +115,6 @@ __global__ void interleave_kernel(const float* __restrict__ a, const float* __re
   }
 }
 
-__global__ void copy_rows_kernel(const float* __restrict__ src, int lds, float* __restrict__ dst,
-                                 int ldd, int rows, int cols) {
-  const long n = (long)rows * cols;
-  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n;
-       i += (long)gridDim.x * blockDim.x) {
-    const long r = i / cols;
-    const int c = (int)(i - r * cols);
-    dst[r * ldd + c] = src[r * lds + c];
-  }
-}
 
 inline unsigned grid1d(long n) {
   long g = (n + 255) / 256;
@@ -182,11 +172,5 @@ int interleave_rows(const float* a, const float* b, float* out, int rows, int K,
   return check_launch("interleave_kernel");
 }
 
-int copy_rows(const float* src, int lds, float* dst, int ldd, int rows, int cols,
-              hipStream_t stream) {
-  hipLaunchKernelGGL(copy_rows_kernel, dim3(grid1d((long)rows * cols)), dim3(256), 0, stream, src,
-                     lds, dst, ldd, rows, cols);
-  return check_launch("copy_rows_kernel");
-}
 
 }  // namespace lx

@@ -68,6 +68,7 @@ struct lx_qwen2 {
   std::vector<Layer> layers;
   // activations, sized for max_ctx rows
   float *x, *hn, *qkv, *att, *act;
+  float* ws = nullptr;  // split-K partial sums
   int* pos;     // pos[i] = i
   // single-token decode state (lx_decode.hip kernels)
   int* d_pos = nullptr;       // position of the token being decoded
@@ -86,32 +87,53 @@ struct lx_qwen2 {
 
 namespace {
 
-// Prefill layer (rows >= 1 query rows at positions pos[0..rows), appended to
-// the cache at row0).
-int layer_body(lx_qwen2* m, Layer& L, int rows, const int* pos, int row0, hipStream_t s) {
+// Width of the split-K partial workspace: the largest splits * rows * N over
+// the three split projections and every prefill length up to max_ctx.
+size_t splitk_ws_floats(int max_ctx, int H, int QKV, int I) {
+  size_t best = 0;
+  // splits depend on M only through the tile count, so the largest M of each
+  // 64-row band (and max_ctx itself) bounds every length
+  for (int M = 64;; M += 64) {
+    const int rows = M < max_ctx ? M : max_ctx;
+    const int shapes[3][2] = {{QKV, H}, {H, H}, {H, I}};
+    for (const auto& sh : shapes) {
+      int ks = 0;
+      const int splits = gemm_splitk_plan(rows, sh[0], sh[1], &ks);
+      const size_t n = (size_t)splits * rows * sh[0];
+      if (n > best) best = n;
+    }
+    if (M >= max_ctx) break;
+  }
+  return best;
+}
+
+// Prefill layer (src/llm/llm.cpp:141-173) over L rows at positions m->pos[0..L).
+// On entry m->hn holds input_layernorm(x); on exit x is the layer output and
+// m->hn holds next_norm(x) (the next layer's input_layernorm or the final norm).
+//   q/k/v: split-K partials, then bias + NEOX rotary + cache append in one pass;
+//   attention (causal, GQA) reads q and the cache;
+//   o_proj: split-K partials, then residual + post_attention_layernorm;
+//   gate/up with the SwiGLU epilogue;
+//   down_proj: split-K partials, then residual + next_norm.
+int prefill_layer(lx_qwen2* m, Layer& L, int rows, const float* next_norm, hipStream_t s) {
   const int H = m->H, KV = m->KV, QKV = m->QKV;
-  // input_layernorm + q/k/v (+bias) + NEOX rotary on q and k (src/llm/llm.cpp:145-156)
-  LX_TRY(lx_rmsnorm_f32(m->x, L.in_norm, m->hn, rows, H, m->eps, s));
-  LX_TRY(lx_linear_f32(m->hn, H, L.qkv_w, L.qkv_b, m->qkv, QKV, rows, QKV, H, nullptr, s));
-  LX_TRY(lx_rope_neox_f32(m->qkv, pos, rows, m->NH, m->HD, QKV, m->theta, s));
-  LX_TRY(lx_rope_neox_f32(m->qkv + H, pos, rows, m->NKV, m->HD, QKV, m->theta, s));
-  // cache the roped key and raw value at rows [row0, row0 + rows)
-  LX_TRY(copy_rows(m->qkv + H, QKV, L.k_cache + (long)row0 * KV, KV, rows, KV, s));
-  LX_TRY(copy_rows(m->qkv + H + KV, QKV, L.v_cache + (long)row0 * KV, KV, rows, KV, s));
-  const int Tk = row0 + rows;
+  int ks = 0;
+  int sp = gemm_splitk_plan(rows, QKV, H, &ks);
+  LX_TRY(gemm_splitk_partials(m->hn, H, L.qkv_w, H, m->ws, rows, QKV, H, sp, ks, s));
+  LX_TRY(splitk_qkv_rope_cache(m->ws, sp, rows, L.qkv_b, m->NH, m->NKV, m->pos, m->rope_tab,
+                               m->qkv, QKV, L.k_cache, L.v_cache, 0, s));
   const float scale = 1.0f / std::sqrt((float)m->HD);
-  LX_TRY(lx_attention_f32(m->qkv, QKV, L.k_cache, KV, L.v_cache, KV, m->att, H, 1, rows, Tk,
-                          m->NH, m->NKV, m->HD, scale, /*causal*/ 1, /*q_offset*/ row0, s));
-  lx_epilogue resid{};
-  resid.kind = LX_EPI_RESID;
-  LX_TRY(lx_linear_f32(m->att, H, L.o_w, nullptr, m->x, H, rows, H, H, &resid, s));
-  // post_attention_layernorm + SwiGLU MLP (src/llm/llm.cpp:165-170)
-  LX_TRY(lx_rmsnorm_f32(m->x, L.post_norm, m->hn, rows, H, m->eps, s));
+  LX_TRY(lx_attention_f32(m->qkv, QKV, L.k_cache, KV, L.v_cache, KV, m->att, H, 1, rows, rows,
+                          m->NH, m->NKV, m->HD, scale, /*causal*/ 1, /*q_offset*/ 0, s));
+  sp = gemm_splitk_plan(rows, H, H, &ks);
+  LX_TRY(gemm_splitk_partials(m->att, H, L.o_w, H, m->ws, rows, H, H, sp, ks, s));
+  LX_TRY(splitk_resid_rmsnorm(m->ws, sp, rows, H, nullptr, m->x, L.post_norm, m->eps, m->hn, s));
   lx_epilogue swiglu{};
   swiglu.kind = LX_EPI_SWIGLU_PAIRED;
   LX_TRY(lx_linear_f32(m->hn, H, L.gu_w, nullptr, m->act, m->I, rows, 2 * m->I, H, &swiglu, s));
-  LX_TRY(lx_linear_f32(m->act, m->I, L.down_w, nullptr, m->x, H, rows, H, m->I, &resid, s));
-  return LX_OK;
+  sp = gemm_splitk_plan(rows, H, m->I, &ks);
+  LX_TRY(gemm_splitk_partials(m->act, m->I, L.down_w, m->I, m->ws, rows, H, m->I, sp, ks, s));
+  return splitk_resid_rmsnorm(m->ws, sp, rows, H, nullptr, m->x, next_norm, m->eps, m->hn, s);
 }
 
 // One decode layer (src/llm/llm.cpp:254-289) as five launches: RMSNorm + QKV
@@ -271,6 +293,7 @@ extern "C" int lx_qwen2_create(const lx_qwen2_weights* w, int max_ctx, lx_qwen2*
   m->qkv = A(rows * QKV);
   m->att = A(rows * H);
   m->act = A(rows * I);
+  m->ws = A(splitk_ws_floats(max_ctx, H, QKV, I));
   m->max_splits = dec_attention_splits(max_ctx);
   m->part_stride = ((long)m->max_splits * (m->NH / m->NKV) * (m->HD + 2) + 31) / 32 * 32;
   m->part = A((size_t)m->part_stride * m->NKV);
@@ -397,13 +420,14 @@ extern "C" int lx_qwen2_prefill(lx_qwen2* m, const float* lm_input, int L, float
     return LX_ERR_LAUNCH;
   }
   m->cache_len = 0;
+  LX_TRY(lx_rmsnorm_f32(m->x, m->layers[0].in_norm, m->hn, L, H, m->eps, s));
   for (int l = 0; l < m->NL; ++l) {
-    LX_TRY(layer_body(m, m->layers[l], L, m->pos, 0, s));
+    const float* next_norm = l + 1 < m->NL ? m->layers[l + 1].in_norm : m->final_norm;
+    LX_TRY(prefill_layer(m, m->layers[l], L, next_norm, s));
     if (hidden)
       (void)hipMemcpyAsync(hidden + (size_t)l * L * H, m->x, sizeof(float) * (size_t)L * H,
                            hipMemcpyDeviceToDevice, s);
   }
-  LX_TRY(lx_rmsnorm_f32(m->x, m->final_norm, m->hn, L, H, m->eps, s));
   if (final_norm)
     (void)hipMemcpyAsync(final_norm, m->hn, sizeof(float) * (size_t)L * H, hipMemcpyDeviceToDevice,
                          s);

@@ -159,3 +159,25 @@ def test_decode_graph_matches_eager_and_crosses_splits(gpu, qwen):
         assert orc.rel_err(vd[:n0 + 5].cpu().numpy(), o.v_cache[layer, :n0 + 5]) < TOL
     eager.close()
     graph.close()
+
+
+@pytest.mark.parametrize("L", [1, 37, 300])
+def test_prefill_ragged_lengths(gpu, qwen, L):
+    """Prefill at lengths that leave partial 64-row tiles and change the
+    split-K plan (1 row: one tile per column band; 300 rows: five bands)."""
+    cfg, params, _, lm = qwen
+    announce(f"qwen2 prefill L={L}")
+    lm_in = torch.from_numpy(orc.normal((L, cfg.hidden), 300 + L, 1, 0.5)).to(gpu)
+    logits, hidden, final = lm.prefill(lm_in, capture=True)
+    torch.cuda.synchronize()
+    o = orc.Qwen2(params, cfg, cap=2304)
+    rl, rh, rf = o.prefill(lm_in.cpu().numpy(), capture=True)
+    for layer in range(cfg.n_layers):
+        assert orc.rel_err(hidden[layer].cpu().numpy(), rh[layer]) < TOL, layer
+    assert orc.rel_err(final.cpu().numpy(), rf) < TOL
+    assert orc.rel_err(logits.cpu().numpy(), rl) < TOL
+    assert lm.cache_len == L
+    for layer in (0, cfg.n_layers - 1):
+        k, v = lm.cache_views(layer)
+        assert orc.rel_err(k[:L].cpu().numpy(), o.k_cache[layer, :L]) < TOL
+        assert orc.rel_err(v[:L].cpu().numpy(), o.v_cache[layer, :L]) < TOL
