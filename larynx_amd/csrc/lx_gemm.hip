@@ -293,7 +293,12 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void gemm_tile_kernel(
 // Operand rows past M (or N) are read from the last valid row and only reach
 // output rows (columns) the epilogue never stores, so they need no mask; with
 // KMASK (K not a multiple of BK) the columns past K are stored to LDS as zeros.
-template <int EPI, int BK, int KS, bool IL, bool KMASK>
+// With XB (BK = 32 only) the barrier sits inside the slab: the first 12 MFMAs
+// of the slab run alongside the LDS writes of the next slab and the global
+// loads, then the barrier, then the next slab's fragment reads are issued and
+// the last 4 MFMAs (operands already in registers) cover their latency, so the
+// matrix pipe does not drain at every barrier.
+template <int EPI, int BK, int KS, bool IL, bool KMASK, bool XB = false>
 __global__ __launch_bounds__(256 * KS) void gemm_pipe_kernel(
     const float* X, int ldx, const float* W, int ldw,
     const float* __restrict__ bias, float* Y, int ldy, int M, int N, int K, int ksplit,
@@ -437,13 +442,67 @@ __global__ __launch_bounds__(256 * KS) void gemm_pipe_kernel(
     __syncthreads();                                                                   \
   } while (0)
 
-  // Both halves run unconditionally (a surplus half multiplies the zeros its
-  // slab holds; the launcher sets KMASK whenever the slab count is not a
-  // multiple of 2 KS), so the loop has a single back-edge state for the waits.
-  for (int it = 0; it < iters; it += 2) {
-    LX_SLAB(it, 0, sa1, sw1);
-    LX_SLAB(it + 1, 1, sa0, sw0);
+  // Cross-barrier slab (XB): fragments FA/FB of this slab are in registers on
+  // entry; the next slab's go to NA/NB after the barrier.
+#define LX_SLAB_XB(IT, BUF, SNA, SNW, FA, FB, NA, NB)                                  \
+  do {                                                                                 \
+    _Pragma("unroll") for (int j = 0; j < 3; ++j)                                       \
+      _Pragma("unroll") for (int e = 0; e < 4; ++e)                                     \
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(FA[j][e], FB[j][e], acc, 0, 0, 0);   \
+    LX_SSTORE(SNA, SNW, (BUF) ^ 1, LX_KT((IT) + 1));                                   \
+    LX_GLOAD(SNA, SNW, LX_KC((IT) + 3));                                               \
+    /* 12 MFMAs with the 2L DS writes and 2L global loads between them */           \
+    _Pragma("unroll") for (int q = 0; q < 2 * L; ++q) {                                 \
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                               \
+      __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);                               \
+    }                                                                                  \
+    _Pragma("unroll") for (int q = 0; q < 2 * L; ++q) {                                 \
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                               \
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                               \
+    }                                                                                  \
+    __builtin_amdgcn_sched_group_barrier(0x008, 12 - 4 * L, 0);                        \
+    __syncthreads();                                                                   \
+    {                                                                                  \
+      const float* nab = As + ((BUF) ^ 1) * BM * LDA + (wm * 32 + r) * LDA + h * 16;    \
+      const float* nwb = Ws + ((BUF) ^ 1) * BN * LDA + (wn * 32 + r) * LDA + h * 16;    \
+      _Pragma("unroll") for (int j = 0; j < 4; ++j) {                                   \
+        NA[j] = *reinterpret_cast<const floatx4*>(nab + 4 * j);                        \
+        NB[j] = *reinterpret_cast<const floatx4*>(nwb + 4 * j);                        \
+      }                                                                                \
+    }                                                                                  \
+    _Pragma("unroll") for (int e = 0; e < 4; ++e)                                       \
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(FA[3][e], FB[3][e], acc, 0, 0, 0);     \
+    /* the 8 fragment reads first, then the 4 MFMAs that cover them */              \
+    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);                                 \
+    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);                                 \
+  } while (0)
+
+  if (XB) {
+    static_assert(!XB || BK == 32, "XB needs one 32-wide sub-slab per slab");
+    floatx4 fa0[4], fb0[4], fa1[4], fb1[4];
+    {
+      const float* ab = As + (wm * 32 + r) * LDA + h * 16;
+      const float* wb = Ws + (wn * 32 + r) * LDA + h * 16;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        fa0[j] = *reinterpret_cast<const floatx4*>(ab + 4 * j);
+        fb0[j] = *reinterpret_cast<const floatx4*>(wb + 4 * j);
+      }
+    }
+    for (int it = 0; it < iters; it += 2) {
+      LX_SLAB_XB(it, 0, sa1, sw1, fa0, fb0, fa1, fb1);
+      LX_SLAB_XB(it + 1, 1, sa0, sw0, fa1, fb1, fa0, fb0);
+    }
+  } else {
+    // Both halves run unconditionally (a surplus half multiplies the zeros its
+    // slab holds; the launcher sets KMASK whenever the slab count is not a
+    // multiple of 2 KS), so the loop has a single back-edge state for the waits.
+    for (int it = 0; it < iters; it += 2) {
+      LX_SLAB(it, 0, sa1, sw1);
+      LX_SLAB(it + 1, 1, sa0, sw0);
+    }
   }
+#undef LX_SLAB_XB
 #undef LX_SLAB
 #undef LX_KC
 #undef LX_KT
@@ -493,11 +552,11 @@ struct Split {
   int ldw = 0;
 };
 
-template <int EPI, int BK, int KS, bool IL, bool KMASK>
+template <int EPI, int BK, int KS, bool IL, bool KMASK, bool XB>
 int launch_pipe_k(const float* x, int ldx, const float* W, const float* bias, float* y, int ldy,
                   int M, int N, int K, const EpiArgs& ep, hipStream_t stream,
                   const Split& sp) {
-  auto kern = gemm_pipe_kernel<EPI, BK, KS, IL, KMASK>;
+  auto kern = gemm_pipe_kernel<EPI, BK, KS, IL, KMASK, XB>;
   const size_t lds = PipeCfg<BK, KS>::lds();
   if (lds > 64 * 1024) {
     static bool attr_set = false;
@@ -518,17 +577,17 @@ int launch_pipe_k(const float* x, int ldx, const float* W, const float* bias, fl
 
 // The unmasked kernel needs every K slice to be whole slabs and its slab
 // count a multiple of 2 KS (the loop runs two slabs per k-group per iteration).
-template <int EPI, int BK, int KS, bool IL>
+template <int EPI, int BK, int KS, bool IL, bool XB = false>
 int launch_pipe(const float* x, int ldx, const float* W, const float* bias, float* y, int ldy,
                 int M, int N, int K, const EpiArgs& ep, hipStream_t stream, Split sp = Split()) {
   if (sp.ksplit <= 0) sp.ksplit = K;
   if (sp.ldw <= 0) sp.ldw = K;
   const int step = 2 * KS * BK;
   const bool exact = sp.ksplit % step == 0 && (K % sp.ksplit) % step == 0;
-  return exact ? launch_pipe_k<EPI, BK, KS, IL, false>(x, ldx, W, bias, y, ldy, M, N, K, ep,
-                                                       stream, sp)
-               : launch_pipe_k<EPI, BK, KS, IL, true>(x, ldx, W, bias, y, ldy, M, N, K, ep,
-                                                      stream, sp);
+  return exact ? launch_pipe_k<EPI, BK, KS, IL, false, XB>(x, ldx, W, bias, y, ldy, M, N, K, ep,
+                                                           stream, sp)
+               : launch_pipe_k<EPI, BK, KS, IL, true, XB>(x, ldx, W, bias, y, ldy, M, N, K, ep,
+                                                          stream, sp);
 }
 
 template <int BM, int BN, int BK, int WM, int WN, int KS>
@@ -715,11 +774,13 @@ int gemv_epi(const float* x, int ldx, const float* W, const float* bias, float* 
   return check_launch("gemv_epi_kernel");
 }
 
-// Configurations the sweep hook can select:
+// Configurations.  The library selects among 4, 5, 7 and 8; the others are
+// built only into the tuning sweep:
 //   0: tiled 64 x 64, BK 32, split-K 2        1: tiled 128 x 64, BK 32
 //   2: pipelined BK 32                        3: pipelined BK 32, split-K 2
 //   4: pipelined BK 32, interleaved           5: pipelined BK 32, split-K 2, interleaved
 //   6: pipelined BK 64, interleaved
+//   7: pipelined BK 32, cross-barrier slabs   8: as 7 with split-K 2
 using Cfg0 = TileCfg<64, 64, 32, 2, 2, 2>;
 using Cfg1 = TileCfg<128, 64, 32, 2, 2, 1>;
 
@@ -727,13 +788,17 @@ template <int EPI>
 int dispatch_cfg(int cfg, const float* x, int ldx, const float* W, const float* bias, float* y,
                  int ldy, int M, int N, int K, const EpiArgs& ep, hipStream_t s) {
   switch (cfg) {
+    case 4: return launch_pipe<EPI, 32, 1, true>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
+    case 5: return launch_pipe<EPI, 32, 2, true>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
+    case 7: return launch_pipe<EPI, 32, 1, true, true>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
+    case 8: return launch_pipe<EPI, 32, 2, true, true>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
+#ifdef LX_GEMM_SWEEP
     case 0: return launch_tile<EPI, Cfg0>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
     case 1: return launch_tile<EPI, Cfg1>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
     case 2: return launch_pipe<EPI, 32, 1, false>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
     case 3: return launch_pipe<EPI, 32, 2, false>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
-    case 4: return launch_pipe<EPI, 32, 1, true>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
-    case 5: return launch_pipe<EPI, 32, 2, true>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
     case 6: return launch_pipe<EPI, 64, 1, true>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
+#endif
   }
   set_error("linear: unknown tile configuration %d", cfg);
   return LX_ERR_ARG;
@@ -761,17 +826,18 @@ int dispatch_gemm(int kind, int cfg, const float* x, int ldx, const float* W, co
 
 // Tile configuration by shape, from an on-device sweep over the estimator's
 // projections at B*T = 1000 and 6000 rows (MI355X, graph-replayed launches
-// under continuous load): with fewer than 2048 tiles (two workgroups or fewer
-// per CU at B*T = 1000) intra-workgroup split-K 2 gives each SIMD a second
-// wave (QKV 54.3 us = 116 TFLOP/s, out 23.3 us, FF0 38.4 us, FF2 39.8 us);
-// with many tiles, or K <= 512 (too few slabs to split), the unsplit kernel
-// wins (out 110.6 vs 112.7 us at B*T = 6000; input projection 8.9 vs 10.7 us).
+// under continuous load).  Cross-barrier slabs win everywhere (2-7% over the
+// plain interleaved schedule).  With fewer than 2048 tiles (two workgroups or
+// fewer per CU at B*T = 1000) intra-workgroup split-K 2 gives each SIMD a
+// second wave (QKV 54.1 us = 116 TFLOP/s, out 23.0 us, FF0 38.8 us, FF2
+// 38.2 us); with many tiles, or K <= 512 (too few slabs to split), the unsplit
+// kernel wins (QKV at B*T = 6000: 314 us = 120 TFLOP/s).
 // Split-K partial GEMMs aim for this many workgroups (two per CU).
 constexpr long kSplitTargetWgs = 512;
 
 int pick_config(int M, int N, int K) {
   const long tiles = (long)((M + 63) / 64) * ((N + 63) / 64);
-  return (K <= 512 || tiles >= 2048) ? 4 : 5;
+  return (K <= 512 || tiles >= 2048) ? 7 : 8;
 }
 
 int gemm_splitk_partials(const float* x, int ldx, const float* W, int ldw, float* ws, int M,
@@ -789,7 +855,8 @@ int gemm_splitk_partials(const float* x, int ldx, const float* W, int ldw, float
   sp.splits = splits;
   sp.ksplit = ksplit;
   sp.ldw = ldw;
-  return launch_pipe<LX_EPI_NONE, 32, 1, true>(x, ldx, W, nullptr, ws, N, M, N, K, ep, stream, sp);
+  return launch_pipe<LX_EPI_NONE, 32, 1, true, true>(x, ldx, W, nullptr, ws, N, M, N, K, ep, stream,
+                                                     sp);
 }
 
 int gemm_splitk_plan(int M, int N, int K, int* ksplit) {
