@@ -22,25 +22,38 @@ namespace {
 
 constexpr int kHD = 64;  // head dim handled by these kernels
 
-// Flash attention, 4 waves per workgroup: a 64-query tile of one (batch, head)
-// split as 2 query sub-tiles (32 queries each) x 2 key halves.  Every 64-key
-// tile of K and V is loaded once into LDS (coalesced, double buffered) and
-// read by all four waves; wave (qs, ks) scores its 32 queries against keys
-// [ks*32, ks*32 + 32) of each tile.  The two key halves of a query sub-tile
-// are merged through LDS at the end in a fixed order (deterministic).
+// Flash attention, 2 x KS waves per workgroup: a 64-query tile of one
+// (batch, head) split as 2 query sub-tiles (32 queries each) x KS key parts.
+// Every (32 KS)-key tile of K and V is loaded once into LDS (coalesced, double
+// buffered) and read by all waves; wave (qs, ks) scores its 32 queries against
+// keys [ks*32, ks*32 + 32) of each tile.  The KS key parts of a query sub-tile
+// are merged through LDS at the end in a fixed order (deterministic).  KS = 4
+// gives the short sequences (few query tiles) two waves per SIMD.
 // Softmax runs in base 2: q is pre-scaled by scale * log2(e), so p = exp2(s - m).
 constexpr int kQT = 64;          // queries per workgroup
-constexpr int kKT = 64;          // keys per LDS tile
 constexpr int kLD = kHD + 4;     // LDS row stride (floats)
-constexpr size_t kFlashLds = (size_t)2 * 2 * kKT * kLD * sizeof(float);  // K,V x 2 buffers
+constexpr float kLazy = 8.0f;    // reference-max slack of the online softmax (log2 units)
 
-__global__ __launch_bounds__(256) void attn_flash_kernel(
+template <int KS>
+constexpr size_t flash_lds() {
+  // K, V x 2 buffers of 32 KS rows; reused after the loop for the merge
+  // ((KS - 1) partial states of 64 lanes x 34 floats per query sub-tile) and
+  // the transposed output tile (2 x 32 rows of kLD).
+  return (size_t)2 * 2 * 32 * KS * kLD * sizeof(float);
+}
+
+template <int KS>
+__global__ __launch_bounds__(128 * KS) void attn_flash_kernel(
     const float* __restrict__ q, int ldq, const float* __restrict__ k, int ldk,
     const float* __restrict__ v, int ldv, float* __restrict__ o, int ldo, int Tq, int Tk,
     int rep, float qscale, int causal, int q_offset) {
+  constexpr int KT = 32 * KS;    // keys per LDS tile
+  constexpr int NT = 128 * KS;   // threads
+  static_assert(KT * 16 == 4 * NT, "4 float4 per thread per operand tile");
+  static_assert(2 * (KS - 1) * 64 * 34 + 2 * 32 * kLD <= 2 * 2 * KT * kLD, "merge space");
   extern __shared__ __attribute__((aligned(16))) float lds[];
-  float* Ks = lds;                       // [2][kKT][kLD]
-  float* Vs = lds + 2 * kKT * kLD;       // [2][kKT][kLD]
+  float* Ks = lds;                      // [2][KT][kLD]
+  float* Vs = lds + 2 * KT * kLD;       // [2][KT][kLD]
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int qs = wave & 1, ks = wave >> 1;
@@ -58,18 +71,18 @@ __global__ __launch_bounds__(256) void attn_flash_kernel(
   }
   const int my_q = q_offset + q0 + r;
   const int kend = causal ? min(Tk, q_offset + min(qt0 + kQT - 1, Tq - 1) + 1) : Tk;
-  const int ntiles = (kend + kKT - 1) / kKT;
+  const int ntiles = (kend + KT - 1) / KT;
 
-  // K/V tile loader: 2 x 1024 float4 per tile, 8 per thread.
+  // K/V tile loader: 2 x 16 KT float4 per tile, 4 + 4 per thread.
   const float* kbase = k + (long)b * Tk * ldk + g * kHD;
   const float* vbase = v + (long)b * Tk * ldv + g * kHD;
   floatx4 rk[4], rv[4];
   auto gload = [&](int t) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int idx = tid + 256 * j;
+      const int idx = tid + NT * j;
       const int row = idx >> 4, c = (idx & 15) * 4;
-      const int key = min(t * kKT + row, Tk - 1);
+      const int key = min(t * KT + row, Tk - 1);
       rk[j] = *reinterpret_cast<const floatx4*>(kbase + (long)key * ldk + c);
       rv[j] = *reinterpret_cast<const floatx4*>(vbase + (long)key * ldv + c);
     }
@@ -77,10 +90,10 @@ __global__ __launch_bounds__(256) void attn_flash_kernel(
   auto sstore = [&](int buf) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int idx = tid + 256 * j;
+      const int idx = tid + NT * j;
       const int row = idx >> 4, c = (idx & 15) * 4;
-      *reinterpret_cast<floatx4*>(Ks + (buf * kKT + row) * kLD + c) = rk[j];
-      *reinterpret_cast<floatx4*>(Vs + (buf * kKT + row) * kLD + c) = rv[j];
+      *reinterpret_cast<floatx4*>(Ks + (buf * KT + row) * kLD + c) = rk[j];
+      *reinterpret_cast<floatx4*>(Vs + (buf * KT + row) * kLD + c) = rv[j];
     }
   };
 
@@ -100,9 +113,9 @@ __global__ __launch_bounds__(256) void attn_flash_kernel(
   for (int t = 0; t < ntiles; ++t) {
     const int buf = t & 1;
     if (t + 1 < ntiles) gload(t + 1);
-    const int kb = t * kKT + ks * 32;  // first key of this wave's half tile
+    const int kb = t * KT + ks * 32;  // first key of this wave's part of the tile
     if (kb < kend) {
-      const float* krow = Ks + (buf * kKT + ks * 32 + r) * kLD + h * 32;
+      const float* krow = Ks + (buf * KT + ks * 32 + r) * kLD + h * 32;
       floatx16 s;
 #pragma unroll
       for (int i = 0; i < 16; ++i) s[i] = 0.0f;
@@ -128,27 +141,38 @@ __global__ __launch_bounds__(256) void attn_flash_kernel(
 #pragma unroll
       for (int i = 1; i < 16; ++i) mloc = fmaxf(mloc, s[i]);
       mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-      const float m_new = fmaxf(m_run, mloc);
-      const float m_use = m_new == -INFINITY ? 0.0f : m_new;  // fully masked so far
-      // v_exp_f32 directly: every argument is <= 0 (or -inf -> 0), where the
-      // hardware exp2 is accurate to about 1 ulp; results below 2^-126 flush
-      // to zero, far under the weight of any unmasked key.
-      const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+      // Lazy rescaling: m_run is the softmax reference, not necessarily the
+      // running maximum.  It moves (and O, l are rescaled) only when a lane's
+      // maximum exceeds it by more than kLazy (log2 units), so p <= 2^kLazy
+      // and the sums stay far from overflow; softmax is invariant to the
+      // reference, so O / l is unchanged.  Most tiles skip the rescale and the
+      // PV products chain straight onto the previous tile's.
+      const bool move = mloc > m_run + kLazy;  // false while the lane is fully masked
+      if (__builtin_amdgcn_read_exec() & __ballot(move)) {
+        const float m_new = move ? mloc : m_run;
+        // lanes that keep their reference multiply by exactly 1
+        const float alpha = move ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
+        l_run *= alpha;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          o0[i] *= alpha;
+          o1[i] *= alpha;
+        }
+        m_run = m_new;
+      }
+      const float m_use = m_run == -INFINITY ? 0.0f : m_run;  // fully masked so far
+      // v_exp_f32 directly: every argument is <= kLazy (or -inf -> 0), where
+      // the hardware exp2 is accurate to about 1 ulp; results below 2^-126
+      // flush to zero, far under the weight of any unmasked key.
       float psum = 0.0f;
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         s[i] = __builtin_amdgcn_exp2f(s[i] - m_use);
         psum += s[i];
       }
-      l_run = l_run * alpha + psum;
-      m_run = m_new;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        o0[i] *= alpha;
-        o1[i] *= alpha;
-      }
+      l_run += psum;
       // O^T += V^T P^T: register i supplies k index key_h(i) for lane half h.
-      const float* vt = Vs + (buf * kKT + ks * 32) * kLD;
+      const float* vt = Vs + (buf * KT + ks * 32) * kLD;
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const float* vrow = vt + ((i >> 2) * 8 + h * 4 + (i & 3)) * kLD;
@@ -160,42 +184,61 @@ __global__ __launch_bounds__(256) void attn_flash_kernel(
     __syncthreads();
   }
 
-  // Merge the key halves: ks = 1 publishes (m, l, O^T) per lane, ks = 0 combines.
-  float* xch = lds + qs * (64 * 34);  // per query sub-tile: 64 lanes x (32 O + m + l)
+  // Merge the key parts: ks > 0 publish (m, l, O^T) per lane, ks = 0 combines
+  // them in part order.
   const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
-  if (ks == 1) {
+  float* xch = lds + qs * ((KS - 1) * 64 * 34);  // per query sub-tile
+  if (ks > 0) {
+    float* mine = xch + (ks - 1) * (64 * 34);
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      xch[i * 64 + lane] = o0[i];
-      xch[(16 + i) * 64 + lane] = o1[i];
+      mine[i * 64 + lane] = o0[i];
+      mine[(16 + i) * 64 + lane] = o1[i];
     }
-    xch[32 * 64 + lane] = m_run;
-    xch[33 * 64 + lane] = l_tot;
+    mine[32 * 64 + lane] = m_run;
+    mine[33 * 64 + lane] = l_tot;
   }
   __syncthreads();
-  float* ot = lds + 2 * (64 * 34) + qs * (32 * kLD);  // transposed output tile [32 q][kLD]
+  float* otile = lds + 2 * (KS - 1) * 64 * 34;    // transposed output tiles [2][32 q][kLD]
+  float* ot = otile + qs * (32 * kLD);
   if (ks == 0) {
-    const float m1 = xch[32 * 64 + lane], l1 = xch[33 * 64 + lane];
-    const float m = fmaxf(m_run, m1);
-    const float a0 = exp2f(m_run - m), a1 = exp2f(m1 - m);
-    const float inv = 1.0f / (l_tot * a0 + l1 * a1);
+    float m = m_run;
+#pragma unroll
+    for (int p = 0; p < KS - 1; ++p) m = fmaxf(m, xch[p * (64 * 34) + 32 * 64 + lane]);
+    const float a0 = exp2f(m_run - m);
+    float l = l_tot * a0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      o0[i] *= a0;
+      o1[i] *= a0;
+    }
+#pragma unroll
+    for (int p = 0; p < KS - 1; ++p) {
+      const float* other = xch + p * (64 * 34);
+      const float ap = exp2f(other[32 * 64 + lane] - m);
+      l += other[33 * 64 + lane] * ap;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        o0[i] += other[i * 64 + lane] * ap;
+        o1[i] += other[(16 + i) * 64 + lane] * ap;
+      }
+    }
+    const float inv = 1.0f / l;
     // register i of tile t is channel t*32 + (i/4)*8 + h*4 + i%4 of query r
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int d = (i >> 2) * 8 + h * 4 + (i & 3);
-      ot[r * kLD + d] = (o0[i] * a0 + xch[i * 64 + lane] * a1) * inv;
-      ot[r * kLD + 32 + d] = (o1[i] * a0 + xch[(16 + i) * 64 + lane] * a1) * inv;
+      ot[r * kLD + d] = o0[i] * inv;
+      ot[r * kLD + 32 + d] = o1[i] * inv;
     }
   }
   __syncthreads();
   // coalesced store of both sub-tiles: 64 queries x 16 float4
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int idx = tid + 256 * j;
+  for (int idx = tid; idx < kQT * 16; idx += NT) {
     const int row = idx >> 4, c = (idx & 15) * 4;  // row 0..63 = qs*32 + local row
     const int qi = qt0 + row;
     if (qi < Tq) {
-      const float* src = lds + 2 * (64 * 34) + (row >> 5) * (32 * kLD) + (row & 31) * kLD + c;
+      const float* src = otile + (row >> 5) * (32 * kLD) + (row & 31) * kLD + c;
       *reinterpret_cast<floatx4*>(o + ((long)b * Tq + qi) * ldo + head * kHD + c) =
           *reinterpret_cast<const floatx4*>(src);
     }
@@ -226,19 +269,24 @@ extern "C" int lx_attention_f32(const float* q, int ldq, const float* k, int ldk
   LX_REQUIRE(q_offset >= 0, "attention: q_offset < 0");
   if (causal) LX_REQUIRE(q_offset + Tq <= Tk, "attention: causal needs q_offset + Tq <= Tk");
   const int rep = n_heads / n_kv_heads;
+  dim3 grid((Tq + kQT - 1) / kQT, n_heads, B);
+  const float log2e = 1.4426950408889634f;
+  // Two key parts (4 waves, 64-key tiles).  Four parts (8 waves on 128-key
+  // tiles, two waves per SIMD even with one workgroup per CU) measured slower
+  // on MI355X for the DiT at T = 500 (26.3 vs 24.8 us) and the Qwen2 prefill
+  // (14.8 vs 14.4 us), and equal at T = 3000.
+  constexpr int KS = 2;
   static bool attr_set = false;
   if (!attr_set) {
-    if (hipFuncSetAttribute((const void*)attn_flash_kernel,
+    if (hipFuncSetAttribute((const void*)attn_flash_kernel<KS>,
                             hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)kFlashLds) != hipSuccess) {
-      set_error("attention: cannot raise the LDS limit to %zu bytes", kFlashLds);
+                            (int)flash_lds<KS>()) != hipSuccess) {
+      set_error("attention: cannot raise the LDS limit to %zu bytes", flash_lds<KS>());
       return LX_ERR_LAUNCH;
     }
     attr_set = true;
   }
-  dim3 grid((Tq + kQT - 1) / kQT, n_heads, B);
-  const float log2e = 1.4426950408889634f;
-  hipLaunchKernelGGL(attn_flash_kernel, grid, dim3(256), kFlashLds, stream, q, ldq, k, ldk, v,
-                     ldv, o, ldo, Tq, Tk, rep, scale * log2e, causal, q_offset);
+  hipLaunchKernelGGL(attn_flash_kernel<KS>, grid, dim3(128 * KS), flash_lds<KS>(), stream, q, ldq,
+                     k, ldk, v, ldv, o, ldo, Tq, Tk, rep, scale * log2e, causal, q_offset);
   return check_launch("attn_flash_kernel");
 }

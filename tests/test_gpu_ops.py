@@ -291,6 +291,31 @@ def test_attention_dit(gpu, ops, B, T):
     assert orc.rel_err(o, ref) < TOL
 
 
+@pytest.mark.parametrize("slope,causal", [(0.05, False), (0.15, False), (0.15, True),
+                                          (-0.15, False)])
+def test_attention_reference_moves(gpu, ops, slope, causal):
+    """Scores that ramp along the keys: the softmax reference of the online
+    pass moves on every 64-key tile (slope 0.15 gives ~14 log2 units per
+    tile, above the 8-unit slack), drifts by less than its slack per tile
+    (0.05: ~4.6), or never moves after the first tile (falling scores).  The
+    logits stay below ~100 so that the fp32 q.k itself (absolute error about
+    |q.k| 2^-24 sqrt(64)) stays well inside the tolerance."""
+    announce(f"attention ramp slope={slope} causal={causal}")
+    B, T, D = 1, 700, 1024
+    qkv = rnd((B, T, 3 * D), 7, 0.2)
+    # every head's q carries a fixed direction u; key j carries slope * j * u
+    u = np.zeros(64, np.float32)
+    u[:8] = 1.0 / np.sqrt(8.0)
+    for hh in range(16):
+        qkv[0, :, hh * 64:(hh + 1) * 64] += 8.0 * u
+        qkv[0, :, D + hh * 64:D + (hh + 1) * 64] += (slope * np.arange(T, dtype=np.float32))[:, None] * u
+    qd = dev(qkv, gpu)
+    o = ops.attention(qd[..., :D], qd[..., D:2 * D], qd[..., 2 * D:], 16, causal=causal).cpu().numpy()
+    ref = orc.attention(qkv[..., :D], qkv[..., D:2 * D], qkv[..., 2 * D:], 16, causal=causal)
+    assert np.isfinite(o).all()
+    assert orc.rel_err(o, ref) < TOL
+
+
 @pytest.mark.parametrize("Tq,Tk,off", [(256, 256, 0), (37, 37, 0), (5, 300, 295), (1, 2048, 2047)])
 def test_attention_qwen_causal_gqa(gpu, ops, Tq, Tk, off):
     announce(f"attention qwen Tq={Tq} Tk={Tk}")
