@@ -24,7 +24,7 @@ struct Table {
   float v[N];
 };
 
-constexpr int kGatherChunk = 240;  // ids per launch: 960 bytes of kernel arguments
+constexpr int kGatherChunk = 960;  // ids per launch: 3840 of the 4096 bytes of kernel arguments
 struct IdChunk {
   int id[kGatherChunk];
 };
