@@ -314,7 +314,9 @@ typedef struct lx_qwen2 lx_qwen2;
 
 /* Replaces LLM::load's weight upload (src/llm/llm.cpp:50-61); the tables are
  * referenced, the layer weights re-packed (QKV fused, gate/up interleaved).
- * max_ctx bounds prompt + generated tokens (KV cache capacity). */
+ * max_ctx bounds prompt + generated tokens (KV cache capacity), 1..4096.
+ * Geometry: head_dim 64, hidden <= 2048, intermediate <= 6144, at most 8
+ * query heads per kv head (Qwen2-0.5B: 896 / 4864 / 14:2); else LX_ERR_ARG. */
 int lx_qwen2_create(const lx_qwen2_weights* w, int max_ctx, lx_qwen2** out);
 void lx_qwen2_destroy(lx_qwen2* m);
 
@@ -335,7 +337,12 @@ int lx_qwen2_prefill(lx_qwen2* m, const float* lm_input, int L, float* logits,
 
 /* LLM::decode (src/llm/llm.cpp:218-327): one token (HOST id in
  * [0, speech_vocab)) at position cache_len, appends to the device KV cache.
- * logits: device (speech_vocab); final_norm: device (H) or NULL. */
+ * logits: device (speech_vocab); final_norm: device (H) or NULL.
+ * The position lives in device memory, so the layer stack is captured into a
+ * HIP graph on the first decode (on a stream of the object's own) and
+ * replayed on `stream` for every later token; with LX_DECODE_GRAPH=0 in the
+ * environment at create time it is launched eagerly instead.  Calls on one
+ * object must not overlap. */
 int lx_qwen2_decode(lx_qwen2* m, int token, float* logits, float* final_norm,
                     hipStream_t stream);
 
