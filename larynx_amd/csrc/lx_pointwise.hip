@@ -57,7 +57,7 @@ __global__ __launch_bounds__(kEwBlock) void gelu_kernel(const float* h, float* y
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       const long i = min(i0 + (long)u * kEwBlock, n4 - 1);
-      v[u] = reinterpret_cast<const float4*>(h)[i];
+      v[u] = ld_nt(reinterpret_cast<const float4*>(h) + i);
     }
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
@@ -68,7 +68,7 @@ __global__ __launch_bounds__(kEwBlock) void gelu_kernel(const float* h, float* y
         o.y = gelu_tanh(v[u].y);
         o.z = gelu_tanh(v[u].z);
         o.w = gelu_tanh(v[u].w);
-        reinterpret_cast<float4*>(y)[i] = o;
+        st_nt(reinterpret_cast<float4*>(y) + i, o);
       }
     }
   }
@@ -77,32 +77,32 @@ __global__ __launch_bounds__(kEwBlock) void gelu_kernel(const float* h, float* y
   if (t < n) y[t] = gelu_tanh(h[t]);
 }
 
+// x[row, :] += gate[row / T, :] * y[row, :].  Threads own float4 columns and
+// walk rows (kUnroll rows in flight per thread), so the gate float4 and the
+// batch index come from 32-bit row arithmetic, not a division per element.
 __global__ __launch_bounds__(kEwBlock) void gated_residual_kernel(
     float* x, const float* __restrict__ y, const float* __restrict__ gate, long gate_stride,
-    long rows, int T, int D4) {
-  const long n4 = rows * D4;
-  const long stride = (long)gridDim.x * kEwBlock * kUnroll;
-  for (long i0 = (long)blockIdx.x * kEwBlock * kUnroll + threadIdx.x; i0 < n4; i0 += stride) {
-    float4 a[kUnroll], v[kUnroll];
+    int rows, int T, int D4) {
+  for (int c4 = threadIdx.x; c4 < D4; c4 += kEwBlock) {
+    for (int r0 = blockIdx.x * kUnroll; r0 < rows; r0 += gridDim.x * kUnroll) {
+      float4 a[kUnroll], v[kUnroll];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const long i = min(i0 + (long)u * kEwBlock, n4 - 1);
-      a[u] = reinterpret_cast<const float4*>(x)[i];
-      v[u] = reinterpret_cast<const float4*>(y)[i];
-    }
+      for (int u = 0; u < kUnroll; ++u) {
+        const long i = (long)min(r0 + u, rows - 1) * D4 + c4;
+        a[u] = ld_nt(reinterpret_cast<const float4*>(x) + i);
+        v[u] = ld_nt(reinterpret_cast<const float4*>(y) + i);
+      }
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const long i = i0 + (long)u * kEwBlock;
-      if (i < n4) {
-        const long row = i / D4;
-        const int c4 = (int)(i - row * D4);
-        const int b = (int)(row / T);
-        const float4 g = reinterpret_cast<const float4*>(gate + (long)b * gate_stride)[c4];
-        a[u].x += v[u].x * g.x;
-        a[u].y += v[u].y * g.y;
-        a[u].z += v[u].z * g.z;
-        a[u].w += v[u].w * g.w;
-        reinterpret_cast<float4*>(x)[i] = a[u];
+      for (int u = 0; u < kUnroll; ++u) {
+        const int row = r0 + u;
+        if (row < rows) {
+          const float4 g = reinterpret_cast<const float4*>(gate + (long)(row / T) * gate_stride)[c4];
+          a[u].x += v[u].x * g.x;
+          a[u].y += v[u].y * g.y;
+          a[u].z += v[u].z * g.z;
+          a[u].w += v[u].w * g.w;
+          st_nt(reinterpret_cast<float4*>(x) + (long)row * D4 + c4, a[u]);
+        }
       }
     }
   }
@@ -119,8 +119,8 @@ __global__ __launch_bounds__(kEwBlock) void swiglu_kernel(const float* __restric
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       const long i = min(i0 + (long)u * kEwBlock, n4 - 1);
-      g[u] = reinterpret_cast<const float4*>(gate)[i];
-      u4[u] = reinterpret_cast<const float4*>(up)[i];
+      g[u] = ld_nt(reinterpret_cast<const float4*>(gate) + i);
+      u4[u] = ld_nt(reinterpret_cast<const float4*>(up) + i);
     }
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
@@ -131,7 +131,7 @@ __global__ __launch_bounds__(kEwBlock) void swiglu_kernel(const float* __restric
         o.y = silu_mul(g[u].y, u4[u].y);
         o.z = silu_mul(g[u].z, u4[u].z);
         o.w = silu_mul(g[u].w, u4[u].w);
-        reinterpret_cast<float4*>(out)[i] = o;
+        st_nt(reinterpret_cast<float4*>(out) + i, o);
       }
     }
   }
@@ -139,10 +139,10 @@ __global__ __launch_bounds__(kEwBlock) void swiglu_kernel(const float* __restric
   if (t < n) out[t] = silu_mul(gate[t], up[t]);
 }
 
-// Partial interleaved rotary: thread = (row, pair).  blockIdx.y selects q / k.
+// Partial interleaved rotary: thread = (row, pair); one sincos per pair serves
+// both q and k (same position).
 __global__ void rope_partial_kernel(float* q, float* k, const int* __restrict__ pos,
                                     long rows, int T, int ld, int half, Table<64> inv) {
-  float* base = blockIdx.y == 0 ? q : k;
   const long n = rows * half;
   const long stride = (long)gridDim.x * blockDim.x;
   for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
@@ -152,12 +152,12 @@ __global__ void rope_partial_kernel(float* q, float* k, const int* __restrict__ 
     float ang = (float)pos[t] * inv.v[p];
     float s, c;
     sincosf(ang, &s, &c);
-    float2* ptr = reinterpret_cast<float2*>(base + row * ld) + p;
-    float2 x = *ptr;
-    float2 o;
-    o.x = x.x * c - x.y * s;
-    o.y = x.y * c + x.x * s;
-    *ptr = o;
+    float2* pq = reinterpret_cast<float2*>(q + row * ld) + p;
+    float2* pk = k ? reinterpret_cast<float2*>(k + row * ld) + p : nullptr;
+    float2 xq = ld_nt(pq);
+    float2 xk = k ? ld_nt(pk) : make_float2(0.f, 0.f);
+    st_nt(pq, make_float2(xq.x * c - xq.y * s, xq.y * c + xq.x * s));
+    if (k) st_nt(pk, make_float2(xk.x * c - xk.y * s, xk.y * c + xk.x * s));
   }
 }
 
@@ -176,9 +176,9 @@ __global__ void rope_neox_kernel(float* qk, const int* __restrict__ pos, long ro
     float s, c;
     sincosf(ang, &s, &c);
     float* ptr = qk + row * ld + h * hd + p;
-    float x0 = ptr[0], x1 = ptr[half];
-    ptr[0] = x0 * c - x1 * s;
-    ptr[half] = x1 * c + x0 * s;
+    float x0 = __builtin_nontemporal_load(ptr), x1 = __builtin_nontemporal_load(ptr + half);
+    __builtin_nontemporal_store(x0 * c - x1 * s, ptr);
+    __builtin_nontemporal_store(x1 * c + x0 * s, ptr + half);
   }
 }
 
@@ -200,7 +200,7 @@ __global__ void gather_kernel4(const float4* __restrict__ table, int D4, IdChunk
                                float4* out) {
   const float4* src = table + (long)ids.id[blockIdx.x] * D4;
   float4* dst = out + (long)blockIdx.x * D4;
-  for (int i = threadIdx.x; i < D4; i += blockDim.x) dst[i] = src[i];
+  for (int i = threadIdx.x; i < D4; i += blockDim.x) st_nt(dst + i, ld_nt(src + i));
 }
 
 __global__ void gather_kernel1(const float* __restrict__ table, int D, IdChunk ids,
@@ -232,9 +232,13 @@ extern "C" int lx_gated_residual_f32(float* x, const float* y, const float* gate
   LX_REQUIRE(gate_stride >= D && gate_stride % 4 == 0, "gated_residual: bad gate_stride");
   LX_REQUIRE(((uintptr_t)x | (uintptr_t)y | (uintptr_t)gate) % 16 == 0,
              "gated_residual: pointers must be 16-byte aligned");
-  long rows = (long)B * T;
-  hipLaunchKernelGGL(gated_residual_kernel, dim3(ew_grid(rows * D / 4)), dim3(kEwBlock), 0,
-                     stream, x, y, gate, gate_stride, rows, T, D / 4);
+  LX_REQUIRE((long)B * T * (D / 4) < (1L << 31), "gated_residual: too many elements");
+  const int rows = B * T;
+  // kUnroll rows per block pass; D/4 columns over the block's threads
+  long g = (rows + kUnroll - 1) / kUnroll;
+  if (g > 8192) g = 8192;
+  hipLaunchKernelGGL(gated_residual_kernel, dim3((unsigned)g), dim3(kEwBlock), 0, stream, x, y,
+                     gate, gate_stride, rows, T, D / 4);
   return check_launch("gated_residual_kernel");
 }
 
@@ -264,7 +268,7 @@ extern "C" int lx_rope_partial_interleaved_f32(float* q, float* k, const int* po
   rope_inv_freq(base, rot_dim, inv.v);
   long rows = (long)B * T;
   int half = rot_dim / 2;
-  dim3 grid(grid_for(rows * half, 256), k ? 2 : 1);
+  dim3 grid(grid_for(rows * half, 256));
   hipLaunchKernelGGL(rope_partial_kernel, grid, dim3(256), 0, stream, q, k, pos, rows, T, ld,
                      half, inv);
   return check_launch("rope_partial_kernel");

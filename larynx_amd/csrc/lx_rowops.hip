@@ -3,8 +3,9 @@
 // One wave64 owns one row.  The row is read once into registers (float4 per
 // lane per 256 channels), mean and centred variance are two shuffle
 // reductions over those registers, and the output is written once: one HBM
-// read + one HBM write per element.  The (1 + scale) / shift vectors of the
-// block's batch are staged in LDS once per workgroup.
+// read + one HBM write per element, both with the streaming cache policy.
+// The (1 + scale) / shift vectors of the block's batch are staged in LDS once
+// per workgroup.
 #include "lx_common.hpp"
 
 namespace lx {
@@ -33,7 +34,7 @@ __global__ __launch_bounds__(kRowsPerBlock * kWave) void adaln_kernel(
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
     int i = lane + j * kWave;
-    v[j] = i < D4 ? xr[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    v[j] = i < D4 ? ld_nt(xr + i) : make_float4(0.f, 0.f, 0.f, 0.f);
   }
   const int b_first = row0 / T;
   const int last_row = min(row0 + kRowsPerBlock, rows) - 1;
@@ -79,7 +80,7 @@ __global__ __launch_bounds__(kRowsPerBlock * kWave) void adaln_kernel(
       o.y = ((v[j].y - mean) * rstd) * m.y + h.y;
       o.z = ((v[j].z - mean) * rstd) * m.z + h.z;
       o.w = ((v[j].w - mean) * rstd) * m.w + h.w;
-      yr[i] = o;
+      st_nt(yr + i, o);
     }
   }
 }
@@ -98,7 +99,7 @@ __global__ __launch_bounds__(kRowsPerBlock * kWave) void rmsnorm_kernel(
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
     int i = lane + j * kWave;
-    v[j] = i < D4 ? xr[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    v[j] = i < D4 ? ld_nt(xr + i) : make_float4(0.f, 0.f, 0.f, 0.f);
   }
   for (int i = threadIdx.x; i < D4; i += blockDim.x)
     reinterpret_cast<float4*>(smem)[i] = reinterpret_cast<const float4*>(w)[i];
@@ -121,7 +122,7 @@ __global__ __launch_bounds__(kRowsPerBlock * kWave) void rmsnorm_kernel(
       o.y = (v[j].y * r) * g.y;
       o.z = (v[j].z * r) * g.z;
       o.w = (v[j].w * r) * g.w;
-      yr[i] = o;
+      st_nt(yr + i, o);
     }
   }
 }

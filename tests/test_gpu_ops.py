@@ -102,6 +102,21 @@ def test_gelu(gpu, ops, n):
     assert orc.rel_err(y, orc.gelu_tanh(h)) < TOL
 
 
+def test_gelu_wide_range(gpu, ops):
+    """Saturated tails (e^(-2u) overflowing to inf, or vanishing) and the region
+    around 0, where the exp/reciprocal form of the tanh identity is evaluated."""
+    announce("gelu wide range")
+    h = np.concatenate([np.linspace(-60, 60, 24001, dtype=np.float32),
+                        np.array([0.0, -0.0, 1e-30, -1e-30, 1e-6, -1e-6], np.float32)])
+    y = ops.gelu_tanh(dev(h, gpu)).cpu().numpy()
+    ref = orc.gelu_tanh(h)
+    assert np.all(np.isfinite(y))
+    assert orc.rel_err(y, ref) < TOL
+    # elementwise, relative to the local scale: the small-|x| region is not hidden
+    # by the tails' large values
+    assert np.max(np.abs(y - ref) / np.maximum(np.abs(ref), 1e-3)) < 1e-4
+
+
 @pytest.mark.parametrize("T", [500, 3000, 5])
 def test_gated_residual(gpu, ops, T):
     announce(f"gated_residual T={T}")
