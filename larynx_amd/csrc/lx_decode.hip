@@ -66,7 +66,9 @@ __global__ __launch_bounds__(256) void dec_gemv_kernel(DecGemvArgs a) {
   // it does not wait for the weight stream (loads retire in order)
   float inv_lane = 0.0f;
   if (EPI == DEC_QKV_ROPE) inv_lane = a.inv_freq[lane & 31];
-  // weight stream first: every load of the wave's rows in flight together.
+  // weight stream first: every load of the wave's rows in flight together,
+  // with the streaming cache policy (1.46 GB of weights per token cannot stay
+  // cached).
   // Loads are unconditional (row and k clamped into the matrix) so none of
   // them waits behind a branch; lanes past K see x = 0, rows past N are
   // discarded.
@@ -76,7 +78,7 @@ __global__ __launch_bounds__(256) void dec_gemv_kernel(DecGemvArgs a) {
   for (int r = 0; r < R; ++r)
 #pragma unroll
     for (int j = 0; j < NL; ++j)
-      w[r][j] = W4[min(rows[r], a.N - 1) * K4 + min(lane + j * 64, K4 - 1)];
+      w[r][j] = ld_nt(W4 + min(rows[r], a.N - 1) * K4 + min(lane + j * 64, K4 - 1));
   // everything the epilogue reads is requested before the first wait
   int pos = 0;
   if (EPI == DEC_QKV_ROPE) pos = *a.pos;

@@ -35,12 +35,13 @@ __global__ __launch_bounds__(kGemvWaves * kWave) void gemv_kernel(
     for (int r = 0; r < kGemvRows; ++r)
 #pragma unroll
       for (int b = 0; b < kGemvBMax; ++b) acc[r][b] = 0.0f;
-#pragma unroll 2
+#pragma unroll 4
     for (int k4 = lane; k4 < K4; k4 += kWave) {
       float4 w[kGemvRows];
+      // weights are read exactly once per call: streaming cache policy
 #pragma unroll
       for (int r = 0; r < kGemvRows; ++r)
-        w[r] = (n0 + r < N) ? reinterpret_cast<const float4*>(W + (n0 + r) * K)[k4]
+        w[r] = (n0 + r < N) ? ld_nt(reinterpret_cast<const float4*>(W + (n0 + r) * K) + k4)
                             : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
       for (int b = 0; b < kGemvBMax; ++b) {
