@@ -15,6 +15,8 @@ Also reported on the same JSON line:
   fused_ops     achieved HBM GB/s of every fused op at the configs' shapes, with
                 each launch on a distinct buffer set (> 256 MB rotation, so the
                 MALL does not serve the reads);
+  flow_infer    the whole FlowDecoder inference of a 10 s utterance (frontend +
+                10 Euler steps), host token ids in, output mel frames out;
   cpu_baseline  the CPU oracle's Euler step on this host's cores (bounded sample).
 
 Usage: python bench.py [--steps K] [--warmup W] [--T 500] [--no-cpu]
@@ -42,6 +44,8 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-fused", action="store_true", help="skip the fused-op GB/s sweep")
     ap.add_argument("--no-llm", action="store_true", help="skip the Qwen2 prefill/decode timing")
+    ap.add_argument("--no-flow", action="store_true",
+                    help="skip the whole-utterance FlowDecoder inference timing")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only launch the dominant GEMM (QKV + rotary, T=500) and a plain "
                          "device copy of known size, for rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE")
@@ -285,6 +289,33 @@ def long_utterance(torch, est, dev, g, steps=3):
     return {"T": T, "ms_per_step": round(ms, 3), "mel_frames_per_s": round(T / ms * 1e3, 1)}
 
 
+def flow_infer(torch, dev, g, dit_params, n_prompt=50, n_tokens=200, prompt_frames=100):
+    """Whole FlowDecoder::infer of a 10 s utterance (250 tokens -> 500 mel frames,
+    100 prompt frames): frontend + 10 CFG Euler steps + output copy, host token
+    ids in, mel frames past the prompt out."""
+    from larynx_amd.flow import FlowDecoder, flow_frontend_param_shapes
+    front = {n: torch.randn(*sh, device=dev, generator=g) * 0.02
+             for n, sh in flow_frontend_param_shapes()}
+    dec = FlowDecoder(front, dit_params, max_tokens=n_prompt + n_tokens)
+    pt = torch.randint(0, 6561, (n_prompt,), generator=g, device=dev).cpu().tolist()
+    tk = torch.randint(0, 6561, (n_tokens,), generator=g, device=dev).cpu().tolist()
+    MT = 2 * (n_prompt + n_tokens)
+    pf = torch.randn(prompt_frames, 80, device=dev, generator=g)
+    spk = torch.randn(192, device=dev, generator=g)
+    z = torch.randn(80, MT, device=dev, generator=g)
+    dec.infer(pt, tk, pf, spk, z)
+    torch.cuda.synchronize()
+    n = 3
+    t0 = time.perf_counter()
+    for _ in range(n):
+        dec.infer(pt, tk, pf, spk, z)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / n
+    dec.close()
+    return {"tokens": n_prompt + n_tokens, "mel_frames": MT, "prompt_frames": prompt_frames,
+            "ms": round(ms, 3), "out_mel_frames_per_s": round((MT - prompt_frames) / ms * 1e3, 1)}
+
+
 def qwen2_lm(torch, dev, g):
     """Qwen2-0.5B (24 layers, full vocabularies): prefill at L=256 (160 text + 96
     speech-prompt rows) and single-token decode against KV caches of 1 / 256 / 1024 /
@@ -431,7 +462,7 @@ def main():
     for name, shape in dit_param_shapes(cfg):
         params[name] = torch.randn(*shape, device=dev, generator=g) * 0.02
     est = DiTEstimator(params, cfg, B=2, max_T=max(T, 3000))
-    del params
+    dit_params = params
     x = torch.randn(80, T, device=dev, generator=g)
     mu = torch.randn(80, T, device=dev, generator=g)
     cond = torch.randn(80, T, device=dev, generator=g)
@@ -478,6 +509,8 @@ def main():
                 "avg_us": round(dom["avg_us"], 2), "flop_per_launch": dom["flop"]}
     gemm_flop_step = 22 * sum(k["flop"] for k in kernels.values())
     long_t = long_utterance(torch, est, dev, g)
+    flow = None if args.no_flow else flow_infer(torch, dev, g, dit_params)
+    del dit_params, params
     fused = {} if args.no_fused else fused_ops_gbs(torch, ops, dev)
     est.close()
     qwen = None if args.no_llm else qwen2_lm(torch, dev, g)
@@ -509,6 +542,7 @@ def main():
         "kernels": {k: {kk: round(vv, 2) for kk, vv in v.items() if kk in
                         ("avg_us", "tflops", "hipblaslt_us")} for k, v in kernels.items()},
         "long_utterance": long_t,
+        "flow_infer": flow,
         "qwen2": qwen,
         "fused_ops": {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv)
                           for kk, vv in v.items()} for k, v in fused.items()},

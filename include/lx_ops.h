@@ -285,6 +285,55 @@ int lx_cfm_step(lx_dit* dit, float* x, const float* mu, const float* cond,
                 hipStream_t stream);
 
 /* ------------------------------------------------------------------------ */
+/* Flow decoder: frontend + estimator + CFM (FlowDecoder::infer)             */
+/* ------------------------------------------------------------------------ */
+
+/* Frontend weights, torch layouts, device pointers.  Mirrors the frontend
+ * tensors of FlowWeights (src/flow/internal.h:49-57; GGUF names
+ * input_embedding.weight, spk_embed_affine_layer.*, pre_lookahead_layer.*,
+ * src/flow/gguf.cpp:45-53). */
+typedef struct lx_flow_frontend_weights {
+  int vocab;      /* 6561 speech tokens                        */
+  int spk_in;     /* 192: speaker embedding width (<= 1024)    */
+  int channels;   /* 1024: PreLookahead conv1 output channels  */
+  const float* input_embedding;                          /* (vocab, mel)        */
+  const float* spk_affine_w; const float* spk_affine_b;  /* (mel, spk_in), (mel)*/
+  const float* pre_conv1_w; const float* pre_conv1_b;    /* (channels, mel, 4)  */
+  const float* pre_conv2_w; const float* pre_conv2_b;    /* (mel, channels, 3)  */
+} lx_flow_frontend_weights;
+
+typedef struct lx_flow lx_flow;
+
+/* FlowDecoder::load equivalent over already-resident weights: builds the
+ * frontend (weights re-packed for the im2col GEMMs) and a B = 2 estimator for
+ * up to max_tokens speech tokens (MEL_T = 2 * max_tokens frames).  Replaces
+ * FlowDecoder::load (src/flow/flow.cpp:49-61) minus the GGUF file read. */
+int lx_flow_create(const lx_dit_weights* dit, const lx_flow_frontend_weights* fw,
+                   int max_tokens, lx_flow** out);
+void lx_flow_destroy(lx_flow* flow);
+
+/* FlowDebug pre-DiT stages (include/larynx/flow/flow.h:15-22); NULL disables
+ * each: spk (mel), token_embed (Tseq, mel), prelookahead (Tseq, mel),
+ * mu (mel, MEL_T), cond (mel, MEL_T). */
+typedef struct lx_flow_capture {
+  float* spk; float* token_embed; float* prelookahead; float* mu; float* cond;
+} lx_flow_capture;
+int lx_flow_set_capture(lx_flow* flow, const lx_flow_capture* cap);
+
+/* FlowDecoder::infer (src/flow/flow.cpp:111-290, finalize = true):
+ *   prompt_tokens[n_prompt], tokens[n_tokens]: HOST speech token ids; negative
+ *     ids are clamped to 0 as the reference does, ids >= vocab -> LX_ERR_RANGE;
+ *   prompt_feat: (mel_len1, mel) prompt mel frames; spk_embedding: (spk_in);
+ *   noise_z: (mel, MEL_T) CFM start noise, MEL_T = 2 (n_prompt + n_tokens);
+ *   mel: out, (mel, MEL_T - mel_len1).
+ * Frontend (spk affine, token gather, PreLookahead, mu/cond) then the 10-step
+ * CFG Euler solve.  mel_len1 must be below MEL_T. */
+int lx_flow_infer(lx_flow* flow, const int32_t* prompt_tokens, int n_prompt,
+                  const int32_t* tokens, int n_tokens, const float* prompt_feat, int mel_len1,
+                  const float* spk_embedding, const float* noise_z, float* mel,
+                  hipStream_t stream);
+
+/* ------------------------------------------------------------------------ */
 /* Qwen2 LM (host C++ over the ops above; device-resident KV cache)          */
 /* ------------------------------------------------------------------------ */
 

@@ -76,6 +76,16 @@ class DitCapture(C.Structure):
                 ("time_embed", "input_proj", "conv_pos", "input_embed", "blocks", "norm_out")]
 
 
+class FlowFrontendWeights(C.Structure):
+    _fields_ = [("vocab", C.c_int), ("spk_in", C.c_int), ("channels", C.c_int)] + [
+        (n, fp) for n in ("input_embedding", "spk_affine_w", "spk_affine_b", "pre_conv1_w",
+                          "pre_conv1_b", "pre_conv2_w", "pre_conv2_b")]
+
+
+class FlowCapture(C.Structure):
+    _fields_ = [(n, fp) for n in ("spk", "token_embed", "prelookahead", "mu", "cond")]
+
+
 _QWEN_LAYER_FIELDS = ["q_w", "q_b", "k_w", "k_b", "v_w", "v_b", "o_w", "gate_w", "up_w",
                       "down_w", "in_norm", "post_norm"]
 
@@ -133,6 +143,12 @@ SIGNATURES = [
      [C.c_void_p, fp, fp, fp, fp, C.c_int, C.c_int, C.c_float, stream_t]),
     ("lx_cfm_step", C.c_int,
      [C.c_void_p, fp, fp, fp, fp, C.c_int, C.c_float, C.c_float, C.c_float, stream_t]),
+    ("lx_flow_create", C.c_int,
+     [C.POINTER(DitWeights), C.POINTER(FlowFrontendWeights), C.c_int, C.POINTER(C.c_void_p)]),
+    ("lx_flow_destroy", None, [C.c_void_p]),
+    ("lx_flow_set_capture", C.c_int, [C.c_void_p, C.POINTER(FlowCapture)]),
+    ("lx_flow_infer", C.c_int,
+     [C.c_void_p, ip, C.c_int, ip, C.c_int, fp, C.c_int, fp, fp, fp, stream_t]),
     ("lx_qwen2_create", C.c_int,
      [C.POINTER(Qwen2Weights), C.c_int, C.POINTER(C.c_void_p)]),
     ("lx_qwen2_destroy", None, [C.c_void_p]),

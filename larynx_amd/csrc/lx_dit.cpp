@@ -33,27 +33,6 @@ constexpr float kLnEps = 1e-6f;    // LN_EPS (src/flow/internal.h:34)
 constexpr float kRopeBase = 10000.0f;  // ROPE_FREQ_BASE (src/flow/internal.h:35)
 constexpr int kRotDim = 64;        // ROT_DIM (src/flow/internal.h:25)
 
-#define LX_TRY(expr)         \
-  do {                       \
-    int _rc = (expr);        \
-    if (_rc != LX_OK) return _rc; \
-  } while (0)
-
-struct Arena {
-  std::vector<void*> ptrs;
-  ~Arena() {
-    for (void* p : ptrs) (void)hipFree(p);
-  }
-  template <typename T>
-  T* alloc(size_t n) {
-    void* p = nullptr;
-    if (n == 0) n = 1;
-    if (hipMalloc(&p, n * sizeof(T)) != hipSuccess) return nullptr;
-    ptrs.push_back(p);
-    return static_cast<T*>(p);
-  }
-};
-
 }  // namespace
 
 struct lx_dit {

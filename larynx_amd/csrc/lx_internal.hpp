@@ -2,9 +2,34 @@
 // host-side estimator / Qwen2 code.
 #pragma once
 
+#include <vector>
+
 #include "lx_common.hpp"
 
 namespace lx {
+
+// Device allocations of a composite object (lx_dit, lx_qwen2, lx_flow), made
+// at create time and released together when the object is destroyed.
+struct Arena {
+  std::vector<void*> ptrs;
+  ~Arena() {
+    for (void* p : ptrs) (void)hipFree(p);
+  }
+  template <typename T>
+  T* alloc(size_t n) {
+    void* p = nullptr;
+    if (n == 0) n = 1;
+    if (hipMalloc(&p, n * sizeof(T)) != hipSuccess) return nullptr;
+    ptrs.push_back(p);
+    return static_cast<T*>(p);
+  }
+};
+
+#define LX_TRY(expr)              \
+  do {                            \
+    int _rc = (expr);             \
+    if (_rc != LX_OK) return _rc; \
+  } while (0)
 
 // y[b, n] = act_out(sum_k W[n, k] * act_in(x[b, k]) + bias[n]); act: 0 none, 1 silu.
 int gemv(const float* x, int B, int K, const float* W, const float* bias, float* y, long N,
@@ -115,6 +140,19 @@ int dec_attention_max_ctx();  // largest cache the merge pass covers
 // x = table[row]; *d_pos = pos.
 int dec_begin(const float* table, long row, int D, float* x, int* d_pos, int pos,
               hipStream_t stream);
+
+// ---- flow frontend (lx_frontend.hip) ----
+// y[o] = W[o, :] . (x / sqrt(max(|x|^2, 1e-12))) + b[o]; x (K <= 1024), W (N, K).
+int flow_spk_affine(const float* x, int K, const float* W, const float* b, float* y, int N,
+                    hipStream_t s);
+// A[t, k*C + c] = f(x[t + k - pad_left, c]) (0 outside [0, T)); f = leaky_relu(0.01) if leaky.
+int flow_im2col(const float* x, int T, int C, int Kw, int pad_left, int leaky, float* A,
+                hipStream_t s);
+// mu[c, t'] = pre[t' / ratio, c]; cond[c, t'] = prompt_feat[t', c] (t' < mel_len1) else 0.
+int flow_pack_mu_cond(const float* pre, int Tseq, int ratio, const float* prompt_feat,
+                      int mel_len1, int mel, float* mu, float* cond, hipStream_t s);
+// Conv1d weight (OC, IC, K) -> (OC, K * IC) with column k * IC + ic.
+int conv_kmajor_pack(const float* w, int OC, int IC, int K, float* wp, hipStream_t s);
 
 // Grouped conv + Mish with tap-major packed weights (lx_conv_pos_mish_f32).
 int conv_pos_mish_packed(const float* x, const float* wp, const float* bias, const float* resid,

@@ -27,27 +27,6 @@ namespace {
 constexpr int kSosToken = 6561;     // SOS_TOKEN (src/llm/internal.h:33)
 constexpr int kTaskIdToken = 6563;  // TASK_ID_TOKEN (src/llm/internal.h:34)
 
-#define LX_TRY(expr)              \
-  do {                            \
-    int _rc = (expr);             \
-    if (_rc != LX_OK) return _rc; \
-  } while (0)
-
-struct Arena {
-  std::vector<void*> ptrs;
-  ~Arena() {
-    for (void* p : ptrs) (void)hipFree(p);
-  }
-  template <typename T>
-  T* alloc(size_t n) {
-    void* p = nullptr;
-    if (n == 0) n = 1;
-    if (hipMalloc(&p, n * sizeof(T)) != hipSuccess) return nullptr;
-    ptrs.push_back(p);
-    return static_cast<T*>(p);
-  }
-};
-
 struct Layer {
   float *qkv_w, *qkv_b, *o_w, *gu_w, *down_w, *in_norm, *post_norm;
   float *k_cache, *v_cache;  // (max_ctx, KV)

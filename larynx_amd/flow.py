@@ -11,7 +11,8 @@ from dataclasses import dataclass
 
 import torch
 
-from ._lib import DitBlockWeights, DitCapture, DitWeights, check, lib
+from ._lib import (DitBlockWeights, DitCapture, DitWeights, FlowCapture, FlowFrontendWeights,
+                   check, lib)
 from .ops import stream
 
 
@@ -88,6 +89,43 @@ def _ptr(params, name, shape):
     return C.c_void_p(t.data_ptr())
 
 
+_TOP_KEYS = {
+    "time_mlp_0_w": "time_embed.time_mlp.0.weight",
+    "time_mlp_0_b": "time_embed.time_mlp.0.bias",
+    "time_mlp_2_w": "time_embed.time_mlp.2.weight",
+    "time_mlp_2_b": "time_embed.time_mlp.2.bias",
+    "input_proj_w": "input_embed.proj.weight",
+    "input_proj_b": "input_embed.proj.bias",
+    "conv_pos_1_w": "input_embed.conv_pos_embed.conv1.0.weight",
+    "conv_pos_1_b": "input_embed.conv_pos_embed.conv1.0.bias",
+    "conv_pos_2_w": "input_embed.conv_pos_embed.conv2.0.weight",
+    "conv_pos_2_b": "input_embed.conv_pos_embed.conv2.0.bias",
+    "norm_out_w": "norm_out.linear.weight",
+    "norm_out_b": "norm_out.linear.bias",
+    "proj_out_w": "proj_out.weight",
+    "proj_out_b": "proj_out.bias",
+}
+
+
+def _dit_weights(params, cfg):
+    """lx_dit_weights over a dict of CUDA tensors (the block array is kept
+    alive as an attribute of the returned struct)."""
+    shapes = dict(dit_param_shapes(cfg))
+    blocks = (DitBlockWeights * cfg.depth)()
+    for i in range(cfg.depth):
+        for field, key in _BLOCK_KEYS.items():
+            name = f"transformer_blocks.{i}.{key}"
+            setattr(blocks[i], field, _ptr(params, name, shapes[name]))
+    w = DitWeights()
+    w.dim, w.depth, w.heads, w.head_dim = cfg.dim, cfg.depth, cfg.heads, cfg.head_dim
+    w.ff_inner, w.mel_dim = cfg.ff_inner, cfg.mel_dim
+    for field, name in _TOP_KEYS.items():
+        setattr(w, field, _ptr(params, name, shapes[name]))
+    w.blocks = blocks
+    w._keep = blocks
+    return w
+
+
 class DiTEstimator:
     """Device-resident DiT estimator for batches of B rows and up to max_T frames.
 
@@ -97,34 +135,7 @@ class DiTEstimator:
 
     def __init__(self, params, cfg: DiTConfig = DiTConfig(), B: int = 2, max_T: int = 500):
         self.cfg, self.B, self.max_T = cfg, B, max_T
-        shapes = dict(dit_param_shapes(cfg))
-        blocks = (DitBlockWeights * cfg.depth)()
-        for i in range(cfg.depth):
-            for field, key in _BLOCK_KEYS.items():
-                name = f"transformer_blocks.{i}.{key}"
-                setattr(blocks[i], field, _ptr(params, name, shapes[name]))
-        w = DitWeights()
-        w.dim, w.depth, w.heads, w.head_dim = cfg.dim, cfg.depth, cfg.heads, cfg.head_dim
-        w.ff_inner, w.mel_dim = cfg.ff_inner, cfg.mel_dim
-        top = {
-            "time_mlp_0_w": "time_embed.time_mlp.0.weight",
-            "time_mlp_0_b": "time_embed.time_mlp.0.bias",
-            "time_mlp_2_w": "time_embed.time_mlp.2.weight",
-            "time_mlp_2_b": "time_embed.time_mlp.2.bias",
-            "input_proj_w": "input_embed.proj.weight",
-            "input_proj_b": "input_embed.proj.bias",
-            "conv_pos_1_w": "input_embed.conv_pos_embed.conv1.0.weight",
-            "conv_pos_1_b": "input_embed.conv_pos_embed.conv1.0.bias",
-            "conv_pos_2_w": "input_embed.conv_pos_embed.conv2.0.weight",
-            "conv_pos_2_b": "input_embed.conv_pos_embed.conv2.0.bias",
-            "norm_out_w": "norm_out.linear.weight",
-            "norm_out_b": "norm_out.linear.bias",
-            "proj_out_w": "proj_out.weight",
-            "proj_out_b": "proj_out.bias",
-        }
-        for field, name in top.items():
-            setattr(w, field, _ptr(params, name, shapes[name]))
-        w.blocks = blocks
+        w = _dit_weights(params, cfg)
         torch.cuda.synchronize()  # parameters must be materialised before the copy stream
         h = C.c_void_p()
         check(lib.lx_dit_create(C.byref(w), B, max_T, C.byref(h)))
@@ -137,7 +148,10 @@ class DiTEstimator:
             self._h = None
 
     def __del__(self):
-        self.close()
+        try:
+            self.close()
+        except Exception:  # interpreter shutdown: the library may be gone already
+            pass
 
     @property
     def handle(self):
@@ -181,6 +195,116 @@ class DiTEstimator:
         check(lib.lx_cfm_solve(self._h, x.data_ptr(), mu.data_ptr(), cond.data_ptr(),
                                spks.data_ptr(), T, n_steps, float(cfg_rate), stream()))
         return x
+
+
+@dataclass(frozen=True)
+class FlowConfig:
+    """Frontend constants of src/flow/internal.h:19-29 (cosyvoice3.yaml)."""
+    vocab: int = 6561
+    spk_in: int = 192
+    channels: int = 1024
+    pre_lookahead: int = 3
+    token_mel_ratio: int = 2
+
+
+def flow_frontend_param_shapes(cfg: DiTConfig = DiTConfig(), fcfg: FlowConfig = FlowConfig()):
+    """Ordered (name, shape) list of the frontend parameters (torch layouts;
+    the GGUF names of src/flow/gguf.cpp:45-53)."""
+    mel = cfg.mel_dim
+    return [
+        ("input_embedding.weight", (fcfg.vocab, mel)),
+        ("spk_embed_affine_layer.weight", (mel, fcfg.spk_in)),
+        ("spk_embed_affine_layer.bias", (mel,)),
+        ("pre_lookahead_layer.conv1.weight", (fcfg.channels, mel, fcfg.pre_lookahead + 1)),
+        ("pre_lookahead_layer.conv1.bias", (fcfg.channels,)),
+        ("pre_lookahead_layer.conv2.weight", (mel, fcfg.channels, 3)),
+        ("pre_lookahead_layer.conv2.bias", (mel,)),
+    ]
+
+
+_FRONT_FIELDS = {
+    "input_embedding": "input_embedding.weight",
+    "spk_affine_w": "spk_embed_affine_layer.weight",
+    "spk_affine_b": "spk_embed_affine_layer.bias",
+    "pre_conv1_w": "pre_lookahead_layer.conv1.weight",
+    "pre_conv1_b": "pre_lookahead_layer.conv1.bias",
+    "pre_conv2_w": "pre_lookahead_layer.conv2.weight",
+    "pre_conv2_b": "pre_lookahead_layer.conv2.bias",
+}
+
+
+class FlowDecoder:
+    """FlowDecoder (include/larynx/flow/flow.h:37-82) on liblxops: the frontend
+    (speaker affine, token embedding, PreLookaheadLayer, mel-rate mu and prompt
+    cond), then the 10-step CFG Euler solve of the 22-block estimator.
+
+    `front_params` maps flow_frontend_param_shapes() names and `dit_params`
+    dit_param_shapes() names to CUDA fp32 tensors (copied at construction).
+    """
+
+    def __init__(self, front_params, dit_params, cfg: DiTConfig = DiTConfig(),
+                 fcfg: FlowConfig = FlowConfig(), max_tokens: int = 250):
+        self.cfg, self.fcfg, self.max_tokens = cfg, fcfg, max_tokens
+        dw = _dit_weights(dit_params, cfg)
+        shapes = dict(flow_frontend_param_shapes(cfg, fcfg))
+        fw = FlowFrontendWeights()
+        fw.vocab, fw.spk_in, fw.channels = fcfg.vocab, fcfg.spk_in, fcfg.channels
+        for field, name in _FRONT_FIELDS.items():
+            setattr(fw, field, _ptr(front_params, name, shapes[name]))
+        torch.cuda.synchronize()
+        h = C.c_void_p()
+        check(lib.lx_flow_create(C.byref(dw), C.byref(fw), max_tokens, C.byref(h)))
+        self._h = h
+        self._capture = None
+
+    def close(self):
+        if getattr(self, "_h", None):
+            lib.lx_flow_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:  # interpreter shutdown: the library may be gone already
+            pass
+
+    def set_capture(self, capture):
+        """capture: dict with any of spk, token_embed, prelookahead, mu, cond ->
+        preallocated CUDA tensors (FlowDebug, include/larynx/flow/flow.h:15-22)."""
+        cap = FlowCapture()
+        if capture:
+            for k, v in capture.items():
+                setattr(cap, k, C.c_void_p(v.data_ptr()))
+        self._capture = capture
+        check(lib.lx_flow_set_capture(self._h, C.byref(cap)))
+
+    def infer(self, prompt_tokens, tokens, prompt_feat, spk_embedding, noise_z):
+        """Speech tokens -> mel frames past the prompt, (mel, MEL_T - mel_len1).
+
+        prompt_tokens / tokens: int sequences (host); prompt_feat (mel_len1, mel),
+        spk_embedding (spk_in,), noise_z (mel, MEL_T): CUDA fp32 tensors, with
+        MEL_T = token_mel_ratio * (len(prompt_tokens) + len(tokens))."""
+        import numpy as np
+        pt = np.ascontiguousarray(prompt_tokens, dtype=np.int32)
+        tk = np.ascontiguousarray(tokens, dtype=np.int32)
+        mel = self.cfg.mel_dim
+        MT = self.fcfg.token_mel_ratio * (len(pt) + len(tk))
+        pf = prompt_feat.reshape(-1, mel)
+        if tuple(noise_z.shape[-2:]) != (mel, MT) or noise_z.numel() != mel * MT:
+            raise ValueError(f"noise_z {tuple(noise_z.shape)} must be ({mel}, {MT})")
+        if spk_embedding.numel() != self.fcfg.spk_in:
+            raise ValueError(f"spk_embedding must have {self.fcfg.spk_in} values")
+        for t in (pf, spk_embedding, noise_z):
+            if not (t.is_cuda and t.dtype == torch.float32 and t.is_contiguous()):
+                raise ValueError("prompt_feat, spk_embedding and noise_z must be contiguous "
+                                 "CUDA float32 tensors")
+        out = torch.empty(mel, MT - pf.shape[0], device=noise_z.device, dtype=torch.float32)
+        check(lib.lx_flow_infer(self._h, C.c_void_p(pt.ctypes.data), len(pt),
+                                C.c_void_p(tk.ctypes.data), len(tk), C.c_void_p(pf.data_ptr()),
+                                pf.shape[0], C.c_void_p(spk_embedding.data_ptr()),
+                                C.c_void_p(noise_z.data_ptr()), C.c_void_p(out.data_ptr()),
+                                stream()))
+        return out
 
 
 def cfm_t_span(n_steps=10):

@@ -490,6 +490,86 @@ int orc_cfm_solve(const orc_dit* w, int T, float* x, const float* mu, const floa
 
 /* ---- Qwen2 --------------------------------------------------------------- */
 
+/* Flow frontend, restating src/flow/flow.cpp:139-156 with
+ *   l2_normalize  src/flow/ops.cpp:106-112 (x / sqrt(max(sum x^2, 1e-12))),
+ *   PreLookahead  src/flow/prelookahead.cpp:8-20 (conv1 k=4 over the input
+ *                 padded by 3 zeros on the right, leaky_relu slope 0.01,
+ *                 conv2 k=3 over 2 zeros on the left, + input),
+ *   repeat_interleave_2_ne0  src/flow/ops.cpp:114-122 (each token -> 2 frames),
+ *   cond = ggml_pad(prompt_feat^T) (flow.cpp:155-156).
+ * Convolutions accumulate in fp64; every stage is stored fp32. */
+int orc_flow_frontend(const orc_flow_front* w, const int* ids, int Tseq, const float* prompt_feat,
+                      int mel_len1, const float* spk_embedding, float* spk, float* token_embed,
+                      float* pre, float* mu, float* cond) {
+  const int mel = w->mel, ch = w->channels, K1 = 4, K2 = 3;
+  for (int i = 0; i < Tseq; ++i)
+    if (ids[i] < 0 || ids[i] >= w->vocab) return -3;
+  /* speaker affine */
+  double ss = 0.0;
+  for (int k = 0; k < w->spk_in; ++k) ss += (double)spk_embedding[k] * spk_embedding[k];
+  if (ss < 1e-12) ss = 1e-12;
+  const double den = sqrt(ss);
+  for (int o = 0; o < mel; ++o) {
+    double acc = 0.0;
+    for (int k = 0; k < w->spk_in; ++k)
+      acc += (double)w->spk_affine_w[(long)o * w->spk_in + k] * (float)(spk_embedding[k] / den);
+    spk[o] = (float)(acc + w->spk_affine_b[o]);
+  }
+  float* emb = (float*)malloc(sizeof(float) * (size_t)Tseq * mel);
+  float* y1 = (float*)malloc(sizeof(float) * (size_t)Tseq * ch);
+  float* h = (float*)malloc(sizeof(float) * (size_t)Tseq * mel);
+  if (!emb || !y1 || !h) {
+    free(emb);
+    free(y1);
+    free(h);
+    return -4;
+  }
+  for (int t = 0; t < Tseq; ++t)
+    memcpy(emb + (long)t * mel, w->input_embedding + (long)ids[t] * mel, sizeof(float) * mel);
+  /* conv1: y1[t][oc] = b1[oc] + sum_{k<4, c} W1[oc][c][k] x[t + k][c] (x = 0 past T) */
+#pragma omp parallel for schedule(static)
+  for (int t = 0; t < Tseq; ++t) {
+    for (int oc = 0; oc < ch; ++oc) {
+      double acc = 0.0;
+      for (int k = 0; k < K1; ++k) {
+        const int src = t + k;
+        if (src >= Tseq) continue;
+        for (int c = 0; c < mel; ++c)
+          acc += (double)w->pre_conv1_w[((long)oc * mel + c) * K1 + k] * emb[(long)src * mel + c];
+      }
+      const float v = (float)(acc + w->pre_conv1_b[oc]);
+      y1[(long)t * ch + oc] = v > 0.0f ? v : 0.01f * v; /* leaky_relu(0.01) */
+    }
+  }
+  /* conv2: h[t][oc] = b2[oc] + sum_{k<3, c} W2[oc][c][k] y1[t + k - 2][c] (0 before 0), + x */
+#pragma omp parallel for schedule(static)
+  for (int t = 0; t < Tseq; ++t) {
+    for (int oc = 0; oc < mel; ++oc) {
+      double acc = 0.0;
+      for (int k = 0; k < K2; ++k) {
+        const int src = t + k - (K2 - 1);
+        if (src < 0) continue;
+        for (int c = 0; c < ch; ++c)
+          acc += (double)w->pre_conv2_w[((long)oc * ch + c) * K2 + k] * y1[(long)src * ch + c];
+      }
+      const float conv = (float)(acc + w->pre_conv2_b[oc]);
+      h[(long)t * mel + oc] = conv + emb[(long)t * mel + oc];
+    }
+  }
+  const int MT = 2 * Tseq;
+  for (int c = 0; c < mel; ++c)
+    for (int t = 0; t < MT; ++t) {
+      mu[(long)c * MT + t] = h[(long)(t / 2) * mel + c];
+      cond[(long)c * MT + t] = t < mel_len1 ? prompt_feat[(long)t * mel + c] : 0.0f;
+    }
+  if (token_embed) memcpy(token_embed, emb, sizeof(float) * (size_t)Tseq * mel);
+  if (pre) memcpy(pre, h, sizeof(float) * (size_t)Tseq * mel);
+  free(emb);
+  free(y1);
+  free(h);
+  return 0;
+}
+
 int orc_qwen2_build_lm_input(const orc_qwen2* w, const int* text, int n_text, const int* speech,
                              int n_speech, float* out) {
   for (int i = 0; i < n_text; ++i)

@@ -89,6 +89,23 @@ int orc_cfm_step(const orc_dit* w, int T, float* x, const float* mu, const float
 int orc_cfm_solve(const orc_dit* w, int T, float* x, const float* mu, const float* cond,
                   const float* spks, int n_steps, float cfg_rate);
 
+/* ---- Flow frontend (FlowDecoder::infer before the CFM solve) ---------------- */
+typedef struct orc_flow_front {
+  int vocab, spk_in, mel, channels;
+  const float *input_embedding;           /* (vocab, mel)            */
+  const float *spk_affine_w, *spk_affine_b; /* (mel, spk_in), (mel)   */
+  const float *pre_conv1_w, *pre_conv1_b;   /* (channels, mel, 4)     */
+  const float *pre_conv2_w, *pre_conv2_b;   /* (mel, channels, 3)     */
+} orc_flow_front;
+
+/* ids: Tseq clamped token ids (prompt then tokens); prompt_feat (mel_len1, mel);
+ * spk_embedding (spk_in).  Outputs (any may be NULL except mu/cond/spk):
+ * spk (mel), token_embed (Tseq, mel), pre (Tseq, mel), mu (mel, 2 Tseq),
+ * cond (mel, 2 Tseq).  Returns 0, or -3 for an id outside the table. */
+int orc_flow_frontend(const orc_flow_front* w, const int* ids, int Tseq, const float* prompt_feat,
+                      int mel_len1, const float* spk_embedding, float* spk, float* token_embed,
+                      float* pre, float* mu, float* cond);
+
 /* ---- Qwen2 -------------------------------------------------------------- */
 typedef struct orc_qwen2_layer {
   const float *q_w, *q_b, *k_w, *k_b, *v_w, *v_b, *o_w, *gate_w, *up_w, *down_w, *in_norm,

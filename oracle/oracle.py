@@ -56,6 +56,12 @@ class OrcQwen(C.Structure):
     ]
 
 
+class OrcFlowFront(C.Structure):
+    _fields_ = [("vocab", C.c_int), ("spk_in", C.c_int), ("mel", C.c_int), ("channels", C.c_int)] + [
+        (n, vp) for n in ("input_embedding", "spk_affine_w", "spk_affine_b", "pre_conv1_w",
+                          "pre_conv1_b", "pre_conv2_w", "pre_conv2_b")]
+
+
 def _load():
     if not os.path.exists(LIB_PATH):
         raise ImportError(f"{LIB_PATH} not built (make -C oracle)")
@@ -87,6 +93,8 @@ def _load():
                                    C.c_float, C.c_float]),
         "orc_cfm_solve": (C.c_int, [C.POINTER(OrcDit), C.c_int, f32p, f32p, f32p, f32p, C.c_int,
                                     C.c_float]),
+        "orc_flow_frontend": (C.c_int, [C.POINTER(OrcFlowFront), i32p, C.c_int, vp, C.c_int, f32p,
+                                        f32p, vp, vp, f32p, f32p]),
         "orc_qwen2_build_lm_input": (C.c_int, [C.POINTER(OrcQwen), i32p, C.c_int, i32p, C.c_int,
                                                f32p]),
         "orc_qwen2_forward": (C.c_int, [C.POINTER(OrcQwen), f32p, C.c_int, C.c_int, f32p, f32p,
@@ -317,6 +325,62 @@ class Dit:
                                n_steps, cfg_rate)
         assert rc == 0, rc
         return x
+
+
+_FRONT_KEYS = {
+    "input_embedding": "input_embedding.weight",
+    "spk_affine_w": "spk_embed_affine_layer.weight", "spk_affine_b": "spk_embed_affine_layer.bias",
+    "pre_conv1_w": "pre_lookahead_layer.conv1.weight", "pre_conv1_b": "pre_lookahead_layer.conv1.bias",
+    "pre_conv2_w": "pre_lookahead_layer.conv2.weight", "pre_conv2_b": "pre_lookahead_layer.conv2.bias",
+}
+
+
+class Flow:
+    """Oracle FlowDecoder::infer (frontend + CFM solve) over numpy params: the
+    frontend names of larynx_amd.flow.flow_frontend_param_shapes plus the
+    estimator's (Dit) names."""
+
+    def __init__(self, front_params, dit_params, mel=80, **dit_kw):
+        self._keep = {k: c32(v) for k, v in front_params.items()}
+        w = OrcFlowFront()
+        emb = self._keep["input_embedding.weight"]
+        w.vocab, w.mel = emb.shape
+        w.spk_in = self._keep["spk_embed_affine_layer.weight"].shape[1]
+        w.channels = self._keep["pre_lookahead_layer.conv1.weight"].shape[0]
+        for f, key in _FRONT_KEYS.items():
+            setattr(w, f, _vp(self._keep[key]))
+        self.w = w
+        self.mel = mel
+        self.dit = Dit(dit_params, mel_dim=mel, **dit_kw) if dit_params is not None else None
+
+    def frontend(self, prompt_tokens, tokens, prompt_feat, spk_embedding):
+        """-> dict spk (mel,), token_embed (Tseq, mel), prelookahead (Tseq, mel),
+        mu (mel, MEL_T), cond (mel, MEL_T)."""
+        ids = np.concatenate([np.asarray(prompt_tokens, np.int64), np.asarray(tokens, np.int64)])
+        ids = np.ascontiguousarray(np.maximum(ids, 0), dtype=np.int32)  # token.clamp(min=0)
+        T = len(ids)
+        pf = c32(prompt_feat).reshape(-1, self.mel)
+        out = {"spk": np.empty(self.mel, np.float32),
+               "token_embed": np.empty((T, self.mel), np.float32),
+               "prelookahead": np.empty((T, self.mel), np.float32),
+               "mu": np.empty((self.mel, 2 * T), np.float32),
+               "cond": np.empty((self.mel, 2 * T), np.float32)}
+        rc = lib.orc_flow_frontend(C.byref(self.w), ids, T, _vp(pf), pf.shape[0],
+                                   c32(spk_embedding).reshape(-1), out["spk"],
+                                   _vp(out["token_embed"]), _vp(out["prelookahead"]), out["mu"],
+                                   out["cond"])
+        if rc == -3:
+            raise IndexError("token id out of range")
+        assert rc == 0, rc
+        return out
+
+    def infer(self, prompt_tokens, tokens, prompt_feat, spk_embedding, noise_z, n_steps=10,
+              cfg_rate=0.7):
+        """-> mel (mel, MEL_T - mel_len1), the frontend then the CFG Euler solve."""
+        st = self.frontend(prompt_tokens, tokens, prompt_feat, spk_embedding)
+        x = self.dit.cfm_solve(noise_z, st["mu"], st["cond"], st["spk"], n_steps, cfg_rate)
+        mel_len1 = c32(prompt_feat).reshape(-1, self.mel).shape[0]
+        return x[:, mel_len1:], st
 
 
 _QKEYS = {

@@ -4,9 +4,11 @@ PyTorch modules (Larynx tests/flow_reference.py), imported from
 /root/reference in the build container only.
 
 What is pinned here, and why an import is needed: the composed DiT.forward
-(flow_reference.py:355-400), CausalConditionalCFM.solve_euler (:476-501) and
-torch's exact fp32 rounding of SinusPositionEmbedding (:125-137) and
-RotaryEmbedding / apply_rotary_pos_emb (:52-106).  Per-op semantics are pinned
+(flow_reference.py:355-400), CausalConditionalCFM.solve_euler (:476-501), the
+whole CausalMaskedDiffWithDiT inference with its frontend stages
+(PreLookaheadLayer :406-431, manual_inference :597-665), and torch's exact fp32
+rounding of SinusPositionEmbedding (:125-137) and RotaryEmbedding /
+apply_rotary_pos_emb (:52-106).  Per-op semantics are pinned
 by closed forms and library routines in tests/test_oracle_*.py instead.
 
 Weights and inputs come from the oracle's counter-based generator
@@ -28,12 +30,13 @@ sys.path.insert(0, REF_TESTS)
 
 import flow_reference as fr  # noqa: E402  (reference module, build container only)
 
-from larynx_amd.flow import DiTConfig, dit_param_shapes  # noqa: E402
+from larynx_amd.flow import DiTConfig, dit_param_shapes, flow_frontend_param_shapes  # noqa: E402
 from oracle import oracle as orc  # noqa: E402
 
 OUT = os.path.dirname(os.path.abspath(__file__))
 WEIGHT_SEED = 20260101
 INPUT_SEED = 1234
+FRONT_SEED = 20260202
 
 
 def build_dit(cfg, seed):
@@ -106,6 +109,52 @@ def main():
                         weight_seed=np.int64(WEIGHT_SEED), z=z, mu=mu1, cond=cond1, spks=spk1,
                         t_span=t_span.numpy(), feat=feat.numpy())
     print("flow_cfm_T24.npz written")
+
+    # Whole FlowDecoder inference (CausalMaskedDiffWithDiT.inference, finalize=True) through
+    # the reference's step-by-step replica with stage captures (flow_reference.py:597-665):
+    # the validation case of include/larynx/flow/flow.h:12-14 (4 prompt + 8 tokens -> 24 mel
+    # frames, 8 prompt frames -> 16 output frames).  Frontend weights ~N(0, 0.02) except the
+    # token embedding table ~N(0, 1); the CFM start noise replaces the module's seed bank.
+    model = fr.CausalMaskedDiffWithDiT(
+        input_size=80, output_size=80, spk_embed_dim=192, output_type="mel", vocab_size=fr.VOCAB,
+        input_frame_rate=25, token_mel_ratio=2, pre_lookahead_len=3,
+        pre_lookahead_layer=fr.PreLookaheadLayer(in_channels=80, channels=1024,
+                                                 pre_lookahead_len=3),
+        decoder=dec)
+    front = orc.make_params(flow_frontend_param_shapes(cfg), FRONT_SEED)
+    front["input_embedding.weight"] = orc.normal((fr.VOCAB, 80), FRONT_SEED, 100)
+    res = model.load_state_dict({k: torch.from_numpy(v) for k, v in front.items()},
+                                strict=False)
+    assert not res.unexpected_keys, res.unexpected_keys
+    assert all(k.startswith("decoder.") for k in res.missing_keys), res.missing_keys
+    model.eval()
+    prompt_tokens = np.array([[3, 1500, 6560, 42]], dtype=np.int64)
+    tokens = np.array([[7, -1, 4095, 6000, 12, 0, 3333, 999]], dtype=np.int64)  # -1: clamp
+    prompt_feat = orc.normal((1, 8, 80), INPUT_SEED, 30)
+    spk_embedding = orc.normal((1, 192), INPUT_SEED, 31)
+    noise = orc.normal((1, 80, 24), INPUT_SEED, 32)
+    dec.rand_noise = torch.from_numpy(noise)
+    cap = {}
+    with torch.no_grad():
+        feat = fr.manual_inference(model, torch.from_numpy(prompt_tokens),
+                                   torch.from_numpy(tokens), torch.from_numpy(prompt_feat),
+                                   torch.from_numpy(spk_embedding), cap)
+        # the module's own inference() agrees with the step-by-step replica
+        ref_feat, _ = model.inference(torch.from_numpy(tokens), torch.tensor([8]),
+                                      torch.from_numpy(prompt_tokens), torch.tensor([4]),
+                                      torch.from_numpy(prompt_feat), torch.tensor([8]),
+                                      torch.from_numpy(spk_embedding), streaming=False,
+                                      finalize=True)
+    assert torch.allclose(feat, ref_feat, rtol=0, atol=1e-5), (feat - ref_feat).abs().max()
+    np.savez_compressed(os.path.join(OUT, "flow_infer_T24.npz"),
+                        weight_seed=np.int64(WEIGHT_SEED), front_seed=np.int64(FRONT_SEED),
+                        prompt_tokens=prompt_tokens[0].astype(np.int32),
+                        tokens=tokens[0].astype(np.int32), prompt_feat=prompt_feat[0],
+                        spk_embedding=spk_embedding[0], noise=noise[0],
+                        spk=cap["spk"][0].numpy(), token_embed=cap["token_embed"][0].numpy(),
+                        prelookahead=cap["prelookahead"][0].numpy(), mu=cap["mu"][0].numpy(),
+                        cond=cap["cond"][0].numpy(), feat=feat[0].numpy())
+    print("flow_infer_T24.npz written")
 
     # Rotary at the long-utterance length: fp32 angle rounding matters at T=3000.
     T_long = 3000

@@ -2,8 +2,10 @@
 
 Flow: against the golden vectors that tests/golden/make_flow_golden.py wrote
 from the reference's own PyTorch modules (tests/flow_reference.py of Larynx):
-22-block DiT.forward at T=24, the 10-step CFG Euler solve, the rotary at
-T=3000 and the timestep sinusoid.
+22-block DiT.forward at T=24, the 10-step CFG Euler solve, the whole
+FlowDecoder inference with its frontend stages (speaker affine, token
+embedding, PreLookaheadLayer, mu, cond), the rotary at T=3000 and the timestep
+sinusoid.
 
 Qwen2: against a transformers Qwen2Model built locally from a hand-written
 config with the oracle's synthetic weights (an independent implementation of
@@ -19,7 +21,7 @@ import torch
 from conftest import GOLDEN
 from oracle import oracle as orc
 
-from larynx_amd.flow import DiTConfig, dit_param_shapes
+from larynx_amd.flow import DiTConfig, dit_param_shapes, flow_frontend_param_shapes
 from larynx_amd.llm import Qwen2Config, qwen2_param_shapes
 
 
@@ -47,6 +49,100 @@ def test_cfm_solve_matches_reference_modules(dit_golden):
     c = np.load(os.path.join(GOLDEN, "flow_cfm_T24.npz"))
     feat = dit.cfm_solve(c["z"][0], c["mu"][0], c["cond"][0], c["spks"][0], 10, 0.7)
     assert orc.rel_err(feat, c["feat"][0]) < 1e-5
+
+
+def flow_front_params(g):
+    """Frontend weights of flow_infer_T24.npz, regenerated from its seed."""
+    front = orc.make_params(flow_frontend_param_shapes(DiTConfig()), int(g["front_seed"]))
+    front["input_embedding.weight"] = orc.normal((6561, 80), int(g["front_seed"]), 100)
+    return front
+
+
+def test_flow_infer_matches_reference_modules(dit_golden):
+    """CausalMaskedDiffWithDiT.inference: 4 prompt + 8 tokens (one negative id,
+    clamped to 0), 8 prompt frames, 16 output frames; every frontend stage and
+    the final mel against the reference's own modules."""
+    _, dit = dit_golden
+    g = np.load(os.path.join(GOLDEN, "flow_infer_T24.npz"))
+    flow = orc.Flow(flow_front_params(g), None)
+    flow.dit = dit
+    mel, st = flow.infer(g["prompt_tokens"], g["tokens"], g["prompt_feat"], g["spk_embedding"],
+                         g["noise"])
+    assert orc.rel_err(st["spk"], g["spk"]) < 1e-6
+    assert np.array_equal(st["token_embed"], g["token_embed"])  # a gather: bit-exact
+    assert orc.rel_err(st["prelookahead"], g["prelookahead"]) < 1e-6
+    assert orc.rel_err(st["mu"], g["mu"]) < 1e-6
+    assert np.array_equal(st["cond"], g["cond"])  # a copy + zero pad
+    assert mel.shape == (80, 16)
+    assert orc.rel_err(mel, g["feat"]) < 1e-5
+
+
+def test_flow_frontend_closed_forms():
+    """Invariants the frontend math fixes, independently of the reference import:
+    the speaker projection is scale-invariant (l2-normalised input) and an all-zero
+    embedding hits the 1e-12 clamp (output = bias); PreLookahead with zero conv
+    weights is the identity (residual only) plus the conv2 bias; a token's mu
+    frames are its two repeats; cond is the transposed prompt then zeros."""
+    rng = np.random.default_rng(5)
+    mel, ch, spk_in, vocab = 80, 32, 192, 50
+    p = {"input_embedding.weight": rng.standard_normal((vocab, mel)).astype(np.float32),
+         "spk_embed_affine_layer.weight": rng.standard_normal((mel, spk_in)).astype(np.float32),
+         "spk_embed_affine_layer.bias": rng.standard_normal(mel).astype(np.float32),
+         "pre_lookahead_layer.conv1.weight": np.zeros((ch, mel, 4), np.float32),
+         "pre_lookahead_layer.conv1.bias": np.zeros(ch, np.float32),
+         "pre_lookahead_layer.conv2.weight": np.zeros((mel, ch, 3), np.float32),
+         "pre_lookahead_layer.conv2.bias": rng.standard_normal(mel).astype(np.float32)}
+    flow = orc.Flow(p, None)
+    spk = rng.standard_normal(spk_in).astype(np.float32)
+    pf = rng.standard_normal((3, mel)).astype(np.float32)
+    a = flow.frontend([1, 2], [3, 4, 5], pf, spk)
+    b = flow.frontend([1, 2], [3, 4, 5], pf, 7.0 * spk)
+    assert np.abs(a["spk"] - b["spk"]).max() < 1e-5
+    z = flow.frontend([1], [2], pf[:1], np.zeros(spk_in, np.float32))
+    assert np.array_equal(z["spk"], p["spk_embed_affine_layer.bias"])
+    ids = [1, 2, 3, 4, 5]
+    emb = p["input_embedding.weight"][ids]
+    np.testing.assert_allclose(a["prelookahead"], emb + p["pre_lookahead_layer.conv2.bias"],
+                               rtol=0, atol=1e-6)
+    assert np.array_equal(a["mu"][:, 0::2], a["prelookahead"].T)
+    assert np.array_equal(a["mu"][:, 1::2], a["prelookahead"].T)
+    assert np.array_equal(a["cond"][:, :3], pf.T) and not a["cond"][:, 3:].any()
+    with pytest.raises(IndexError):
+        flow.frontend([1], [vocab], pf[:1], spk)
+
+
+def test_flow_prelookahead_matches_torch_conv():
+    """PreLookahead against torch.nn.functional.conv1d / leaky_relu in float64 at a
+    length where both paddings and interior frames matter."""
+    import torch.nn.functional as F
+    rng = np.random.default_rng(6)
+    mel, ch, vocab, T = 80, 48, 40, 17
+    p = {"input_embedding.weight": rng.standard_normal((vocab, mel)).astype(np.float32),
+         "spk_embed_affine_layer.weight": np.zeros((mel, 192), np.float32),
+         "spk_embed_affine_layer.bias": np.zeros(mel, np.float32),
+         "pre_lookahead_layer.conv1.weight": (0.1 * rng.standard_normal((ch, mel, 4))).astype(np.float32),
+         "pre_lookahead_layer.conv1.bias": (0.1 * rng.standard_normal(ch)).astype(np.float32),
+         "pre_lookahead_layer.conv2.weight": (0.1 * rng.standard_normal((mel, ch, 3))).astype(np.float32),
+         "pre_lookahead_layer.conv2.bias": (0.1 * rng.standard_normal(mel)).astype(np.float32)}
+    ids = rng.integers(0, vocab, T)
+    out = orc.Flow(p, None).frontend([], ids, np.zeros((0, mel), np.float32),
+                                     np.ones(192, np.float32))
+    x = torch.from_numpy(p["input_embedding.weight"][ids].T[None].astype(np.float64))
+    w1 = torch.from_numpy(p["pre_lookahead_layer.conv1.weight"].astype(np.float64))
+    b1 = torch.from_numpy(p["pre_lookahead_layer.conv1.bias"].astype(np.float64))
+    w2 = torch.from_numpy(p["pre_lookahead_layer.conv2.weight"].astype(np.float64))
+    b2 = torch.from_numpy(p["pre_lookahead_layer.conv2.bias"].astype(np.float64))
+    y = F.leaky_relu(F.conv1d(F.pad(x, (0, 3)), w1, b1), 0.01)
+    y = F.conv1d(F.pad(y, (2, 0)), w2, b2) + x
+    assert orc.rel_err(out["prelookahead"], y[0].T.numpy()) < 1e-6
+    # planted mistakes the pin must see: lookahead padding on the wrong side,
+    # conv2 padded symmetrically, and the residual dropped
+    bad1 = F.conv1d(F.pad(F.leaky_relu(F.conv1d(F.pad(x, (3, 0)), w1, b1), 0.01), (2, 0)), w2,
+                    b2) + x
+    bad2 = F.conv1d(F.pad(F.leaky_relu(F.conv1d(F.pad(x, (0, 3)), w1, b1), 0.01), (1, 1)), w2,
+                    b2) + x
+    for bad in (bad1, bad2, y - x):
+        assert orc.rel_err(out["prelookahead"], bad[0].T.numpy()) > 1e-2
 
 
 def test_rotary_T3000_matches_reference_modules():
