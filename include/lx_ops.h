@@ -405,6 +405,45 @@ const float* lx_qwen2_cache_value(const lx_qwen2* m, int layer);
  * load a synthetic cache through the pointers above (benchmarks, tests). */
 int lx_qwen2_set_cache_len(lx_qwen2* m, int len);
 
+/* ------------------------------------------------------------------------ */
+/* GGUF v3 weight files and the model loaders over them                      */
+/* ------------------------------------------------------------------------ */
+
+/* A parsed GGUF v3 file (docs/WEIGHT_FORMAT.md §1-3 of the reference; read there
+ * by ggml's gguf_init_from_file + upload_gguf_weights,
+ * include/larynx/backend.h:48-87).  lx_gguf_open validates the header, the
+ * metadata and every tensor's extent against the file size, then (unless
+ * LX_GGUF_HOST_ONLY) streams the data section into one device allocation
+ * owned by the object.  Only unquantised tensor types are accepted (F32, F16,
+ * BF16, F64, I8..I64); the CosyVoice3 checkpoints are all F32.  Bad files are
+ * LX_ERR_ARG with a message naming the problem. */
+typedef struct lx_gguf lx_gguf;
+enum { LX_GGUF_HOST_ONLY = 1 };
+int lx_gguf_open(const char* path, int flags, lx_gguf** out);
+void lx_gguf_close(lx_gguf* gguf);
+int lx_gguf_n_tensors(const lx_gguf* gguf);
+/* Index of a tensor by name (the PyTorch state_dict key), or -1. */
+int lx_gguf_find(const lx_gguf* gguf, const char* name);
+/* name (owned by the object), ggml type, n_dims and ne[4] (fastest first,
+ * i.e. the torch shape reversed; unused dims 1), byte size.  Any out pointer
+ * may be NULL. */
+int lx_gguf_tensor_info(const lx_gguf* gguf, int index, const char** name, int* type,
+                        int* n_dims, int64_t* ne, uint64_t* nbytes);
+/* Device pointer of a tensor's data (NULL in host-only mode). */
+const void* lx_gguf_tensor_data(const lx_gguf* gguf, int index);
+/* String-valued metadata (general.architecture, general.name), or NULL. */
+const char* lx_gguf_get_string(const lx_gguf* gguf, const char* key);
+
+/* FlowDecoder::load (src/flow/flow.cpp:49-61, src/flow/gguf.cpp:24-135): the
+ * flow checkpoint's tensors (frontend names at the top level, the estimator
+ * under decoder.estimator.), geometry read from their shapes; the file's
+ * device copy is released once the decoder has packed its own. */
+int lx_flow_load(const char* path, int max_tokens, lx_flow** out);
+/* LLM::load (src/llm/llm.cpp:50-61, src/llm/gguf.cpp:30-100): names under
+ * llm.model.model. plus speech_embedding / llm_decoder; the model keeps the
+ * file's device copy (it references the embedding tables) until destroy. */
+int lx_qwen2_load(const char* path, int max_ctx, lx_qwen2** out);
+
 #ifdef __cplusplus
 }
 #endif

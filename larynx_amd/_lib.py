@@ -17,6 +17,8 @@ LX_ERR_RANGE = -3
 LX_ERR_ALLOC = -4
 LX_ERR_STATE = -5
 
+LX_GGUF_HOST_ONLY = 1
+
 LX_EPI_NONE = 0
 LX_EPI_GELU_TANH = 1
 LX_EPI_GATED_RESID = 2
@@ -149,6 +151,17 @@ SIGNATURES = [
     ("lx_flow_set_capture", C.c_int, [C.c_void_p, C.POINTER(FlowCapture)]),
     ("lx_flow_infer", C.c_int,
      [C.c_void_p, ip, C.c_int, ip, C.c_int, fp, C.c_int, fp, fp, fp, stream_t]),
+    ("lx_gguf_open", C.c_int, [C.c_char_p, C.c_int, C.POINTER(C.c_void_p)]),
+    ("lx_gguf_close", None, [C.c_void_p]),
+    ("lx_gguf_n_tensors", C.c_int, [C.c_void_p]),
+    ("lx_gguf_find", C.c_int, [C.c_void_p, C.c_char_p]),
+    ("lx_gguf_tensor_info", C.c_int,
+     [C.c_void_p, C.c_int, C.POINTER(C.c_char_p), C.POINTER(C.c_int), C.POINTER(C.c_int),
+      C.POINTER(C.c_int64), C.POINTER(C.c_uint64)]),
+    ("lx_gguf_tensor_data", C.c_void_p, [C.c_void_p, C.c_int]),
+    ("lx_gguf_get_string", C.c_char_p, [C.c_void_p, C.c_char_p]),
+    ("lx_flow_load", C.c_int, [C.c_char_p, C.c_int, C.POINTER(C.c_void_p)]),
+    ("lx_qwen2_load", C.c_int, [C.c_char_p, C.c_int, C.POINTER(C.c_void_p)]),
     ("lx_qwen2_create", C.c_int,
      [C.POINTER(Qwen2Weights), C.c_int, C.POINTER(C.c_void_p)]),
     ("lx_qwen2_destroy", None, [C.c_void_p]),

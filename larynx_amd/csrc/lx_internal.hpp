@@ -154,6 +154,11 @@ int flow_pack_mu_cond(const float* pre, int Tseq, int ratio, const float* prompt
 // Conv1d weight (OC, IC, K) -> (OC, K * IC) with column k * IC + ic.
 int conv_kmajor_pack(const float* w, int OC, int IC, int K, float* wp, hipStream_t s);
 
+// ---- weight files (lx_gguf.cpp / lx_qwen2.cpp) ----
+// Hands the model the GGUF object whose device memory it references (the
+// embedding tables); the model closes it when it is destroyed.
+void qwen2_adopt_weights(lx_qwen2* m, lx_gguf* g);
+
 // Grouped conv + Mish with tap-major packed weights (lx_conv_pos_mish_f32).
 int conv_pos_mish_packed(const float* x, const float* wp, const float* bias, const float* resid,
                          float* y, int B, int T, int C, int G, int K, hipStream_t stream);

@@ -58,11 +58,15 @@ struct lx_qwen2 {
   bool use_graph = true;      // replay the layer stack as one HIP graph
   hipStream_t cap_stream = nullptr;
   hipGraphExec_t graph = nullptr;
+  lx_gguf* weights_file = nullptr;  // set by lx_qwen2_load: holds the referenced tables
   ~lx_qwen2() {
     if (graph) (void)hipGraphExecDestroy(graph);
     if (cap_stream) (void)hipStreamDestroy(cap_stream);
+    if (weights_file) lx_gguf_close(weights_file);
   }
 };
+
+void lx::qwen2_adopt_weights(lx_qwen2* m, lx_gguf* g) { m->weights_file = g; }
 
 namespace {
 

@@ -257,6 +257,32 @@ class FlowDecoder:
         self._h = h
         self._capture = None
 
+    @classmethod
+    def load(cls, path, max_tokens: int = 250):
+        """FlowDecoder::load: a flow.gguf checkpoint (geometry from its tensors)."""
+        from .gguf import GgufFile
+        hdr = GgufFile(path, device=False)
+        shape = {n: s for n, _, s, _ in hdr.tensors()}
+        hdr.close()
+        E = "decoder.estimator."
+        depth = 0
+        while f"{E}transformer_blocks.{depth}.attn_norm.linear.weight" in shape:
+            depth += 1
+        vocab, mel = shape.get("input_embedding.weight", (0, 0))
+        dim = shape.get(E + "input_embed.proj.weight", (0, 0))[0]
+        ff = shape.get(E + "transformer_blocks.0.ff.ff.0.0.weight", (0, 0))[0]
+        cfg = DiTConfig(dim=dim, depth=depth, heads=max(dim // 64, 1), ff_inner=ff, mel_dim=mel)
+        fcfg = FlowConfig(vocab=vocab,
+                          spk_in=shape.get("spk_embed_affine_layer.weight", (0, 0))[1],
+                          channels=shape.get("pre_lookahead_layer.conv1.weight", (0,))[0])
+        self = cls.__new__(cls)
+        self.cfg, self.fcfg, self.max_tokens = cfg, fcfg, max_tokens
+        h = C.c_void_p()
+        check(lib.lx_flow_load(str(path).encode(), max_tokens, C.byref(h)))
+        self._h = h
+        self._capture = None
+        return self
+
     def close(self):
         if getattr(self, "_h", None):
             lib.lx_flow_destroy(self._h)

@@ -105,13 +105,43 @@ class Qwen2LM:
         check(lib.lx_qwen2_create(C.byref(w), max_ctx, C.byref(h)))
         self._h = h
 
+    @classmethod
+    def load(cls, path, max_ctx: int = 4096):
+        """LLM::load: an llm.gguf checkpoint (geometry from its tensors; the model
+        keeps the file's device copy, which holds the embedding tables)."""
+        from .gguf import GgufFile
+        hdr = GgufFile(path, device=False)
+        shape = {n: s for n, _, s, _ in hdr.tensors()}
+        hdr.close()
+        M = "llm.model.model."
+        n_layers = 0
+        while f"{M}layers.{n_layers}.self_attn.q_proj.weight" in shape:
+            n_layers += 1
+        text_vocab, H = shape.get(M + "embed_tokens.weight", (0, 0))
+        cfg = Qwen2Config(hidden=H, intermediate=shape.get(M + "layers.0.mlp.gate_proj.weight",
+                                                           (0, 0))[0],
+                          n_heads=H // 64,
+                          n_kv_heads=shape.get(M + "layers.0.self_attn.k_proj.weight",
+                                               (0, 0))[0] // 64,
+                          n_layers=n_layers, text_vocab=text_vocab,
+                          speech_vocab=shape.get("speech_embedding.weight", (0, 0))[0])
+        self = cls.__new__(cls)
+        self.cfg, self.max_ctx, self._params = cfg, max_ctx, None
+        h = C.c_void_p()
+        check(lib.lx_qwen2_load(str(path).encode(), max_ctx, C.byref(h)))
+        self._h = h
+        return self
+
     def close(self):
         if getattr(self, "_h", None):
             lib.lx_qwen2_destroy(self._h)
             self._h = None
 
     def __del__(self):
-        self.close()
+        try:
+            self.close()
+        except Exception:  # interpreter shutdown: the library may be gone already
+            pass
 
     def build_lm_input(self, text_tokens, prompt_speech_tokens, device="cuda"):
         """lm_input (L, H) = [sos; embed_tokens(text); task_id; speech_emb(prompt)]."""
