@@ -64,6 +64,12 @@ def test_argument_errors_need_no_device():
     assert lib.lx_linear_f32(fake, 6, fake, None, fake, 6, 8, 8, 6, None, None) == LX_ERR_ARG
     assert lib.lx_conv_pos_mish_f32(fake, fake, fake, None, fake, 1, 8, 1024, 8, 31,
                                     None) == LX_ERR_ARG  # 128 channels per group
+    # composite objects: null handles and empty token lists are refused on the host
+    assert lib.lx_flow_infer(None, None, 0, None, 0, None, 0, None, None, None,
+                             None) == LX_ERR_ARG
+    out = C.c_void_p()
+    assert lib.lx_flow_load(b"/nonexistent/flow.gguf", 250, C.byref(out)) == LX_ERR_ARG
+    assert b"cannot open" in lib.lx_last_error() and not out.value
 
 
 def _c_layout(struct, fields):
@@ -90,7 +96,8 @@ def _c_layout(struct, fields):
 @pytest.mark.parametrize("struct,cls", [
     ("lx_epilogue", "Epilogue"), ("lx_dit_block_weights", "DitBlockWeights"),
     ("lx_dit_weights", "DitWeights"), ("lx_dit_capture", "DitCapture"),
-    ("lx_qwen2_layer_weights", "Qwen2LayerWeights"), ("lx_qwen2_weights", "Qwen2Weights")])
+    ("lx_qwen2_layer_weights", "Qwen2LayerWeights"), ("lx_qwen2_weights", "Qwen2Weights"),
+    ("lx_flow_frontend_weights", "FlowFrontendWeights"), ("lx_flow_capture", "FlowCapture")])
 def test_struct_layouts_match_header(struct, cls):
     import larynx_amd._lib as L
     py = getattr(L, cls)
