@@ -32,6 +32,7 @@ constexpr int kConvG = 16;         // CONV_POS_GROUPS (src/flow/internal.h:33)
 constexpr float kLnEps = 1e-6f;    // LN_EPS (src/flow/internal.h:34)
 constexpr float kRopeBase = 10000.0f;  // ROPE_FREQ_BASE (src/flow/internal.h:35)
 constexpr int kRotDim = 64;        // ROT_DIM (src/flow/internal.h:25)
+constexpr int kProjSplitMax = 8;   // K slices of the proj_out split-K (the plan's cap)
 
 }  // namespace
 
@@ -51,11 +52,12 @@ struct lx_dit {
   float *proj_w, *proj_b;
 
   // activations (sized for B x max_T)
-  float *t_dev, *temb, *tmlp_work, *emb;
+  float *temb, *tmlp_work, *emb;
   float *A0, *xe, *c1, *h, *xn, *qkv, *att, *ff, *P;
+  float* Pws;          // split-K slices of proj_out (kProjSplitMax x rows x mel)
+  int proj_splits = 1; // slices of the last forward's proj_out
+  long proj_slice = 0; // floats between slices
   int* pos;
-  // CFM (B == 2) inputs
-  float *x_in, *mu_in, *cond_in, *spks_in;
 
   lx_dit_capture cap{};
   hipStream_t create_stream = nullptr;
@@ -75,21 +77,27 @@ int copy_d2d(float* dst, const float* src, size_t n, hipStream_t s) {
   return LX_OK;
 }
 
-// Everything up to the proj_out rows P (B*T, mel).
-int forward_core(lx_dit* m, const float* x, const float* mu, const float* cond, const float* spks,
-                 const float* t, int T, hipStream_t s) {
+// Everything up to the proj_out rows: their split-K slices in Pws
+// (m->proj_splits slices, m->proj_slice floats apart; the bias is added by
+// whoever sums them).  x of batch b starts at x + b * x_bstride; with cfg set,
+// mu / cond / spks are the conditional row's and the unconditional row gets
+// zeros.  t is read from device memory (tdev) or, when tdev is null, from the
+// host array thost.
+int forward_core(lx_dit* m, const float* x, long x_bstride, const float* mu, const float* cond,
+                 const float* spks, int cfg, const float* tdev, const float* thost, int T,
+                 hipStream_t s) {
   const int B = m->B, D = m->D, mel = m->mel;
   const int rows = B * T;
   // Time embedding (a6) and every AdaLN modulation of this step in one GEMV.
-  LX_TRY(lx_time_mlp_f32(t, B, m->tm0_w, m->tm0_b, m->tm2_w, m->tm2_b, D, m->tmlp_work,
-                         m->temb, s));
+  LX_TRY(time_mlp(tdev, thost, B, m->tm0_w, m->tm0_b, m->tm2_w, m->tm2_b, D, m->tmlp_work, m->temb,
+                  s));
   LX_TRY(gemv(m->temb, B, D, m->ada_w, m->ada_b, m->emb, m->NA, m->NA, /*silu in*/ 1, 0, s));
   if (m->cap.time_embed)
     (void)hipMemcpyAsync(m->cap.time_embed, m->temb, sizeof(float) * B * D,
                          hipMemcpyDeviceToDevice, s);
 
   // InputEmbedding: proj(concat[x, cond, mu, spks]) + conv_pos_embed.
-  LX_TRY(dit_pack_input(x, cond, mu, spks, m->A0, B, T, mel, s));
+  LX_TRY(dit_pack_input(x, x_bstride, cond, mu, spks, cfg, m->A0, B, T, mel, s));
   LX_TRY(lx_linear_f32(m->A0, 4 * mel, m->in_w, m->in_b, m->xe, D, rows, D, 4 * mel, nullptr, s));
   LX_TRY(conv_pos_mish_packed(m->xe, m->conv1_wp, m->conv1_b, nullptr, m->c1, B, T, D, kConvG,
                               kConvK, s));
@@ -157,8 +165,19 @@ int forward_core(lx_dit* m, const float* x, const float* mu, const float* cond, 
   if (m->cap.norm_out)
     (void)hipMemcpyAsync(m->cap.norm_out, m->xn, sizeof(float) * rows * D, hipMemcpyDeviceToDevice,
                          s);
-  LX_TRY(lx_linear_f32(m->xn, D, m->proj_w, m->proj_b, m->P, mel, rows, mel, D, nullptr, s));
+  // proj_out (N = mel = 80 columns, 2 x 16 tiles at B*T = 1000): split-K slices
+  // fill the device; the slice sum + bias is fused into the consumer.
+  int ks = 0;
+  const int splits = gemm_splitk_plan(rows, mel, D, &ks);
+  LX_TRY(gemm_splitk_partials(m->xn, D, m->proj_w, D, m->Pws, rows, mel, D, splits, ks, s));
+  m->proj_splits = splits;
+  m->proj_slice = (long)rows * mel;
   return check_launch("dit forward");
+}
+
+// P = the proj_out rows of the last forward (slice sum + bias).
+int proj_rows(lx_dit* m, int T, hipStream_t s) {
+  return proj_reduce(m->Pws, m->proj_splits, m->proj_slice, m->proj_b, m->P, m->B * T, m->mel, s);
 }
 
 }  // namespace
@@ -218,9 +237,8 @@ extern "C" int lx_dit_create(const lx_dit_weights* w, int B, int max_T, lx_dit**
   m->proj_w = A((size_t)mel * D);
   m->proj_b = A(mel);
   const size_t rows = (size_t)B * max_T;
-  m->t_dev = A(B);
   m->temb = A((size_t)B * D);
-  m->tmlp_work = A((size_t)B * (kFreqDim + D));
+  m->tmlp_work = A((size_t)B * D);
   m->emb = A((size_t)B * m->NA);
   m->A0 = A(rows * 4 * mel);
   m->xe = A(rows * D);
@@ -231,12 +249,9 @@ extern "C" int lx_dit_create(const lx_dit_weights* w, int B, int max_T, lx_dit**
   m->att = A(rows * D);
   m->ff = A(rows * F);
   m->P = A(rows * mel);
+  m->Pws = A(rows * mel * kProjSplitMax);
   m->pos = a.alloc<int>(max_T);
   ok = ok && m->pos;
-  m->x_in = A((size_t)2 * mel * max_T);
-  m->mu_in = A((size_t)2 * mel * max_T);
-  m->cond_in = A((size_t)2 * mel * max_T);
-  m->spks_in = A((size_t)2 * mel);
   if (!ok) {
     delete m;
     set_error("dit_create: device allocation failed");
@@ -320,7 +335,8 @@ extern "C" int lx_dit_forward(lx_dit* m, const float* x, const float* mu, const 
                               hipStream_t s) {
   LX_REQUIRE(m && x && mu && cond && spks && t && dphi, "dit_forward: null argument");
   LX_REQUIRE(T >= 1 && T <= m->max_T, "dit_forward: T=%d outside [1, %d]", T, m->max_T);
-  LX_TRY(forward_core(m, x, mu, cond, spks, t, T, s));
+  LX_TRY(forward_core(m, x, (long)m->mel * T, mu, cond, spks, 0, t, nullptr, T, s));
+  LX_TRY(proj_rows(m, T, s));
   return dit_unpack_output(m->P, dphi, m->B, T, m->mel, s);
 }
 
@@ -330,16 +346,13 @@ extern "C" int lx_cfm_step(lx_dit* m, float* x, const float* mu, const float* co
   LX_REQUIRE(m && x && mu && cond && spks, "cfm_step: null argument");
   LX_REQUIRE(m->B == 2, "cfm_step: the estimator must be built with B == 2 (CFG pair)");
   LX_REQUIRE(T >= 1 && T <= m->max_T, "cfm_step: T=%d outside [1, %d]", T, m->max_T);
-  const long n = (long)m->mel * T;
-  // Batch-2 inputs: conditional row 0, unconditional row 1 (= 0) (src/flow/flow.cpp:215-224).
-  LX_TRY(fill_batch(m->x_in, x, n, 2, 0, s));
-  LX_TRY(fill_batch(m->mu_in, mu, n, 2, 1, s));
-  LX_TRY(fill_batch(m->cond_in, cond, n, 2, 1, s));
-  LX_TRY(fill_batch(m->spks_in, spks, m->mel, 2, 1, s));
-  LX_TRY(fill_f32(m->t_dev, 2, t, s));
-  LX_TRY(forward_core(m, m->x_in, m->mu_in, m->cond_in, m->spks_in, m->t_dev, T, s));
+  // Batch-2 inputs (src/flow/flow.cpp:215-224): both rows read x (batch stride
+  // 0); mu, cond and spks feed the conditional row, zeros the unconditional one.
+  const float tt[2] = {t, t};
+  LX_TRY(forward_core(m, x, 0, mu, cond, spks, 1, nullptr, tt, T, s));
   // combined = (1+cfg) dphi_cond - cfg dphi_uncond; x += dt * combined (flow.cpp:256-259)
-  return cfm_euler_update(x, m->P, T, m->mel, dt, 1.0f + cfg_rate, cfg_rate, s);
+  return cfm_euler_update(x, m->Pws, m->proj_splits, m->proj_slice, m->proj_b, T, m->mel, dt,
+                          1.0f + cfg_rate, cfg_rate, s);
 }
 
 extern "C" int lx_cfm_solve(lx_dit* m, float* x, const float* mu, const float* cond,
@@ -356,17 +369,13 @@ extern "C" int lx_cfm_solve(lx_dit* m, float* x, const float* mu, const float* c
     float tt = (float)i / (float)n_steps;
     t_span[i] = 1.0f - cosf(tt * 0.5f * PI);
   }
-  const long n = (long)m->mel * T;
-  LX_TRY(fill_batch(m->mu_in, mu, n, 2, 1, s));
-  LX_TRY(fill_batch(m->cond_in, cond, n, 2, 1, s));
-  LX_TRY(fill_batch(m->spks_in, spks, m->mel, 2, 1, s));
   float t = t_span[0];
   float dt = t_span[1] - t_span[0];
   for (int step = 1; step <= n_steps; ++step) {
-    LX_TRY(fill_batch(m->x_in, x, n, 2, 0, s));
-    LX_TRY(fill_f32(m->t_dev, 2, t, s));
-    LX_TRY(forward_core(m, m->x_in, m->mu_in, m->cond_in, m->spks_in, m->t_dev, T, s));
-    LX_TRY(cfm_euler_update(x, m->P, T, m->mel, dt, 1.0f + cfg_rate, cfg_rate, s));
+    const float tt[2] = {t, t};
+    LX_TRY(forward_core(m, x, 0, mu, cond, spks, 1, nullptr, tt, T, s));
+    LX_TRY(cfm_euler_update(x, m->Pws, m->proj_splits, m->proj_slice, m->proj_b, T, m->mel, dt,
+                            1.0f + cfg_rate, cfg_rate, s));
     t += dt;
     if (step < n_steps) dt = t_span[step + 1] - t;
   }

@@ -3,6 +3,8 @@
 // are weight-streaming (HBM-bound on W), so each wave owns R output rows at a
 // time, keeps R float4 weight loads in flight per lane, and reduces with
 // wave64 shuffles.  The activations are staged in LDS with act_in applied.
+#include <cstring>
+
 #include "lx_common.hpp"
 #include "lx_internal.hpp"
 
@@ -13,17 +15,13 @@ constexpr int kGemvWaves = 4;
 constexpr int kGemvRows = 4;
 constexpr int kGemvBMax = 8;
 
-template <int ACT_IN, int ACT_OUT>
-__global__ __launch_bounds__(kGemvWaves * kWave) void gemv_kernel(
-    const float* __restrict__ x, int B, int K, const float* __restrict__ W,
-    const float* __restrict__ bias, float* __restrict__ y, long N, long ldy) {
-  extern __shared__ float xs[];  // B * K
-  for (int i = threadIdx.x; i < B * K; i += blockDim.x) {
-    float v = x[i];
-    if (ACT_IN == 1) v = v / (1.0f + expf(-v));
-    xs[i] = v;
-  }
-  __syncthreads();
+// Dot products of the staged activations xs (B x K, LDS) with rows of W: each
+// wave owns kGemvRows output rows at a time.
+template <int ACT_OUT>
+__device__ __forceinline__ void gemv_rows(const float* xs, int B, int K,
+                                          const float* __restrict__ W,
+                                          const float* __restrict__ bias, float* __restrict__ y,
+                                          long N, long ldy) {
   const int wave = threadIdx.x / kWave;
   const int lane = threadIdx.x % kWave;
   const int K4 = K >> 2;
@@ -70,6 +68,67 @@ __global__ __launch_bounds__(kGemvWaves * kWave) void gemv_kernel(
   }
 }
 
+template <int ACT_IN, int ACT_OUT>
+__global__ __launch_bounds__(kGemvWaves * kWave) void gemv_kernel(
+    const float* __restrict__ x, int B, int K, const float* __restrict__ W,
+    const float* __restrict__ bias, float* __restrict__ y, long N, long ldy) {
+  extern __shared__ __attribute__((aligned(16))) float xs[];  // B * K
+  // Stage act_in(x): float4 loads, all of a thread's loads issued before the
+  // first LDS store (B * K is at most 16K floats: 16 float4 per thread).
+  const int n4 = (B * K) >> 2;
+  const float4* x4 = reinterpret_cast<const float4*>(x);
+  float4* xs4 = reinterpret_cast<float4*>(xs);
+  for (int i0 = threadIdx.x; i0 < n4; i0 += 4 * (int)blockDim.x) {
+    float4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int i = i0 + u * (int)blockDim.x;
+      v[u] = i < n4 ? x4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int i = i0 + u * (int)blockDim.x;
+      if (i < n4) {
+        if (ACT_IN == 1) {
+          v[u].x = v[u].x / (1.0f + expf(-v[u].x));
+          v[u].y = v[u].y / (1.0f + expf(-v[u].y));
+          v[u].z = v[u].z / (1.0f + expf(-v[u].z));
+          v[u].w = v[u].w / (1.0f + expf(-v[u].w));
+        }
+        xs4[i] = v[u];
+      }
+    }
+  }
+  __syncthreads();
+  gemv_rows<ACT_OUT>(xs, B, K, W, bias, y, N, ldy);
+}
+
+// First layer of the time MLP with the sinusoidal embedding of t (a6) formed
+// in LDS: xs[b, j] = sin(scale t_b c_j), xs[b, half + j] = cos(scale t_b c_j),
+// the same expression as the standalone timestep kernel.  t comes from device
+// memory (tdev) or, when tdev is null, from the kernel arguments.
+struct TimeArgs {
+  float c[128];  // c_j = exp(-j ln(1e4) / (half - 1))
+  float t[kGemvBMax];
+};
+
+__global__ __launch_bounds__(kGemvWaves * kWave) void time_mlp0_kernel(
+    const float* __restrict__ tdev, TimeArgs ta, int B, int half, float scale,
+    const float* __restrict__ W, const float* __restrict__ bias, float* __restrict__ y, long N) {
+  extern __shared__ __attribute__((aligned(16))) float xs[];  // B * 2 half
+  for (int i = threadIdx.x; i < B * half; i += blockDim.x) {
+    const int b = i / half, j = i - b * half;
+    const float ts = scale * (tdev ? tdev[b] : ta.t[b]);
+    const float ang = ts * ta.c[j];
+    float sn, cs;
+    sincosf(ang, &sn, &cs);
+    xs[b * 2 * half + j] = sn;
+    xs[b * 2 * half + half + j] = cs;
+  }
+  __syncthreads();
+  gemv_rows<1>(xs, B, 2 * half, W, bias, y, N, N);
+}
+
 }  // namespace
 
 int gemv(const float* x, int B, int K, const float* W, const float* bias, float* y, long N,
@@ -78,7 +137,7 @@ int gemv(const float* x, int B, int K, const float* W, const float* bias, float*
   LX_REQUIRE(B > 0 && B <= kGemvBMax && K > 0 && K % 4 == 0 && N > 0,
              "gemv: bad shape B=%d K=%d N=%ld", B, K, N);
   LX_REQUIRE((size_t)B * K * sizeof(float) <= 64 * 1024, "gemv: B*K too large for LDS");
-  LX_REQUIRE(((uintptr_t)W) % 16 == 0, "gemv: W must be 16-byte aligned");
+  LX_REQUIRE(((uintptr_t)W | (uintptr_t)x) % 16 == 0, "gemv: x and W must be 16-byte aligned");
   long rows_per_block = (long)kGemvWaves * kGemvRows;
   long g = (N + rows_per_block - 1) / rows_per_block;
   if (g > 4096) g = 4096;
@@ -95,6 +154,26 @@ int gemv(const float* x, int B, int K, const float* W, const float* bias, float*
   return check_launch("gemv_kernel");
 }
 
+int time_mlp(const float* tdev, const float* thost, int B, const float* w0, const float* b0,
+             const float* w2, const float* b2, int D, float* hid, float* out, hipStream_t stream) {
+  LX_REQUIRE((tdev || thost) && w0 && b0 && w2 && b2 && hid && out, "time_mlp: null pointer");
+  LX_REQUIRE(B > 0 && B <= kGemvBMax && D > 0 && D % 4 == 0, "time_mlp: bad shape");
+  LX_REQUIRE(((uintptr_t)w0 | (uintptr_t)hid) % 16 == 0, "time_mlp: w0 and work must be 16-byte aligned");
+  const int half = 128;  // SinusPositionEmbedding(256)
+  TimeArgs ta;
+  std::memset(&ta, 0, sizeof(ta));
+  timestep_coeff(half, ta.c);
+  if (!tdev)
+    for (int b = 0; b < B; ++b) ta.t[b] = thost[b];
+  const long rows_per_block = (long)kGemvWaves * kGemvRows;
+  const long g = (D + rows_per_block - 1) / rows_per_block;
+  hipLaunchKernelGGL(time_mlp0_kernel, dim3((unsigned)g), dim3(kGemvWaves * kWave),
+                     (size_t)B * 2 * half * sizeof(float), stream, tdev, ta, B, half, 1000.0f, w0,
+                     b0, hid, (long)D);
+  LX_TRY(check_launch("time_mlp0_kernel"));
+  return gemv(hid, B, D, w2, b2, out, D, D, 0, 0, stream);
+}
+
 }  // namespace lx
 
 using namespace lx;
@@ -107,14 +186,7 @@ extern "C" int lx_adaln_emb_f32(const float* c, const float* W, const float* bia
 extern "C" int lx_time_mlp_f32(const float* t, int B, const float* w0, const float* b0,
                                const float* w2, const float* b2, int D, float* work,
                                float* out, hipStream_t stream) {
-  LX_REQUIRE(t && w0 && b0 && w2 && b2 && work && out, "time_mlp: null pointer");
-  LX_REQUIRE(B > 0 && B <= kGemvBMax && D > 0 && D % 4 == 0, "time_mlp: bad shape");
-  const int F = 256;  // SinusPositionEmbedding(256)
-  float* sinus = work;
-  float* hid = work + (long)B * F;
-  int rc = lx_timestep_embed_f32(t, B, F / 2, 1000.0f, sinus, stream);
-  if (rc) return rc;
-  rc = gemv(sinus, B, F, w0, b0, hid, D, D, 0, /*act_out=silu*/ 1, stream);
-  if (rc) return rc;
-  return gemv(hid, B, D, w2, b2, out, D, D, 0, 0, stream);
+  LX_REQUIRE(t && work, "time_mlp: null pointer");
+  // work: B * (256 + D) floats; the hidden layer uses the last B * D of them.
+  return time_mlp(t, nullptr, B, w0, b0, w2, b2, D, work + (long)B * 256, out, stream);
 }

@@ -35,23 +35,43 @@ struct Arena {
 int gemv(const float* x, int B, int K, const float* W, const float* bias, float* y, long N,
          long ldy, int act_in, int act_out, hipStream_t stream);
 
+// Sinusoid coefficients c_j = exp(-j ln(1e4) / (half - 1)), j < half (host).
+void timestep_coeff(int half, float* c);
+
+// TimestepEmbedding on the device: sinusoid(256, scale 1000) of t -> Linear ->
+// SiLU -> Linear, the sinusoid formed inside the first layer's kernel.  t is
+// read from device memory (tdev) or, when tdev is null, taken from the host
+// array thost (B values).  hid: B * D floats of scratch.
+int time_mlp(const float* tdev, const float* thost, int B, const float* w0, const float* b0,
+             const float* w2, const float* b2, int D, float* hid, float* out, hipStream_t stream);
+
 // Skinny-M path of lx_linear_f32 (M <= 8) with the same epilogue contract.
 int gemv_epi(const float* x, int ldx, const float* W, const float* bias, float* y, int ldy,
              int M, int N, int K, const lx_epilogue* epi, hipStream_t stream);
 
 // DiT input packing: A[b*T + t, :] = [x[b,:,t], cond[b,:,t], mu[b,:,t], spks[b,:]]
-// (the concat order of src/flow/dit.cpp:109), A row stride 4*mel.
-int dit_pack_input(const float* x, const float* cond, const float* mu, const float* spks,
-                   float* A, int B, int T, int mel, hipStream_t stream);
+// (the concat order of src/flow/dit.cpp:109), A row stride 4*mel.  x of batch b
+// starts at x + b * x_bstride (mel*T for a (B, mel, T) tensor; 0 feeds the same
+// x to every batch row, as the CFG pair does).  cfg != 0: cond, mu, spks are
+// the conditional row's tensors and the other rows get zeros
+// (src/flow/flow.cpp:215-224).
+int dit_pack_input(const float* x, long x_bstride, const float* cond, const float* mu,
+                   const float* spks, int cfg, float* A, int B, int T, int mel,
+                   hipStream_t stream);
 
 // (B*T, mel) row-major -> (B, mel, T): the proj_out permute + cont of
 // src/flow/dit.cpp:139-140.
 int dit_unpack_output(const float* P, float* dphi, int B, int T, int mel, hipStream_t stream);
 
 // CFG combine + Euler update straight from the proj_out rows:
-// x[c, t] += dt * (a * P[t, c] - b * P[T + t, c]).
-int cfm_euler_update(float* x, const float* P, int T, int mel, float dt, float a, float b,
-                     hipStream_t stream);
+// x[c, t] += dt * (a * P[t, c] - b * P[T + t, c]), where P is the sum of
+// `splits` K slices `slice` floats apart (slice order) plus bias (may be null).
+int cfm_euler_update(float* x, const float* P, int splits, long slice, const float* bias, int T,
+                     int mel, float dt, float a, float b, hipStream_t stream);
+
+// P (rows, mel) = sum of the split-K slices of ws (slice order) + bias.
+int proj_reduce(const float* ws, int splits, long slice, const float* bias, float* P, int rows,
+                int mel, hipStream_t stream);
 
 // Duplicate a (rows, n) block into (copies * rows, n) (CFG batch [v; v] / [v; 0]).
 int fill_batch(float* dst, const float* src, long n, int copies, int zero_tail,

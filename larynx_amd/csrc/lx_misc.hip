@@ -9,11 +9,13 @@ namespace {
 
 // A[b*T + t, j]: j in [0,mel) x, [mel,2mel) cond, [2mel,3mel) mu, [3mel,4mel) spks.
 // 32x32 tiles through LDS so both the (C, T) reads and the (T, 4C) writes
-// are coalesced.
-__global__ __launch_bounds__(256) void pack_input_kernel(const float* __restrict__ x,
+// are coalesced.  x rows of batch b start at b * xbs (0: one x for every row).
+// With cfg set, cond / mu / spks are single (unbatched) tensors for batch 0 and
+// zero for the other rows (the unconditional half of the CFG pair).
+__global__ __launch_bounds__(256) void pack_input_kernel(const float* __restrict__ x, long xbs,
                                                          const float* __restrict__ cond,
                                                          const float* __restrict__ mu,
-                                                         const float* __restrict__ spks,
+                                                         const float* __restrict__ spks, int cfg,
                                                          float* __restrict__ A, int T, int mel) {
   __shared__ float tile[32][33];
   const int b = blockIdx.z;
@@ -26,7 +28,10 @@ __global__ __launch_bounds__(256) void pack_input_kernel(const float* __restrict
   for (int i = ty; i < 32; i += 8) {
     const int c = c0 + i, t = t0 + tx;
     float v = 0.0f;
-    if (c < mel && t < T) v = src == 3 ? spks[(long)b * mel + c] : s[((long)b * mel + c) * T + t];
+    if (c < mel && t < T && (src == 0 || !cfg || b == 0))
+      v = src == 3   ? spks[(long)b * mel + c]
+          : src == 0 ? s[(long)b * xbs + (long)c * T + t]
+                     : s[((long)b * mel + c) * T + t];
     tile[i][tx] = v;
   }
   __syncthreads();
@@ -57,10 +62,20 @@ __global__ __launch_bounds__(256) void unpack_output_kernel(const float* __restr
   }
 }
 
+// Row t, column c of the proj_out rows: the K slices of a split-K product
+// summed in slice order, then the bias (P itself when splits = 1, no bias).
+__device__ __forceinline__ float proj_row_val(const float* __restrict__ P, int splits, long slice,
+                                              const float* __restrict__ bias, long idx, int c) {
+  float v = P[idx];
+  for (int s = 1; s < splits; ++s) v += P[s * slice + idx];
+  return bias ? v + bias[c] : v;
+}
+
 // x[c, t] += dt * (a * P[t, c] - bb * P[T + t, c])
 __global__ __launch_bounds__(256) void euler_kernel(float* __restrict__ x,
-                                                    const float* __restrict__ P, int T, int mel,
-                                                    float dt, float a, float bb) {
+                                                    const float* __restrict__ P, int splits,
+                                                    long slice, const float* __restrict__ bias,
+                                                    int T, int mel, float dt, float a, float bb) {
   __shared__ float t0s[32][33], t1s[32][33];
   const int ctiles = (mel + 31) / 32;
   const int ct = blockIdx.x % ctiles, tt = blockIdx.x / ctiles;
@@ -69,8 +84,8 @@ __global__ __launch_bounds__(256) void euler_kernel(float* __restrict__ x,
   for (int i = ty; i < 32; i += 8) {
     const int t = t0 + i, c = c0 + tx;
     const bool ok = c < mel && t < T;
-    t0s[i][tx] = ok ? P[(long)t * mel + c] : 0.0f;
-    t1s[i][tx] = ok ? P[((long)T + t) * mel + c] : 0.0f;
+    t0s[i][tx] = ok ? proj_row_val(P, splits, slice, bias, (long)t * mel + c, c) : 0.0f;
+    t1s[i][tx] = ok ? proj_row_val(P, splits, slice, bias, ((long)T + t) * mel + c, c) : 0.0f;
   }
   __syncthreads();
   for (int i = ty; i < 32; i += 8) {
@@ -81,6 +96,15 @@ __global__ __launch_bounds__(256) void euler_kernel(float* __restrict__ x,
       *xp = *xp + dt * comb;
     }
   }
+}
+
+// P[r, c] = sum of the K slices (slice order) + bias[c]
+__global__ void proj_reduce_kernel(const float* __restrict__ ws, int splits, long slice,
+                                   const float* __restrict__ bias, float* __restrict__ P, int mel,
+                                   long n) {
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (long)gridDim.x * blockDim.x)
+    P[i] = proj_row_val(ws, splits, slice, bias, i, (int)(i % mel));
 }
 
 __global__ void fill_batch_kernel(float* dst, const float* __restrict__ src, long n, int copies,
@@ -125,11 +149,12 @@ inline unsigned grid1d(long n) {
 
 }  // namespace
 
-int dit_pack_input(const float* x, const float* cond, const float* mu, const float* spks,
-                   float* A, int B, int T, int mel, hipStream_t stream) {
+int dit_pack_input(const float* x, long x_bstride, const float* cond, const float* mu,
+                   const float* spks, int cfg, float* A, int B, int T, int mel,
+                   hipStream_t stream) {
   const int ctiles = (mel + 31) / 32, ttiles = (T + 31) / 32;
   hipLaunchKernelGGL(pack_input_kernel, dim3(ctiles * ttiles, 4, B), dim3(256), 0, stream, x,
-                     cond, mu, spks, A, T, mel);
+                     x_bstride, cond, mu, spks, cfg, A, T, mel);
   return check_launch("pack_input_kernel");
 }
 
@@ -140,12 +165,20 @@ int dit_unpack_output(const float* P, float* dphi, int B, int T, int mel, hipStr
   return check_launch("unpack_output_kernel");
 }
 
-int cfm_euler_update(float* x, const float* P, int T, int mel, float dt, float a, float b,
-                     hipStream_t stream) {
+int cfm_euler_update(float* x, const float* P, int splits, long slice, const float* bias, int T,
+                     int mel, float dt, float a, float b, hipStream_t stream) {
   const int ctiles = (mel + 31) / 32, ttiles = (T + 31) / 32;
-  hipLaunchKernelGGL(euler_kernel, dim3(ctiles * ttiles), dim3(256), 0, stream, x, P, T, mel, dt,
-                     a, b);
+  hipLaunchKernelGGL(euler_kernel, dim3(ctiles * ttiles), dim3(256), 0, stream, x, P, splits,
+                     slice, bias, T, mel, dt, a, b);
   return check_launch("euler_kernel");
+}
+
+int proj_reduce(const float* ws, int splits, long slice, const float* bias, float* P, int rows,
+                int mel, hipStream_t stream) {
+  const long n = (long)rows * mel;
+  hipLaunchKernelGGL(proj_reduce_kernel, dim3(grid1d(n)), dim3(256), 0, stream, ws, splits, slice,
+                     bias, P, mel, n);
+  return check_launch("proj_reduce_kernel");
 }
 
 int fill_batch(float* dst, const float* src, long n, int copies, int zero_tail,

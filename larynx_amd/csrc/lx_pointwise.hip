@@ -211,6 +211,14 @@ __global__ void gather_kernel1(const float* __restrict__ table, int D, IdChunk i
 }
 
 }  // namespace
+
+// Coefficients exactly as the reference host loop forms them
+// (src/flow/flow_matching.cpp:161-163): fp32 product then expf.
+void timestep_coeff(int half, float* c) {
+  const float step = (float)(std::log(10000.0) / (double)(half - 1));
+  for (int j = 0; j < half; ++j) c[j] = expf(-(float)j * step);
+}
+
 }  // namespace lx
 
 using namespace lx;
@@ -293,12 +301,9 @@ extern "C" int lx_timestep_embed_f32(const float* t, int B, int half_dim, float 
                                      float* out, hipStream_t stream) {
   LX_REQUIRE(t && out, "timestep_embed: null pointer");
   LX_REQUIRE(B > 0 && half_dim > 1 && half_dim <= 256, "timestep_embed: bad shape");
-  // Coefficients exactly as the reference host loop forms them
-  // (src/flow/flow_matching.cpp:161-163): fp32 product then expf.
   Table<256> coeff;
   std::memset(&coeff, 0, sizeof(coeff));
-  const float step = (float)(std::log(10000.0) / (double)(half_dim - 1));
-  for (int j = 0; j < half_dim; ++j) coeff.v[j] = expf(-(float)j * step);
+  timestep_coeff(half_dim, coeff.v);
   hipLaunchKernelGGL(timestep_kernel, dim3(B), dim3(128), 0, stream, t, B, half_dim, scale, out,
                      coeff);
   return check_launch("timestep_kernel");
