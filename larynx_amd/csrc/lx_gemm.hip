@@ -27,6 +27,7 @@ namespace {
 
 struct EpiArgs {
   int kind;
+  int vec;  // y, bias, gate rows 16-byte aligned: float4 epilogue path
   int rows_per_batch;
   const float* gate;
   long gate_stride;
@@ -93,6 +94,41 @@ __device__ __forceinline__ void epilogue4(float* Y, int ldy, int m, int n, int N
     for (int e = 0; e < 4; ++e)
       if (e < nv) yp[e] = vv[e];
   }
+}
+
+// float4 epilogue of 4 columns n..n+3 (all < N) of row m with its operands
+// already loaded: b = bias[n..n+3], g = gate row segment, yo = the residual.
+// Same per-component operations as epilogue4.
+template <int EPI>
+__device__ __forceinline__ void epilogue4v(float* Y, int ldy, int m, int n, float4 v, float4 b,
+                                           float4 g, float4 yo, int posm, const EpiArgs& ep) {
+  float vv[4] = {v.x + b.x, v.y + b.y, v.z + b.z, v.w + b.w};
+  if (EPI == LX_EPI_SWIGLU_PAIRED) {
+    float2 o;
+    o.x = (vv[0] / (1.0f + expf(-vv[0]))) * vv[1];
+    o.y = (vv[2] / (1.0f + expf(-vv[2]))) * vv[3];
+    *reinterpret_cast<float2*>(Y + (long)m * ldy + (n >> 1)) = o;
+    return;
+  }
+  if (EPI == LX_EPI_GELU_TANH) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) vv[e] = gelu_tanh(vv[e]);
+  }
+  if (EPI == LX_EPI_ROPE_PARTIAL) {
+    const int cs = n % ep.section;
+    if (n < ep.sections * ep.section && cs < ep.rot_dim) {
+      const float p = (float)posm;
+      const int i0 = cs >> 1;
+      rotate_pair(vv[0], vv[1], p * ep.inv_freq[i0]);
+      rotate_pair(vv[2], vv[3], p * ep.inv_freq[i0 + 1]);
+    }
+  }
+  float4 o = make_float4(vv[0], vv[1], vv[2], vv[3]);
+  if (EPI == LX_EPI_GATED_RESID)
+    o = make_float4(yo.x + vv[0] * g.x, yo.y + vv[1] * g.y, yo.z + vv[2] * g.z, yo.w + vv[3] * g.w);
+  else if (EPI == LX_EPI_RESID)
+    o = make_float4(yo.x + vv[0], yo.y + vv[1], yo.z + vv[2], yo.w + vv[3]);
+  *reinterpret_cast<float4*>(Y + (long)m * ldy + n) = o;
 }
 
 // Tiled NT GEMM.  BM x BN output tile per workgroup; WM x WN waves per k-group,
@@ -298,7 +334,7 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void gemm_tile_kernel(
 // loads, then the barrier, then the next slab's fragment reads are issued and
 // the last 4 MFMAs (operands already in registers) cover their latency, so the
 // matrix pipe does not drain at every barrier.
-template <int EPI, int BK, int KS, bool IL, bool KMASK, bool XB = false>
+template <int EPI, int BK, int KS, bool IL, bool KMASK, bool XB = false, bool BUF = true>
 __global__ __launch_bounds__(256 * KS) void gemm_pipe_kernel(
     const float* X, int ldx, const float* W, int ldw,
     const float* __restrict__ bias, float* Y, int ldy, int M, int N, int K, int ksplit,
@@ -317,7 +353,17 @@ __global__ __launch_bounds__(256 * KS) void gemm_pipe_kernel(
   int id = blockIdx.x;
   const int full = (nwg / 8) * 8;
   if (id < full) id = (id % 8) * (full / 8) + id / 8;
-  const int m0 = (id % tiles_m) * BM, n0 = (id / tiles_m) * BN;
+  // Runs of 8 M-tiles with N fastest across a run: the contiguous id range of
+  // one XCD covers a compact block of A rows and W rows (fewer L2 refills).
+  int mt, nt;
+  {
+    const int grp = id / (8 * tiles_n);
+    const int gs = min(8, tiles_m - grp * 8);
+    const int in = id - grp * 8 * tiles_n;
+    mt = grp * 8 + in % gs;
+    nt = in / gs;
+  }
+  const int m0 = mt * BM, n0 = nt * BN;
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -334,24 +380,42 @@ __global__ __launch_bounds__(256 * KS) void gemm_pipe_kernel(
   Y += (long)blockIdx.y * M * ldy;
   K = min(ksplit, K - (int)blockIdx.y * ksplit);
 
+  // Operand loads.  BUF: through buffer descriptors over the K slice, each
+  // lane's byte offset fixed for the whole loop and the slab advancing through
+  // the scalar offset, so the loop carries no address arithmetic; rows past M
+  // (N) lie beyond the descriptor's range and read as zeros (the host keeps
+  // every offset below 2^31).  Otherwise: 64-bit addresses with rows clamped
+  // into range.  Columns past K (KMASK) are zeroed when stored to LDS.
   const float* pa[L];
   const float* pw[L];
+  int oa[L], ow[L];
   int cc[L], rr[L];
+  const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)X, (short)0, BUF ? (int)(((long)(M - 1) * ldx + K) * 4) : 0, 0x00020000);
+  const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)W, (short)0, BUF ? (int)(((long)(N - 1) * ldw + K) * 4) : 0, 0x00020000);
 #pragma unroll
   for (int i = 0; i < L; ++i) {
     const int idx = gtid + i * GT;
     rr[i] = idx / (BK / 4);
     cc[i] = (idx % (BK / 4)) * 4;
+    oa[i] = ((m0 + rr[i]) * ldx + cc[i]) * 4;
+    ow[i] = ((n0 + rr[i]) * ldw + cc[i]) * 4;
     pa[i] = X + (long)min(m0 + rr[i], M - 1) * ldx;
     pw[i] = W + (long)min(n0 + rr[i], N - 1) * ldw;
   }
   floatx4 sa0[L], sw0[L], sa1[L], sw1[L];  // two register stages
-#define LX_GLOAD(SA, SW, KT)                                                         \
-  do {                                                                               \
-    _Pragma("unroll") for (int i = 0; i < L; ++i) {                                   \
-      SA[i] = *reinterpret_cast<const floatx4*>(pa[i] + min((KT) * BK + cc[i], K - 4)); \
-      SW[i] = *reinterpret_cast<const floatx4*>(pw[i] + min((KT) * BK + cc[i], K - 4)); \
-    }                                                                                \
+#define LX_GLOAD(SA, SW, KT)                                                            \
+  do {                                                                                  \
+    _Pragma("unroll") for (int i = 0; i < L; ++i) {                                      \
+      if (BUF) {                                                                        \
+        SA[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, oa[i], (KT) * (BK * 4), 0);  \
+        SW[i] = __builtin_amdgcn_raw_buffer_load_b128(wrs, ow[i], (KT) * (BK * 4), 0);  \
+      } else {                                                                          \
+        SA[i] = *reinterpret_cast<const floatx4*>(pa[i] + min((KT) * BK + cc[i], K - 4)); \
+        SW[i] = *reinterpret_cast<const floatx4*>(pw[i] + min((KT) * BK + cc[i], K - 4)); \
+      }                                                                                 \
+    }                                                                                   \
   } while (0)
 #define LX_SSTORE(SA, SW, BUF, KT)                                                   \
   do {                                                                               \
@@ -509,6 +573,30 @@ __global__ __launch_bounds__(256 * KS) void gemm_pipe_kernel(
 #undef LX_GLOAD
 #undef LX_SSTORE
 
+  // Epilogue operands of this thread's output float4s (bias, gate, residual,
+  // rotary position) are loaded before the k-group reduction, so their
+  // latency overlaps it.
+  constexpr int SLOTS = BM * BN / 4 / NT;
+  float4 eb[SLOTS], eg[SLOTS], ey[SLOTS];
+  int epos[SLOTS];
+  const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int j = 0; j < SLOTS; ++j) {
+    const int idx = tid + j * NT;
+    const int m = m0 + idx / (BN / 4), n = n0 + (idx % (BN / 4)) * 4;
+    const bool ok = ep.vec && m < M && n + 4 <= N;
+    eb[j] = (ok && bias) ? *reinterpret_cast<const float4*>(bias + n) : z4;
+    eg[j] = z4;
+    ey[j] = z4;
+    epos[j] = 0;
+    if (EPI == LX_EPI_GATED_RESID && ok)
+      eg[j] = *reinterpret_cast<const float4*>(
+          ep.gate + (long)(m / ep.rows_per_batch) * ep.gate_stride + n);
+    if ((EPI == LX_EPI_GATED_RESID || EPI == LX_EPI_RESID) && ok)
+      ey[j] = *reinterpret_cast<const float4*>(Y + (long)m * ldy + n);
+    if (EPI == LX_EPI_ROPE_PARTIAL && ok) epos[j] = ep.pos[m % ep.rows_per_batch];
+  }
+
   constexpr int LDC = BN + 4;
   float* Cs = smem;
 #pragma unroll
@@ -525,12 +613,18 @@ __global__ __launch_bounds__(256 * KS) void gemm_pipe_kernel(
     }
     __syncthreads();
   }
-  for (int idx = tid; idx < BM * BN / 4; idx += NT) {
+#pragma unroll
+  for (int j = 0; j < SLOTS; ++j) {
+    const int idx = tid + j * NT;
     const int row = idx / (BN / 4), c = (idx % (BN / 4)) * 4;
     const int m = m0 + row, n = n0 + c;
-    if (m < M && n < N)
-      epilogue4<EPI>(Y, ldy, m, n, N, bias,
-                     *reinterpret_cast<const float4*>(Cs + row * LDC + c), ep);
+    if (m < M && n < N) {
+      const float4 v = *reinterpret_cast<const float4*>(Cs + row * LDC + c);
+      if (ep.vec && n + 4 <= N)
+        epilogue4v<EPI>(Y, ldy, m, n, v, eb[j], eg[j], ey[j], epos[j], ep);
+      else
+        epilogue4<EPI>(Y, ldy, m, n, N, bias, v, ep);
+    }
   }
 }
 
@@ -552,11 +646,11 @@ struct Split {
   int ldw = 0;
 };
 
-template <int EPI, int BK, int KS, bool IL, bool KMASK, bool XB>
+template <int EPI, int BK, int KS, bool IL, bool KMASK, bool XB, bool BUF>
 int launch_pipe_k(const float* x, int ldx, const float* W, const float* bias, float* y, int ldy,
                   int M, int N, int K, const EpiArgs& ep, hipStream_t stream,
                   const Split& sp) {
-  auto kern = gemm_pipe_kernel<EPI, BK, KS, IL, KMASK, XB>;
+  auto kern = gemm_pipe_kernel<EPI, BK, KS, IL, KMASK, XB, BUF>;
   const size_t lds = PipeCfg<BK, KS>::lds();
   if (lds > 64 * 1024) {
     static bool attr_set = false;
@@ -575,6 +669,13 @@ int launch_pipe_k(const float* x, int ldx, const float* W, const float* bias, fl
   return check_launch("gemm_pipe_kernel");
 }
 
+// Buffer-descriptor loads need every operand byte offset, including the rows
+// of the last tile past M (N), below 2^31.
+inline bool buffer_loads_fit(int M, int ldx, int N, int ldw) {
+  const long lim = 1L << 31;
+  return ((long)(M + 64) * ldx + 64) * 4 < lim && ((long)(N + 64) * ldw + 64) * 4 < lim;
+}
+
 // The unmasked kernel needs every K slice to be whole slabs and its slab
 // count a multiple of 2 KS (the loop runs two slabs per k-group per iteration).
 template <int EPI, int BK, int KS, bool IL, bool XB = false>
@@ -584,10 +685,13 @@ int launch_pipe(const float* x, int ldx, const float* W, const float* bias, floa
   if (sp.ldw <= 0) sp.ldw = K;
   const int step = 2 * KS * BK;
   const bool exact = sp.ksplit % step == 0 && (K % sp.ksplit) % step == 0;
-  return exact ? launch_pipe_k<EPI, BK, KS, IL, false, XB>(x, ldx, W, bias, y, ldy, M, N, K, ep,
-                                                           stream, sp)
-               : launch_pipe_k<EPI, BK, KS, IL, true, XB>(x, ldx, W, bias, y, ldy, M, N, K, ep,
-                                                          stream, sp);
+  if (!buffer_loads_fit(M, ldx, N, sp.ldw))  // operands past 2 GiB: 64-bit addressing
+    return launch_pipe_k<EPI, BK, KS, IL, true, XB, false>(x, ldx, W, bias, y, ldy, M, N, K, ep,
+                                                           stream, sp);
+  return exact ? launch_pipe_k<EPI, BK, KS, IL, false, XB, true>(x, ldx, W, bias, y, ldy, M, N, K,
+                                                                 ep, stream, sp)
+               : launch_pipe_k<EPI, BK, KS, IL, true, XB, true>(x, ldx, W, bias, y, ldy, M, N, K,
+                                                                ep, stream, sp);
 }
 
 template <int BM, int BN, int BK, int WM, int WN, int KS>
@@ -704,6 +808,18 @@ __global__ __launch_bounds__(256) void gemv_epi_kernel(const float* __restrict__
   }
 }
 
+// float4 epilogue: output rows, bias and gate rows 16-byte aligned (the
+// paired SwiGLU output stores float2: 8-byte alignment suffices for it, and
+// 16 bytes is asked anyway).
+bool epi_vec_ok(const EpiArgs& ep, const float* y, int ldy, const float* bias) {
+  const bool swi = ep.kind == LX_EPI_SWIGLU_PAIRED;
+  bool ok = ((uintptr_t)y % 16 == 0) && (swi ? ldy % 2 == 0 : ldy % 4 == 0) &&
+            ((uintptr_t)bias % 16 == 0);
+  if (ep.kind == LX_EPI_GATED_RESID)
+    ok = ok && (uintptr_t)ep.gate % 16 == 0 && ep.gate_stride % 4 == 0;
+  return ok;
+}
+
 int make_epi(const lx_epilogue* e, int N, EpiArgs* out) {
   std::memset(out, 0, sizeof(*out));
   out->kind = e ? e->kind : LX_EPI_NONE;
@@ -774,8 +890,8 @@ int gemv_epi(const float* x, int ldx, const float* W, const float* bias, float* 
   return check_launch("gemv_epi_kernel");
 }
 
-// Configurations.  The library selects among 4, 5, 7 and 8; the others are
-// built only into the tuning sweep:
+// Configurations.  The library selects 7 or 8; the others are built only
+// into the tuning sweep:
 //   0: tiled 64 x 64, BK 32, split-K 2        1: tiled 128 x 64, BK 32
 //   2: pipelined BK 32                        3: pipelined BK 32, split-K 2
 //   4: pipelined BK 32, interleaved           5: pipelined BK 32, split-K 2, interleaved
@@ -788,11 +904,11 @@ template <int EPI>
 int dispatch_cfg(int cfg, const float* x, int ldx, const float* W, const float* bias, float* y,
                  int ldy, int M, int N, int K, const EpiArgs& ep, hipStream_t s) {
   switch (cfg) {
-    case 4: return launch_pipe<EPI, 32, 1, true>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
-    case 5: return launch_pipe<EPI, 32, 2, true>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
     case 7: return launch_pipe<EPI, 32, 1, true, true>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
     case 8: return launch_pipe<EPI, 32, 2, true, true>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
 #ifdef LX_GEMM_SWEEP
+    case 4: return launch_pipe<EPI, 32, 1, true>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
+    case 5: return launch_pipe<EPI, 32, 2, true>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
     case 0: return launch_tile<EPI, Cfg0>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
     case 1: return launch_tile<EPI, Cfg1>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
     case 2: return launch_pipe<EPI, 32, 1, false>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
@@ -826,18 +942,21 @@ int dispatch_gemm(int kind, int cfg, const float* x, int ldx, const float* W, co
 
 // Tile configuration by shape, from an on-device sweep over the estimator's
 // projections at B*T = 1000 and 6000 rows (MI355X, graph-replayed launches
-// under continuous load).  Cross-barrier slabs win everywhere (2-7% over the
-// plain interleaved schedule).  With fewer than 2048 tiles (two workgroups or
-// fewer per CU at B*T = 1000) intra-workgroup split-K 2 gives each SIMD a
-// second wave (QKV 54.1 us = 116 TFLOP/s, out 23.0 us, FF0 38.8 us, FF2
-// 38.2 us); with many tiles, or K <= 512 (too few slabs to split), the unsplit
-// kernel wins (QKV at B*T = 6000: 314 us = 120 TFLOP/s).
+// under continuous load, buffer-descriptor loads).  Cross-barrier slabs win
+// everywhere.  With one tile per CU (256 tiles: out, FF2 at B*T = 1000)
+// intra-workgroup split-K 2 gives each SIMD a second wave (19.2 / 33.8 us).
+// From 512 tiles up the unsplit 4-wave kernel wins: several of its workgroups
+// fit on a CU at once (37 KB of LDS each), so a 768-tile launch (QKV at
+// B*T = 1000: 50.6 us = 124 TFLOP/s) is resident in one round, whereas the
+// split-K 2 kernel (74 KB) runs it in two and the paired workgroups of a CU,
+// finishing together, can be re-placed two to a CU in the partial second round
+// (65 us).  K <= 512 has too few slabs to split.
 // Split-K partial GEMMs aim for this many workgroups (two per CU).
 constexpr long kSplitTargetWgs = 512;
 
 int pick_config(int M, int N, int K) {
   const long tiles = (long)((M + 63) / 64) * ((N + 63) / 64);
-  return (K <= 512 || tiles >= 2048) ? 7 : 8;
+  return (K <= 512 || tiles >= 512) ? 7 : 8;
 }
 
 int gemm_splitk_partials(const float* x, int ldx, const float* W, int ldw, float* ws, int M,
@@ -851,6 +970,7 @@ int gemm_splitk_partials(const float* x, int ldx, const float* W, int ldw, float
   EpiArgs ep;
   int rc = make_epi(nullptr, N, &ep);
   if (rc) return rc;
+  ep.vec = epi_vec_ok(ep, ws, N, nullptr);
   Split sp;
   sp.splits = splits;
   sp.ksplit = ksplit;
@@ -894,6 +1014,7 @@ extern "C" int lx_linear_f32(const float* x, int ldx, const float* W, const floa
   if (rc) return rc;
   if (kind == LX_EPI_SWIGLU_PAIRED)
     LX_REQUIRE(ldy % 2 == 0, "linear: SWIGLU_PAIRED needs even ldy");
+  ep.vec = epi_vec_ok(ep, y, ldy, bias);
   const long tiles = (long)((M + 63) / 64) * ((N + 63) / 64);
   LX_REQUIRE(tiles < (1L << 31), "linear: too many tiles");
   return dispatch_gemm(kind, pick_config(M, N, K), x, ldx, W, bias, y, ldy, M, N, K, ep, stream);
@@ -907,6 +1028,7 @@ extern "C" int lx_gemm_sweep(int cfg, int kind, const float* x, int ldx, const f
   EpiArgs ep;
   int rc = make_epi(epi, N, &ep);
   if (rc) return rc;
+  ep.vec = epi_vec_ok(ep, y, ldy, bias);
   return dispatch_gemm(kind, cfg, x, ldx, W, bias, y, ldy, M, N, K, ep, stream);
 }
 #endif
