@@ -326,15 +326,20 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void gemm_tile_kernel(
 // slab body (one basic block) carries scheduling-group barriers that spread the
 // DS reads, DS writes and global loads between the MFMAs of the wave's single
 // accumulator chain, so they issue in the MFMA shadow instead of in bursts.
-// Operand rows past M (or N) are read from the last valid row and only reach
-// output rows (columns) the epilogue never stores, so they need no mask; with
-// KMASK (K not a multiple of BK) the columns past K are stored to LDS as zeros.
-// With XB (BK = 32 only) the barrier sits inside the slab: the first 12 MFMAs
-// of the slab run alongside the LDS writes of the next slab and the global
-// loads, then the barrier, then the next slab's fragment reads are issued and
-// the last 4 MFMAs (operands already in registers) cover their latency, so the
-// matrix pipe does not drain at every barrier.
-template <int EPI, int BK, int KS, bool IL, bool KMASK, bool XB = false, bool BUF = true>
+// Operand rows past M (or N) read as zeros (buffer loads) or repeat the last
+// valid row (64-bit loads); either way they only reach output rows (columns)
+// the epilogue never stores.  With KMASK (K not a multiple of BK) the columns
+// past K are stored to LDS as zeros.
+// With XB (BK = 32 only; the path the library runs) the barrier sits inside
+// the slab: the first three quarters of the slab's MFMAs run alongside the LDS
+// writes of the next slab and the global loads, then the barrier, then the
+// next slab's fragment reads are issued and the last quarter (operands already
+// in registers) covers their latency, so the matrix pipe does not drain at
+// every barrier.  MF16 selects the wave's 32 x 32 output as four independent
+// 16 x 16 accumulator chains on v_mfma_f32_16x16x4f32 instead of one
+// v_mfma_f32_32x32x2f32 chain.
+template <int EPI, int BK, int KS, bool IL, bool KMASK, bool XB = false, bool BUF = true,
+          bool MF16 = false>
 __global__ __launch_bounds__(256 * KS) void gemm_pipe_kernel(
     const float* X, int ldx, const float* W, int ldw,
     const float* __restrict__ bias, float* Y, int ldy, int M, int N, int K, int ksplit,
@@ -541,7 +546,69 @@ __global__ __launch_bounds__(256 * KS) void gemm_pipe_kernel(
     __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);                                 \
   } while (0)
 
-  if (XB) {
+  // Cross-barrier slab (XB) on 16x16x4 MFMAs: the wave's 32 x 32 output is
+  // 2 x 2 independent 16 x 16 blocks (four accumulator chains).  Lane l feeds
+  // row/column l % 16 of a block and k group g = l / 16, which owns k = g*8 .. g*8+7
+  // of the slab: MFMA step s (0..7) sums k = {0, 8, 16, 24} + s, so each lane's
+  // operands for a slab are 8 contiguous floats (two ds_read_b128) per block row.
+  // Steps 0-5 (24 MFMAs) run before the barrier with the DS writes and global
+  // loads between them; steps 6-7 (8 MFMAs) run after it and cover the next
+  // slab's fragment reads.
+#define LX_MF16(FA, FB, S)                                                             \
+  _Pragma("unroll") for (int bi = 0; bi < 2; ++bi)                                      \
+    _Pragma("unroll") for (int bj = 0; bj < 2; ++bj)                                    \
+      acc4[bi][bj] = __builtin_amdgcn_mfma_f32_16x16x4f32(FA[bi][(S) >> 2][(S) & 3],     \
+                                                          FB[bj][(S) >> 2][(S) & 3],     \
+                                                          acc4[bi][bj], 0, 0, 0)
+#define LX_SLAB_XB16(IT, BUF, SNA, SNW, FA, FB, NA, NB)                                  \
+  do {                                                                                 \
+    _Pragma("unroll") for (int s_ = 0; s_ < 6; ++s_) { LX_MF16(FA, FB, s_); }             \
+    LX_SSTORE(SNA, SNW, (BUF) ^ 1, LX_KT((IT) + 1));                                   \
+    LX_GLOAD(SNA, SNW, LX_KC((IT) + 3));                                               \
+    _Pragma("unroll") for (int q = 0; q < 2 * L; ++q) {                                 \
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);                               \
+      __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);                               \
+    }                                                                                  \
+    _Pragma("unroll") for (int q = 0; q < 2 * L; ++q) {                                 \
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);                               \
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                               \
+    }                                                                                  \
+    __builtin_amdgcn_sched_group_barrier(0x008, 24 - 8 * L, 0);                        \
+    __syncthreads();                                                                   \
+    LX_FRAG16(NA, NB, (BUF) ^ 1);                                                      \
+    LX_MF16(FA, FB, 6);                                                                \
+    LX_MF16(FA, FB, 7);                                                                \
+    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);                                 \
+    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);                                 \
+  } while (0)
+#define LX_FRAG16(NA, NB, BUF)                                                         \
+  do {                                                                                 \
+    const float* nab = As + (BUF) * BM * LDA + (wm * 32 + (lane & 15)) * LDA + (lane >> 4) * 8; \
+    const float* nwb = Ws + (BUF) * BN * LDA + (wn * 32 + (lane & 15)) * LDA + (lane >> 4) * 8; \
+    _Pragma("unroll") for (int b_ = 0; b_ < 2; ++b_)                                    \
+      _Pragma("unroll") for (int q_ = 0; q_ < 2; ++q_) {                                \
+        NA[b_][q_] = *reinterpret_cast<const floatx4*>(nab + b_ * 16 * LDA + 4 * q_);    \
+        NB[b_][q_] = *reinterpret_cast<const floatx4*>(nwb + b_ * 16 * LDA + 4 * q_);    \
+      }                                                                                \
+  } while (0)
+
+  floatx4 acc4[2][2];
+#pragma unroll
+  for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+    for (int bj = 0; bj < 2; ++bj)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc4[bi][bj][i] = 0.0f;
+
+  if (XB && MF16) {
+    static_assert(!XB || BK == 32, "XB needs one 32-wide sub-slab per slab");
+    floatx4 fa0[2][2], fb0[2][2], fa1[2][2], fb1[2][2];
+    LX_FRAG16(fa0, fb0, 0);
+    for (int it = 0; it < iters; it += 2) {
+      LX_SLAB_XB16(it, 0, sa1, sw1, fa0, fb0, fa1, fb1);
+      LX_SLAB_XB16(it + 1, 1, sa0, sw0, fa1, fb1, fa0, fb0);
+    }
+  } else   if (XB) {
     static_assert(!XB || BK == 32, "XB needs one 32-wide sub-slab per slab");
     floatx4 fa0[4], fb0[4], fa1[4], fb1[4];
     {
@@ -567,6 +634,9 @@ __global__ __launch_bounds__(256 * KS) void gemm_pipe_kernel(
     }
   }
 #undef LX_SLAB_XB
+#undef LX_SLAB_XB16
+#undef LX_FRAG16
+#undef LX_MF16
 #undef LX_SLAB
 #undef LX_KC
 #undef LX_KT
@@ -604,9 +674,15 @@ __global__ __launch_bounds__(256 * KS) void gemm_pipe_kernel(
     if (kg == g) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const int row = wm * 32 + (i >> 2) * 8 + h * 4 + (i & 3);
-        const int col = wn * 32 + r;
-        float v = acc[i];
+        // 32x32x2: register i of lane (r, h) is row (i/4)*8 + h*4 + i%4, col r;
+        // 16x16x4 blocks: register v of block (bi, bj), lane l is row
+        // bi*16 + 4*(l/16) + v, col bj*16 + l%16
+        constexpr bool B16 = XB && MF16;
+        const int bi = i >> 3, bj = (i >> 2) & 1, v4 = i & 3;
+        const int row = B16 ? wm * 32 + bi * 16 + 4 * (lane >> 4) + v4
+                            : wm * 32 + (i >> 2) * 8 + h * 4 + (i & 3);
+        const int col = B16 ? wn * 32 + bj * 16 + (lane & 15) : wn * 32 + r;
+        float v = B16 ? acc4[bi][bj][v4] : acc[i];
         if (g < KS - 1) v += Cs[row * LDC + col];
         Cs[row * LDC + col] = v;
       }
@@ -646,11 +722,11 @@ struct Split {
   int ldw = 0;
 };
 
-template <int EPI, int BK, int KS, bool IL, bool KMASK, bool XB, bool BUF>
+template <int EPI, int BK, int KS, bool IL, bool KMASK, bool XB, bool BUF, bool MF16>
 int launch_pipe_k(const float* x, int ldx, const float* W, const float* bias, float* y, int ldy,
                   int M, int N, int K, const EpiArgs& ep, hipStream_t stream,
                   const Split& sp) {
-  auto kern = gemm_pipe_kernel<EPI, BK, KS, IL, KMASK, XB, BUF>;
+  auto kern = gemm_pipe_kernel<EPI, BK, KS, IL, KMASK, XB, BUF, MF16>;
   const size_t lds = PipeCfg<BK, KS>::lds();
   if (lds > 64 * 1024) {
     static bool attr_set = false;
@@ -678,7 +754,7 @@ inline bool buffer_loads_fit(int M, int ldx, int N, int ldw) {
 
 // The unmasked kernel needs every K slice to be whole slabs and its slab
 // count a multiple of 2 KS (the loop runs two slabs per k-group per iteration).
-template <int EPI, int BK, int KS, bool IL, bool XB = false>
+template <int EPI, int BK, int KS, bool IL, bool XB = false, bool MF16 = false>
 int launch_pipe(const float* x, int ldx, const float* W, const float* bias, float* y, int ldy,
                 int M, int N, int K, const EpiArgs& ep, hipStream_t stream, Split sp = Split()) {
   if (sp.ksplit <= 0) sp.ksplit = K;
@@ -686,12 +762,12 @@ int launch_pipe(const float* x, int ldx, const float* W, const float* bias, floa
   const int step = 2 * KS * BK;
   const bool exact = sp.ksplit % step == 0 && (K % sp.ksplit) % step == 0;
   if (!buffer_loads_fit(M, ldx, N, sp.ldw))  // operands past 2 GiB: 64-bit addressing
-    return launch_pipe_k<EPI, BK, KS, IL, true, XB, false>(x, ldx, W, bias, y, ldy, M, N, K, ep,
-                                                           stream, sp);
-  return exact ? launch_pipe_k<EPI, BK, KS, IL, false, XB, true>(x, ldx, W, bias, y, ldy, M, N, K,
-                                                                 ep, stream, sp)
-               : launch_pipe_k<EPI, BK, KS, IL, true, XB, true>(x, ldx, W, bias, y, ldy, M, N, K,
-                                                                ep, stream, sp);
+    return launch_pipe_k<EPI, BK, KS, IL, true, XB, false, MF16>(x, ldx, W, bias, y, ldy, M, N, K,
+                                                                 ep, stream, sp);
+  return exact ? launch_pipe_k<EPI, BK, KS, IL, false, XB, true, MF16>(x, ldx, W, bias, y, ldy, M,
+                                                                       N, K, ep, stream, sp)
+               : launch_pipe_k<EPI, BK, KS, IL, true, XB, true, MF16>(x, ldx, W, bias, y, ldy, M,
+                                                                      N, K, ep, stream, sp);
 }
 
 template <int BM, int BN, int BK, int WM, int WN, int KS>
@@ -890,13 +966,14 @@ int gemv_epi(const float* x, int ldx, const float* W, const float* bias, float* 
   return check_launch("gemv_epi_kernel");
 }
 
-// Configurations.  The library selects 7 or 8; the others are built only
+// Configurations.  The library selects 7, 8 or 9; the others are built only
 // into the tuning sweep:
 //   0: tiled 64 x 64, BK 32, split-K 2        1: tiled 128 x 64, BK 32
 //   2: pipelined BK 32                        3: pipelined BK 32, split-K 2
 //   4: pipelined BK 32, interleaved           5: pipelined BK 32, split-K 2, interleaved
 //   6: pipelined BK 64, interleaved
 //   7: pipelined BK 32, cross-barrier slabs   8: as 7 with split-K 2
+//   9: as 7 on four 16x16x4 accumulator chains
 using Cfg0 = TileCfg<64, 64, 32, 2, 2, 2>;
 using Cfg1 = TileCfg<128, 64, 32, 2, 2, 1>;
 
@@ -906,6 +983,8 @@ int dispatch_cfg(int cfg, const float* x, int ldx, const float* W, const float* 
   switch (cfg) {
     case 7: return launch_pipe<EPI, 32, 1, true, true>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
     case 8: return launch_pipe<EPI, 32, 2, true, true>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
+    case 9:
+      return launch_pipe<EPI, 32, 1, true, true, true>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
 #ifdef LX_GEMM_SWEEP
     case 4: return launch_pipe<EPI, 32, 1, true>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
     case 5: return launch_pipe<EPI, 32, 2, true>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
@@ -950,12 +1029,16 @@ int dispatch_gemm(int kind, int cfg, const float* x, int ldx, const float* W, co
 // B*T = 1000: 50.6 us = 124 TFLOP/s) is resident in one round, whereas the
 // split-K 2 kernel (74 KB) runs it in two and the paired workgroups of a CU,
 // finishing together, can be re-placed two to a CU in the partial second round
-// (65 us).  K <= 512 has too few slabs to split.
+// (65 us).  K <= 512 has too few slabs to split.  From 768 tiles (three or
+// more workgroups per CU) four 16x16x4 accumulator chains per wave beat one
+// 32x32x2 chain (QKV at B*T = 1000: 51.5 vs 52.2 us; the T = 3000 step 4%
+// faster); below that the single chain is equal or ahead.
 // Split-K partial GEMMs aim for this many workgroups (two per CU).
 constexpr long kSplitTargetWgs = 512;
 
 int pick_config(int M, int N, int K) {
   const long tiles = (long)((M + 63) / 64) * ((N + 63) / 64);
+  if (tiles >= 768) return 9;
   return (K <= 512 || tiles >= 512) ? 7 : 8;
 }
 
