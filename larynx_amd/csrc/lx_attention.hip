@@ -42,7 +42,7 @@ constexpr size_t flash_lds() {
   return (size_t)2 * 2 * 32 * KS * kLD * sizeof(float);
 }
 
-template <int KS>
+template <int KS, bool BUF>
 __global__ __launch_bounds__(128 * KS) void attn_flash_kernel(
     const float* __restrict__ q, int ldq, const float* __restrict__ k, int ldk,
     const float* __restrict__ v, int ldv, float* __restrict__ o, int ldo, int Tq, int Tk,
@@ -73,18 +73,30 @@ __global__ __launch_bounds__(128 * KS) void attn_flash_kernel(
   const int kend = causal ? min(Tk, q_offset + min(qt0 + kQT - 1, Tq - 1) + 1) : Tk;
   const int ntiles = (kend + KT - 1) / KT;
 
-  // K/V tile loader: 2 x 16 KT float4 per tile, 4 + 4 per thread.
+  // K/V tile loader: 2 x 16 KT float4 per tile, 4 + 4 per thread.  BUF: buffer
+  // descriptors over this (batch, kv head)'s rows, per-lane byte offsets fixed
+  // and the tile advancing through the scalar offset; keys past Tk read as
+  // zeros (they are masked).  Otherwise 64-bit addresses with keys clamped.
   const float* kbase = k + (long)b * Tk * ldk + g * kHD;
   const float* vbase = v + (long)b * Tk * ldv + g * kHD;
+  const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)kbase, (short)0, BUF ? (int)(((long)(Tk - 1) * ldk + kHD) * 4) : 0, 0x00020000);
+  const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)vbase, (short)0, BUF ? (int)(((long)(Tk - 1) * ldv + kHD) * 4) : 0, 0x00020000);
   floatx4 rk[4], rv[4];
   auto gload = [&](int t) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int idx = tid + NT * j;
       const int row = idx >> 4, c = (idx & 15) * 4;
-      const int key = min(t * KT + row, Tk - 1);
-      rk[j] = *reinterpret_cast<const floatx4*>(kbase + (long)key * ldk + c);
-      rv[j] = *reinterpret_cast<const floatx4*>(vbase + (long)key * ldv + c);
+      if (BUF) {
+        rk[j] = __builtin_amdgcn_raw_buffer_load_b128(krs, (row * ldk + c) * 4, t * KT * ldk * 4, 0);
+        rv[j] = __builtin_amdgcn_raw_buffer_load_b128(vrs, (row * ldv + c) * 4, t * KT * ldv * 4, 0);
+      } else {
+        const int key = min(t * KT + row, Tk - 1);
+        rk[j] = *reinterpret_cast<const floatx4*>(kbase + (long)key * ldk + c);
+        rv[j] = *reinterpret_cast<const floatx4*>(vbase + (long)key * ldv + c);
+      }
     }
   };
   auto sstore = [&](int buf) {
@@ -276,17 +288,22 @@ extern "C" int lx_attention_f32(const float* q, int ldq, const float* k, int ldk
   // on MI355X for the DiT at T = 500 (26.3 vs 24.8 us) and the Qwen2 prefill
   // (14.8 vs 14.4 us), and equal at T = 3000.
   constexpr int KS = 2;
-  static bool attr_set = false;
-  if (!attr_set) {
-    if (hipFuncSetAttribute((const void*)attn_flash_kernel<KS>,
-                            hipFuncAttributeMaxDynamicSharedMemorySize,
+  // Buffer loads need every K/V byte offset (up to the last tile's rows past
+  // Tk) below 2^31.
+  const long lim = 1L << 31;
+  const long kt = 32 * KS;
+  const bool buf = ((long)(Tk + kt) * ldk + kHD) * 4 < lim && ((long)(Tk + kt) * ldv + kHD) * 4 < lim;
+  auto kern = buf ? attn_flash_kernel<KS, true> : attn_flash_kernel<KS, false>;
+  static bool attr_set[2] = {false, false};
+  if (!attr_set[buf]) {
+    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                             (int)flash_lds<KS>()) != hipSuccess) {
       set_error("attention: cannot raise the LDS limit to %zu bytes", flash_lds<KS>());
       return LX_ERR_LAUNCH;
     }
-    attr_set = true;
+    attr_set[buf] = true;
   }
-  hipLaunchKernelGGL(attn_flash_kernel<KS>, grid, dim3(128 * KS), flash_lds<KS>(), stream, q, ldq,
-                     k, ldk, v, ldv, o, ldo, Tq, Tk, rep, scale * log2e, causal, q_offset);
+  hipLaunchKernelGGL(kern, grid, dim3(128 * KS), flash_lds<KS>(), stream, q, ldq, k, ldk, v, ldv,
+                     o, ldo, Tq, Tk, rep, scale * log2e, causal, q_offset);
   return check_launch("attn_flash_kernel");
 }

@@ -16,8 +16,9 @@ constexpr int kGemvRows = 4;
 constexpr int kGemvBMax = 8;
 
 // Dot products of the staged activations xs (B x K, LDS) with rows of W: each
-// wave owns kGemvRows output rows at a time.
-template <int ACT_OUT>
+// wave owns R output rows at a time (R = 4 streams large W with 4 rows of
+// loads in flight per lane; R = 1 spreads a small W over more workgroups).
+template <int R, int ACT_OUT>
 __device__ __forceinline__ void gemv_rows(const float* xs, int B, int K,
                                           const float* __restrict__ W,
                                           const float* __restrict__ bias, float* __restrict__ y,
@@ -26,19 +27,23 @@ __device__ __forceinline__ void gemv_rows(const float* xs, int B, int K,
   const int lane = threadIdx.x % kWave;
   const int K4 = K >> 2;
   const float4* xs4 = reinterpret_cast<const float4*>(xs);
-  const long step = (long)gridDim.x * kGemvWaves * kGemvRows;
-  for (long n0 = ((long)blockIdx.x * kGemvWaves + wave) * kGemvRows; n0 < N; n0 += step) {
-    float acc[kGemvRows][kGemvBMax];
+  const long step = (long)gridDim.x * kGemvWaves * R;
+  for (long n0 = ((long)blockIdx.x * kGemvWaves + wave) * R; n0 < N; n0 += step) {
+    // bias first: its latency overlaps the weight stream
+    float bv[R];
 #pragma unroll
-    for (int r = 0; r < kGemvRows; ++r)
+    for (int r = 0; r < R; ++r) bv[r] = (bias && n0 + r < N) ? bias[n0 + r] : 0.0f;
+    float acc[R][kGemvBMax];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
 #pragma unroll
       for (int b = 0; b < kGemvBMax; ++b) acc[r][b] = 0.0f;
 #pragma unroll 4
     for (int k4 = lane; k4 < K4; k4 += kWave) {
-      float4 w[kGemvRows];
+      float4 w[R];
       // weights are read exactly once per call: streaming cache policy
 #pragma unroll
-      for (int r = 0; r < kGemvRows; ++r)
+      for (int r = 0; r < R; ++r)
         w[r] = (n0 + r < N) ? ld_nt(reinterpret_cast<const float4*>(W + (n0 + r) * K) + k4)
                             : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
@@ -46,19 +51,19 @@ __device__ __forceinline__ void gemv_rows(const float* xs, int B, int K,
         if (b < B) {
           float4 xv = xs4[b * K4 + k4];
 #pragma unroll
-          for (int r = 0; r < kGemvRows; ++r)
+          for (int r = 0; r < R; ++r)
             acc[r][b] += (w[r].x * xv.x + w[r].y * xv.y) + (w[r].z * xv.z + w[r].w * xv.w);
         }
       }
     }
 #pragma unroll
-    for (int r = 0; r < kGemvRows; ++r) {
+    for (int r = 0; r < R; ++r) {
 #pragma unroll
       for (int b = 0; b < kGemvBMax; ++b) {
         if (b < B) {
           float s = wave_sum(acc[r][b]);
           if (lane == 0 && n0 + r < N) {
-            float v = s + (bias ? bias[n0 + r] : 0.0f);
+            float v = s + bv[r];
             if (ACT_OUT == 1) v = v / (1.0f + expf(-v));
             y[b * ldy + n0 + r] = v;
           }
@@ -68,7 +73,7 @@ __device__ __forceinline__ void gemv_rows(const float* xs, int B, int K,
   }
 }
 
-template <int ACT_IN, int ACT_OUT>
+template <int ACT_IN, int ACT_OUT, int R>
 __global__ __launch_bounds__(kGemvWaves * kWave) void gemv_kernel(
     const float* __restrict__ x, int B, int K, const float* __restrict__ W,
     const float* __restrict__ bias, float* __restrict__ y, long N, long ldy) {
@@ -100,7 +105,7 @@ __global__ __launch_bounds__(kGemvWaves * kWave) void gemv_kernel(
     }
   }
   __syncthreads();
-  gemv_rows<ACT_OUT>(xs, B, K, W, bias, y, N, ldy);
+  gemv_rows<R, ACT_OUT>(xs, B, K, W, bias, y, N, ldy);
 }
 
 // First layer of the time MLP with the sinusoidal embedding of t (a6) formed
@@ -126,7 +131,7 @@ __global__ __launch_bounds__(kGemvWaves * kWave) void time_mlp0_kernel(
     xs[b * 2 * half + half + j] = cs;
   }
   __syncthreads();
-  gemv_rows<1>(xs, B, 2 * half, W, bias, y, N, N);
+  gemv_rows<1, 1>(xs, B, 2 * half, W, bias, y, N, N);
 }
 
 }  // namespace
@@ -138,19 +143,32 @@ int gemv(const float* x, int B, int K, const float* W, const float* bias, float*
              "gemv: bad shape B=%d K=%d N=%ld", B, K, N);
   LX_REQUIRE((size_t)B * K * sizeof(float) <= 64 * 1024, "gemv: B*K too large for LDS");
   LX_REQUIRE(((uintptr_t)W | (uintptr_t)x) % 16 == 0, "gemv: x and W must be 16-byte aligned");
-  long rows_per_block = (long)kGemvWaves * kGemvRows;
+  // Four rows per wave once there are enough rows to fill the device with
+  // them (the stacked AdaLN projection), one row per wave below that (the
+  // time MLP: 1024 rows -> 256 workgroups).
+  const bool wide = N >= 4L * kGemvWaves * 256 * kGemvRows;
+  long rows_per_block = (long)kGemvWaves * (wide ? kGemvRows : 1);
   long g = (N + rows_per_block - 1) / rows_per_block;
   if (g > 4096) g = 4096;
   dim3 grid((unsigned)g), block(kGemvWaves * kWave);
   size_t lds = (size_t)B * K * sizeof(float);
-  if (act_in == 0 && act_out == 0)
-    hipLaunchKernelGGL((gemv_kernel<0, 0>), grid, block, lds, stream, x, B, K, W, bias, y, N, ldy);
-  else if (act_in == 1 && act_out == 0)
-    hipLaunchKernelGGL((gemv_kernel<1, 0>), grid, block, lds, stream, x, B, K, W, bias, y, N, ldy);
-  else if (act_in == 0 && act_out == 1)
-    hipLaunchKernelGGL((gemv_kernel<0, 1>), grid, block, lds, stream, x, B, K, W, bias, y, N, ldy);
-  else
-    hipLaunchKernelGGL((gemv_kernel<1, 1>), grid, block, lds, stream, x, B, K, W, bias, y, N, ldy);
+#define LX_GEMV_LAUNCH(AI, AO)                                                                  \
+  if (wide)                                                                                     \
+    hipLaunchKernelGGL((gemv_kernel<AI, AO, kGemvRows>), grid, block, lds, stream, x, B, K, W, \
+                       bias, y, N, ldy);                                                        \
+  else                                                                                          \
+    hipLaunchKernelGGL((gemv_kernel<AI, AO, 1>), grid, block, lds, stream, x, B, K, W, bias, y, \
+                       N, ldy);
+  if (act_in == 0 && act_out == 0) {
+    LX_GEMV_LAUNCH(0, 0)
+  } else if (act_in == 1 && act_out == 0) {
+    LX_GEMV_LAUNCH(1, 0)
+  } else if (act_in == 0 && act_out == 1) {
+    LX_GEMV_LAUNCH(0, 1)
+  } else {
+    LX_GEMV_LAUNCH(1, 1)
+  }
+#undef LX_GEMV_LAUNCH
   return check_launch("gemv_kernel");
 }
 
@@ -165,7 +183,7 @@ int time_mlp(const float* tdev, const float* thost, int B, const float* w0, cons
   timestep_coeff(half, ta.c);
   if (!tdev)
     for (int b = 0; b < B; ++b) ta.t[b] = thost[b];
-  const long rows_per_block = (long)kGemvWaves * kGemvRows;
+  const long rows_per_block = kGemvWaves;  // one row per wave
   const long g = (D + rows_per_block - 1) / rows_per_block;
   hipLaunchKernelGGL(time_mlp0_kernel, dim3((unsigned)g), dim3(kGemvWaves * kWave),
                      (size_t)B * 2 * half * sizeof(float), stream, tdev, ta, B, half, 1000.0f, w0,

@@ -62,12 +62,21 @@ __global__ __launch_bounds__(256) void unpack_output_kernel(const float* __restr
   }
 }
 
+constexpr int kProjSlicesMax = 8;  // K slices the proj_out consumers sum
+
 // Row t, column c of the proj_out rows: the K slices of a split-K product
 // summed in slice order, then the bias (P itself when splits = 1, no bias).
+// Every slice's load is issued before the first add (slices past `splits`
+// re-read slice 0 and are dropped).
 __device__ __forceinline__ float proj_row_val(const float* __restrict__ P, int splits, long slice,
                                               const float* __restrict__ bias, long idx, int c) {
-  float v = P[idx];
-  for (int s = 1; s < splits; ++s) v += P[s * slice + idx];
+  float p[kProjSlicesMax];
+#pragma unroll
+  for (int s = 0; s < kProjSlicesMax; ++s) p[s] = P[(s < splits ? s : 0) * slice + idx];
+  float v = p[0];
+#pragma unroll
+  for (int s = 1; s < kProjSlicesMax; ++s)
+    if (s < splits) v += p[s];
   return bias ? v + bias[c] : v;
 }
 
@@ -167,6 +176,7 @@ int dit_unpack_output(const float* P, float* dphi, int B, int T, int mel, hipStr
 
 int cfm_euler_update(float* x, const float* P, int splits, long slice, const float* bias, int T,
                      int mel, float dt, float a, float b, hipStream_t stream) {
+  LX_REQUIRE(splits >= 1 && splits <= kProjSlicesMax, "euler: %d K slices", splits);
   const int ctiles = (mel + 31) / 32, ttiles = (T + 31) / 32;
   hipLaunchKernelGGL(euler_kernel, dim3(ctiles * ttiles), dim3(256), 0, stream, x, P, splits,
                      slice, bias, T, mel, dt, a, b);
@@ -175,6 +185,7 @@ int cfm_euler_update(float* x, const float* P, int splits, long slice, const flo
 
 int proj_reduce(const float* ws, int splits, long slice, const float* bias, float* P, int rows,
                 int mel, hipStream_t stream) {
+  LX_REQUIRE(splits >= 1 && splits <= kProjSlicesMax, "proj_reduce: %d K slices", splits);
   const long n = (long)rows * mel;
   hipLaunchKernelGGL(proj_reduce_kernel, dim3(grid1d(n)), dim3(256), 0, stream, ws, splits, slice,
                      bias, P, mel, n);
