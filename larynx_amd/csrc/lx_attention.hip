@@ -22,41 +22,45 @@ namespace {
 
 constexpr int kHD = 64;  // head dim handled by these kernels
 
-// Flash attention, 2 x KS waves per workgroup: a 64-query tile of one
-// (batch, head) split as 2 query sub-tiles (32 queries each) x KS key parts.
-// Every (32 KS)-key tile of K and V is loaded once into LDS (coalesced, double
-// buffered) and read by all waves; wave (qs, ks) scores its 32 queries against
-// keys [ks*32, ks*32 + 32) of each tile.  The KS key parts of a query sub-tile
-// are merged through LDS at the end in a fixed order (deterministic).  KS = 4
-// gives the short sequences (few query tiles) two waves per SIMD.
+// Flash attention, QS x KS waves per workgroup: a (32 QS)-query tile of one
+// (batch, head) split as QS query sub-tiles (32 queries each) x KS key parts.
+// Every (32 KS)-key tile of K and V is loaded once into LDS (coalesced) and
+// read by all waves; wave (qs, ks) scores its 32 queries against keys
+// [ks*32, ks*32 + 32) of each tile.  The KS key parts of a query sub-tile are
+// merged through LDS at the end in a fixed order (deterministic).
+// DB: K/V double buffered in LDS (one barrier per tile); otherwise one LDS
+// buffer (two barriers per tile), the next tile waiting in registers, which
+// halves the LDS of a workgroup so that two fit on a CU.
 // Softmax runs in base 2: q is pre-scaled by scale * log2(e), so p = exp2(s - m).
-constexpr int kQT = 64;          // queries per workgroup
 constexpr int kLD = kHD + 4;     // LDS row stride (floats)
 constexpr float kLazy = 8.0f;    // reference-max slack of the online softmax (log2 units)
 
-template <int KS>
+template <int QS, int KS, bool DB>
 constexpr size_t flash_lds() {
-  // K, V x 2 buffers of 32 KS rows; reused after the loop for the merge
+  // K, V x (1 or 2) buffers of 32 KS rows; reused after the loop for the merge
   // ((KS - 1) partial states of 64 lanes x 34 floats per query sub-tile) and
-  // the transposed output tile (2 x 32 rows of kLD).
-  return (size_t)2 * 2 * 32 * KS * kLD * sizeof(float);
+  // the transposed output tile (QS x 32 rows of kLD).
+  return (size_t)2 * (DB ? 2 : 1) * 32 * KS * kLD * sizeof(float);
 }
 
-template <int KS, bool BUF>
-__global__ __launch_bounds__(128 * KS) void attn_flash_kernel(
+template <int QS, int KS, bool DB, bool BUF>
+__global__ __launch_bounds__(64 * QS * KS) void attn_flash_kernel(
     const float* __restrict__ q, int ldq, const float* __restrict__ k, int ldk,
     const float* __restrict__ v, int ldv, float* __restrict__ o, int ldo, int Tq, int Tk,
     int rep, float qscale, int causal, int q_offset) {
+  constexpr int kQT = 32 * QS;   // queries per workgroup
   constexpr int KT = 32 * KS;    // keys per LDS tile
-  constexpr int NT = 128 * KS;   // threads
-  static_assert(KT * 16 == 4 * NT, "4 float4 per thread per operand tile");
-  static_assert(2 * (KS - 1) * 64 * 34 + 2 * 32 * kLD <= 2 * 2 * KT * kLD, "merge space");
+  constexpr int NT = 64 * QS * KS;   // threads
+  constexpr int LPT = KT * 16 / NT;  // float4 per thread per operand tile
+  static_assert(LPT * NT == KT * 16, "operand tile must split evenly over the threads");
+  static_assert(QS * (KS - 1) * 64 * 34 + QS * 32 * kLD <= 2 * (DB ? 2 : 1) * KT * kLD,
+                "merge space");
   extern __shared__ __attribute__((aligned(16))) float lds[];
-  float* Ks = lds;                      // [2][KT][kLD]
-  float* Vs = lds + 2 * KT * kLD;       // [2][KT][kLD]
+  float* Ks = lds;                                  // [DB ? 2 : 1][KT][kLD]
+  float* Vs = lds + (DB ? 2 : 1) * KT * kLD;        // [DB ? 2 : 1][KT][kLD]
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int qs = wave & 1, ks = wave >> 1;
+  const int qs = wave % QS, ks = wave / QS;
   const int lane = tid & 63, r = lane & 31, h = lane >> 5;
   const int head = blockIdx.y, b = blockIdx.z, g = head / rep;
   const int qt0 = blockIdx.x * kQT;
@@ -73,20 +77,21 @@ __global__ __launch_bounds__(128 * KS) void attn_flash_kernel(
   const int kend = causal ? min(Tk, q_offset + min(qt0 + kQT - 1, Tq - 1) + 1) : Tk;
   const int ntiles = (kend + KT - 1) / KT;
 
-  // K/V tile loader: 2 x 16 KT float4 per tile, 4 + 4 per thread.  BUF: buffer
-  // descriptors over this (batch, kv head)'s rows, per-lane byte offsets fixed
-  // and the tile advancing through the scalar offset; keys past Tk read as
-  // zeros (they are masked).  Otherwise 64-bit addresses with keys clamped.
+  // K/V tile loader: 2 x 16 KT float4 per tile, LPT + LPT per thread.  BUF:
+  // buffer descriptors over this (batch, kv head)'s rows, per-lane byte
+  // offsets fixed and the tile advancing through the scalar offset; keys past
+  // Tk read as zeros (they are masked).  Otherwise 64-bit addresses with keys
+  // clamped.
   const float* kbase = k + (long)b * Tk * ldk + g * kHD;
   const float* vbase = v + (long)b * Tk * ldv + g * kHD;
   const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
       (void*)kbase, (short)0, BUF ? (int)(((long)(Tk - 1) * ldk + kHD) * 4) : 0, 0x00020000);
   const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
       (void*)vbase, (short)0, BUF ? (int)(((long)(Tk - 1) * ldv + kHD) * 4) : 0, 0x00020000);
-  floatx4 rk[4], rv[4];
+  floatx4 rk[LPT], rv[LPT];
   auto gload = [&](int t) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < LPT; ++j) {
       const int idx = tid + NT * j;
       const int row = idx >> 4, c = (idx & 15) * 4;
       if (BUF) {
@@ -101,7 +106,7 @@ __global__ __launch_bounds__(128 * KS) void attn_flash_kernel(
   };
   auto sstore = [&](int buf) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < LPT; ++j) {
       const int idx = tid + NT * j;
       const int row = idx >> 4, c = (idx & 15) * 4;
       *reinterpret_cast<floatx4*>(Ks + (buf * KT + row) * kLD + c) = rk[j];
@@ -123,7 +128,7 @@ __global__ __launch_bounds__(128 * KS) void attn_flash_kernel(
   }
   __syncthreads();
   for (int t = 0; t < ntiles; ++t) {
-    const int buf = t & 1;
+    const int buf = DB ? (t & 1) : 0;
     if (t + 1 < ntiles) gload(t + 1);
     const int kb = t * KT + ks * 32;  // first key of this wave's part of the tile
     if (kb < kend) {
@@ -192,14 +197,20 @@ __global__ __launch_bounds__(128 * KS) void attn_flash_kernel(
         o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(vrow[32 + r], s[i], o1, 0, 0, 0);
       }
     }
-    if (t + 1 < ntiles) sstore(buf ^ 1);
-    __syncthreads();
+    if (DB) {
+      if (t + 1 < ntiles) sstore(buf ^ 1);
+      __syncthreads();
+    } else {
+      __syncthreads();  // every wave is done with the tile before it is replaced
+      if (t + 1 < ntiles) sstore(0);
+      __syncthreads();
+    }
   }
 
   // Merge the key parts: ks > 0 publish (m, l, O^T) per lane, ks = 0 combines
   // them in part order.
   const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
-  float* xch = lds + qs * ((KS - 1) * 64 * 34);  // per query sub-tile
+  float* xch = lds + qs * ((KS - 1) * 64 * 34);  // per query sub-tile (QS of them)
   if (ks > 0) {
     float* mine = xch + (ks - 1) * (64 * 34);
 #pragma unroll
@@ -211,7 +222,7 @@ __global__ __launch_bounds__(128 * KS) void attn_flash_kernel(
     mine[33 * 64 + lane] = l_tot;
   }
   __syncthreads();
-  float* otile = lds + 2 * (KS - 1) * 64 * 34;    // transposed output tiles [2][32 q][kLD]
+  float* otile = lds + QS * (KS - 1) * 64 * 34;   // transposed output tiles [QS][32 q][kLD]
   float* ot = otile + qs * (32 * kLD);
   if (ks == 0) {
     float m = m_run;
@@ -245,9 +256,9 @@ __global__ __launch_bounds__(128 * KS) void attn_flash_kernel(
     }
   }
   __syncthreads();
-  // coalesced store of both sub-tiles: 64 queries x 16 float4
+  // coalesced store of the sub-tiles: kQT queries x 16 float4
   for (int idx = tid; idx < kQT * 16; idx += NT) {
-    const int row = idx >> 4, c = (idx & 15) * 4;  // row 0..63 = qs*32 + local row
+    const int row = idx >> 4, c = (idx & 15) * 4;  // row = qs*32 + local row
     const int qi = qt0 + row;
     if (qi < Tq) {
       const float* src = otile + (row >> 5) * (32 * kLD) + (row & 31) * kLD + c;
@@ -281,29 +292,40 @@ extern "C" int lx_attention_f32(const float* q, int ldq, const float* k, int ldk
   LX_REQUIRE(q_offset >= 0, "attention: q_offset < 0");
   if (causal) LX_REQUIRE(q_offset + Tq <= Tk, "attention: causal needs q_offset + Tq <= Tk");
   const int rep = n_heads / n_kv_heads;
-  dim3 grid((Tq + kQT - 1) / kQT, n_heads, B);
   const float log2e = 1.4426950408889634f;
-  // Two key parts (4 waves, 64-key tiles).  Four parts (8 waves on 128-key
-  // tiles, two waves per SIMD even with one workgroup per CU) measured slower
-  // on MI355X for the DiT at T = 500 (26.3 vs 24.8 us) and the Qwen2 prefill
-  // (14.8 vs 14.4 us), and equal at T = 3000.
-  constexpr int KS = 2;
   // Buffer loads need every K/V byte offset (up to the last tile's rows past
   // Tk) below 2^31.
   const long lim = 1L << 31;
-  const long kt = 32 * KS;
-  const bool buf = ((long)(Tk + kt) * ldk + kHD) * 4 < lim && ((long)(Tk + kt) * ldv + kHD) * 4 < lim;
-  auto kern = buf ? attn_flash_kernel<KS, true> : attn_flash_kernel<KS, false>;
-  static bool attr_set[2] = {false, false};
-  if (!attr_set[buf]) {
+  const bool buf = ((long)(Tk + 128) * ldk + kHD) * 4 < lim && ((long)(Tk + 128) * ldv + kHD) * 4 < lim;
+  // Two layouts.  64-query workgroups (2 query sub-tiles x 2 key parts, 64-key
+  // tiles double buffered, 70 KB of LDS) whenever they cover the CUs (DiT at
+  // T = 500: 256 workgroups, 24.9 us; T = 3000: 1504).  A grid smaller than
+  // the device (the Qwen2 prefill at L = 256: 56 workgroups) takes 32-query
+  // workgroups of 4 key parts over single-buffered 128-key tiles instead:
+  // twice the workgroups, four waves each (13.9 -> 9.8 us).  At T = 500 that
+  // layout is slower (27.8 us: the 4-part merge and two barriers per tile
+  // cost more than the second resident workgroup per CU returns).
+  const long wg64 = (long)((Tq + 63) / 64) * n_heads * B;
+  const bool small = wg64 < 256;
+  auto pick = [&]() {
+    if (small)
+      return buf ? attn_flash_kernel<1, 4, false, true> : attn_flash_kernel<1, 4, false, false>;
+    return buf ? attn_flash_kernel<2, 2, true, true> : attn_flash_kernel<2, 2, true, false>;
+  };
+  auto kern = pick();
+  const int qt = small ? 32 : 64;
+  const size_t lds = small ? flash_lds<1, 4, false>() : flash_lds<2, 2, true>();
+  static bool attr_set[2][2] = {{false, false}, {false, false}};
+  if (!attr_set[small][buf]) {
     if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)flash_lds<KS>()) != hipSuccess) {
-      set_error("attention: cannot raise the LDS limit to %zu bytes", flash_lds<KS>());
+                            (int)lds) != hipSuccess) {
+      set_error("attention: cannot raise the LDS limit to %zu bytes", lds);
       return LX_ERR_LAUNCH;
     }
-    attr_set[buf] = true;
+    attr_set[small][buf] = true;
   }
-  hipLaunchKernelGGL(kern, grid, dim3(128 * KS), flash_lds<KS>(), stream, q, ldq, k, ldk, v, ldv,
-                     o, ldo, Tq, Tk, rep, scale * log2e, causal, q_offset);
+  dim3 grid((Tq + qt - 1) / qt, n_heads, B);
+  hipLaunchKernelGGL(kern, grid, dim3(256), lds, stream, q, ldq, k, ldk, v, ldv, o, ldo, Tq, Tk,
+                     rep, scale * log2e, causal, q_offset);
   return check_launch("attn_flash_kernel");
 }
