@@ -650,21 +650,39 @@ __global__ __launch_bounds__(256 * KS) void gemm_pipe_kernel(
   float4 eb[SLOTS], eg[SLOTS], ey[SLOTS];
   int epos[SLOTS];
   const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
+  // Loads read an in-range address unconditionally and the value is selected
+  // afterwards (a selected address would fall back to flat loads with a stack
+  // copy of the zero vector); with ep.vec every pointer involved is 16-byte
+  // aligned.
 #pragma unroll
   for (int j = 0; j < SLOTS; ++j) {
-    const int idx = tid + j * NT;
-    const int m = m0 + idx / (BN / 4), n = n0 + (idx % (BN / 4)) * 4;
-    const bool ok = ep.vec && m < M && n + 4 <= N;
-    eb[j] = (ok && bias) ? *reinterpret_cast<const float4*>(bias + n) : z4;
+    eb[j] = z4;
     eg[j] = z4;
     ey[j] = z4;
     epos[j] = 0;
-    if (EPI == LX_EPI_GATED_RESID && ok)
-      eg[j] = *reinterpret_cast<const float4*>(
-          ep.gate + (long)(m / ep.rows_per_batch) * ep.gate_stride + n);
-    if ((EPI == LX_EPI_GATED_RESID || EPI == LX_EPI_RESID) && ok)
-      ey[j] = *reinterpret_cast<const float4*>(Y + (long)m * ldy + n);
-    if (EPI == LX_EPI_ROPE_PARTIAL && ok) epos[j] = ep.pos[m % ep.rows_per_batch];
+  }
+  if (ep.vec) {
+#pragma unroll
+    for (int j = 0; j < SLOTS; ++j) {
+      const int idx = tid + j * NT;
+      const int m = m0 + idx / (BN / 4), n = n0 + (idx % (BN / 4)) * 4;
+      const bool ok = m < M && n + 4 <= N;
+      const int mc = ok ? m : 0, nc = ok ? n : 0;
+      if (bias) {
+        const float4 t = *reinterpret_cast<const float4*>(bias + nc);
+        eb[j] = ok ? t : z4;
+      }
+      if (EPI == LX_EPI_GATED_RESID) {
+        const float4 t = *reinterpret_cast<const float4*>(
+            ep.gate + (long)(mc / ep.rows_per_batch) * ep.gate_stride + nc);
+        eg[j] = ok ? t : z4;
+      }
+      if (EPI == LX_EPI_GATED_RESID || EPI == LX_EPI_RESID) {
+        const float4 t = *reinterpret_cast<const float4*>(Y + (long)mc * ldy + nc);
+        ey[j] = ok ? t : z4;
+      }
+      if (EPI == LX_EPI_ROPE_PARTIAL) epos[j] = ep.pos[mc % ep.rows_per_batch];
+    }
   }
 
   constexpr int LDC = BN + 4;
