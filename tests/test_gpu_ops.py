@@ -233,6 +233,28 @@ def test_linear_plain(gpu, ops, M, N, K):
     assert orc.rel_err(y, orc.linear(x, W, b)) < TOL
 
 
+@pytest.mark.parametrize("M,N,K", [(1000, 3072, 1000), (1000, 1024, 1024), (200, 200, 96)])
+def test_linear_strided_and_unaligned(gpu, ops, M, N, K):
+    """Row strides past K / N through the buffer-descriptor loads, and an output
+    that is not 16-byte aligned (scalar epilogue path); (1000, 3072, 1000) is a
+    768-tile launch with a K tail (16x16x4 chains, masked slabs)."""
+    announce(f"linear strided/unaligned M={M} N={N} K={K}")
+    x, W, b = rnd((M, K), 1), rnd((N, K), 2, 0.03), rnd((N,), 3)
+    ref = orc.linear(x, W, b)
+    wide = torch.zeros(M, K + 20, device=gpu)
+    wide[:, 4:4 + K] = dev(x, gpu)
+    xv = wide[:, 4:4 + K]  # row stride K + 20, 16-byte aligned start
+    outa = torch.full((M, N + 12), 7.0, device=gpu)
+    ops.linear(xv, dev(W, gpu), dev(b, gpu), out=outa[:, :N])
+    assert orc.rel_err(outa[:, :N].cpu().numpy(), ref) < TOL
+    assert torch.all(outa[:, N:] == 7.0)  # columns past N untouched
+    outu = torch.full((M, N + 13), 7.0, device=gpu)
+    ep = ops.Epilogue(kind=ops.LX_EPI_GELU_TANH)
+    ops.linear(xv, dev(W, gpu), dev(b, gpu), epilogue=ep, out=outu[:, 1:1 + N])
+    assert orc.rel_err(outu[:, 1:1 + N].cpu().numpy(), orc.gelu_tanh(ref)) < TOL
+    assert torch.all(outu[:, 0] == 7.0) and torch.all(outu[:, 1 + N:] == 7.0)
+
+
 @pytest.mark.parametrize("M", [1000, 6000, 5])
 def test_linear_gelu_epilogue(gpu, ops, M):
     announce(f"linear+gelu M={M}")
