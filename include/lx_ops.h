@@ -167,7 +167,9 @@ typedef struct lx_epilogue {
 
 /* Linear: y = epi(x @ W^T + bias).  x: (M, K) with row stride ldx; W: (N, K)
  * row-major (torch nn.Linear weight == ggml [K, N]); bias: (N) or NULL;
- * y: (M, N) with row stride ldy (N/2 columns for SWIGLU_PAIRED).  K % 4 == 0.
+ * y: (M, N) with row stride ldy (N/2 columns for SWIGLU_PAIRED).  K and ldx
+ * multiples of 4, x and W 16-byte aligned; y needs no alignment (aligned
+ * outputs take the float4 epilogue).
  * Replaces linear() = ggml_mul_mat + ggml_add (src/flow/ops.cpp:20-26,
  * src/llm/ops.cpp:13-19) plus whatever node the epilogue absorbs.
  * epi may be NULL (== LX_EPI_NONE). */
