@@ -2,7 +2,8 @@
 // channels, kernel K) + bias + Mish (+ residual), as an implicit GEMM on the
 // matrix cores.  Per (batch, group, 64-frame tile) the input window
 // [64 + K - 1 frames x 64 channels] sits in LDS for the whole kernel and the
-// 64x64 weight slab of each tap streams through a double-buffered LDS slot:
+// 64x64 weight slab of each tap streams through a double-buffered LDS slot
+// (one per tap group, see conv_mish_kernel):
 //   out[t, oc] = sum_k sum_ic window[t + k, ic] * w_k[oc, ic].
 // Weights are pre-packed tap-major, wp[g][k][oc][ic], so each tap slab is a
 // contiguous 16 KB read.
@@ -16,89 +17,130 @@ constexpr int CG = 64;        // channels per group
 constexpr int TT = 64;        // frames per tile
 constexpr int LDW = CG + 4;   // LDS row stride
 
-template <int KMAX>
-__global__ __launch_bounds__(256) void conv_mish_kernel(const float* __restrict__ x,
-                                                        const float* __restrict__ wp,
-                                                        const float* __restrict__ bias,
-                                                        const float* resid, float* y, int T,
-                                                        int C, int K) {
+// NG groups of 4 waves (2 x 2 waves of 32 x 32 outputs each).  With NG = 2 the
+// groups split the taps, group 0 taps [0, K0), group 1 taps [K0, K) with
+// K0 = ceil(K / 2), each with its own double-buffered tap slab, the input
+// window shared: a grid of one workgroup per CU then has two waves per SIMD
+// to hide the per-tap slab wait and barrier, and the two partial tiles are
+// summed through LDS in a fixed order (group 1 then group 0).  Large grids
+// (several workgroups per CU) take NG = 1, whose 43 KB of LDS fits three.
+template <int KMAX, int NG>
+__global__ __launch_bounds__(256 * NG) void conv_mish_kernel(const float* __restrict__ x,
+                                                             const float* __restrict__ wp,
+                                                             const float* __restrict__ bias,
+                                                             const float* resid, float* y, int T,
+                                                             int C, int K) {
+  constexpr int kConvGroups = NG;
+  constexpr int kConvThreads = 256 * NG;
   extern __shared__ __attribute__((aligned(16))) float smem[];
   float* xw = smem;                           // [TT + KMAX - 1][LDW]
-  float* wk = smem + (TT + KMAX - 1) * LDW;   // [2][CG][LDW]
   const int t0 = blockIdx.x * TT;
   const int g = blockIdx.y;
   const int b = blockIdx.z;
   const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int kg = wave >> 2;                   // tap group
+  const int wm = (wave >> 1) & 1, wn = wave & 1;
   const int r = lane & 31, h = lane >> 5;
+  const int gtid = tid & 255;
+  float* wk = smem + (TT + KMAX - 1) * LDW + kg * 2 * CG * LDW;  // this group's [2][CG][LDW]
 
-  // Input window: frames t0-(K-1) .. t0+TT-1, zero outside [0, T).
-  const int nrow = TT + K - 1;
-  for (int i = tid; i < nrow * (CG / 4); i += 256) {
-    const int row = i / (CG / 4), c4 = (i % (CG / 4)) * 4;
-    const int tg = t0 - (K - 1) + row;
-    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (tg >= 0 && tg < T)
-      v = *reinterpret_cast<const float4*>(x + ((long)b * T + tg) * C + g * CG + c4);
-    *reinterpret_cast<float4*>(xw + row * LDW + c4) = v;
+  // Input window: frames t0-(K-1) .. t0+TT-1, zero outside [0, T); every
+  // thread's loads are issued before its LDS stores.
+  constexpr int kWin = (TT + KMAX - 1) * (CG / 4);                 // float4 slots (max)
+  constexpr int kWinPer = (kWin + kConvThreads - 1) / kConvThreads;
+  const int nwin = (TT + K - 1) * (CG / 4);
+  {
+    float4 v[kWinPer];
+#pragma unroll
+    for (int u = 0; u < kWinPer; ++u) {
+      const int i = tid + u * kConvThreads;
+      const int row = i / (CG / 4), c4 = (i % (CG / 4)) * 4;
+      const int tg = t0 - (K - 1) + row;
+      v[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (i < nwin && tg >= 0 && tg < T)
+        v[u] = *reinterpret_cast<const float4*>(x + ((long)b * T + tg) * C + g * CG + c4);
+    }
+#pragma unroll
+    for (int u = 0; u < kWinPer; ++u) {
+      const int i = tid + u * kConvThreads;
+      if (i < nwin) *reinterpret_cast<float4*>(xw + (i / (CG / 4)) * LDW + (i % (CG / 4)) * 4) = v[u];
+    }
   }
+  const int K0 = (K + NG - 1) / NG;
+  const int kbeg = kg == 0 ? 0 : K0;
+  const int kcnt = kg == 0 ? K0 : K - K0;     // this group's taps (K0 or K0 - 1)
   const float* wg = wp + (long)g * K * CG * CG;
-  // Tap slabs: 64 oc x 64 ic = 1024 float4, four per thread, register staged
-  // (native vectors, no lambdas: keeps the staging in VGPRs).
+  // Tap slabs: 64 oc x 64 ic = 1024 float4, four per thread of the group,
+  // register staged (native vectors, no lambdas: keeps the staging in VGPRs).
   floatx4 wr0, wr1, wr2, wr3;
 #define LX_WLOAD(k)                                                              \
   do {                                                                           \
     const floatx4* src = reinterpret_cast<const floatx4*>(wg + (long)(k) * CG * CG); \
-    wr0 = src[tid];                                                              \
-    wr1 = src[tid + 256];                                                        \
-    wr2 = src[tid + 512];                                                        \
-    wr3 = src[tid + 768];                                                        \
+    wr0 = src[gtid];                                                             \
+    wr1 = src[gtid + 256];                                                       \
+    wr2 = src[gtid + 512];                                                       \
+    wr3 = src[gtid + 768];                                                       \
   } while (0)
 #define LX_WSTORE(buf)                                                           \
   do {                                                                           \
     float* dst = wk + (buf) * CG * LDW;                                          \
-    *reinterpret_cast<floatx4*>(dst + ((tid) >> 4) * LDW + ((tid) & 15) * 4) = wr0; \
-    *reinterpret_cast<floatx4*>(dst + ((tid + 256) >> 4) * LDW + ((tid) & 15) * 4) = wr1; \
-    *reinterpret_cast<floatx4*>(dst + ((tid + 512) >> 4) * LDW + ((tid) & 15) * 4) = wr2; \
-    *reinterpret_cast<floatx4*>(dst + ((tid + 768) >> 4) * LDW + ((tid) & 15) * 4) = wr3; \
+    *reinterpret_cast<floatx4*>(dst + ((gtid) >> 4) * LDW + ((gtid) & 15) * 4) = wr0; \
+    *reinterpret_cast<floatx4*>(dst + ((gtid + 256) >> 4) * LDW + ((gtid) & 15) * 4) = wr1; \
+    *reinterpret_cast<floatx4*>(dst + ((gtid + 512) >> 4) * LDW + ((gtid) & 15) * 4) = wr2; \
+    *reinterpret_cast<floatx4*>(dst + ((gtid + 768) >> 4) * LDW + ((gtid) & 15) * 4) = wr3; \
   } while (0)
-  LX_WLOAD(0);
-  LX_WSTORE(0);
+  if (kcnt > 0) {
+    LX_WLOAD(kbeg);
+    LX_WSTORE(0);
+  }
   __syncthreads();
 
   floatx16 acc;
 #pragma unroll
   for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
-  for (int k = 0; k < K; ++k) {
-    const int buf = k & 1;
-    if (k + 1 < K) LX_WLOAD(k + 1);
-    const float* a = xw + (wm * 32 + r + k) * LDW + h * 32;
-    const float* w = wk + buf * CG * LDW + (wn * 32 + r) * LDW + h * 32;
+  // Both groups run K0 iterations (uniform barriers); a group with fewer taps
+  // idles through its last one.
+  for (int kk = 0; kk < K0; ++kk) {
+    const int buf = kk & 1;
+    const bool live = kk < kcnt;
+    if (kk + 1 < kcnt) LX_WLOAD(kbeg + kk + 1);
+    if (live) {
+      const float* a = xw + (wm * 32 + r + kbeg + kk) * LDW + h * 32;
+      const float* w = wk + buf * CG * LDW + (wn * 32 + r) * LDW + h * 32;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const floatx4 av = *reinterpret_cast<const floatx4*>(a + 4 * j);
-      const floatx4 bv = *reinterpret_cast<const floatx4*>(w + 4 * j);
+      for (int j = 0; j < 8; ++j) {
+        const floatx4 av = *reinterpret_cast<const floatx4*>(a + 4 * j);
+        const floatx4 bv = *reinterpret_cast<const floatx4*>(w + 4 * j);
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[e], bv[e], acc, 0, 0, 0);
+        for (int e = 0; e < 4; ++e)
+          acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[e], bv[e], acc, 0, 0, 0);
+      }
     }
-    if (k + 1 < K) LX_WSTORE(buf ^ 1);
+    if (kk + 1 < kcnt) LX_WSTORE(buf ^ 1);
     __syncthreads();
   }
 #undef LX_WLOAD
 #undef LX_WSTORE
-  // Epilogue through LDS (reuse the window region: TT x LDW floats).
+  // Reduce the two tap groups through LDS (reuse the window region: TT x LDW
+  // floats), group 1 first, then the epilogue over 64 x 64 outputs.
   float* cs = smem;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int row = wm * 32 + (i >> 2) * 8 + h * 4 + (i & 3);
-    cs[row * LDW + wn * 32 + r] = acc[i];
-  }
-  __syncthreads();
+  for (int grp = kConvGroups - 1; grp >= 0; --grp) {
+    if (kg == grp) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int idx = tid + 256 * j;
+      for (int i = 0; i < 16; ++i) {
+        const int row = wm * 32 + (i >> 2) * 8 + h * 4 + (i & 3);
+        float v = acc[i];
+        if (grp < kConvGroups - 1) v += cs[row * LDW + wn * 32 + r];
+        cs[row * LDW + wn * 32 + r] = v;
+      }
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int j = 0; j < TT * CG / 4 / kConvThreads; ++j) {
+    const int idx = tid + kConvThreads * j;
     const int row = idx >> 4, c4 = (idx & 15) * 4;
     const int t = t0 + row;
     if (t >= T) continue;
@@ -160,10 +202,24 @@ int conv_pos_mish_packed(const float* x, const float* wp, const float* bias, con
   LX_REQUIRE(x != y, "conv_pos_mish: y must not alias x");
   LX_REQUIRE(((uintptr_t)x | (uintptr_t)y | (uintptr_t)wp | (uintptr_t)(resid ? resid : x)) % 16 == 0,
              "conv_pos_mish: pointers must be 16-byte aligned");
-  const size_t lds = ((size_t)(TT + 32 - 1) * LDW + 2 * CG * LDW) * sizeof(float);
   dim3 grid((T + TT - 1) / TT, G, B);
-  hipLaunchKernelGGL(conv_mish_kernel<32>, grid, dim3(256), lds, stream, x, wp, bias, resid, y, T,
-                     C, K);
+  // Two tap groups when the grid gives each CU at most two workgroups
+  // (T = 500: 256 workgroups, 48.5 -> 43.4 us); one otherwise (T = 3000: 1504
+  // workgroups, three resident per CU: 230 us, against 242 with two groups).
+  const bool two = (long)grid.x * grid.y * grid.z <= 2 * 256;
+  const int ng = two ? 2 : 1;
+  const size_t lds = ((size_t)(TT + 32 - 1) * LDW + (size_t)ng * 2 * CG * LDW) * sizeof(float);
+  auto kern = two ? conv_mish_kernel<32, 2> : conv_mish_kernel<32, 1>;
+  static bool attr_set[2] = {false, false};
+  if (lds > 64 * 1024 && !attr_set[two]) {
+    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)lds) != hipSuccess) {
+      set_error("conv_pos_mish: cannot raise the LDS limit to %zu bytes", lds);
+      return LX_ERR_LAUNCH;
+    }
+    attr_set[two] = true;
+  }
+  hipLaunchKernelGGL(kern, grid, dim3(256 * ng), lds, stream, x, wp, bias, resid, y, T, C, K);
   return check_launch("conv_mish_kernel");
 }
 
