@@ -375,3 +375,17 @@ def test_conv_pos_mish(gpu, ops, B, T):
     assert orc.rel_err(y, orc.conv_pos_mish(x, w, b, r)) < TOL
     y0 = ops.conv_pos_mish(dev(x, gpu), wp, dev(b, gpu)).cpu().numpy()
     assert orc.rel_err(y0, orc.conv_pos_mish(x, w, b)) < TOL
+
+
+@pytest.mark.parametrize("T,K", [(50, 1), (50, 2), (50, 32), (2100, 2), (2100, 17)])
+def test_conv_pos_mish_kernel_sizes(gpu, ops, T, K):
+    """Tap counts other than the model's 31 over both launch shapes: grids of at most 512
+    workgroups split the taps over two groups (K = 1 leaves the second group none, K = 17
+    gives it one fewer), larger grids (T = 2100: 528) run them in one."""
+    announce(f"conv_pos B=1 T={T} K={K}")
+    Cc = 1024
+    x, r = rnd((1, T, Cc), 5), rnd((1, T, Cc), 6)
+    w, b = rnd((Cc, 64, K), 7, 0.03), rnd((Cc,), 8, 0.03)
+    wp = ops.conv_pack_weight(dev(w, gpu))
+    y = ops.conv_pos_mish(dev(x, gpu), wp, dev(b, gpu), dev(r, gpu), kernel=K).cpu().numpy()
+    assert orc.rel_err(y, orc.conv_pos_mish(x, w, b, r)) < TOL
