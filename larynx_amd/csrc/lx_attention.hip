@@ -315,15 +315,9 @@ extern "C" int lx_attention_f32(const float* q, int ldq, const float* k, int ldk
   auto kern = pick();
   const int qt = small ? 32 : 64;
   const size_t lds = small ? flash_lds<1, 4, false>() : flash_lds<2, 2, true>();
-  static bool attr_set[2][2] = {{false, false}, {false, false}};
-  if (!attr_set[small][buf]) {
-    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)lds) != hipSuccess) {
-      set_error("attention: cannot raise the LDS limit to %zu bytes", lds);
-      return LX_ERR_LAUNCH;
-    }
-    attr_set[small][buf] = true;
-  }
+  static LdsLimit once[2][2];  // [small][buf]
+  const int rc = raise_lds_limit((const void*)kern, lds, once[small][buf], "attention");
+  if (rc) return rc;
   dim3 grid((Tq + qt - 1) / qt, n_heads, B);
   hipLaunchKernelGGL(kern, grid, dim3(256), lds, stream, q, ldq, k, ldk, v, ldv, o, ldo, Tq, Tk,
                      rep, scale * log2e, causal, q_offset);

@@ -4,7 +4,9 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdarg>
+#include <cstddef>
 #include <cstdio>
 
 #include "lx_ops.h"
@@ -26,6 +28,31 @@ int check_launch(const char* what);
       return LX_ERR_ARG;             \
     }                                \
   } while (0)
+
+// Devices (ids 0-63) on which one kernel's dynamic-LDS limit has been raised.
+struct LdsLimit {
+  std::atomic<unsigned long long> devices{0};
+};
+
+// Raises `kern`'s dynamic LDS limit to `bytes` on the current device, once per
+// device (the attribute belongs to each device's copy of the code object).
+// Concurrent first calls may both set it, which is harmless.
+inline int raise_lds_limit(const void* kern, size_t bytes, LdsLimit& once, const char* what) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    set_error("%s: hipGetDevice failed", what);
+    return LX_ERR_LAUNCH;
+  }
+  const unsigned long long bit = dev >= 0 && dev < 64 ? 1ull << dev : 0ull;
+  if (bit && (once.devices.load(std::memory_order_acquire) & bit)) return LX_OK;
+  if (hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes) !=
+      hipSuccess) {
+    set_error("%s: cannot raise the LDS limit to %zu bytes", what, bytes);
+    return LX_ERR_LAUNCH;
+  }
+  once.devices.fetch_or(bit, std::memory_order_release);
+  return LX_OK;
+}
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));

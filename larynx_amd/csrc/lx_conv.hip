@@ -210,14 +210,10 @@ int conv_pos_mish_packed(const float* x, const float* wp, const float* bias, con
   const int ng = two ? 2 : 1;
   const size_t lds = ((size_t)(TT + 32 - 1) * LDW + (size_t)ng * 2 * CG * LDW) * sizeof(float);
   auto kern = two ? conv_mish_kernel<32, 2> : conv_mish_kernel<32, 1>;
-  static bool attr_set[2] = {false, false};
-  if (lds > 64 * 1024 && !attr_set[two]) {
-    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)lds) != hipSuccess) {
-      set_error("conv_pos_mish: cannot raise the LDS limit to %zu bytes", lds);
-      return LX_ERR_LAUNCH;
-    }
-    attr_set[two] = true;
+  static LdsLimit once[2];  // [two]
+  if (lds > 64 * 1024) {
+    const int rc = raise_lds_limit((const void*)kern, lds, once[two], "conv_pos_mish");
+    if (rc) return rc;
   }
   hipLaunchKernelGGL(kern, grid, dim3(256 * ng), lds, stream, x, wp, bias, resid, y, T, C, K);
   return check_launch("conv_mish_kernel");

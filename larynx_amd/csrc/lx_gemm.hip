@@ -747,15 +747,9 @@ int launch_pipe_k(const float* x, int ldx, const float* W, const float* bias, fl
   auto kern = gemm_pipe_kernel<EPI, BK, KS, IL, KMASK, XB, BUF, MF16>;
   const size_t lds = PipeCfg<BK, KS>::lds();
   if (lds > 64 * 1024) {
-    static bool attr_set = false;
-    if (!attr_set) {
-      if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                              (int)lds) != hipSuccess) {
-        set_error("linear: cannot raise the LDS limit to %zu bytes", lds);
-        return LX_ERR_LAUNCH;
-      }
-      attr_set = true;
-    }
+    static LdsLimit once;  // per instantiation
+    const int rc = raise_lds_limit((const void*)kern, lds, once, "linear");
+    if (rc) return rc;
   }
   const long tiles = (long)((M + 63) / 64) * ((N + 63) / 64);
   hipLaunchKernelGGL(kern, dim3((unsigned)tiles, sp.splits), dim3(PipeCfg<BK, KS>::threads), lds,
@@ -805,15 +799,9 @@ int launch_tile(const float* x, int ldx, const float* W, const float* bias, floa
   auto kern = gemm_tile_kernel<EPI, CFG::bm, CFG::bn, CFG::bk, CFG::wm, CFG::wn, CFG::ks>;
   const size_t lds = CFG::lds();
   if (lds > 64 * 1024) {
-    static bool attr_set = false;  // once per instantiation
-    if (!attr_set) {
-      if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                              (int)lds) != hipSuccess) {
-        set_error("linear: cannot raise the LDS limit to %zu bytes", lds);
-        return LX_ERR_LAUNCH;
-      }
-      attr_set = true;
-    }
+    static LdsLimit once;  // per instantiation
+    const int rc = raise_lds_limit((const void*)kern, lds, once, "linear");
+    if (rc) return rc;
   }
   const long tiles = (long)((M + CFG::bm - 1) / CFG::bm) * ((N + CFG::bn - 1) / CFG::bn);
   hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(CFG::threads), lds, stream, x, ldx, W, K,
