@@ -305,21 +305,33 @@ extern "C" int lx_attention_f32(const float* q, int ldq, const float* k, int ldk
   // twice the workgroups, four waves each (13.9 -> 9.8 us).  At T = 500 that
   // layout is slower (27.8 us: the 4-part merge and two barriers per tile
   // cost more than the second resident workgroup per CU returns).
+  // A third layout, 128-query workgroups of 4 query sub-tiles x 2 key parts
+  // (512 threads, 70 KB: every K/V tile feeds twice the queries), when its
+  // grid is a whole number of workgroups per CU: T = 3000 (768 workgroups)
+  // 612 -> 571 us, T = 2000 283 -> 262, T = 1000 75.9 -> 73.8.  Grids that
+  // leave a partial round (T = 1500: 384 workgroups; 2500: 640) run slower
+  // than the 64-query layout and keep it.
   const long wg64 = (long)((Tq + 63) / 64) * n_heads * B;
-  const bool small = wg64 < 256;
+  const long wg128 = (long)((Tq + 127) / 128) * n_heads * B;
+  const int layout = wg64 < 256 ? 0 : (wg128 % 256 == 0 ? 2 : 1);  // small / 64-query / wide
   auto pick = [&]() {
-    if (small)
+    if (layout == 0)
       return buf ? attn_flash_kernel<1, 4, false, true> : attn_flash_kernel<1, 4, false, false>;
+    if (layout == 2)
+      return buf ? attn_flash_kernel<4, 2, true, true> : attn_flash_kernel<4, 2, true, false>;
     return buf ? attn_flash_kernel<2, 2, true, true> : attn_flash_kernel<2, 2, true, false>;
   };
   auto kern = pick();
-  const int qt = small ? 32 : 64;
-  const size_t lds = small ? flash_lds<1, 4, false>() : flash_lds<2, 2, true>();
-  static LdsLimit once[2][2];  // [small][buf]
-  const int rc = raise_lds_limit((const void*)kern, lds, once[small][buf], "attention");
+  const int qt = layout == 0 ? 32 : layout == 1 ? 64 : 128;
+  const int threads = layout == 2 ? 512 : 256;
+  const size_t lds = layout == 0   ? flash_lds<1, 4, false>()
+                     : layout == 1 ? flash_lds<2, 2, true>()
+                                   : flash_lds<4, 2, true>();
+  static LdsLimit once[3][2];  // [layout][buf]
+  const int rc = raise_lds_limit((const void*)kern, lds, once[layout][buf], "attention");
   if (rc) return rc;
   dim3 grid((Tq + qt - 1) / qt, n_heads, B);
-  hipLaunchKernelGGL(kern, grid, dim3(256), lds, stream, q, ldq, k, ldk, v, ldv, o, ldo, Tq, Tk,
+  hipLaunchKernelGGL(kern, grid, dim3(threads), lds, stream, q, ldq, k, ldk, v, ldv, o, ldo, Tq, Tk,
                      rep, scale * log2e, causal, q_offset);
   return check_launch("attn_flash_kernel");
 }

@@ -317,7 +317,8 @@ def test_linear_swiglu_and_resid_epilogues(gpu, ops, M):
     assert orc.rel_err(rd.cpu().numpy(), ref) < TOL
 
 
-@pytest.mark.parametrize("B,T", [(2, 500), (2, 45), (1, 1), (2, 3000)])
+@pytest.mark.parametrize("B,T", [(2, 500), (2, 45), (1, 1), (2, 3000), (2, 1000), (2, 1020),
+                                 (1, 2000), (2, 1500)])
 def test_attention_dit(gpu, ops, B, T):
     announce(f"attention dit B={B} T={T}")
     D = 1024
@@ -325,6 +326,21 @@ def test_attention_dit(gpu, ops, B, T):
     qd = dev(qkv, gpu)
     o = ops.attention(qd[..., :D], qd[..., D:2 * D], qd[..., 2 * D:], 16).cpu().numpy()
     ref = orc.attention(qkv[..., :D], qkv[..., D:2 * D], qkv[..., 2 * D:], 16)
+    assert orc.rel_err(o, ref) < TOL
+
+
+@pytest.mark.parametrize("B,T", [(2, 1000), (1, 2000)])
+def test_attention_wide_layout_causal(gpu, ops, B, T):
+    """Causal masking through the 128-query layout (grids of a whole number of
+    workgroups per CU), with a query offset on the second case."""
+    announce(f"attention wide causal B={B} T={T}")
+    D = 1024
+    off = 0 if B == 2 else 48
+    q = rnd((B, T, D), 11)
+    k, v = rnd((B, T + off, D), 12), rnd((B, T + off, D), 13)
+    o = ops.attention(dev(q, gpu), dev(k, gpu), dev(v, gpu), 16, causal=True,
+                      q_offset=off).cpu().numpy()
+    ref = orc.attention(q, k, v, 16, causal=True, q_offset=off)
     assert orc.rel_err(o, ref) < TOL
 
 
