@@ -255,6 +255,27 @@ def test_linear_strided_and_unaligned(gpu, ops, M, N, K):
     assert torch.all(outu[:, 0] == 7.0) and torch.all(outu[:, 1 + N:] == 7.0)
 
 
+def test_linear_operands_past_2gib(gpu, ops):
+    """x of 540000 x 1024 floats (2.2 GB): byte offsets pass 2^31, so the GEMM takes
+    its 64-bit-address operand loads (rows clamped into range) instead of the
+    buffer-descriptor loads.  Rows sampled at both ends, the middle and a tile edge
+    are checked against float64 products on the host."""
+    announce("linear M=540000 N=64 K=1024 (64-bit operand addressing)")
+    M, N, K = 540000, 64, 1024
+    g = torch.Generator(device=gpu).manual_seed(5)
+    x = torch.randn(M, K, device=gpu, generator=g)
+    W = torch.randn(N, K, device=gpu, generator=g) * 0.03
+    b = torch.randn(N, device=gpu, generator=g)
+    y = ops.linear(x, W, b)
+    rows = torch.tensor([0, 1, 63, 64, 270001, M - 65, M - 64, M - 1], device=gpu)
+    xs = x[rows].cpu().numpy().astype(np.float64)
+    ref = xs @ W.cpu().numpy().astype(np.float64).T + b.cpu().numpy().astype(np.float64)
+    got = y[rows].cpu().numpy()
+    assert np.abs(got - ref).max() / np.abs(ref).max() < TOL
+    del x, y
+    torch.cuda.empty_cache()
+
+
 @pytest.mark.parametrize("M", [1000, 6000, 5])
 def test_linear_gelu_epilogue(gpu, ops, M):
     announce(f"linear+gelu M={M}")
