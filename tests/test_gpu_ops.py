@@ -350,6 +350,32 @@ def test_attention_dit(gpu, ops, B, T):
     assert orc.rel_err(o, ref) < TOL
 
 
+@pytest.mark.parametrize("Tq", [64, 2500, 2048])
+def test_attention_kv_past_2gib(gpu, ops, Tq):
+    """K and V rows of a fused (180000, 3072) buffer (2.2 GB, row stride 3072): byte
+    offsets pass 2^31, so every layout (Tq = 64: 32-query workgroups; 2500: 64-query;
+    2048: 128-query) loads K/V through 64-bit addresses with keys clamped into range.
+    Sampled queries are checked against a float64 softmax(q k^T) v computed with torch."""
+    announce(f"attention Tq={Tq} Tk=180000 (64-bit K/V addressing)")
+    Tk, H, D = 180000, 16, 1024
+    g = torch.Generator(device=gpu).manual_seed(6)
+    q = torch.randn(1, Tq, D, device=gpu, generator=g)
+    kv = torch.randn(1, Tk, 3 * D, device=gpu, generator=g)
+    k, v = kv[..., :D], kv[..., 2 * D:]
+    o = ops.attention(q, k, v, H)
+    sel = [0, 1, Tq // 2, Tq - 1]
+    for h in (0, 7, 15):
+        c = slice(h * 64, h * 64 + 64)
+        qs = q[0, sel, c].double() * 0.125
+        s = qs @ k[0, :, c].double().T
+        p = torch.softmax(s, dim=1)
+        ref = (p @ v[0, :, c].double()).cpu().numpy()
+        got = o[0, sel, c].cpu().numpy()
+        assert np.abs(got - ref).max() / np.abs(ref).max() < TOL
+    del q, kv, k, v, o
+    torch.cuda.empty_cache()
+
+
 @pytest.mark.parametrize("B,T", [(2, 1000), (1, 2000)])
 def test_attention_wide_layout_causal(gpu, ops, B, T):
     """Causal masking through the 128-query layout (grids of a whole number of
