@@ -157,7 +157,7 @@ __global__ __launch_bounds__(64 * QS * KS) void attn_flash_kernel(
       float mloc = s[0];
 #pragma unroll
       for (int i = 1; i < 16; ++i) mloc = fmaxf(mloc, s[i]);
-      mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+      mloc = fmaxf(mloc, lane_xor32(mloc));
       // Lazy rescaling: m_run is the softmax reference, not necessarily the
       // running maximum.  It moves (and O, l are rescaled) only when a lane's
       // maximum exceeds it by more than kLazy (log2 units), so p <= 2^kLazy
@@ -209,7 +209,7 @@ __global__ __launch_bounds__(64 * QS * KS) void attn_flash_kernel(
 
   // Merge the key parts: ks > 0 publish (m, l, O^T) per lane, ks = 0 combines
   // them in part order.
-  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+  const float l_tot = l_run + lane_xor32(l_run);
   float* xch = lds + qs * ((KS - 1) * 64 * 34);  // per query sub-tile (QS of them)
   if (ks > 0) {
     float* mine = xch + (ks - 1) * (64 * 34);

@@ -86,15 +86,49 @@ __device__ __forceinline__ void st_nt(float2* p, float2 v) {
   __builtin_nontemporal_store(v.y, &p->y);
 }
 
+// Wave64 reductions without the LDS crossbar: DPP moves within each 16-lane
+// row, then the gfx950 half-row / half-wave swaps.  Each step combines two
+// groups that already hold uniform partial results (lane ^ 1, lane ^ 2, the
+// other quad of each 8-lane half row, the other half of each row, lane ^ 16,
+// lane ^ 32), and a + b == b + a, so every lane ends with the same bits.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1, 0, 3, 2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2, 3, 0, 1]
+constexpr int kDppHalfMirror = 0x141; // lane i <-> 7 - i within each 8 lanes
+constexpr int kDppMirror = 0x140;     // lane i <-> 15 - i within each 16 lanes
+
+// Value held by lane ^ 16 / lane ^ 32.
+__device__ __forceinline__ float lane_xor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return __uint_as_float((__lane_id() & 16) ? r[0] : r[1]);
+}
+__device__ __forceinline__ float lane_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return __uint_as_float((__lane_id() & 32) ? r[0] : r[1]);
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = kWave / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+  v += dpp_mov<kDppXor1>(v);
+  v += dpp_mov<kDppXor2>(v);
+  v += dpp_mov<kDppHalfMirror>(v);
+  v += dpp_mov<kDppMirror>(v);
+  v += lane_xor16(v);
+  v += lane_xor32(v);
   return v;
 }
 
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int off = kWave / 2; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+  v = fmaxf(v, dpp_mov<kDppXor1>(v));
+  v = fmaxf(v, dpp_mov<kDppXor2>(v));
+  v = fmaxf(v, dpp_mov<kDppHalfMirror>(v));
+  v = fmaxf(v, dpp_mov<kDppMirror>(v));
+  v = fmaxf(v, lane_xor16(v));
+  v = fmaxf(v, lane_xor32(v));
   return v;
 }
 
