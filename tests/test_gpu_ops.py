@@ -376,6 +376,19 @@ def test_attention_kv_past_2gib(gpu, ops, Tq):
     torch.cuda.empty_cache()
 
 
+@pytest.mark.parametrize("causal", [False, True])
+def test_attention_wide_layout_gqa(gpu, ops, causal):
+    """Grouped-query heads (16 query heads over 4 kv heads) through the 128-query layout
+    (B=2, T=1000: 256 workgroups), with K/V rows narrower than Q rows."""
+    announce(f"attention wide gqa causal={causal}")
+    B, T, D, KVD = 2, 1000, 1024, 256
+    q = rnd((B, T, D), 14)
+    k, v = rnd((B, T, KVD), 15), rnd((B, T, KVD), 16)
+    o = ops.attention(dev(q, gpu), dev(k, gpu), dev(v, gpu), 16, 4, causal=causal).cpu().numpy()
+    ref = orc.attention(q, k, v, 16, 4, causal=causal)
+    assert orc.rel_err(o, ref) < TOL
+
+
 @pytest.mark.parametrize("B,T", [(2, 1000), (1, 2000)])
 def test_attention_wide_layout_causal(gpu, ops, B, T):
     """Causal masking through the 128-query layout (grids of a whole number of
