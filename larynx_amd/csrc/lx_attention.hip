@@ -297,7 +297,7 @@ extern "C" int lx_attention_f32(const float* q, int ldq, const float* k, int ldk
   // Tk) below 2^31.
   const long lim = 1L << 31;
   const bool buf = ((long)(Tk + 128) * ldk + kHD) * 4 < lim && ((long)(Tk + 128) * ldv + kHD) * 4 < lim;
-  // Two layouts.  64-query workgroups (2 query sub-tiles x 2 key parts, 64-key
+  // Three layouts.  64-query workgroups (2 query sub-tiles x 2 key parts, 64-key
   // tiles double buffered, 70 KB of LDS) whenever they cover the CUs (DiT at
   // T = 500: 256 workgroups, 24.9 us; T = 3000: 1504).  A grid smaller than
   // the device (the Qwen2 prefill at L = 256: 56 workgroups) takes 32-query
@@ -305,9 +305,9 @@ extern "C" int lx_attention_f32(const float* q, int ldq, const float* k, int ldk
   // twice the workgroups, four waves each (13.9 -> 9.8 us).  At T = 500 that
   // layout is slower (27.8 us: the 4-part merge and two barriers per tile
   // cost more than the second resident workgroup per CU returns).
-  // A third layout, 128-query workgroups of 4 query sub-tiles x 2 key parts
-  // (512 threads, 70 KB: every K/V tile feeds twice the queries), when its
-  // grid is a whole number of workgroups per CU: T = 3000 (768 workgroups)
+  // The third, 128-query workgroups of 4 query sub-tiles x 2 key parts (512
+  // threads, 70 KB: every K/V tile feeds twice the queries), replaces the
+  // 64-query layout when its grid is a whole number of workgroups per CU: T = 3000 (768 workgroups)
   // 612 -> 571 us, T = 2000 283 -> 262, T = 1000 75.9 -> 73.8.  Grids that
   // leave a partial round (T = 1500: 384 workgroups; 2500: 640) run slower
   // than the 64-query layout and keep it.
