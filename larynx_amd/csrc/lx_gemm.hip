@@ -131,225 +131,33 @@ __device__ __forceinline__ void epilogue4v(float* Y, int ldy, int m, int n, floa
   *reinterpret_cast<float4*>(Y + (long)m * ldy + n) = o;
 }
 
-// Tiled NT GEMM.  BM x BN output tile per workgroup; WM x WN waves per k-group,
-// each owning (BM/WM) x (BN/WN) as 32x32 MFMA tiles; KS k-groups split the K
-// slabs of one tile between them (KS * WM * WN waves per workgroup, reduced
-// through LDS in a fixed order, so results are deterministic).  Each k-group
-// double-buffers its BK-wide slabs in LDS with the next slab's global loads in
-// flight during the current slab's MFMAs.  Loads always hit valid addresses
-// (rows / k clamped into range) and out-of-range values are zeroed by a
-// select on the data, so they stay plain global_load_dwordx4.
-template <int EPI, int BM, int BN, int BK, int WM, int WN, int KS>
-__global__ __launch_bounds__(64 * WM * WN * KS) void gemm_tile_kernel(
-    const float* __restrict__ X, int ldx, const float* __restrict__ W, int ldw,
-    const float* __restrict__ bias, float* Y, int ldy, int M, int N, int K, int ksplit,
-    EpiArgs ep) {
-  constexpr int GT = 64 * WM * WN;             // threads per k-group
-  constexpr int NT = GT * KS;
-  constexpr int LDA = BK + 4;
-  constexpr int TM = BM / WM / 32, TN = BN / WN / 32;
-  constexpr int A4 = BM * BK / 4, W4 = BN * BK / 4;
-  constexpr int LA = A4 / GT, LW = W4 / GT;
-  static_assert(A4 % GT == 0 && W4 % GT == 0, "slab must split evenly over the k-group");
-  static_assert(TM >= 1 && TN >= 1 && BK % 32 == 0, "bad tile");
-  extern __shared__ __attribute__((aligned(16))) float smem[];
-
-  const int tiles_m = (M + BM - 1) / BM;
-  const int tiles_n = (N + BN - 1) / BN;
-  const int nwg = tiles_m * tiles_n;
-  int id = blockIdx.x;
-  const int full = (nwg / 8) * 8;
-  if (id < full) id = (id % 8) * (full / 8) + id / 8;  // XCD-contiguous runs
-  const int m0 = (id % tiles_m) * BM, n0 = (id / tiles_m) * BN;
-
-  const int tid = threadIdx.x;
-  // wave index through readfirstlane: the compiler then treats everything
-  // derived from it (k-group, slab index) as wave-uniform (scalar branches).
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int lane = tid & 63;
-  const int kg = wave / (WM * WN);
-  const int wl = wave % (WM * WN);
-  const int wm = wl / WN, wn = wl % WN;
-  const int r = lane & 31, h = lane >> 5;
-  const int gtid = tid % GT;
-  float* As = smem + kg * 2 * (BM + BN) * LDA;
-  float* Ws = As + 2 * BM * LDA;
-  // K slice of this workgroup (blockIdx.y; one slice unless split-K partials)
-  X += (long)blockIdx.y * ksplit;
-  W += (long)blockIdx.y * ksplit;
-  Y += (long)blockIdx.y * M * ldy;
-  K = min(ksplit, K - (int)blockIdx.y * ksplit);
-
-  // Per-thread load slots: clamped row pointers and validity.
-  const float* pa[LA];
-  const float* pw[LW];
-  int ca[LA], cw[LW];
-  bool oka[LA], okw[LW];
-#pragma unroll
-  for (int i = 0; i < LA; ++i) {
-    const int idx = gtid + i * GT;
-    const int row = idx / (BK / 4);
-    ca[i] = (idx % (BK / 4)) * 4;
-    oka[i] = m0 + row < M;
-    pa[i] = X + (long)min(m0 + row, M - 1) * ldx;
-  }
-#pragma unroll
-  for (int i = 0; i < LW; ++i) {
-    const int idx = gtid + i * GT;
-    const int row = idx / (BK / 4);
-    cw[i] = (idx % (BK / 4)) * 4;
-    okw[i] = n0 + row < N;
-    pw[i] = W + (long)min(n0 + row, N - 1) * ldw;
-  }
-  // Raw loads go to registers untouched; out-of-range lanes are zeroed when
-  // the slab is written to LDS, after the MFMAs, so no wait on the loads is
-  // forced at the top of the iteration.
-  floatx4 ra[LA], rb[LW];  // native vectors: selects stay in VGPRs (no stack copies)
-  auto gload = [&](int kt) {
-#pragma unroll
-    for (int i = 0; i < LA; ++i)
-      ra[i] = *reinterpret_cast<const floatx4*>(pa[i] + min(kt * BK + ca[i], K - 4));
-#pragma unroll
-    for (int i = 0; i < LW; ++i)
-      rb[i] = *reinterpret_cast<const floatx4*>(pw[i] + min(kt * BK + cw[i], K - 4));
-  };
-  auto sstore = [&](int buf, int kt) {
-#pragma unroll
-    for (int i = 0; i < LA; ++i) {
-      const int idx = gtid + i * GT;
-      const bool ok = oka[i] && kt * BK + ca[i] < K;
-      floatx4 v;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] = ok ? ra[i][e] : 0.0f;
-      *reinterpret_cast<floatx4*>(As + buf * BM * LDA + (idx / (BK / 4)) * LDA + ca[i]) = v;
-    }
-#pragma unroll
-    for (int i = 0; i < LW; ++i) {
-      const int idx = gtid + i * GT;
-      const bool ok = okw[i] && kt * BK + cw[i] < K;
-      floatx4 v;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] = ok ? rb[i][e] : 0.0f;
-      *reinterpret_cast<floatx4*>(Ws + buf * BN * LDA + (idx / (BK / 4)) * LDA + cw[i]) = v;
-    }
-  };
-
-  floatx16 acc[TM][TN];
-#pragma unroll
-  for (int a = 0; a < TM; ++a)
-#pragma unroll
-    for (int b = 0; b < TN; ++b)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) acc[a][b][i] = 0.0f;
-
-  const int nk = (K + BK - 1) / BK;
-  const int iters = (nk + KS - 1) / KS;  // uniform trip count: barriers match across k-groups
-  if (kg < nk) {
-    gload(kg);
-    sstore(0, kg);
-  }
-  __syncthreads();
-  int buf = 0;
-  for (int it = 0; it < iters; ++it) {
-    const int kt = it * KS + kg;
-    const bool more = kt + KS < nk;
-    if (more) gload(kt + KS);
-    if (kt < nk) {
-#pragma unroll
-      for (int s32 = 0; s32 < BK / 32; ++s32) {
-        floatx4 af[TM][4], bf[TN][4];  // native vectors: component indexing stays in VGPRs
-#pragma unroll
-        for (int a = 0; a < TM; ++a) {
-          const float* p = As + buf * BM * LDA + ((wm * TM + a) * 32 + r) * LDA + s32 * 32 + h * 16;
-#pragma unroll
-          for (int j = 0; j < 4; ++j) af[a][j] = *reinterpret_cast<const floatx4*>(p + 4 * j);
-        }
-#pragma unroll
-        for (int b = 0; b < TN; ++b) {
-          const float* p = Ws + buf * BN * LDA + ((wn * TN + b) * 32 + r) * LDA + s32 * 32 + h * 16;
-#pragma unroll
-          for (int j = 0; j < 4; ++j) bf[b][j] = *reinterpret_cast<const floatx4*>(p + 4 * j);
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-#pragma unroll
-            for (int a = 0; a < TM; ++a)
-#pragma unroll
-              for (int b = 0; b < TN; ++b)
-                acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[a][j][e], bf[b][j][e],
-                                                                  acc[a][b], 0, 0, 0);
-      }
-    }
-    if (more) sstore(buf ^ 1, kt + KS);
-    __syncthreads();
-    buf ^= 1;
-  }
-
-  // k-group reduction into the LDS tile, highest group first (fixed order);
-  // accumulator register i of lane (r, h) is row (i/4)*8 + h*4 + i%4, col r.
-  constexpr int LDC = BN + 4;
-  float* Cs = smem;
-#pragma unroll
-  for (int g = KS - 1; g >= 0; --g) {
-    if (kg == g) {
-#pragma unroll
-      for (int a = 0; a < TM; ++a)
-#pragma unroll
-        for (int b = 0; b < TN; ++b)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const int row = (wm * TM + a) * 32 + (i >> 2) * 8 + h * 4 + (i & 3);
-            const int col = (wn * TN + b) * 32 + r;
-            float v = acc[a][b][i];
-            if (g < KS - 1) v += Cs[row * LDC + col];
-            Cs[row * LDC + col] = v;
-          }
-    }
-    __syncthreads();
-  }
-  for (int idx = tid; idx < BM * BN / 4; idx += NT) {
-    const int row = idx / (BN / 4), c = (idx % (BN / 4)) * 4;
-    const int m = m0 + row, n = n0 + c;
-    if (m < M && n < N)
-      epilogue4<EPI>(Y, ldy, m, n, N, bias,
-                     *reinterpret_cast<const float4*>(Cs + row * LDC + c), ep);
-  }
-}
-
-// Pipelined variant of the tiled kernel for 64 x 64 tiles, 4 waves (2 x 2) per
-// k-group: global loads run two slabs ahead of the MFMAs (two register
-// stages, statically indexed by unrolling the slab loop by 2), and within a
-// slab the LDS fragments of the next 32-wide sub-slab are read while the
-// current sub-slab's MFMAs issue.  One barrier per slab.  With IL set, the
-// slab body (one basic block) carries scheduling-group barriers that spread the
-// DS reads, DS writes and global loads between the MFMAs of the wave's single
-// accumulator chain, so they issue in the MFMA shadow instead of in bursts.
+// Pipelined NT GEMM for 64 x 64 output tiles, 4 waves (2 x 2) per k-group
+// (KS k-groups split the K slabs of one tile between them and are reduced
+// through LDS in a fixed order, so results are deterministic).  Global loads
+// run two 32-wide slabs ahead of the MFMAs in two register stages, statically
+// indexed by unrolling the slab loop by 2; LDS is double buffered.
+// Cross-barrier slabs: the barrier sits inside the slab.  The first three
+// quarters of a slab's MFMAs run alongside the LDS writes of the next slab and
+// the global loads (scheduling-group barriers spread them between the MFMAs),
+// then the barrier, then the next slab's fragment reads are issued and the last
+// quarter (operands already in registers) covers their latency, so the matrix
+// pipe does not drain at every barrier.
 // Operand rows past M (or N) read as zeros (buffer loads) or repeat the last
 // valid row (64-bit loads); either way they only reach output rows (columns)
 // the epilogue never stores.  With KMASK (K not a multiple of BK) the columns
-// past K are stored to LDS as zeros.
-// With XB (BK = 32 only; the path the library runs) the barrier sits inside
-// the slab: the first three quarters of the slab's MFMAs run alongside the LDS
-// writes of the next slab and the global loads, then the barrier, then the
-// next slab's fragment reads are issued and the last quarter (operands already
-// in registers) covers their latency, so the matrix pipe does not drain at
-// every barrier.  MF16 selects the wave's 32 x 32 output as four independent
-// 16 x 16 accumulator chains on v_mfma_f32_16x16x4f32 instead of one
-// v_mfma_f32_32x32x2f32 chain.
-template <int EPI, int BK, int KS, bool IL, bool KMASK, bool XB = false, bool BUF = true,
-          bool MF16 = false>
+// past K are stored to LDS as zeros.  MF16 selects the wave's 32 x 32 output
+// as four independent 16 x 16 accumulator chains on v_mfma_f32_16x16x4f32
+// instead of one v_mfma_f32_32x32x2f32 chain.
+template <int EPI, int KS, bool KMASK, bool BUF = true, bool MF16 = false>
 __global__ __launch_bounds__(256 * KS) void gemm_pipe_kernel(
     const float* X, int ldx, const float* W, int ldw,
     const float* __restrict__ bias, float* Y, int ldy, int M, int N, int K, int ksplit,
     EpiArgs ep) {
-  constexpr int BM = 64, BN = 64, GT = 256, NT = GT * KS;
+  constexpr int BM = 64, BN = 64, BK = 32, GT = 256, NT = GT * KS;
   constexpr int LDA = BK + 4;
   constexpr int A4 = BM * BK / 4;          // float4 per operand slab
   constexpr int L = A4 / GT;               // float4 per thread per operand
-  constexpr int S32 = BK / 32;             // 32-wide sub-slabs
-  static_assert(A4 % GT == 0 && BK % 32 == 0, "bad slab");
+  static_assert(A4 % GT == 0, "bad slab");
   extern __shared__ __attribute__((aligned(16))) float smem[];
 
   const int tiles_m = (M + BM - 1) / BM;
@@ -462,55 +270,6 @@ __global__ __launch_bounds__(256 * KS) void gemm_pipe_kernel(
   asm volatile("" ::: "memory");
   __syncthreads();
 
-  // One slab: MFMAs on LDS buffer BUF, then the next slab (held in stage
-  // SNEXT) goes to the other buffer and stage SNEXT reloads three slabs ahead.
-#define LX_SLAB(IT, BUF, SNA, SNW)                                                     \
-  do {                                                                                 \
-    /* No branch around the MFMAs: a surplus slab (past the end of K; only when   \
-       KMASK) holds zeros in LDS, so it adds exact zeros and the body stays one     \
-       scheduling region. */                                                         \
-    const float* ab = As + (BUF) * BM * LDA + (wm * 32 + r) * LDA + h * 16;           \
-    const float* wb = Ws + (BUF) * BN * LDA + (wn * 32 + r) * LDA + h * 16;           \
-    floatx4 af[2][4], bf[2][4];                                                        \
-    _Pragma("unroll") for (int j = 0; j < 4; ++j) {                                     \
-      af[0][j] = *reinterpret_cast<const floatx4*>(ab + 4 * j);                        \
-      bf[0][j] = *reinterpret_cast<const floatx4*>(wb + 4 * j);                        \
-    }                                                                                  \
-    _Pragma("unroll") for (int s = 0; s < S32; ++s) {                                   \
-      if (s + 1 < S32) {                                                               \
-        _Pragma("unroll") for (int j = 0; j < 4; ++j) {                                 \
-          af[(s + 1) & 1][j] = *reinterpret_cast<const floatx4*>(ab + (s + 1) * 32 + 4 * j); \
-          bf[(s + 1) & 1][j] = *reinterpret_cast<const floatx4*>(wb + (s + 1) * 32 + 4 * j); \
-        }                                                                              \
-      }                                                                                \
-      _Pragma("unroll") for (int j = 0; j < 4; ++j)                                     \
-        _Pragma("unroll") for (int e = 0; e < 4; ++e)                                   \
-          acc = __builtin_amdgcn_mfma_f32_32x32x2f32(af[s & 1][j][e], bf[s & 1][j][e], acc, 0, 0, 0); \
-    }                                                                                  \
-    LX_SSTORE(SNA, SNW, (BUF) ^ 1, LX_KT((IT) + 1));                                   \
-    LX_GLOAD(SNA, SNW, LX_KC((IT) + 3));                                               \
-    if (IL) {                                                                          \
-      /* interleave: two DS reads up front, then MFMAs alternating with the        \
-         remaining DS reads (8 per 32-wide sub-slab), the DS writes and the global  \
-         loads (2 L each), then the remaining MFMAs (16 per sub-slab) */            \
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);                               \
-      _Pragma("unroll") for (int q = 0; q < 8 * S32 - 2; ++q) {                         \
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                             \
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                             \
-      }                                                                                \
-      _Pragma("unroll") for (int q = 0; q < 2 * L; ++q) {                               \
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                             \
-        __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);                             \
-      }                                                                                \
-      _Pragma("unroll") for (int q = 0; q < 2 * L; ++q) {                               \
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                             \
-        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                             \
-      }                                                                                \
-      __builtin_amdgcn_sched_group_barrier(0x008, 16 * S32 - (8 * S32 - 2) - 4 * L, 0); \
-    }                                                                                  \
-    __syncthreads();                                                                   \
-  } while (0)
-
   // Cross-barrier slab (XB): fragments FA/FB of this slab are in registers on
   // entry; the next slab's go to NA/NB after the barrier.
 #define LX_SLAB_XB(IT, BUF, SNA, SNW, FA, FB, NA, NB)                                  \
@@ -600,16 +359,17 @@ __global__ __launch_bounds__(256 * KS) void gemm_pipe_kernel(
 #pragma unroll
       for (int i = 0; i < 4; ++i) acc4[bi][bj][i] = 0.0f;
 
-  if (XB && MF16) {
-    static_assert(!XB || BK == 32, "XB needs one 32-wide sub-slab per slab");
+  // Both slabs of an iteration run unconditionally (a surplus slab multiplies
+  // the zeros it holds; the launcher sets KMASK whenever the slab count is not
+  // a multiple of 2 KS), so the loop has a single back-edge state for the waits.
+  if (MF16) {
     floatx4 fa0[2][2], fb0[2][2], fa1[2][2], fb1[2][2];
     LX_FRAG16(fa0, fb0, 0);
     for (int it = 0; it < iters; it += 2) {
       LX_SLAB_XB16(it, 0, sa1, sw1, fa0, fb0, fa1, fb1);
       LX_SLAB_XB16(it + 1, 1, sa0, sw0, fa1, fb1, fa0, fb0);
     }
-  } else   if (XB) {
-    static_assert(!XB || BK == 32, "XB needs one 32-wide sub-slab per slab");
+  } else {
     floatx4 fa0[4], fb0[4], fa1[4], fb1[4];
     {
       const float* ab = As + (wm * 32 + r) * LDA + h * 16;
@@ -624,20 +384,11 @@ __global__ __launch_bounds__(256 * KS) void gemm_pipe_kernel(
       LX_SLAB_XB(it, 0, sa1, sw1, fa0, fb0, fa1, fb1);
       LX_SLAB_XB(it + 1, 1, sa0, sw0, fa1, fb1, fa0, fb0);
     }
-  } else {
-    // Both halves run unconditionally (a surplus half multiplies the zeros its
-    // slab holds; the launcher sets KMASK whenever the slab count is not a
-    // multiple of 2 KS), so the loop has a single back-edge state for the waits.
-    for (int it = 0; it < iters; it += 2) {
-      LX_SLAB(it, 0, sa1, sw1);
-      LX_SLAB(it + 1, 1, sa0, sw0);
-    }
   }
 #undef LX_SLAB_XB
 #undef LX_SLAB_XB16
 #undef LX_FRAG16
 #undef LX_MF16
-#undef LX_SLAB
 #undef LX_KC
 #undef LX_KT
 #undef LX_GLOAD
@@ -695,7 +446,7 @@ __global__ __launch_bounds__(256 * KS) void gemm_pipe_kernel(
         // 32x32x2: register i of lane (r, h) is row (i/4)*8 + h*4 + i%4, col r;
         // 16x16x4 blocks: register v of block (bi, bj), lane l is row
         // bi*16 + 4*(l/16) + v, col bj*16 + l%16
-        constexpr bool B16 = XB && MF16;
+        constexpr bool B16 = MF16;
         const int bi = i >> 3, bj = (i >> 2) & 1, v4 = i & 3;
         const int row = B16 ? wm * 32 + bi * 16 + 4 * (lane >> 4) + v4
                             : wm * 32 + (i >> 2) * 8 + h * 4 + (i & 3);
@@ -722,8 +473,9 @@ __global__ __launch_bounds__(256 * KS) void gemm_pipe_kernel(
   }
 }
 
-template <int BK, int KS>
+template <int KS>
 struct PipeCfg {
+  static constexpr int BK = 32;
   static constexpr int threads = 256 * KS;
   static size_t lds() {
     size_t a = (size_t)KS * 2 * (64 + 64) * (BK + 4) * sizeof(float);
@@ -740,19 +492,19 @@ struct Split {
   int ldw = 0;
 };
 
-template <int EPI, int BK, int KS, bool IL, bool KMASK, bool XB, bool BUF, bool MF16>
+template <int EPI, int KS, bool KMASK, bool BUF, bool MF16>
 int launch_pipe_k(const float* x, int ldx, const float* W, const float* bias, float* y, int ldy,
                   int M, int N, int K, const EpiArgs& ep, hipStream_t stream,
                   const Split& sp) {
-  auto kern = gemm_pipe_kernel<EPI, BK, KS, IL, KMASK, XB, BUF, MF16>;
-  const size_t lds = PipeCfg<BK, KS>::lds();
+  auto kern = gemm_pipe_kernel<EPI, KS, KMASK, BUF, MF16>;
+  const size_t lds = PipeCfg<KS>::lds();
   if (lds > 64 * 1024) {
     static LdsLimit once;  // per instantiation
     const int rc = raise_lds_limit((const void*)kern, lds, once, "linear");
     if (rc) return rc;
   }
   const long tiles = (long)((M + 63) / 64) * ((N + 63) / 64);
-  hipLaunchKernelGGL(kern, dim3((unsigned)tiles, sp.splits), dim3(PipeCfg<BK, KS>::threads), lds,
+  hipLaunchKernelGGL(kern, dim3((unsigned)tiles, sp.splits), dim3(PipeCfg<KS>::threads), lds,
                      stream, x, ldx, W, sp.ldw, bias, y, ldy, M, N, K, sp.ksplit, ep);
   return check_launch("gemm_pipe_kernel");
 }
@@ -766,47 +518,20 @@ inline bool buffer_loads_fit(int M, int ldx, int N, int ldw) {
 
 // The unmasked kernel needs every K slice to be whole slabs and its slab
 // count a multiple of 2 KS (the loop runs two slabs per k-group per iteration).
-template <int EPI, int BK, int KS, bool IL, bool XB = false, bool MF16 = false>
+template <int EPI, int KS, bool MF16 = false>
 int launch_pipe(const float* x, int ldx, const float* W, const float* bias, float* y, int ldy,
                 int M, int N, int K, const EpiArgs& ep, hipStream_t stream, Split sp = Split()) {
   if (sp.ksplit <= 0) sp.ksplit = K;
   if (sp.ldw <= 0) sp.ldw = K;
-  const int step = 2 * KS * BK;
+  const int step = 2 * KS * PipeCfg<KS>::BK;
   const bool exact = sp.ksplit % step == 0 && (K % sp.ksplit) % step == 0;
   if (!buffer_loads_fit(M, ldx, N, sp.ldw))  // operands past 2 GiB: 64-bit addressing
-    return launch_pipe_k<EPI, BK, KS, IL, true, XB, false, MF16>(x, ldx, W, bias, y, ldy, M, N, K,
-                                                                 ep, stream, sp);
-  return exact ? launch_pipe_k<EPI, BK, KS, IL, false, XB, true, MF16>(x, ldx, W, bias, y, ldy, M,
-                                                                       N, K, ep, stream, sp)
-               : launch_pipe_k<EPI, BK, KS, IL, true, XB, true, MF16>(x, ldx, W, bias, y, ldy, M,
-                                                                      N, K, ep, stream, sp);
-}
-
-template <int BM, int BN, int BK, int WM, int WN, int KS>
-struct TileCfg {
-  static constexpr int bm = BM, bn = BN, bk = BK, wm = WM, wn = WN, ks = KS;
-  static constexpr int threads = 64 * WM * WN * KS;
-  static size_t lds() {
-    size_t a = (size_t)KS * 2 * (BM + BN) * (BK + 4) * sizeof(float);
-    size_t c = (size_t)BM * (BN + 4) * sizeof(float);
-    return a > c ? a : c;
-  }
-};
-
-template <int EPI, class CFG>
-int launch_tile(const float* x, int ldx, const float* W, const float* bias, float* y, int ldy,
-                int M, int N, int K, const EpiArgs& ep, hipStream_t stream) {
-  auto kern = gemm_tile_kernel<EPI, CFG::bm, CFG::bn, CFG::bk, CFG::wm, CFG::wn, CFG::ks>;
-  const size_t lds = CFG::lds();
-  if (lds > 64 * 1024) {
-    static LdsLimit once;  // per instantiation
-    const int rc = raise_lds_limit((const void*)kern, lds, once, "linear");
-    if (rc) return rc;
-  }
-  const long tiles = (long)((M + CFG::bm - 1) / CFG::bm) * ((N + CFG::bn - 1) / CFG::bn);
-  hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(CFG::threads), lds, stream, x, ldx, W, K,
-                     bias, y, ldy, M, N, K, K, ep);
-  return check_launch("gemm_tile_kernel");
+    return launch_pipe_k<EPI, KS, true, false, MF16>(x, ldx, W, bias, y, ldy, M, N, K, ep,
+                                                     stream, sp);
+  return exact ? launch_pipe_k<EPI, KS, false, true, MF16>(x, ldx, W, bias, y, ldy, M, N, K, ep,
+                                                           stream, sp)
+               : launch_pipe_k<EPI, KS, true, true, MF16>(x, ldx, W, bias, y, ldy, M, N, K, ep,
+                                                          stream, sp);
 }
 
 // Skinny-M variant: one wave per output column pair, the M (<= 8) rows of x
@@ -972,34 +697,16 @@ int gemv_epi(const float* x, int ldx, const float* W, const float* bias, float* 
   return check_launch("gemv_epi_kernel");
 }
 
-// Configurations.  The library selects 7, 8 or 9; the others are built only
-// into the tuning sweep:
-//   0: tiled 64 x 64, BK 32, split-K 2        1: tiled 128 x 64, BK 32
-//   2: pipelined BK 32                        3: pipelined BK 32, split-K 2
-//   4: pipelined BK 32, interleaved           5: pipelined BK 32, split-K 2, interleaved
-//   6: pipelined BK 64, interleaved
-//   7: pipelined BK 32, cross-barrier slabs   8: as 7 with split-K 2
-//   9: as 7 on four 16x16x4 accumulator chains
-using Cfg0 = TileCfg<64, 64, 32, 2, 2, 2>;
-using Cfg1 = TileCfg<128, 64, 32, 2, 2, 1>;
-
+// Configurations: 7 = one k-group (4 waves), 8 = as 7 with intra-workgroup
+// split-K 2, 9 = as 7 on four 16x16x4 accumulator chains.
 template <int EPI>
 int dispatch_cfg(int cfg, const float* x, int ldx, const float* W, const float* bias, float* y,
                  int ldy, int M, int N, int K, const EpiArgs& ep, hipStream_t s) {
   switch (cfg) {
-    case 7: return launch_pipe<EPI, 32, 1, true, true>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
-    case 8: return launch_pipe<EPI, 32, 2, true, true>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
+    case 7: return launch_pipe<EPI, 1>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
+    case 8: return launch_pipe<EPI, 2>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
     case 9:
-      return launch_pipe<EPI, 32, 1, true, true, true>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
-#ifdef LX_GEMM_SWEEP
-    case 4: return launch_pipe<EPI, 32, 1, true>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
-    case 5: return launch_pipe<EPI, 32, 2, true>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
-    case 0: return launch_tile<EPI, Cfg0>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
-    case 1: return launch_tile<EPI, Cfg1>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
-    case 2: return launch_pipe<EPI, 32, 1, false>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
-    case 3: return launch_pipe<EPI, 32, 2, false>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
-    case 6: return launch_pipe<EPI, 64, 1, true>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
-#endif
+      return launch_pipe<EPI, 1, true>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
   }
   set_error("linear: unknown tile configuration %d", cfg);
   return LX_ERR_ARG;
@@ -1064,7 +771,7 @@ int gemm_splitk_partials(const float* x, int ldx, const float* W, int ldw, float
   sp.splits = splits;
   sp.ksplit = ksplit;
   sp.ldw = ldw;
-  return launch_pipe<LX_EPI_NONE, 32, 1, true, true>(x, ldx, W, nullptr, ws, N, M, N, K, ep, stream,
+  return launch_pipe<LX_EPI_NONE, 1>(x, ldx, W, nullptr, ws, N, M, N, K, ep, stream,
                                                      sp);
 }
 
@@ -1108,16 +815,3 @@ extern "C" int lx_linear_f32(const float* x, int ldx, const float* W, const floa
   LX_REQUIRE(tiles < (1L << 31), "linear: too many tiles");
   return dispatch_gemm(kind, pick_config(M, N, K), x, ldx, W, bias, y, ldy, M, N, K, ep, stream);
 }
-
-#ifdef LX_GEMM_SWEEP
-// Tuning hook (built only into the sweep library, never into liblxops.so).
-extern "C" int lx_gemm_sweep(int cfg, int kind, const float* x, int ldx, const float* W,
-                             const float* bias, float* y, int ldy, int M, int N, int K,
-                             const lx_epilogue* epi, hipStream_t stream) {
-  EpiArgs ep;
-  int rc = make_epi(epi, N, &ep);
-  if (rc) return rc;
-  ep.vec = epi_vec_ok(ep, y, ldy, bias);
-  return dispatch_gemm(kind, cfg, x, ldx, W, bias, y, ldy, M, N, K, ep, stream);
-}
-#endif

@@ -213,7 +213,7 @@ __global__ void gather_kernel1(const float* __restrict__ table, int D, IdChunk i
 }  // namespace
 
 // Coefficients exactly as the reference host loop forms them
-// (src/flow/flow_matching.cpp:161-163): fp32 product then expf.
+// (src/flow/flow_matching.cpp:14-17): fp32 product then expf.
 void timestep_coeff(int half, float* c) {
   const float step = (float)(std::log(10000.0) / (double)(half - 1));
   for (int j = 0; j < half; ++j) c[j] = expf(-(float)j * step);

@@ -190,7 +190,7 @@ void orc_rope_partial(float* q, const int* pos, int B, int T, int ld, int rot_di
   }
 }
 
-/* Sinusoid of time_embed_host (src/flow/flow_matching.cpp:158-167):
+/* Sinusoid of time_embed_host (src/flow/flow_matching.cpp:14-20):
  * coeff_j = expf(-j * fp32(ln(1e4)/(half-1))), angle = (scale * t) * coeff_j in
  * fp32, then sin / cos. */
 void orc_timestep_embed(const float* t, int B, int half_dim, float scale, float* out) {
@@ -207,7 +207,7 @@ void orc_timestep_embed(const float* t, int B, int half_dim, float scale, float*
 }
 
 /* TimestepEmbedding: sinusoid(256, scale 1000) -> Linear -> SiLU -> Linear.
- * src/flow/flow_matching.cpp:157-189; flow_reference.py:294-304. */
+ * src/flow/flow_matching.cpp:10-42; flow_reference.py:294-304. */
 void orc_time_mlp(const float* t, int B, const float* w0, const float* b0, const float* w2,
                   const float* b2, int D, float* out) {
   float* sinus = (float*)malloc(sizeof(float) * B * 256);
@@ -271,49 +271,129 @@ int orc_embed_gather(const float* table, long n_rows, int D, const int* ids, int
 }
 
 /* softmax(scale q k^T [+ causal]) v per head, GQA head h -> kv h / rep.
- * src/flow/dit.cpp:34-51; src/llm/ops.cpp:32-65. */
+ * src/flow/dit.cpp:34-51; src/llm/ops.cpp:32-65.  Scores, softmax and P.V
+ * are evaluated in fp64.  Work is blocked for speed only (4 queries against 4
+ * keys per register tile, K and V converted to fp64 once): every score is a
+ * full fp64 dot product and every output an fp64 sum, whatever the order. */
+enum { ORC_QB = 4 };
 void orc_attention(const float* q, int ldq, const float* k, int ldk, const float* v, int ldv,
                    float* o, int ldo, int B, int Tq, int Tk, int n_heads, int n_kv_heads,
                    int head_dim, float scale, int causal, int q_offset) {
   const int rep = n_heads / n_kv_heads;
-  const long work = (long)B * n_heads * Tq;
+  const int hd = head_dim;
+  const long kv_elems = (long)B * n_kv_heads * Tk * hd;
+  double* kd = (double*)malloc(sizeof(double) * (kv_elems > 0 ? kv_elems : 1));
+  double* vd = (double*)malloc(sizeof(double) * (kv_elems > 0 ? kv_elems : 1));
+  if (!kd || !vd) {
+    free(kd);
+    free(vd);
+    return;
+  }
+  /* (b, g, j, d) contiguous fp64 copies */
+#pragma omp parallel for schedule(static)
+  for (long r = 0; r < (long)B * n_kv_heads * Tk; ++r) {
+    const int j = (int)(r % Tk);
+    const int g = (int)((r / Tk) % n_kv_heads);
+    const int b = (int)(r / ((long)Tk * n_kv_heads));
+    const float* kr = k + ((long)b * Tk + j) * ldk + g * hd;
+    const float* vr = v + ((long)b * Tk + j) * ldv + g * hd;
+    for (int d = 0; d < hd; ++d) {
+      kd[r * hd + d] = kr[d];
+      vd[r * hd + d] = vr[d];
+    }
+  }
+  const int nqb = (Tq + ORC_QB - 1) / ORC_QB;
+  const long work = (long)B * n_heads * nqb;
 #pragma omp parallel
   {
-    double* sc = (double*)malloc(sizeof(double) * Tk);
-    double* acc = (double*)malloc(sizeof(double) * head_dim);
-#pragma omp for schedule(static)
+    double* sc = (double*)malloc(sizeof(double) * ORC_QB * (Tk > 0 ? Tk : 1));
+    double* qv = (double*)malloc(sizeof(double) * ORC_QB * hd);
+    double* acc = (double*)malloc(sizeof(double) * ORC_QB * hd);
+#pragma omp for schedule(dynamic, 4)
     for (long w = 0; w < work; ++w) {
-      const int i = (int)(w % Tq);
-      const int h = (int)((w / Tq) % n_heads);
-      const int b = (int)(w / ((long)Tq * n_heads));
+      const int qb = (int)(w % nqb);
+      const int h = (int)((w / nqb) % n_heads);
+      const int b = (int)(w / ((long)nqb * n_heads));
       const int g = h / rep;
-      const float* qr = q + ((long)b * Tq + i) * ldq + h * head_dim;
-      const int kend = causal ? (q_offset + i + 1 < Tk ? q_offset + i + 1 : Tk) : Tk;
-      double mx = -INFINITY;
-      for (int j = 0; j < kend; ++j) {
-        const float* kr = k + ((long)b * Tk + j) * ldk + g * head_dim;
-        double s = 0.0;
-        for (int d = 0; d < head_dim; ++d) s += (double)qr[d] * kr[d];
-        s *= scale;
-        sc[j] = s;
-        if (s > mx) mx = s;
+      const int i0 = qb * ORC_QB;
+      const int nq = Tq - i0 < ORC_QB ? Tq - i0 : ORC_QB;
+      int kend[ORC_QB];
+      int kmax = 0;
+      for (int ii = 0; ii < ORC_QB; ++ii) {
+        const int i = i0 + (ii < nq ? ii : nq - 1); /* pad rows repeat the last query */
+        const float* qr = q + ((long)b * Tq + i) * ldq + h * hd;
+        for (int d = 0; d < hd; ++d) qv[ii * hd + d] = qr[d];
+        kend[ii] = causal ? (q_offset + i + 1 < Tk ? q_offset + i + 1 : Tk) : Tk;
+        if (kend[ii] > kmax) kmax = kend[ii];
       }
-      double l = 0.0;
-      for (int j = 0; j < kend; ++j) {
-        sc[j] = exp(sc[j] - mx);
-        l += sc[j];
+      const double* kb = kd + ((long)b * n_kv_heads + g) * Tk * hd;
+      const double* vb = vd + ((long)b * n_kv_heads + g) * Tk * hd;
+      const double* q0 = qv;
+      const double* q1 = qv + hd;
+      const double* q2 = qv + 2 * hd;
+      const double* q3 = qv + 3 * hd;
+      for (int j0 = 0; j0 < kmax; j0 += 4) {
+        const int nj = kmax - j0 < 4 ? kmax - j0 : 4;
+        const double* k0 = kb + (long)j0 * hd;
+        const double* k1 = kb + (long)(j0 + (nj > 1 ? 1 : 0)) * hd;
+        const double* k2 = kb + (long)(j0 + (nj > 2 ? 2 : 0)) * hd;
+        const double* k3 = kb + (long)(j0 + (nj > 3 ? 3 : 0)) * hd;
+        double s00 = 0, s01 = 0, s02 = 0, s03 = 0, s10 = 0, s11 = 0, s12 = 0, s13 = 0;
+        double s20 = 0, s21 = 0, s22 = 0, s23 = 0, s30 = 0, s31 = 0, s32 = 0, s33 = 0;
+#pragma omp simd reduction(+ : s00, s01, s02, s03, s10, s11, s12, s13, s20, s21, s22, s23, s30, \
+                               s31, s32, s33)
+        for (int d = 0; d < hd; ++d) {
+          s00 += q0[d] * k0[d]; s01 += q0[d] * k1[d]; s02 += q0[d] * k2[d]; s03 += q0[d] * k3[d];
+          s10 += q1[d] * k0[d]; s11 += q1[d] * k1[d]; s12 += q1[d] * k2[d]; s13 += q1[d] * k3[d];
+          s20 += q2[d] * k0[d]; s21 += q2[d] * k1[d]; s22 += q2[d] * k2[d]; s23 += q2[d] * k3[d];
+          s30 += q3[d] * k0[d]; s31 += q3[d] * k1[d]; s32 += q3[d] * k2[d]; s33 += q3[d] * k3[d];
+        }
+        const double s4[4][4] = {{s00, s01, s02, s03}, {s10, s11, s12, s13},
+                                 {s20, s21, s22, s23}, {s30, s31, s32, s33}};
+        for (int ii = 0; ii < ORC_QB; ++ii)
+          for (int jj = 0; jj < nj; ++jj) sc[(long)ii * Tk + j0 + jj] = s4[ii][jj] * scale;
       }
-      for (int d = 0; d < head_dim; ++d) acc[d] = 0.0;
-      for (int j = 0; j < kend; ++j) {
-        const float* vr = v + ((long)b * Tk + j) * ldv + g * head_dim;
-        for (int d = 0; d < head_dim; ++d) acc[d] += sc[j] * vr[d];
+      double l[ORC_QB];
+      for (int ii = 0; ii < ORC_QB; ++ii) {
+        double* sr = sc + (long)ii * Tk;
+        double mx = -INFINITY;
+        for (int j = 0; j < kend[ii]; ++j)
+          if (sr[j] > mx) mx = sr[j];
+        double sum = 0.0;
+        for (int j = 0; j < kend[ii]; ++j) {
+          sr[j] = exp(sr[j] - mx);
+          sum += sr[j];
+        }
+        for (int j = kend[ii]; j < kmax; ++j) sr[j] = 0.0;
+        l[ii] = sum;
       }
-      float* orow = o + ((long)b * Tq + i) * ldo + h * head_dim;
-      for (int d = 0; d < head_dim; ++d) orow[d] = (float)(acc[d] / l);
+      for (int x = 0; x < ORC_QB * hd; ++x) acc[x] = 0.0;
+      for (int j = 0; j < kmax; ++j) {
+        const double* vr = vb + (long)j * hd;
+        const double p0 = sc[j], p1 = sc[Tk + j], p2 = sc[2L * Tk + j], p3 = sc[3L * Tk + j];
+        double* a0 = acc;
+        double* a1 = acc + hd;
+        double* a2 = acc + 2 * hd;
+        double* a3 = acc + 3 * hd;
+#pragma omp simd
+        for (int d = 0; d < hd; ++d) {
+          a0[d] += p0 * vr[d];
+          a1[d] += p1 * vr[d];
+          a2[d] += p2 * vr[d];
+          a3[d] += p3 * vr[d];
+        }
+      }
+      for (int ii = 0; ii < nq; ++ii) {
+        float* orow = o + ((long)b * Tq + i0 + ii) * ldo + h * hd;
+        for (int d = 0; d < hd; ++d) orow[d] = (float)(acc[ii * hd + d] / l[ii]);
+      }
     }
     free(sc);
+    free(qv);
     free(acc);
   }
+  free(kd);
+  free(vd);
 }
 
 static double mish_d(double x) {

@@ -14,7 +14,7 @@
  *   - rotary angles: fp32(pos) * fp32 inv_freq, rounded to fp32
  *     (flow_reference.py:79, 96; the HF Qwen2 rotary does the same);
  *   - sinusoid angles: (1000 * t) * expf(-j * fp32(ln(1e4)/127)), in fp32
- *     (src/flow/flow_matching.cpp:161-164).
+ *     (src/flow/flow_matching.cpp:14-17).
  * All tensors are host pointers, row-major in the PyTorch sense.
  */
 #ifndef LX_ORACLE_H
