@@ -17,7 +17,8 @@ Also reported on the same JSON line:
                 MALL does not serve the reads);
   flow_infer    the whole FlowDecoder inference of a 10 s utterance (frontend +
                 10 Euler steps), host token ids in, output mel frames out;
-  cpu_baseline  the CPU oracle's Euler step on this host's cores (bounded sample).
+  cpu_baseline  the reference's fp32 ggml graph for the same Euler step, restated
+                node by node on this host's cores (bounded sample).
 
 Usage: python bench.py [--steps K] [--warmup W] [--T 500] [--no-cpu]
 """
@@ -363,30 +364,44 @@ def qwen2_lm(torch, dev, g):
 
 
 def cpu_baseline(T, seconds):
-    """The CPU oracle's CFG Euler step (22-block DiT, B=2, T) on this host."""
+    """The reference's CPU path for the same step: its ggml graph for one CFG
+    Euler step (22-block DiT, B=2, T) restated node by node in fp32, timed on
+    this host's cores (oracle/lx_ggml_cpu.c; ggml itself is absent).  One
+    warm-up step, then the median of at least five steps (more while under
+    `seconds`)."""
     import numpy as np
     from oracle import oracle as orc
+    from oracle import ggml_cpu
     from larynx_amd.flow import DiTConfig, dit_param_shapes
     params = orc.make_params(dit_param_shapes(DiTConfig()), 1)
-    dit = orc.Dit(params)
+    g = ggml_cpu.GgmlCpuDit(params, B=2, max_T=T)
     x = orc.normal((80, T), 2, 1)
-    mu = orc.normal((80, T), 2, 2)
-    cond = orc.normal((80, T), 2, 3)
-    spks = orc.normal((80,), 2, 4, 1.0 / np.sqrt(80.0))
-    dit.cfm_step(x, mu, cond, spks, 0.0, 0.0123)  # warm-up (page in weights, threads)
+    mu2, cond2, spks2 = g.cfm_inputs(orc.normal((80, T), 2, 2), orc.normal((80, T), 2, 3),
+                                     orc.normal((80,), 2, 4, 1.0 / np.sqrt(80.0)))
+    g.cfm_step(x, mu2, cond2, spks2, 0.0, 0.0123)  # warm-up (page in weights, threads)
     times = []
     t_start = time.perf_counter()
     while True:
         t0 = time.perf_counter()
-        x = dit.cfm_step(x, mu, cond, spks, 0.0123, 0.05)
+        g.cfm_step(x, mu2, cond2, spks2, 0.0123, 0.05)
         times.append(time.perf_counter() - t0)
-        if time.perf_counter() - t_start > seconds or len(times) >= 20:
+        if len(times) >= 5 and (time.perf_counter() - t_start > seconds or len(times) >= 20):
             break
+    g.close()
     t_step = float(np.median(times))
-    return {"value": T / t_step, "unit": "mel frames/s", "cores": orc.lib.orc_get_threads(),
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except AttributeError:
+        affinity = os.cpu_count()
+    return {"value": T / t_step, "unit": "mel frames/s", "cores": ggml_cpu.threads(),
             "kind": "port",
-            "sample": f"{len(times)} CFG Euler step(s) of the 22-block DiT at B=2, T={T} "
-                      f"(median {t_step:.2f} s/step), fp32 storage / fp64 accumulation"}
+            "name": "ggml-equivalent CPU restatement (ggml unavailable offline)",
+            "cpu_model": ggml_cpu.cpu_model(), "nproc": affinity, "isa": ggml_cpu.isa(),
+            "ms_per_step": round(t_step * 1e3, 1),
+            "sample": f"{len(times)} CFG Euler steps of the 22-block DiT at B=2, T={T} through "
+                      f"the reference's fp32 ggml node graph (one pass per node, KQ "
+                      f"materialised, blocked SGEMM), median {t_step:.3f} s/step, "
+                      f"{ggml_cpu.threads()} OpenMP threads"}
 
 
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemm_qkv_rope_T500_traffic.md")
