@@ -178,6 +178,12 @@ SIGNATURES = [
 
 
 def _load():
+    # torch first: liblxops.so must bind to the HIP runtime torch already
+    # carries (its bundled libamdhip64, soname libamdhip64.so.7), which the
+    # dynamic linker then reuses.  Loaded the other way round, liblxops.so pulls
+    # in the system copy and torch later loads its own beside it: two runtimes in
+    # one process, and device allocations fail.
+    import torch  # noqa: F401
     if not os.path.exists(LIB_PATH):
         raise ImportError(
             f"{LIB_PATH} is not built; run `python -c 'import __graft_entry__ as g; g.build()'` "

@@ -116,3 +116,18 @@ def test_product_path_does_not_reference_the_oracle():
                 text = open(os.path.join(dirpath, f), errors="ignore").read()
                 assert "lxoracle" not in text and "import oracle" not in text, f
                 assert "from oracle" not in text, f
+
+
+def test_one_hip_runtime_whatever_the_import_order():
+    """Importing the package before torch must still leave one HIP runtime in
+    the process (torch's), or allocations made through liblxops.so and
+    through torch land in different runtimes."""
+    import subprocess
+    import sys
+    code = ("import larynx_amd, torch\n"
+            "maps = open('/proc/self/maps').read().splitlines()\n"
+            "print(len({l.split()[-1] for l in maps if 'libamdhip64' in l}))\n")
+    out = subprocess.run([sys.executable, "-c", code], cwd=ROOT, capture_output=True, text=True,
+                         timeout=300)
+    assert out.returncode == 0, out.stderr
+    assert out.stdout.strip().splitlines()[-1] == "1"
