@@ -104,6 +104,17 @@ int lx_time_mlp_f32(const float* t, int B, const float* w0, const float* b0,
                     const float* w2, const float* b2, int D, float* work, float* out,
                     hipStream_t stream);
 
+/* lx_time_mlp_f32 without the workspace argument: the hidden layer lives in a
+ * library-owned device array (64 KiB per device, held until the process ends),
+ * so the call allocates nothing and needs no caller memory beyond t, the
+ * weights and out.  No counterpart in the reference: it is for callers that
+ * cannot allocate (code under HIP graph capture, tight serving loops).
+ * B * D <= 16384, else LX_ERR_ARG.  All calls on one device share the array:
+ * calls that overlap on one device (e.g. on two streams) race. */
+int lx_time_mlp_f32_noalloc(const float* t, int B, const float* w0, const float* b0,
+                            const float* w2, const float* b2, int D, float* out,
+                            hipStream_t stream);
+
 /* ------------------------------------------------------------------------ */
 /* Qwen2 fused ops                                                           */
 /* ------------------------------------------------------------------------ */

@@ -121,6 +121,7 @@ SIGNATURES = [
      [fp, fp, fp, C.c_long, C.c_int, C.c_int, C.c_int, stream_t]),
     ("lx_timestep_embed_f32", C.c_int, [fp, C.c_int, C.c_int, C.c_float, fp, stream_t]),
     ("lx_time_mlp_f32", C.c_int, [fp, C.c_int, fp, fp, fp, fp, C.c_int, fp, fp, stream_t]),
+    ("lx_time_mlp_f32_noalloc", C.c_int, [fp, C.c_int, fp, fp, fp, fp, C.c_int, fp, stream_t]),
     ("lx_rmsnorm_f32", C.c_int, [fp, fp, fp, C.c_int, C.c_int, C.c_float, stream_t]),
     ("lx_rope_neox_f32", C.c_int,
      [fp, ip, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, stream_t]),

@@ -3,10 +3,20 @@
 // are weight-streaming (HBM-bound on W), so each wave owns R output rows at a
 // time, keeps R float4 weight loads in flight per lane, and reduces with
 // wave64 shuffles.  The activations are staged in LDS with act_in applied.
+#include <atomic>
 #include <cstring>
+#include <mutex>
 
 #include "lx_common.hpp"
 #include "lx_internal.hpp"
+
+// Hidden layer of lx_time_mlp_f32_noalloc (B * D floats): a device array in
+// place of the caller's workspace, for callers that cannot allocate.  Each
+// device holds its own copy until the process ends; every call on a device
+// shares it, so calls that overlap on one device race.  64 KiB covers every
+// shape the second layer's GEMV accepts (B * D * 4 bytes of LDS <= 64 KiB).
+constexpr long kTimeMlpScratchFloats = 16384;
+static __device__ __align__(256) float scratch[kTimeMlpScratchFloats];
 
 namespace lx {
 namespace {
@@ -207,4 +217,55 @@ extern "C" int lx_time_mlp_f32(const float* t, int B, const float* w0, const flo
   LX_REQUIRE(t && work, "time_mlp: null pointer");
   // work: B * (256 + D) floats; the hidden layer uses the last B * D of them.
   return time_mlp(t, nullptr, B, w0, b0, w2, b2, D, work + (long)B * 256, out, stream);
+}
+
+namespace {
+
+constexpr int kScratchDevices = 64;
+std::atomic<float*> g_scratch_addr[kScratchDevices];
+std::mutex g_scratch_mu;
+
+// Device address of `scratch` on the current device, looked up once per device
+// with that device current (each device's copy lives at its own address; the
+// array's name in host code is only a handle for the lookup).
+int scratch_address(float** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    set_error("time_mlp_noalloc: hipGetDevice failed");
+    return LX_ERR_LAUNCH;
+  }
+  LX_REQUIRE(dev >= 0 && dev < kScratchDevices, "time_mlp_noalloc: device %d out of range", dev);
+  float* p = g_scratch_addr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_addr[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      void* addr = nullptr;
+      const hipError_t e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || !addr) {
+        set_error("time_mlp_noalloc: hipGetSymbolAddress failed: %s", hipGetErrorString(e));
+        return LX_ERR_LAUNCH;
+      }
+      p = static_cast<float*>(addr);
+      g_scratch_addr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return LX_OK;
+}
+
+}  // namespace
+
+extern "C" int lx_time_mlp_f32_noalloc(const float* t, int B, const float* w0, const float* b0,
+                                       const float* w2, const float* b2, int D, float* out,
+                                       hipStream_t stream) {
+  LX_REQUIRE(t, "time_mlp_noalloc: null pointer");
+  LX_REQUIRE(B > 0 && D > 0 && (long)B * D <= kTimeMlpScratchFloats,
+             "time_mlp_noalloc: B*D = %ld exceeds the %ld-float device scratch", (long)B * D,
+             kTimeMlpScratchFloats);
+  float* hid = nullptr;
+  LX_TRY(scratch_address(&hid));
+  // Every element of the hidden layer is written by the first layer's kernel
+  // before the second reads it: nothing has to start at zero.
+  return time_mlp(t, nullptr, B, w0, b0, w2, b2, D, hid, out, stream);
 }
