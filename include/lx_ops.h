@@ -333,6 +333,13 @@ typedef struct lx_flow_capture {
 } lx_flow_capture;
 int lx_flow_set_capture(lx_flow* flow, const lx_flow_capture* cap);
 
+/* The decoder's B = 2 estimator (owned by the decoder, valid until
+ * lx_flow_destroy), for the FlowDebug DiT stages at CFM step 1
+ * (include/larynx/flow/flow.h:24-31; captured in src/flow/flow.cpp:261-270):
+ * lx_dit_set_capture on it, then one lx_dit_forward over the step-1 inputs
+ * ([z; z], [mu; 0], [cond; 0], [spk; 0], t = 0).  NULL for a NULL decoder. */
+lx_dit* lx_flow_estimator(lx_flow* flow);
+
 /* FlowDecoder::infer (src/flow/flow.cpp:111-290, finalize = true):
  *   prompt_tokens[n_prompt], tokens[n_tokens]: HOST speech token ids; negative
  *     ids are clamped to 0 as the reference does, ids >= vocab -> LX_ERR_RANGE;
@@ -377,8 +384,9 @@ typedef struct lx_qwen2 lx_qwen2;
 /* Replaces LLM::load's weight upload (src/llm/llm.cpp:50-61); the tables are
  * referenced, the layer weights re-packed (QKV fused, gate/up interleaved).
  * max_ctx bounds prompt + generated tokens (KV cache capacity), 1..4096.
- * Geometry: head_dim 64, hidden <= 2048, intermediate <= 6144, at most 8
- * query heads per kv head (Qwen2-0.5B: 896 / 4864 / 14:2); else LX_ERR_ARG. */
+ * Geometry: head_dim 64, hidden <= 2048, hidden + 2 * 64 * n_kv_heads <= 2048,
+ * intermediate <= 6144, at most 8 query heads per kv head (Qwen2-0.5B:
+ * 896 / 4864 / 14:2); else LX_ERR_ARG. */
 int lx_qwen2_create(const lx_qwen2_weights* w, int max_ctx, lx_qwen2** out);
 void lx_qwen2_destroy(lx_qwen2* m);
 
@@ -453,8 +461,8 @@ const char* lx_gguf_get_string(const lx_gguf* gguf, const char* key);
  * device copy is released once the decoder has packed its own. */
 int lx_flow_load(const char* path, int max_tokens, lx_flow** out);
 /* LLM::load (src/llm/llm.cpp:50-61, src/llm/gguf.cpp:30-100): names under
- * llm.model.model. plus speech_embedding / llm_decoder; the model keeps the
- * file's device copy (it references the embedding tables) until destroy. */
+ * llm.model.model. plus speech_embedding / llm_decoder; the model copies every
+ * tensor into its own memory and releases the file's device copy. */
 int lx_qwen2_load(const char* path, int max_ctx, lx_qwen2** out);
 
 #ifdef __cplusplus

@@ -149,6 +149,7 @@ SIGNATURES = [
     ("lx_flow_create", C.c_int,
      [C.POINTER(DitWeights), C.POINTER(FlowFrontendWeights), C.c_int, C.POINTER(C.c_void_p)]),
     ("lx_flow_destroy", None, [C.c_void_p]),
+    ("lx_flow_estimator", C.c_void_p, [C.c_void_p]),
     ("lx_flow_set_capture", C.c_int, [C.c_void_p, C.POINTER(FlowCapture)]),
     ("lx_flow_infer", C.c_int,
      [C.c_void_p, ip, C.c_int, ip, C.c_int, fp, C.c_int, fp, fp, fp, stream_t]),

@@ -141,6 +141,8 @@ extern "C" void lx_flow_destroy(lx_flow* f) {
   delete f;
 }
 
+extern "C" lx_dit* lx_flow_estimator(lx_flow* f) { return f ? f->dit : nullptr; }
+
 extern "C" int lx_flow_set_capture(lx_flow* f, const lx_flow_capture* cap) {
   LX_REQUIRE(f, "flow_set_capture: null decoder");
   f->cap = cap ? *cap : lx_flow_capture{};
