@@ -492,7 +492,13 @@ extern "C" int lx_qwen2_load(const char* path, int max_ctx, lx_qwen2** out) {
     lx_gguf_close(g);
     return rc;
   }
-  // the model references the embedding tables in place: it owns the file's memory
-  qwen2_adopt_weights(*out, g);
-  return LX_OK;
+  // create copied every layer; the two embedding tables it referenced in place
+  // move into the model's memory too, and the file's device copy is released
+  rc = qwen2_own_tables(*out);
+  lx_gguf_close(g);
+  if (rc != LX_OK) {
+    lx_qwen2_destroy(*out);
+    *out = nullptr;
+  }
+  return rc;
 }

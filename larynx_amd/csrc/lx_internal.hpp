@@ -175,9 +175,9 @@ int flow_pack_mu_cond(const float* pre, int Tseq, int ratio, const float* prompt
 int conv_kmajor_pack(const float* w, int OC, int IC, int K, float* wp, hipStream_t s);
 
 // ---- weight files (lx_gguf.cpp / lx_qwen2.cpp) ----
-// Hands the model the GGUF object whose device memory it references (the
-// embedding tables); the model closes it when it is destroyed.
-void qwen2_adopt_weights(lx_qwen2* m, lx_gguf* g);
+// Copies the embedding tables the model references into its own device memory
+// (synchronous), so the weight file's device copy can be released.
+int qwen2_own_tables(lx_qwen2* m);
 
 // Grouped conv + Mish with tap-major packed weights (lx_conv_pos_mish_f32).
 int conv_pos_mish_packed(const float* x, const float* wp, const float* bias, const float* resid,

@@ -58,15 +58,30 @@ struct lx_qwen2 {
   bool use_graph = true;      // replay the layer stack as one HIP graph
   hipStream_t cap_stream = nullptr;
   hipGraphExec_t graph = nullptr;
-  lx_gguf* weights_file = nullptr;  // set by lx_qwen2_load: holds the referenced tables
   ~lx_qwen2() {
     if (graph) (void)hipGraphExecDestroy(graph);
     if (cap_stream) (void)hipStreamDestroy(cap_stream);
-    if (weights_file) lx_gguf_close(weights_file);
   }
 };
 
-void lx::qwen2_adopt_weights(lx_qwen2* m, lx_gguf* g) { m->weights_file = g; }
+int lx::qwen2_own_tables(lx_qwen2* m) {
+  const size_t nt = (size_t)m->text_vocab * m->H, ns = (size_t)m->speech_vocab * m->H;
+  float* et = m->arena.alloc<float>(nt);
+  float* se = m->arena.alloc<float>(ns);
+  if (!et || !se) {
+    set_error("qwen2_load: device allocation failed for the embedding tables");
+    return LX_ERR_ALLOC;
+  }
+  if (hipMemcpy(et, m->embed_tokens, nt * sizeof(float), hipMemcpyDeviceToDevice) != hipSuccess ||
+      hipMemcpy(se, m->speech_embedding, ns * sizeof(float), hipMemcpyDeviceToDevice) !=
+          hipSuccess) {
+    set_error("qwen2_load: embedding table copy failed");
+    return LX_ERR_LAUNCH;
+  }
+  m->embed_tokens = et;
+  m->speech_embedding = se;
+  return LX_OK;
+}
 
 namespace {
 
@@ -227,6 +242,10 @@ extern "C" int lx_qwen2_create(const lx_qwen2_weights* w, int max_ctx, lx_qwen2*
   LX_REQUIRE(dec_supported(w->hidden, w->intermediate) && w->n_heads / w->n_kv_heads <= 8,
              "qwen2_create: decode kernels need hidden <= 2048, intermediate <= 6144 and "
              "at most 8 query heads per kv head");
+  // the prefill's fused q|k|v reduce pass holds one projected row per workgroup
+  LX_REQUIRE(w->hidden + 2 * w->n_kv_heads * w->head_dim <= 2048,
+             "qwen2_create: fused q|k|v row of %d floats exceeds 2048 (hidden %d, %d kv heads)",
+             w->hidden + 2 * w->n_kv_heads * w->head_dim, w->hidden, w->n_kv_heads);
   LX_REQUIRE(w->embed_tokens && w->speech_embedding && w->final_norm && w->llm_decoder &&
                  w->layers,
              "qwen2_create: missing tables");

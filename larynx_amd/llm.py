@@ -108,7 +108,7 @@ class Qwen2LM:
     @classmethod
     def load(cls, path, max_ctx: int = 4096):
         """LLM::load: an llm.gguf checkpoint (geometry from its tensors; the model
-        keeps the file's device copy, which holds the embedding tables)."""
+        copies every tensor into its own device memory)."""
         from .gguf import GgufFile
         hdr = GgufFile(path, device=False)
         shape = {n: s for n, _, s, _ in hdr.tensors()}

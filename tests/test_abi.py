@@ -70,6 +70,14 @@ def test_argument_errors_need_no_device():
     out = C.c_void_p()
     assert lib.lx_flow_load(b"/nonexistent/flow.gguf", 250, C.byref(out)) == LX_ERR_ARG
     assert b"cannot open" in lib.lx_last_error() and not out.value
+    # a Qwen2 geometry whose fused q|k|v row the prefill cannot hold is refused
+    # at create time (hidden 2048 with 4 kv heads: 2560 floats)
+    from larynx_amd._lib import Qwen2Weights
+    w = Qwen2Weights()
+    (w.hidden, w.intermediate, w.n_heads, w.n_kv_heads, w.head_dim, w.n_layers, w.text_vocab,
+     w.speech_vocab, w.rms_eps, w.rope_theta) = (2048, 4864, 32, 4, 64, 1, 100, 6761, 1e-6, 1e6)
+    assert lib.lx_qwen2_create(C.byref(w), 16, C.byref(out)) == LX_ERR_ARG
+    assert b"2560" in lib.lx_last_error() and not out.value
 
 
 def _c_layout(struct, fields):
