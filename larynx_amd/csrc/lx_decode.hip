@@ -14,7 +14,8 @@
 //   - the residual adds (src/llm/llm.cpp:281, 289) in the o / down epilogues.
 // Attention over the cache is split-key GQA: one workgroup per (64-key split,
 // kv head) scores all query heads of its group, then one workgroup per query
-// head merges the partial softmax states.
+// head merges the partial softmax states; while the whole cache fits one split
+// the first pass writes the output and the merge pass is left out.
 //
 // The position (= cache length before the token) is read from device memory,
 // so one capture of a layer stack into a HIP graph serves every position.
@@ -399,17 +400,22 @@ int dec_gemv(int epi, const DecGemvArgs& a, hipStream_t s) {
   return LX_ERR_ARG;
 }
 
-int dec_attention(const DecAttnArgs& a, int n_kv_heads, hipStream_t s) {
+int dec_attention(const DecAttnArgs& a, int n_kv_heads, bool one_split, hipStream_t s) {
   const int max_splits = dec_attention_splits(a.max_rows);
   LX_REQUIRE(a.rep >= 1 && a.rep <= kMaxRep && a.ld % 4 == 0 && a.max_rows >= 1 &&
                  max_splits <= 4 * kMergePerWave,
              "dec_attention: bad args");
-  hipLaunchKernelGGL(dec_attn_partial_kernel, dim3(max_splits, n_kv_heads), dim3(256), 0, s, a);
+  // one_split: the caller guarantees position + 1 <= kKeys, so the single
+  // split's workgroups write the normalised output and no merge is launched
+  hipLaunchKernelGGL(dec_attn_partial_kernel, dim3(one_split ? 1 : max_splits, n_kv_heads),
+                     dim3(256), 0, s, a);
   int rc = check_launch("dec_attn_partial_kernel");
-  if (rc) return rc;
+  if (rc || one_split) return rc;
   hipLaunchKernelGGL(dec_attn_merge_kernel, dim3(n_kv_heads * a.rep), dim3(256), 0, s, a);
   return check_launch("dec_attn_merge_kernel");
 }
+
+int dec_attention_split_keys() { return kKeys; }
 
 int dec_attention_splits(int max_ctx) { return (max_ctx + kKeys - 1) / kKeys; }
 int dec_attention_max_ctx() { return 4 * kMergePerWave * kKeys; }

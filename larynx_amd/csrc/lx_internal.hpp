@@ -154,7 +154,9 @@ struct DecAttnArgs {
   long part_group_stride = 0;
   float* out = nullptr;      // (n_heads * 64)
 };
-int dec_attention(const DecAttnArgs& a, int n_kv_heads, hipStream_t stream);
+// one_split: position + 1 <= dec_attention_split_keys() (one launch, no merge).
+int dec_attention(const DecAttnArgs& a, int n_kv_heads, bool one_split, hipStream_t stream);
+int dec_attention_split_keys();
 int dec_attention_splits(int max_ctx);
 int dec_attention_max_ctx();  // largest cache the merge pass covers
 // x = table[row]; *d_pos = pos.

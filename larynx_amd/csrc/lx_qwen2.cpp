@@ -57,9 +57,10 @@ struct lx_qwen2 {
   float* rope_tab = nullptr;  // device copy of the rotary inverse frequencies
   bool use_graph = true;      // replay the layer stack as one HIP graph
   hipStream_t cap_stream = nullptr;
-  hipGraphExec_t graph = nullptr;
+  hipGraphExec_t graph[2] = {nullptr, nullptr};  // [cache fits one attention split]
   ~lx_qwen2() {
-    if (graph) (void)hipGraphExecDestroy(graph);
+    for (hipGraphExec_t g : graph)
+      if (g) (void)hipGraphExecDestroy(g);
     if (cap_stream) (void)hipStreamDestroy(cap_stream);
   }
 };
@@ -134,10 +135,12 @@ int prefill_layer(lx_qwen2* m, Layer& L, int rows, const float* next_norm, hipSt
   return splitk_resid_rmsnorm(m->ws, sp, rows, H, nullptr, m->x, next_norm, m->eps, m->hn, s);
 }
 
-// One decode layer (src/llm/llm.cpp:254-289) as five launches: RMSNorm + QKV
-// + rotary + cache append; split-key attention; o_proj + residual; RMSNorm +
-// gate/up + SwiGLU; down_proj + residual.  The position is read from m->d_pos.
-int decode_layer(lx_qwen2* m, Layer& L, hipStream_t s) {
+// One decode layer (src/llm/llm.cpp:254-289): RMSNorm + QKV + rotary + cache
+// append; split-key attention (partial pass, then the merge pass unless the
+// cache fits one split); o_proj + residual; RMSNorm + gate/up + SwiGLU;
+// down_proj + residual: five launches while the cache fits one split, six
+// after.  The position is read from m->d_pos.
+int decode_layer(lx_qwen2* m, Layer& L, bool one_split, hipStream_t s) {
   const int H = m->H, KV = m->KV;
   DecGemvArgs q;
   q.x = m->x;
@@ -168,7 +171,7 @@ int decode_layer(lx_qwen2* m, Layer& L, hipStream_t s) {
   at.part = m->part;
   at.part_group_stride = m->part_stride;
   at.out = m->att;
-  LX_TRY(dec_attention(at, m->NKV, s));
+  LX_TRY(dec_attention(at, m->NKV, one_split, s));
   DecGemvArgs o;
   o.x = m->att;
   o.W = L.o_w;
@@ -194,14 +197,15 @@ int decode_layer(lx_qwen2* m, Layer& L, hipStream_t s) {
   return dec_gemv(DEC_RESID, d, s);
 }
 
-int decode_stack(lx_qwen2* m, hipStream_t s) {
-  for (auto& L : m->layers) LX_TRY(decode_layer(m, L, s));
+int decode_stack(lx_qwen2* m, bool one_split, hipStream_t s) {
+  for (auto& L : m->layers) LX_TRY(decode_layer(m, L, one_split, s));
   return LX_OK;
 }
 
 // Captures the decode layer stack into a HIP graph on the library's own
-// stream (capture needs a stream other than the legacy default stream).
-int capture_decode(lx_qwen2* m) {
+// stream (capture needs a stream other than the legacy default stream); one
+// graph for caches that fit one attention split, one for longer caches.
+int capture_decode(lx_qwen2* m, bool one_split) {
   if (!m->cap_stream &&
       hipStreamCreateWithFlags(&m->cap_stream, hipStreamNonBlocking) != hipSuccess) {
     set_error("qwen2_decode: stream creation failed");
@@ -211,16 +215,17 @@ int capture_decode(lx_qwen2* m) {
     set_error("qwen2_decode: hipStreamBeginCapture failed");
     return LX_ERR_LAUNCH;
   }
-  int rc = decode_stack(m, m->cap_stream);
+  int rc = decode_stack(m, one_split, m->cap_stream);
   hipGraph_t g = nullptr;
   const hipError_t e = hipStreamEndCapture(m->cap_stream, &g);
   if (rc == LX_OK && (e != hipSuccess || !g)) {
     set_error("qwen2_decode: hipStreamEndCapture failed");
     rc = LX_ERR_LAUNCH;
   }
-  if (rc == LX_OK && hipGraphInstantiate(&m->graph, g, nullptr, nullptr, 0) != hipSuccess) {
+  hipGraphExec_t& exec = m->graph[one_split ? 1 : 0];
+  if (rc == LX_OK && hipGraphInstantiate(&exec, g, nullptr, nullptr, 0) != hipSuccess) {
     set_error("qwen2_decode: hipGraphInstantiate failed");
-    m->graph = nullptr;
+    exec = nullptr;
     rc = LX_ERR_LAUNCH;
   }
   if (g) (void)hipGraphDestroy(g);
@@ -458,14 +463,16 @@ extern "C" int lx_qwen2_decode(lx_qwen2* m, int token, float* logits, float* fin
   const int H = m->H;
   // speech_embedding row of the token (src/llm/llm.cpp:226-230) and its position
   LX_TRY(dec_begin(m->speech_embedding, token, H, m->x, m->d_pos, m->cache_len, s));
+  // the keys [0, cache_len] of every layer fit one attention split: no merge pass
+  const bool one_split = m->cache_len + 1 <= dec_attention_split_keys();
   if (m->use_graph) {
-    if (!m->graph) LX_TRY(capture_decode(m));
-    if (hipGraphLaunch(m->graph, s) != hipSuccess) {
+    if (!m->graph[one_split]) LX_TRY(capture_decode(m, one_split));
+    if (hipGraphLaunch(m->graph[one_split], s) != hipSuccess) {
       set_error("qwen2_decode: hipGraphLaunch failed");
       return LX_ERR_LAUNCH;
     }
   } else {
-    LX_TRY(decode_stack(m, s));
+    LX_TRY(decode_stack(m, one_split, s));
   }
   // final norm + llm_decoder head (src/llm/llm.cpp:291-300)
   DecGemvArgs h;
