@@ -47,10 +47,58 @@ def parse():
     ap.add_argument("--no-llm", action="store_true", help="skip the Qwen2 prefill/decode timing")
     ap.add_argument("--no-flow", action="store_true",
                     help="skip the whole-utterance FlowDecoder inference timing")
+    ap.add_argument("--counter-probe", action="store_true",
+                    help="only launch the T=500 QKV and FF0 projections and attention, for "
+                         "rocprofv3 --pmc passes (matrix-core, VALU and LDS counters)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only launch the dominant GEMM (QKV + rotary, T=500) and a plain "
                          "device copy of known size, for rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE")
     return ap.parse_args()
+
+
+def profiled_kernels(torch, fn):
+    """Kernel launches of fn() as the HIP runtime records them (torch.profiler's
+    device activity: every launch on the device, including liblxops's own):
+    [(name, start_us, duration_us)] in launch order."""
+    from torch.profiler import ProfilerActivity, profile
+    torch.cuda.synchronize()
+    with profile(activities=[ProfilerActivity.CUDA]) as prof:
+        fn()
+        torch.cuda.synchronize()
+    out = []
+    for e in prof.events():
+        if str(getattr(e, "device_type", "")).endswith("CUDA"):
+            dur = e.device_time if hasattr(e, "device_time") else e.cuda_time
+            out.append((e.name, e.time_range.start, dur))
+    out.sort(key=lambda r: r[1])
+    return out
+
+
+def kernel_gbs(records, match, nbytes, note):
+    """Average duration of the launches whose name contains `match` and their
+    algorithmic GB/s; nbytes is one number or a per-launch list (cycled)."""
+    durs = [d for n, _, d in records if match in n]
+    if not durs:
+        return None
+    per = nbytes if isinstance(nbytes, (list, tuple)) else [nbytes]
+    tot_b = sum(per[i % len(per)] for i in range(len(durs)))
+    avg_us = sum(durs) / len(durs)
+    gbs = tot_b / (sum(durs) * 1e-6) / 1e9
+    return {"launches": len(durs), "avg_us": round(avg_us, 3),
+            "bytes_per_launch": round(tot_b / len(durs)), "gbs": round(gbs, 1),
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "note": note}
+
+
+def splitk_slices(M, N, K, target_wgs=512, max_slices=8):
+    """K slices the library's split-K plan gives an (M, N, K) projection
+    (gemm_splitk_plan in larynx_amd/csrc/lx_gemm.hip): about two workgroups per
+    CU, at least four 32-wide slabs per slice, whole slab pairs."""
+    tiles = ((M + 63) // 64) * ((N + 63) // 64)
+    s = (target_wgs + tiles - 1) // tiles
+    s = max(1, min(s, max(1, min(max_slices, K // 128))))
+    ks = (K + s - 1) // s
+    ks = (ks + 63) // 64 * 64
+    return (K + ks - 1) // ks
 
 
 def event_time_ms(fn, n, torch):
@@ -271,6 +319,29 @@ def fused_ops_gbs(torch, ops, dev):
     return res
 
 
+def copy_ceiling_gbs(torch, dev, mib=512, reps=10):
+    """The device's practical streaming ceiling: a plain device-to-device copy
+    (torch copy_) of `mib` MiB into a second buffer (2 x mib MiB moved per copy),
+    timed with HIP events over `reps` copies after a warm-up."""
+    n = mib * 2**20 // 4
+    src = torch.ones(n, device=dev)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    s = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(s)
+    for _ in range(reps):
+        dst.copy_(src)
+    e1.record(s)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    gbs = 2 * n * 4 / (ms * 1e-3) / 1e9
+    del src, dst
+    return {"bytes_moved": 2 * n * 4, "avg_us": round(ms * 1e3, 2), "gbs": round(gbs, 1),
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "kernel": "torch copy_, device to device"}
+
+
 def long_utterance(torch, est, dev, g, steps=3):
     """ms per CFG Euler step at T=3000 (the long-utterance config), same estimator."""
     from larynx_amd.flow import cfm_t_span
@@ -338,6 +409,22 @@ def qwen2_lm(torch, dev, g):
     torch.cuda.synchronize()
     prefill_ms = (time.perf_counter() - t0) * 1e3 / 3
     out = {"prefill_L256_ms": round(prefill_ms, 3), "decode_ms_per_token": {}}
+    L, H, KVW = lm_in.shape[0], cfg.hidden, cfg.n_kv_heads * cfg.head_dim
+    NQKV = H + 2 * KVW
+    rec = profiled_kernels(torch, lambda: lm.prefill(lm_in))
+    s_o = splitk_slices(L, H, H)
+    s_d = splitk_slices(L, H, cfg.intermediate)
+    s_q = splitk_slices(L, NQKV, H)
+    # o_proj and down_proj reduce passes alternate within a layer
+    rr = [(s + 3) * L * H * 4 + H * 4 for s in (s_o, s_d)]
+    out["in_path"] = {
+        "resid_rmsnorm_prefill": kernel_gbs(
+            rec, "resid_rmsnorm_kernel", rr,
+            f"L={L}: {s_o} (o_proj) / {s_d} (down_proj) K slices + residual, next RMSNorm"),
+        "qkv_rope_cache_prefill": kernel_gbs(
+            rec, "qkv_rope_cache_kernel", (s_q + 1) * L * NQKV * 4 + NQKV * 4,
+            f"L={L}: {s_q} K slices + bias, NEOX rotary, q out and K/V cache append"),
+    }
     weight_bytes = sum(t.numel() for n, t in params.items() if n != "embed_tokens.weight") * 4
     out["decode_stream_gbs"] = {}
     for cache in (1, 256, 1024, 2048):
@@ -408,6 +495,40 @@ TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemm_qkv_rope_T500_traffic.md"
 COPY_PROBE_BYTES = 256 << 20
 
 
+def counter_probe(torch, ops, launches=20):
+    """The DiT step's three largest MFMA kernels at T=500, each `launches` times
+    on its own: the QKV projection with the rotary epilogue (M=1000, N=3072,
+    K=1024), FF0 with the GELU epilogue (N=2048) and the 16-head attention
+    (B=2, T=500): the workload of the rocprofv3 --pmc passes whose readings
+    (matrix-core busy, VALU and LDS activity) are summarised per kernel."""
+    dev = torch.device("cuda:0")
+    D, T, B, F = 1024, 500, 2, 2048
+    M = B * T
+    g = torch.Generator(device=dev).manual_seed(4)
+    xd = torch.randn(M, D, device=dev, generator=g)
+    wq = torch.randn(3 * D, D, device=dev, generator=g) * 0.02
+    bq = torch.zeros(3 * D, device=dev)
+    w0 = torch.randn(F, D, device=dev, generator=g) * 0.02
+    b0 = torch.zeros(F, device=dev)
+    pos = torch.arange(T, dtype=torch.int32, device=dev)
+    qkv = torch.empty(M, 3 * D, device=dev)
+    ff = torch.empty(M, F, device=dev)
+    att = torch.empty(B, T, D, device=dev)
+    rope = ops.Epilogue(kind=ops.LX_EPI_ROPE_PARTIAL, rows_per_batch=T, pos=pos.data_ptr(),
+                        rot_dim=64, rope_section=D, rope_sections=2, rope_base=10000.0)
+    gelu = ops.Epilogue(kind=ops.LX_EPI_GELU_TANH)
+    q3 = qkv.view(B, T, 3 * D)
+    torch.cuda.synchronize()
+    for _ in range(launches):
+        ops.linear(xd, wq, bq, rope, out=qkv)
+    for _ in range(launches):
+        ops.linear(xd, w0, b0, gelu, out=ff)
+    for _ in range(launches):
+        ops.attention(q3[..., :D], q3[..., D:2 * D], q3[..., 2 * D:], 16, 16, out=att)
+    torch.cuda.synchronize()
+    print(f"counter probe: {launches} x QKV GEMM, FF0 GEMM, attention (B={B} T={T})", flush=True)
+
+
 def traffic_probe(torch, ops, launches=20):
     """Launch the QKV projection (B*T = 1000, N = 3072, K = 1024, rotary
     epilogue) and a plain 256 MiB device-to-device copy, each `launches` times,
@@ -468,6 +589,9 @@ def main():
     if args.traffic_probe:
         traffic_probe(torch, ops)
         return
+    if args.counter_probe:
+        counter_probe(torch, ops)
+        return
 
     dev = torch.device("cuda:0")
     T = args.T
@@ -513,6 +637,20 @@ def main():
     torch.cuda.synchronize()
     solve_ms = (time.perf_counter() - t1) * 1e3
 
+    # fused kernels as the step launches them (inputs just written by the
+    # producing GEMM, as in the real step), from the runtime's activity records
+    rec = profiled_kernels(torch, lambda: [step(i) for i in range(3)])
+    rows, D, mel = 2 * T, 1024, 80
+    p_slices = splitk_slices(rows, mel, D)
+    in_path = {
+        "adaln_in_step": kernel_gbs(rec, "adaln_kernel", 2 * rows * D * 4 + 2 * 2 * D * 4,
+                                    f"modulated LayerNorm before QKV / FF0, B=2 T={T}"),
+        "euler_in_step": kernel_gbs(rec, "euler_kernel",
+                                    p_slices * rows * mel * 4 + 2 * mel * T * 4 + mel * 4,
+                                    f"{p_slices} proj_out K slices + bias summed, CFG "
+                                    f"combine, x update (80 x {T})"),
+    }
+
     kernels = gemm_kernels(torch, ops, T, dev)
     # dominant kernel: largest share of a step (22 blocks, one launch each)
     dom_name, dom = max(kernels.items(), key=lambda kv: kv[1]["avg_us"] * kv[1]["per_block"])
@@ -527,6 +665,7 @@ def main():
     flow = None if args.no_flow else flow_infer(torch, dev, g, dit_params)
     del dit_params, params
     fused = {} if args.no_fused else fused_ops_gbs(torch, ops, dev)
+    copy_ceiling = copy_ceiling_gbs(torch, dev)
     est.close()
     qwen = None if args.no_llm else qwen2_lm(torch, dev, g)
 
@@ -561,6 +700,8 @@ def main():
         "qwen2": qwen,
         "fused_ops": {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv)
                           for kk, vv in v.items()} for k, v in fused.items()},
+        "fused_in_path": dict(in_path, **(qwen["in_path"] if qwen else {})),
+        "copy_ceiling": copy_ceiling,
         "cpu_baseline": cpu,
     }
     if cpu:

@@ -139,26 +139,33 @@ __global__ __launch_bounds__(kEwBlock) void swiglu_kernel(const float* __restric
   if (t < n) out[t] = silu_mul(gate[t], up[t]);
 }
 
-// Partial interleaved rotary: thread = (row, pair); one sincos per pair serves
-// both q and k (same position).
-__global__ void rope_partial_kernel(float* q, float* k, const int* __restrict__ pos,
-                                    long rows, int T, int ld, int half, Table<64> inv) {
-  const long n = rows * half;
-  const long stride = (long)gridDim.x * blockDim.x;
-  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
-    long row = i / half;
-    int p = (int)(i - row * half);
-    int t = (int)(row % T);
-    float ang = (float)pos[t] * inv.v[p];
-    float s, c;
-    sincosf(ang, &s, &c);
-    float2* pq = reinterpret_cast<float2*>(q + row * ld) + p;
-    float2* pk = k ? reinterpret_cast<float2*>(k + row * ld) + p : nullptr;
-    float2 xq = ld_nt(pq);
-    float2 xk = k ? ld_nt(pk) : make_float2(0.f, 0.f);
-    st_nt(pq, make_float2(xq.x * c - xq.y * s, xq.y * c + xq.x * s));
-    if (k) st_nt(pk, make_float2(xk.x * c - xk.y * s, xk.y * c + xk.x * s));
+// Partial interleaved rotary over a 2-D grid: blockIdx.y = batch, blockIdx.x =
+// a run of RB frames, thread = (frame in the run, pair).  No 64-bit index
+// arithmetic; the q / k pair loads are issued before the position is read and
+// the angle formed, and one sincos per pair serves both q and k (same
+// position).  P = pairs per row rounded up to a power of two (<= 64).
+template <int P>
+__global__ __launch_bounds__(256) void rope_partial_kernel(float* q, float* k,
+                                                           const int* __restrict__ pos, int T,
+                                                           int ld, int half, Table<64> inv) {
+  constexpr int RB = 256 / P;
+  const int p = threadIdx.x % P;
+  const int t = blockIdx.x * RB + threadIdx.x / P;
+  if (t >= T || p >= half) return;
+  const long row = (long)blockIdx.y * T + t;
+  float2* pq = reinterpret_cast<float2*>(q + row * ld) + p;
+  const float2 xq = ld_nt(pq);
+  float2 xk = make_float2(0.f, 0.f);
+  float2* pk = nullptr;
+  if (k) {
+    pk = reinterpret_cast<float2*>(k + row * ld) + p;
+    xk = ld_nt(pk);
   }
+  const float ang = (float)pos[t] * inv.v[p];
+  float sn, cs;
+  sincosf(ang, &sn, &cs);
+  st_nt(pq, make_float2(xq.x * cs - xq.y * sn, xq.y * cs + xq.x * sn));
+  if (k) st_nt(pk, make_float2(xk.x * cs - xk.y * sn, xk.y * cs + xk.x * sn));
 }
 
 // NEOX rotary: thread = (row, head, pair); pair (i, i + hd/2).
@@ -274,11 +281,23 @@ extern "C" int lx_rope_partial_interleaved_f32(float* q, float* k, const int* po
   Table<64> inv;
   std::memset(&inv, 0, sizeof(inv));
   rope_inv_freq(base, rot_dim, inv.v);
-  long rows = (long)B * T;
-  int half = rot_dim / 2;
-  dim3 grid(grid_for(rows * half, 256));
-  hipLaunchKernelGGL(rope_partial_kernel, grid, dim3(256), 0, stream, q, k, pos, rows, T, ld,
-                     half, inv);
+  LX_REQUIRE((long)B * T * ld < (1L << 40) && B <= 65535, "rope_partial: tensor too large");
+  const int half = rot_dim / 2;
+  const int P = half <= 8 ? 8 : half <= 16 ? 16 : half <= 32 ? 32 : 64;
+  const int rb = 256 / P;
+  dim3 grid((T + rb - 1) / rb, B);
+#define LX_ROPE_CASE(PP)                                                                       \
+  case PP:                                                                                     \
+    hipLaunchKernelGGL(rope_partial_kernel<PP>, grid, dim3(256), 0, stream, q, k, pos, T, ld, \
+                       half, inv);                                                             \
+    break;
+  switch (P) {
+    LX_ROPE_CASE(8)
+    LX_ROPE_CASE(16)
+    LX_ROPE_CASE(32)
+    LX_ROPE_CASE(64)
+  }
+#undef LX_ROPE_CASE
   return check_launch("rope_partial_kernel");
 }
 
