@@ -185,8 +185,20 @@ __global__ __launch_bounds__(256 * KS) void gemm_pipe_kernel(
   const int wm = (wave >> 1) & 1, wn = wave & 1;
   const int r = lane & 31, h = lane >> 5;
   const int gtid = tid & (GT - 1);
-  float* As = smem + kg * 2 * (BM + BN) * LDA;
-  float* Ws = As + 2 * BM * LDA;
+  // LDS slab layout.  32x32x2 chains: row-major rows of LDA floats.  16x16x4
+  // chains (MF16): lanes l and l + 16 of a fragment read share a row and sit
+  // 8 floats apart, which two-way conflicts in the row-major layout (the
+  // 128-bit reads serve 32 lanes per pass, one 16-byte slot each over 512
+  // bytes).  So each row is split in halves: k groups 0 and 2 (columns 0-7,
+  // 16-23) in rows of 20 floats, k groups 1 and 3 in a second block kH1
+  // floats on, kH1 = 64 mod 128, which puts the two lane halves on disjoint
+  // slots (conflict-free reads); the staging stores, eight lanes per pass over
+  // 128 bytes, write the same row's k groups 0 and 1 in different passes.
+  constexpr int kRow16 = 20, kH1 = 1344;
+  constexpr int SLAB = MF16 ? kH1 + BM * kRow16 : BM * LDA;  // floats per operand buffer
+  static_assert(!MF16 || (kH1 % 128 == 64 && kH1 >= BM * kRow16), "MF16 slab layout");
+  float* As = smem + kg * 2 * 2 * SLAB;
+  float* Ws = As + 2 * SLAB;
   // K slice of this workgroup (blockIdx.y; one slice unless split-K partials)
   X += (long)blockIdx.y * ksplit;
   W += (long)blockIdx.y * ksplit;
@@ -207,11 +219,24 @@ __global__ __launch_bounds__(256 * KS) void gemm_pipe_kernel(
       (void*)X, (short)0, BUF ? (int)(((long)(M - 1) * ldx + K) * 4) : 0, 0x00020000);
   const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
       (void*)W, (short)0, BUF ? (int)(((long)(N - 1) * ldw + K) * 4) : 0, 0x00020000);
+  int so[L];  // LDS offset of the thread's float4 within a slab
 #pragma unroll
   for (int i = 0; i < L; ++i) {
     const int idx = gtid + i * GT;
-    rr[i] = idx / (BK / 4);
-    cc[i] = (idx % (BK / 4)) * 4;
+    if (MF16) {
+      // wave w, stage i covers rows 8 w + 32 i .. +7; pass p of eight lanes
+      // writes rows (p / 2, p / 2 + 4) at the four chunks of k-group parity
+      // p & 1, so its eight 16-byte stores land on distinct slots
+      const int w = gtid >> 6, ln = gtid & 63, p = ln >> 3, j = ln & 7;
+      rr[i] = 8 * w + 32 * i + (p >> 1) + 4 * (j >> 2);
+      const int c = (j & 1) + ((j >> 1) & 1) * 4 + (p & 1) * 2;  // float4 chunk 0..7
+      cc[i] = 4 * c;
+      so[i] = ((c >> 1) & 1) * kH1 + rr[i] * kRow16 + (c >> 2) * 8 + (c & 1) * 4;
+    } else {
+      rr[i] = idx / (BK / 4);
+      cc[i] = (idx % (BK / 4)) * 4;
+      so[i] = rr[i] * LDA + cc[i];
+    }
     oa[i] = ((m0 + rr[i]) * ldx + cc[i]) * 4;
     ow[i] = ((n0 + rr[i]) * ldw + cc[i]) * 4;
     pa[i] = X + (long)min(m0 + rr[i], M - 1) * ldx;
@@ -241,8 +266,8 @@ __global__ __launch_bounds__(256 * KS) void gemm_pipe_kernel(
           vw[e] = kin ? vw[e] : 0.0f;                                                \
         }                                                                            \
       }                                                                              \
-      *reinterpret_cast<floatx4*>(As + (BUF) * BM * LDA + rr[i] * LDA + cc[i]) = va; \
-      *reinterpret_cast<floatx4*>(Ws + (BUF) * BN * LDA + rr[i] * LDA + cc[i]) = vw; \
+      *reinterpret_cast<floatx4*>(As + (BUF) * SLAB + so[i]) = va;                  \
+      *reinterpret_cast<floatx4*>(Ws + (BUF) * SLAB + so[i]) = vw;                  \
     }                                                                                \
   } while (0)
 
@@ -291,8 +316,8 @@ __global__ __launch_bounds__(256 * KS) void gemm_pipe_kernel(
     __builtin_amdgcn_sched_group_barrier(0x008, 12 - 4 * L, 0);                        \
     __syncthreads();                                                                   \
     {                                                                                  \
-      const float* nab = As + ((BUF) ^ 1) * BM * LDA + (wm * 32 + r) * LDA + h * 16;    \
-      const float* nwb = Ws + ((BUF) ^ 1) * BN * LDA + (wn * 32 + r) * LDA + h * 16;    \
+      const float* nab = As + ((BUF) ^ 1) * SLAB + (wm * 32 + r) * LDA + h * 16;        \
+      const float* nwb = Ws + ((BUF) ^ 1) * SLAB + (wn * 32 + r) * LDA + h * 16;        \
       _Pragma("unroll") for (int j = 0; j < 4; ++j) {                                   \
         NA[j] = *reinterpret_cast<const floatx4*>(nab + 4 * j);                        \
         NB[j] = *reinterpret_cast<const floatx4*>(nwb + 4 * j);                        \
@@ -342,12 +367,13 @@ __global__ __launch_bounds__(256 * KS) void gemm_pipe_kernel(
   } while (0)
 #define LX_FRAG16(NA, NB, BUF)                                                         \
   do {                                                                                 \
-    const float* nab = As + (BUF) * BM * LDA + (wm * 32 + (lane & 15)) * LDA + (lane >> 4) * 8; \
-    const float* nwb = Ws + (BUF) * BN * LDA + (wn * 32 + (lane & 15)) * LDA + (lane >> 4) * 8; \
+    const int f16 = ((lane >> 4) & 1) * kH1 + (lane & 15) * kRow16 + (lane >> 5) * 8;    \
+    const float* nab = As + (BUF) * SLAB + wm * 32 * kRow16 + f16;                      \
+    const float* nwb = Ws + (BUF) * SLAB + wn * 32 * kRow16 + f16;                      \
     _Pragma("unroll") for (int b_ = 0; b_ < 2; ++b_)                                    \
       _Pragma("unroll") for (int q_ = 0; q_ < 2; ++q_) {                                \
-        NA[b_][q_] = *reinterpret_cast<const floatx4*>(nab + b_ * 16 * LDA + 4 * q_);    \
-        NB[b_][q_] = *reinterpret_cast<const floatx4*>(nwb + b_ * 16 * LDA + 4 * q_);    \
+        NA[b_][q_] = *reinterpret_cast<const floatx4*>(nab + b_ * 16 * kRow16 + 4 * q_); \
+        NB[b_][q_] = *reinterpret_cast<const floatx4*>(nwb + b_ * 16 * kRow16 + 4 * q_); \
       }                                                                                \
   } while (0)
 
@@ -477,8 +503,12 @@ template <int KS>
 struct PipeCfg {
   static constexpr int BK = 32;
   static constexpr int threads = 256 * KS;
-  static size_t lds() {
-    size_t a = (size_t)KS * 2 * (64 + 64) * (BK + 4) * sizeof(float);
+  // KS k-groups x 2 operands x 2 buffers of one slab (the split-half MF16
+  // layout: 1344 + 64 x 20 floats; otherwise 64 rows of BK + 4), or the
+  // epilogue's 64 x 68 tile if larger
+  static size_t lds(bool mf16) {
+    const size_t slab = mf16 ? 1344 + 64 * 20 : 64 * (BK + 4);
+    size_t a = (size_t)KS * 2 * 2 * slab * sizeof(float);
     size_t c = (size_t)64 * (64 + 4) * sizeof(float);
     return a > c ? a : c;
   }
@@ -497,7 +527,7 @@ int launch_pipe_k(const float* x, int ldx, const float* W, const float* bias, fl
                   int M, int N, int K, const EpiArgs& ep, hipStream_t stream,
                   const Split& sp) {
   auto kern = gemm_pipe_kernel<EPI, KS, KMASK, BUF, MF16>;
-  const size_t lds = PipeCfg<KS>::lds();
+  const size_t lds = PipeCfg<KS>::lds(MF16);
   if (lds > 64 * 1024) {
     static LdsLimit once;  // per instantiation
     const int rc = raise_lds_limit((const void*)kern, lds, once, "linear");
