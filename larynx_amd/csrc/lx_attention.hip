@@ -47,7 +47,7 @@ template <int QS, int KS, bool DB, bool BUF>
 __global__ __launch_bounds__(64 * QS * KS) void attn_flash_kernel(
     const float* __restrict__ q, int ldq, const float* __restrict__ k, int ldk,
     const float* __restrict__ v, int ldv, float* __restrict__ o, int ldo, int Tq, int Tk,
-    int rep, float qscale, int causal, int q_offset) {
+    int n_heads, int rep, float qscale, int causal, int q_offset) {
   constexpr int kQT = 32 * QS;   // queries per workgroup
   constexpr int KT = 32 * KS;    // keys per LDS tile
   constexpr int NT = 64 * QS * KS;   // threads
@@ -62,8 +62,20 @@ __global__ __launch_bounds__(64 * QS * KS) void attn_flash_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int qs = wave % QS, ks = wave / QS;
   const int lane = tid & 63, r = lane & 31, h = lane >> 5;
-  const int head = blockIdx.y, b = blockIdx.z, g = head / rep;
-  const int qt0 = blockIdx.x * kQT;
+  // XCD-aware work order.  The dispatcher deals workgroups round-robin over
+  // the eight XCDs (linear id mod 8), each with its own L2; renumber them so
+  // that consecutive work items, the query tiles of one (batch, head) that
+  // read the same K and V tiles, run on one XCD and share its L2 copy instead
+  // of each XCD fetching every head's K and V.
+  const int nq = (Tq + kQT - 1) / kQT;
+  int work;
+  {
+    const int n = gridDim.x, x = blockIdx.x & 7, per = n >> 3, rem = n & 7;
+    work = x * per + min(x, rem) + (blockIdx.x >> 3);
+  }
+  const int qtile = work % nq, bh = work / nq;
+  const int head = bh % n_heads, b = bh / n_heads, g = head / rep;
+  const int qt0 = qtile * kQT;
   const int q0 = qt0 + qs * 32;
 
   // Q^T operand: lane holds Q[q0 + r][h*32 + s] * scale * log2(e), s = 0..31.
@@ -207,9 +219,48 @@ __global__ __launch_bounds__(64 * QS * KS) void attn_flash_kernel(
     }
   }
 
+  const float l_tot = l_run + lane_xor32(l_run);
+  if constexpr (KS == 2) {
+    // Two key parts: each wave finalises one half of the 64 channels (part 0
+    // channels 0-31, part 1 channels 32-63).  Both publish (m, l) and the
+    // half they do not own, then combine their own half with the partner's
+    // in part order (part 0's terms first) and store it straight from the
+    // registers: register i of lane (r, h) holds channels (i/4)*8 + h*4 +
+    // i%4 of query r, four consecutive channels per float4.
+    static_assert(QS * 2 * 18 * 64 <= 2 * (DB ? 2 : 1) * KT * kLD, "exchange space");
+    float* pub = lds + (qs * 2 + ks) * (18 * 64);
+    const floatx16& give = ks == 0 ? o1 : o0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) pub[i * 64 + lane] = give[i];
+    pub[16 * 64 + lane] = m_run;
+    pub[17 * 64 + lane] = l_tot;
+    __syncthreads();
+    const float* part = lds + (qs * 2 + (ks ^ 1)) * (18 * 64);
+    const float m_o = part[16 * 64 + lane], l_o = part[17 * 64 + lane];
+    const float m = fmaxf(m_run, m_o);
+    const float a_s = exp2f(m_run - m), a_o = exp2f(m_o - m);
+    const float l = ks == 0 ? l_tot * a_s + l_o * a_o : l_o * a_o + l_tot * a_s;
+    const float inv = 1.0f / l;
+    const floatx16& keep = ks == 0 ? o0 : o1;
+    const int qi = q0 + r;
+    if (qi < Tq) {
+      float* orow = o + ((long)b * Tq + qi) * ldo + head * kHD + ks * 32 + h * 4;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        floatx4 w;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int i = g * 4 + e;
+          const float mine = keep[i] * a_s, other = part[i * 64 + lane] * a_o;
+          w[e] = (ks == 0 ? mine + other : other + mine) * inv;
+        }
+        *reinterpret_cast<floatx4*>(orow + g * 8) = w;
+      }
+    }
+    return;
+  }
   // Merge the key parts: ks > 0 publish (m, l, O^T) per lane, ks = 0 combines
   // them in part order.
-  const float l_tot = l_run + lane_xor32(l_run);
   float* xch = lds + qs * ((KS - 1) * 64 * 34);  // per query sub-tile (QS of them)
   if (ks > 0) {
     float* mine = xch + (ks - 1) * (64 * 34);
@@ -330,8 +381,9 @@ extern "C" int lx_attention_f32(const float* q, int ldq, const float* k, int ldk
   static LdsLimit once[3][2];  // [layout][buf]
   const int rc = raise_lds_limit((const void*)kern, lds, once[layout][buf], "attention");
   if (rc) return rc;
-  dim3 grid((Tq + qt - 1) / qt, n_heads, B);
-  hipLaunchKernelGGL(kern, grid, dim3(threads), lds, stream, q, ldq, k, ldk, v, ldv, o, ldo, Tq, Tk,
-                     rep, scale * log2e, causal, q_offset);
+  const long nwg = (long)((Tq + qt - 1) / qt) * n_heads * B;
+  LX_REQUIRE(nwg < (1L << 31), "attention: %ld workgroups exceed the grid limit", nwg);
+  hipLaunchKernelGGL(kern, dim3((unsigned)nwg), dim3(threads), lds, stream, q, ldq, k, ldk, v, ldv,
+                     o, ldo, Tq, Tk, n_heads, rep, scale * log2e, causal, q_offset);
   return check_launch("attn_flash_kernel");
 }
