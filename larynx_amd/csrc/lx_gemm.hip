@@ -36,6 +36,22 @@ struct EpiArgs {
   float inv_freq[64];
 };
 
+// Split tail: when a launch's tiles leave a partial last round over the CUs,
+// the first n_full tiles run whole and each of the remaining tiles runs as
+// `splits` K slices of `ksplit` columns (workgroups n_full + tile * splits +
+// slice).  A slice publishes its partial tile to ws[tile][slice] and counts its
+// arrival; the slice that arrives last sums the slices in slice order and runs
+// the epilogue, then clears the count for the next launch.  No workgroup waits
+// for another.  splits <= 1: no tail split.
+constexpr int kMaxTailSplits = 8;  // K slices per tail tile
+struct TailArgs {
+  int n_full = 0;
+  int splits = 0;
+  int ksplit = 0;
+  float* ws = nullptr;
+  unsigned* arrivals = nullptr;
+};
+
 __device__ __forceinline__ void rotate_pair(float& x0, float& x1, float ang) {
   float s, c;
   sincosf(ang, &s, &c);
@@ -152,7 +168,7 @@ template <int EPI, int KS, bool KMASK, bool BUF = true, bool MF16 = false>
 __global__ __launch_bounds__(256 * KS) void gemm_pipe_kernel(
     const float* X, int ldx, const float* W, int ldw,
     const float* __restrict__ bias, float* Y, int ldy, int M, int N, int K, int ksplit,
-    EpiArgs ep) {
+    EpiArgs ep, TailArgs ta) {
   constexpr int BM = 64, BN = 64, BK = 32, GT = 256, NT = GT * KS;
   constexpr int LDA = BK + 4;
   constexpr int A4 = BM * BK / 4;          // float4 per operand slab
@@ -164,8 +180,18 @@ __global__ __launch_bounds__(256 * KS) void gemm_pipe_kernel(
   const int tiles_n = (N + BN - 1) / BN;
   const int nwg = tiles_m * tiles_n;
   int id = blockIdx.x;
-  const int full = (nwg / 8) * 8;
-  if (id < full) id = (id % 8) * (full / 8) + id / 8;
+  int slice = blockIdx.y;  // K slice: split-K partial planes, or a tail tile's slice
+  int tail = -1;           // tail tile index (split tail), else -1
+  if (ta.splits > 1 && id >= ta.n_full) {
+    const int j = id - ta.n_full;
+    tail = j / ta.splits;
+    slice = j - tail * ta.splits;
+    id = ta.n_full + tail;
+  } else {
+    const int nperm = ta.splits > 1 ? ta.n_full : nwg;
+    const int full = (nperm / 8) * 8;
+    if (id < full) id = (id % 8) * (full / 8) + id / 8;
+  }
   // Runs of 8 M-tiles with N fastest across a run: the contiguous id range of
   // one XCD covers a compact block of A rows and W rows (fewer L2 refills).
   int mt, nt;
@@ -199,11 +225,15 @@ __global__ __launch_bounds__(256 * KS) void gemm_pipe_kernel(
   static_assert(!MF16 || (kH1 % 128 == 64 && kH1 >= BM * kRow16), "MF16 slab layout");
   float* As = smem + kg * 2 * 2 * SLAB;
   float* Ws = As + 2 * SLAB;
-  // K slice of this workgroup (blockIdx.y; one slice unless split-K partials)
-  X += (long)blockIdx.y * ksplit;
-  W += (long)blockIdx.y * ksplit;
-  Y += (long)blockIdx.y * M * ldy;
-  K = min(ksplit, K - (int)blockIdx.y * ksplit);
+  // K slice of this workgroup (one slice unless split-K partials or a tail
+  // tile's slice)
+  {
+    const int kl = tail >= 0 ? ta.ksplit : ksplit;
+    X += (long)slice * kl;
+    W += (long)slice * kl;
+    if (tail < 0) Y += (long)slice * M * ldy;
+    K = min(kl, K - slice * kl);
+  }
 
   // Operand loads.  BUF: through buffer descriptors over the K slice, each
   // lane's byte offset fixed for the whole loop and the slab advancing through
@@ -484,6 +514,52 @@ __global__ __launch_bounds__(256 * KS) void gemm_pipe_kernel(
     }
     __syncthreads();
   }
+  if (tail >= 0) {
+    // Publish this slice's partial tile, count the arrival, and let the last
+    // slice sum all of them in slice order.  The slices of a tile run on
+    // different XCDs, so the partials are written and read with device-scope
+    // (sc1) 16-byte buffer accesses.  Each thread only touches its own float4
+    // slots of Cs, the ones its epilogue stores below.
+    constexpr int kSc1 = 16;  // cache-policy bits: sc1 = device scope
+    const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
+        ta.ws + (long)tail * ta.splits * (BM * BN), (short)0, ta.splits * (BM * BN) * 4,
+        0x00020000);
+#pragma unroll
+    for (int j = 0; j < SLOTS; ++j) {
+      const int idx = tid + j * NT;
+      const int row = idx / (BN / 4), c = (idx % (BN / 4)) * 4;
+      __builtin_amdgcn_raw_buffer_store_b128(*reinterpret_cast<const floatx4*>(Cs + row * LDC + c),
+                                             prs, (slice * (BM * BN) + row * BN + c) * 4, 0, kSc1);
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // the stores are performed before the count
+    __shared__ int last;
+    __syncthreads();
+    if (tid == 0)
+      last = __hip_atomic_fetch_add(ta.arrivals + tail, 1u, __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(ta.splits - 1);
+    __syncthreads();
+    if (!last) return;
+    // every slice's float4 of a slot is loaded before the first add (slices
+    // past `splits` re-read slice 0 and are not added)
+#pragma unroll
+    for (int j = 0; j < SLOTS; ++j) {
+      const int idx = tid + j * NT;
+      const int row = idx / (BN / 4), c = (idx % (BN / 4)) * 4;
+      floatx4 pv[kMaxTailSplits];
+#pragma unroll
+      for (int sl = 0; sl < kMaxTailSplits; ++sl)
+        pv[sl] = __builtin_amdgcn_raw_buffer_load_b128(
+            prs, ((sl < ta.splits ? sl : 0) * (BM * BN) + row * BN + c) * 4, 0, kSc1);
+      floatx4 sum = {0.0f, 0.0f, 0.0f, 0.0f};
+      const floatx4 own = *reinterpret_cast<const floatx4*>(Cs + row * LDC + c);
+#pragma unroll
+      for (int sl = 0; sl < kMaxTailSplits; ++sl)
+        if (sl < ta.splits) sum += sl == slice ? own : pv[sl];
+      *reinterpret_cast<floatx4*>(Cs + row * LDC + c) = sum;
+    }
+    if (tid == 0)
+      __hip_atomic_store(ta.arrivals + tail, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 #pragma unroll
   for (int j = 0; j < SLOTS; ++j) {
     const int idx = tid + j * NT;
@@ -520,6 +596,7 @@ struct Split {
   int splits = 1;
   int ksplit = 0;
   int ldw = 0;
+  TailArgs tail;  // split tail (tail.splits > 1), with splits == 1
 };
 
 template <int EPI, int KS, bool KMASK, bool BUF, bool MF16>
@@ -534,8 +611,10 @@ int launch_pipe_k(const float* x, int ldx, const float* W, const float* bias, fl
     if (rc) return rc;
   }
   const long tiles = (long)((M + 63) / 64) * ((N + 63) / 64);
-  hipLaunchKernelGGL(kern, dim3((unsigned)tiles, sp.splits), dim3(PipeCfg<KS>::threads), lds,
-                     stream, x, ldx, W, sp.ldw, bias, y, ldy, M, N, K, sp.ksplit, ep);
+  const long wgs =
+      sp.tail.splits > 1 ? sp.tail.n_full + (tiles - sp.tail.n_full) * sp.tail.splits : tiles;
+  hipLaunchKernelGGL(kern, dim3((unsigned)wgs, sp.splits), dim3(PipeCfg<KS>::threads), lds,
+                     stream, x, ldx, W, sp.ldw, bias, y, ldy, M, N, K, sp.ksplit, ep, sp.tail);
   return check_launch("gemm_pipe_kernel");
 }
 
@@ -554,7 +633,9 @@ int launch_pipe(const float* x, int ldx, const float* W, const float* bias, floa
   if (sp.ksplit <= 0) sp.ksplit = K;
   if (sp.ldw <= 0) sp.ldw = K;
   const int step = 2 * KS * PipeCfg<KS>::BK;
-  const bool exact = sp.ksplit % step == 0 && (K % sp.ksplit) % step == 0;
+  bool exact = sp.ksplit % step == 0 && (K % sp.ksplit) % step == 0;
+  if (sp.tail.splits > 1)
+    exact = exact && sp.tail.ksplit % step == 0 && (K % sp.tail.ksplit) % step == 0;
   if (!buffer_loads_fit(M, ldx, N, sp.ldw))  // operands past 2 GiB: 64-bit addressing
     return launch_pipe_k<EPI, KS, true, false, MF16>(x, ldx, W, bias, y, ldy, M, N, K, ep,
                                                      stream, sp);
@@ -731,32 +812,34 @@ int gemv_epi(const float* x, int ldx, const float* W, const float* bias, float* 
 // split-K 2, 9 = as 7 on four 16x16x4 accumulator chains.
 template <int EPI>
 int dispatch_cfg(int cfg, const float* x, int ldx, const float* W, const float* bias, float* y,
-                 int ldy, int M, int N, int K, const EpiArgs& ep, hipStream_t s) {
+                 int ldy, int M, int N, int K, const EpiArgs& ep, hipStream_t s,
+                 const Split& sp) {
   switch (cfg) {
-    case 7: return launch_pipe<EPI, 1>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
-    case 8: return launch_pipe<EPI, 2>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
+    case 7: return launch_pipe<EPI, 1>(x, ldx, W, bias, y, ldy, M, N, K, ep, s, sp);
+    case 8: return launch_pipe<EPI, 2>(x, ldx, W, bias, y, ldy, M, N, K, ep, s, sp);
     case 9:
-      return launch_pipe<EPI, 1, true>(x, ldx, W, bias, y, ldy, M, N, K, ep, s);
+      return launch_pipe<EPI, 1, true>(x, ldx, W, bias, y, ldy, M, N, K, ep, s, sp);
   }
   set_error("linear: unknown tile configuration %d", cfg);
   return LX_ERR_ARG;
 }
 
 int dispatch_gemm(int kind, int cfg, const float* x, int ldx, const float* W, const float* bias,
-                  float* y, int ldy, int M, int N, int K, const EpiArgs& ep, hipStream_t s) {
+                  float* y, int ldy, int M, int N, int K, const EpiArgs& ep, hipStream_t s,
+                  const Split& sp = Split()) {
   switch (kind) {
     case LX_EPI_NONE:
-      return dispatch_cfg<LX_EPI_NONE>(cfg, x, ldx, W, bias, y, ldy, M, N, K, ep, s);
+      return dispatch_cfg<LX_EPI_NONE>(cfg, x, ldx, W, bias, y, ldy, M, N, K, ep, s, sp);
     case LX_EPI_GELU_TANH:
-      return dispatch_cfg<LX_EPI_GELU_TANH>(cfg, x, ldx, W, bias, y, ldy, M, N, K, ep, s);
+      return dispatch_cfg<LX_EPI_GELU_TANH>(cfg, x, ldx, W, bias, y, ldy, M, N, K, ep, s, sp);
     case LX_EPI_GATED_RESID:
-      return dispatch_cfg<LX_EPI_GATED_RESID>(cfg, x, ldx, W, bias, y, ldy, M, N, K, ep, s);
+      return dispatch_cfg<LX_EPI_GATED_RESID>(cfg, x, ldx, W, bias, y, ldy, M, N, K, ep, s, sp);
     case LX_EPI_ROPE_PARTIAL:
-      return dispatch_cfg<LX_EPI_ROPE_PARTIAL>(cfg, x, ldx, W, bias, y, ldy, M, N, K, ep, s);
+      return dispatch_cfg<LX_EPI_ROPE_PARTIAL>(cfg, x, ldx, W, bias, y, ldy, M, N, K, ep, s, sp);
     case LX_EPI_RESID:
-      return dispatch_cfg<LX_EPI_RESID>(cfg, x, ldx, W, bias, y, ldy, M, N, K, ep, s);
+      return dispatch_cfg<LX_EPI_RESID>(cfg, x, ldx, W, bias, y, ldy, M, N, K, ep, s, sp);
     case LX_EPI_SWIGLU_PAIRED:
-      return dispatch_cfg<LX_EPI_SWIGLU_PAIRED>(cfg, x, ldx, W, bias, y, ldy, M, N, K, ep, s);
+      return dispatch_cfg<LX_EPI_SWIGLU_PAIRED>(cfg, x, ldx, W, bias, y, ldy, M, N, K, ep, s, sp);
   }
   set_error("linear: unknown epilogue kind %d", kind);
   return LX_ERR_ARG;
@@ -805,11 +888,54 @@ int gemm_splitk_partials(const float* x, int ldx, const float* W, int ldw, float
                                                      sp);
 }
 
+// Split-tail plan for a one-k-group launch whose tiles leave a partial last
+// round over the 256 CUs (at most half a round): n_full tiles run whole, the
+// rest as `splits` K slices of `ksplit` columns (a multiple of 64, at least
+// 128), the slice count chosen so that the slices spread most evenly over the
+// CUs.  Qwen2 prefill gate/up at L = 256: 608 tiles = 512 + 96, the 96 as 5
+// slices of 192 (480 workgroups: at most 2 slices = 0.4 of a tile more on a
+// CU, against a whole third tile on 96 CUs unsplit).
+bool split_tail_plan(int M, int N, int K, int* n_full, int* splits, int* ksplit) {
+  const long tiles = (long)((M + 63) / 64) * ((N + 63) / 64);
+  if (pick_config(M, N, K) != 7 || tiles <= 256) return false;
+  const long nf = tiles / 256 * 256, tail = tiles - nf;
+  if (tail == 0 || tail > 128) return false;
+  double best = 1.0;  // unsplit: one more whole tile on `tail` CUs
+  int bs = 0, bk = 0;
+  for (int s = 2; s <= kMaxTailSplits; ++s) {
+    int ks = (K + s - 1) / s;
+    ks = (ks + 63) / 64 * 64;
+    if (ks < 128) continue;
+    const int sp = (K + ks - 1) / ks;
+    if (sp < 2) continue;
+    const double cost = (double)((tail * sp + 255) / 256) / sp;
+    if (cost < best - 1e-9) {
+      best = cost;
+      bs = sp;
+      bk = ks;
+    }
+  }
+  if (bs < 2) return false;
+  *n_full = (int)nf;
+  *splits = bs;
+  *ksplit = bk;
+  return true;
+}
+
+size_t split_tail_ws_floats(int M, int N, int K, int* tail_tiles) {
+  int nf = 0, sp = 0, ks = 0;
+  *tail_tiles = 0;
+  if (!split_tail_plan(M, N, K, &nf, &sp, &ks)) return 0;
+  const long tiles = (long)((M + 63) / 64) * ((N + 63) / 64);
+  *tail_tiles = (int)(tiles - nf);
+  return (size_t)(tiles - nf) * sp * 64 * 64;
+}
+
 int gemm_splitk_plan(int M, int N, int K, int* ksplit) {
   const long tiles = (long)((M + 63) / 64) * ((N + 63) / 64);
   int s = (int)((kSplitTargetWgs + tiles - 1) / tiles);
   int max_s = K / 128 > 0 ? K / 128 : 1;  // at least four 32-wide slabs per slice
-  if (max_s > 8) max_s = 8;                   // the reduce passes sum at most 8 slices
+  if (max_s > 9) max_s = 9;                   // the reduce passes sum at most 9 slices
   if (s > max_s) s = max_s;
   if (s < 1) s = 1;
   int ks = (K + s - 1) / s;
@@ -823,9 +949,12 @@ int gemm_splitk_plan(int M, int N, int K, int* ksplit) {
 
 using namespace lx;
 
-extern "C" int lx_linear_f32(const float* x, int ldx, const float* W, const float* bias,
-                             float* y, int ldy, int M, int N, int K, const lx_epilogue* epi,
-                             hipStream_t stream) {
+namespace lx {
+
+// lx_linear_f32, optionally with a split tail over caller-owned scratch.
+int linear_impl(const float* x, int ldx, const float* W, const float* bias, float* y, int ldy,
+                int M, int N, int K, const lx_epilogue* epi, float* ws, size_t ws_floats,
+                unsigned* arrivals, int n_arrivals, hipStream_t stream) {
   LX_REQUIRE(x && W && y, "linear: null pointer");
   LX_REQUIRE(M > 0 && N > 0 && K > 0, "linear: bad shape M=%d N=%d K=%d", M, N, K);
   LX_REQUIRE(K % 4 == 0 && ldx % 4 == 0 && ldx >= K, "linear: K=%d and ldx=%d must be multiples of 4",
@@ -843,5 +972,31 @@ extern "C" int lx_linear_f32(const float* x, int ldx, const float* W, const floa
   ep.vec = epi_vec_ok(ep, y, ldy, bias);
   const long tiles = (long)((M + 63) / 64) * ((N + 63) / 64);
   LX_REQUIRE(tiles < (1L << 31), "linear: too many tiles");
-  return dispatch_gemm(kind, pick_config(M, N, K), x, ldx, W, bias, y, ldy, M, N, K, ep, stream);
+  Split sp;
+  int nf = 0, tsp = 0, tks = 0;
+  if (ws && arrivals && split_tail_plan(M, N, K, &nf, &tsp, &tks) &&
+      (size_t)(tiles - nf) * tsp * 64 * 64 <= ws_floats && tiles - nf <= n_arrivals) {
+    sp.tail.n_full = nf;
+    sp.tail.splits = tsp;
+    sp.tail.ksplit = tks;
+    sp.tail.ws = ws;
+    sp.tail.arrivals = arrivals;
+  }
+  return dispatch_gemm(kind, pick_config(M, N, K), x, ldx, W, bias, y, ldy, M, N, K, ep, stream,
+                       sp);
+}
+
+int linear_split_tail(const float* x, int ldx, const float* W, const float* bias, float* y,
+                      int ldy, int M, int N, int K, const lx_epilogue* epi, float* ws,
+                      size_t ws_floats, unsigned* arrivals, int n_arrivals, hipStream_t stream) {
+  return linear_impl(x, ldx, W, bias, y, ldy, M, N, K, epi, ws, ws_floats, arrivals, n_arrivals,
+                     stream);
+}
+
+}  // namespace lx
+
+extern "C" int lx_linear_f32(const float* x, int ldx, const float* W, const float* bias,
+                             float* y, int ldy, int M, int N, int K, const lx_epilogue* epi,
+                             hipStream_t stream) {
+  return lx::linear_impl(x, ldx, W, bias, y, ldy, M, N, K, epi, nullptr, 0, nullptr, 0, stream);
 }

@@ -96,6 +96,17 @@ int gemm_splitk_partials(const float* x, int ldx, const float* W, int ldw, float
 // Number of K slices (and slice width, a multiple of 64) that gives the
 // (M, N) tile grid about two workgroups per CU.
 int gemm_splitk_plan(int M, int N, int K, int* ksplit);
+// lx_linear_f32 whose tile launch, when its tiles leave a partial last round
+// over the CUs, runs the tail tiles as K slices that the last-arriving slice
+// of each tile sums in slice order (deterministic, no waiting): ws holds up to
+// ws_floats of partial tiles, arrivals one counter per tail tile (n_arrivals of
+// them), zeroed once by the caller and left zeroed by every launch.  Falls back
+// to the plain launch when no split applies or the scratch is too small.
+int linear_split_tail(const float* x, int ldx, const float* W, const float* bias, float* y,
+                      int ldy, int M, int N, int K, const lx_epilogue* epi, float* ws,
+                      size_t ws_floats, unsigned* arrivals, int n_arrivals, hipStream_t stream);
+// Scratch floats a split tail of this shape uses (0: none) and its tail tiles.
+size_t split_tail_ws_floats(int M, int N, int K, int* tail_tiles);
 // x[m, :] += sum_s ws[s][m, :] (+ bias); then, if norm_w, hn[m, :] =
 // RMSNorm(x[m, :]) * norm_w (the next sub-layer's input norm).  Rows of N floats.
 int splitk_resid_rmsnorm(const float* ws, int splits, int M, int N, const float* bias, float* x,

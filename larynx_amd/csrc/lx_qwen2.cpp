@@ -47,7 +47,10 @@ struct lx_qwen2 {
   std::vector<Layer> layers;
   // activations, sized for max_ctx rows
   float *x, *hn, *qkv, *att, *act;
-  float* ws = nullptr;  // split-K partial sums
+  float* ws = nullptr;  // split-K partial sums, and the gate/up split tail's partial tiles
+  size_t ws_floats = 0;
+  unsigned* arrivals = nullptr;  // split-tail arrival counters (zeroed at creation)
+  int n_arrivals = 0;
   int* pos;     // pos[i] = i
   // single-token decode state (lx_decode.hip kernels)
   int* d_pos = nullptr;       // position of the token being decoded
@@ -87,9 +90,11 @@ int lx::qwen2_own_tables(lx_qwen2* m) {
 namespace {
 
 // Width of the split-K partial workspace: the largest splits * rows * N over
-// the three split projections and every prefill length up to max_ctx.
-size_t splitk_ws_floats(int max_ctx, int H, int QKV, int I) {
+// the three split projections, and the gate/up launch's split-tail partials,
+// at every prefill length up to max_ctx; *tails = the most tail tiles.
+size_t splitk_ws_floats(int max_ctx, int H, int QKV, int I, int* tails) {
   size_t best = 0;
+  *tails = 0;
   // splits depend on M only through the tile count, so the largest M of each
   // 64-row band (and max_ctx itself) bounds every length
   for (int M = 64;; M += 64) {
@@ -101,6 +106,10 @@ size_t splitk_ws_floats(int max_ctx, int H, int QKV, int I) {
       const size_t n = (size_t)splits * rows * sh[0];
       if (n > best) best = n;
     }
+    int t = 0;
+    const size_t nt = split_tail_ws_floats(rows, 2 * I, H, &t);
+    if (nt > best) best = nt;
+    if (t > *tails) *tails = t;
     if (M >= max_ctx) break;
   }
   return best;
@@ -129,7 +138,8 @@ int prefill_layer(lx_qwen2* m, Layer& L, int rows, const float* next_norm, hipSt
   LX_TRY(splitk_resid_rmsnorm(m->ws, sp, rows, H, nullptr, m->x, L.post_norm, m->eps, m->hn, s));
   lx_epilogue swiglu{};
   swiglu.kind = LX_EPI_SWIGLU_PAIRED;
-  LX_TRY(lx_linear_f32(m->hn, H, L.gu_w, nullptr, m->act, m->I, rows, 2 * m->I, H, &swiglu, s));
+  LX_TRY(linear_split_tail(m->hn, H, L.gu_w, nullptr, m->act, m->I, rows, 2 * m->I, H, &swiglu,
+                           m->ws, m->ws_floats, m->arrivals, m->n_arrivals, s));
   sp = gemm_splitk_plan(rows, H, m->I, &ks);
   LX_TRY(gemm_splitk_partials(m->act, m->I, L.down_w, m->I, m->ws, rows, H, m->I, sp, ks, s));
   return splitk_resid_rmsnorm(m->ws, sp, rows, H, nullptr, m->x, next_norm, m->eps, m->hn, s);
@@ -300,7 +310,12 @@ extern "C" int lx_qwen2_create(const lx_qwen2_weights* w, int max_ctx, lx_qwen2*
   m->qkv = A(rows * QKV);
   m->att = A(rows * H);
   m->act = A(rows * I);
-  m->ws = A(splitk_ws_floats(max_ctx, H, QKV, I));
+  int tails = 0;
+  m->ws_floats = splitk_ws_floats(max_ctx, H, QKV, I, &tails);
+  m->ws = A(m->ws_floats);
+  m->n_arrivals = tails > 0 ? tails : 1;
+  m->arrivals = a.alloc<unsigned>(m->n_arrivals);
+  ok = ok && m->arrivals;
   m->max_splits = dec_attention_splits(max_ctx);
   m->part_stride = ((long)m->max_splits * (m->NH / m->NKV) * (m->HD + 2) + 31) / 32 * 32;
   m->part = A((size_t)m->part_stride * m->NKV);
@@ -353,6 +368,12 @@ extern "C" int lx_qwen2_create(const lx_qwen2_weights* w, int max_ctx, lx_qwen2*
     if (rc == LX_OK) rc = interleave_rows(lw.gate_w, lw.up_w, L.gu_w, I, H, s);
   }
   if (rc == LX_OK) rc = iota_i32(m->pos, max_ctx, s);
+  // the split tail's arrival counters start at zero; every launch leaves them so
+  if (rc == LX_OK &&
+      hipMemsetAsync(m->arrivals, 0, sizeof(unsigned) * m->n_arrivals, s) != hipSuccess) {
+    set_error("qwen2_create: counter initialisation failed");
+    rc = LX_ERR_LAUNCH;
+  }
   FreqTable inv{};
   rope_inv_freq(m->theta, m->HD, inv.v);
   if (rc == LX_OK && hipMemcpyAsync(m->rope_tab, inv.v, sizeof(float) * (m->HD / 2),

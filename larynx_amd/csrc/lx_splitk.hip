@@ -15,7 +15,7 @@ namespace {
 
 constexpr int kHD = 64;
 
-constexpr int kMaxSplits = 8;  // K slices a reduce pass sums (all loads in flight)
+constexpr int kMaxSplits = 9;  // K slices a reduce pass sums (all loads in flight)
 
 // Sum of the K slices of float4 slot i (< N4) of a row: every slice's load is
 // issued before the first add (slices past `splits` re-read slice 0 and are
