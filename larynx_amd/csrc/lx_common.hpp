@@ -100,6 +100,25 @@ constexpr int kDppXor2 = 0x4E;        // quad_perm [2, 3, 0, 1]
 constexpr int kDppHalfMirror = 0x141; // lane i <-> 7 - i within each 8 lanes
 constexpr int kDppMirror = 0x140;     // lane i <-> 15 - i within each 16 lanes
 
+// sin and cos of a rotary angle: Cody and Waite's additive argument reduction
+// by 2*pi in two parts (the high part 6.28125 has 8 significant bits, so
+// k * 6.28125 and the first subtraction are exact for |k| < 2^16; the low part
+// carries the rest of 2*pi to fp32), then the hardware sine and cosine
+// (v_sin_f32 / v_cos_f32, argument in revolutions) of the reduced angle in
+// [-pi, pi].  Angles past 2^17 rad take the library sincosf.
+__device__ __forceinline__ void rope_sincos(float a, float* s, float* c) {
+  if (fabsf(a) < 131072.0f) {
+    const float k = rintf(a * 0.159154937f);
+    float r = fmaf(-k, 6.28125f, a);
+    r = fmaf(-k, 1.93530717e-3f, r);
+    const float rev = r * 0.159154937f;
+    *s = __builtin_amdgcn_sinf(rev);
+    *c = __builtin_amdgcn_cosf(rev);
+  } else {
+    sincosf(a, s, c);
+  }
+}
+
 // Value held by lane ^ 16 / lane ^ 32.
 __device__ __forceinline__ float lane_xor16(float v) {
   const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,

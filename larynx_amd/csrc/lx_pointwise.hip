@@ -163,7 +163,7 @@ __global__ __launch_bounds__(256) void rope_partial_kernel(float* q, float* k,
   }
   const float ang = (float)pos[t] * inv.v[p];
   float sn, cs;
-  sincosf(ang, &sn, &cs);
+  rope_sincos(ang, &sn, &cs);
   st_nt(pq, make_float2(xq.x * cs - xq.y * sn, xq.y * cs + xq.x * sn));
   if (k) st_nt(pk, make_float2(xk.x * cs - xk.y * sn, xk.y * cs + xk.x * sn));
 }
@@ -181,7 +181,7 @@ __global__ void rope_neox_kernel(float* qk, const int* __restrict__ pos, long ro
     int p = rem - h * half;
     float ang = (float)pos[row] * inv.v[p];
     float s, c;
-    sincosf(ang, &s, &c);
+    rope_sincos(ang, &s, &c);
     float* ptr = qk + row * ld + h * hd + p;
     float x0 = __builtin_nontemporal_load(ptr), x1 = __builtin_nontemporal_load(ptr + half);
     __builtin_nontemporal_store(x0 * c - x1 * s, ptr);
