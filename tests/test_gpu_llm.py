@@ -161,10 +161,12 @@ def test_decode_graph_matches_eager_and_crosses_splits(gpu, qwen):
     graph.close()
 
 
-@pytest.mark.parametrize("L", [1, 37, 300])
+@pytest.mark.parametrize("L", [1, 37, 200, 300])
 def test_prefill_ragged_lengths(gpu, qwen, L):
     """Prefill at lengths that leave partial 64-row tiles and change the
-    split-K plan (1 row: one tile per column band; 300 rows: five bands)."""
+    split-K plan (1 row: one tile per column band; 300 rows: five bands).  At
+    200 rows the gate/up launch splits its tail tiles over K (4 row bands x 152
+    column tiles = 512 whole + 96 sliced), with the last row band partial."""
     cfg, params, _, lm = qwen
     announce(f"qwen2 prefill L={L}")
     lm_in = torch.from_numpy(orc.normal((L, cfg.hidden), 300 + L, 1, 0.5)).to(gpu)
@@ -181,3 +183,20 @@ def test_prefill_ragged_lengths(gpu, qwen, L):
         k, v = lm.cache_views(layer)
         assert orc.rel_err(k[:L].cpu().numpy(), o.k_cache[layer, :L]) < TOL
         assert orc.rel_err(v[:L].cpu().numpy(), o.v_cache[layer, :L]) < TOL
+
+
+def test_prefill_split_tail_is_deterministic(gpu, qwen):
+    """The gate/up launch at L=256 sums the K slices of its tail tiles in slice
+    order whichever slice arrives last: two prefills of the same input give
+    bit-identical hidden states, logits and caches."""
+    cfg, params, _, lm = qwen
+    announce("qwen2 prefill L=256 twice (split tail determinism)")
+    lm_in = torch.from_numpy(orc.normal((256, cfg.hidden), 4040, 1, 0.5)).to(gpu)
+    runs = []
+    for _ in range(2):
+        logits, hidden, final = lm.prefill(lm_in, capture=True)
+        k, v = lm.cache_views(cfg.n_layers - 1)
+        torch.cuda.synchronize()
+        runs.append([t.cpu().numpy().copy() for t in (*hidden, final, logits, k[:256], v[:256])])
+    for a, b in zip(*runs):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
