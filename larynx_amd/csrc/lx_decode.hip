@@ -13,9 +13,10 @@
 //   - silu(gate) * up (src/llm/llm.cpp:284-288) in the gate/up epilogue;
 //   - the residual adds (src/llm/llm.cpp:281, 289) in the o / down epilogues.
 // Attention over the cache is split-key GQA: one workgroup per (64-key split,
-// kv head) scores all query heads of its group, then one workgroup per query
-// head merges the partial softmax states; while the whole cache fits one split
-// the first pass writes the output and the merge pass is left out.
+// kv head) scores all query heads of its group; while the whole cache fits one
+// split that pass writes the output, past it every workgroup of the o_proj
+// launch merges the partial softmax states itself before its rows (five
+// launches per layer at every cache length).
 //
 // The position (= cache length before the token) is read from device memory,
 // so one capture of a layer stack into a HIP graph serves every position.
@@ -30,7 +31,12 @@ namespace {
 constexpr int kHD = 64;      // head_dim
 constexpr int kKeys = 64;    // keys per attention split
 constexpr int kMaxRep = 8;   // query heads per kv head
-constexpr int kMergePerWave = 16;  // splits per merge wave: <= 64 splits, 4096 keys
+constexpr int kMaxHeads = 32;  // query heads of the fused merge + o_proj (hidden <= 2048)
+constexpr int kMaxSplits = 64;     // 64-key splits the merge covers: 4096 keys
+// One partial softmax state per (split, query head): 64 unnormalised output
+// channels, the running maximum at [64] and the sum at [65], padded to 68
+// floats so every record starts 16-byte aligned (float4 reads of the channels).
+constexpr int kPart = 68;
 
 __device__ __forceinline__ float dot4(float4 a, float4 b) {
   return (a.x * b.x + a.y * b.y) + (a.z * b.z + a.w * b.w);
@@ -196,12 +202,12 @@ __global__ __launch_bounds__(256) void dec_gemv_kernel(DecGemvArgs a) {
   }
 }
 
-// Split-key GQA decode attention, partial pass.  grid (max_splits,
-// n_kv_heads), 256 threads.  The workgroup of split `sp` takes keys
+// Split-key GQA decode attention, partial pass.  grid (splits, n_kv_heads),
+// 256 threads.  The workgroup of split `sp` takes keys
 // [64 sp, 64 sp + 64) of its kv head and scores them against the kv head's
 // `rep` query heads (wave w: heads w and w + 4).  With a single split it
 // writes the normalised output; otherwise (max, sum, unnormalised o) per head
-// for dec_attn_merge_kernel.  The K/V tile loads do not wait for the
+// for the merge in dec_merge_o_kernel.  The K/V tile loads do not wait for the
 // position: rows are clamped into the cache and masked afterwards.
 __global__ __launch_bounds__(256) void dec_attn_partial_kernel(DecAttnArgs a) {
   __shared__ float ks[kKeys][kHD + 4];
@@ -236,7 +242,22 @@ __global__ __launch_bounds__(256) void dec_attn_partial_kernel(DecAttnArgs a) {
   *reinterpret_cast<float4*>(&qs[tid >> 4][(tid & 15) * 4]) = q;
   const int Tk = *a.pos + 1;
   const int n_split = (Tk + kKeys - 1) / kKeys;
-  if (sp >= n_split) return;
+  if (sp >= n_split) {
+    // a split past the keys (launches of more than one split only): its state
+    // is the empty one, so the merge adds exact zeros and needs no position
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const int h = wave + 4 * hh;
+      if (h >= a.rep) continue;
+      float* dst = a.part + (long)g * a.part_group_stride + ((long)sp * a.rep + h) * kPart;
+      dst[lane] = 0.0f;
+      if (lane == 0) {
+        dst[kHD] = -INFINITY;
+        dst[kHD + 1] = 0.0f;
+      }
+    }
+    return;
+  }
   const int nk = min(kKeys, Tk - k0);
   __syncthreads();
   // scores: lane = key
@@ -273,7 +294,7 @@ __global__ __launch_bounds__(256) void dec_attn_partial_kernel(DecAttnArgs a) {
     if (n_split == 1) {
       a.out[(long)(g * a.rep + h) * kHD + lane] = acc / l[hh];
     } else {
-      float* dst = a.part + (long)g * a.part_group_stride + ((long)sp * a.rep + h) * (kHD + 2);
+      float* dst = a.part + (long)g * a.part_group_stride + ((long)sp * a.rep + h) * kPart;
       dst[lane] = acc;
       if (lane == 0) {
         dst[kHD] = m[hh];
@@ -283,56 +304,115 @@ __global__ __launch_bounds__(256) void dec_attn_partial_kernel(DecAttnArgs a) {
   }
 }
 
-// Merge pass: grid (n_heads), 256 threads.  Wave w reads splits w, w + 4, ...
-// (all loads of a thread issued together), lane = channel; the rescaled sums
-// are combined across the four waves in LDS.  Nothing to do for one split.
-__global__ __launch_bounds__(256) void dec_attn_merge_kernel(DecAttnArgs a) {
-  __shared__ float red_m[4], red_l[4];
-  __shared__ float red_o[4][kHD];
-  const int h = blockIdx.x, g = h / a.rep, hr = h - g * a.rep;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int Tk = *a.pos + 1;
-  const int n_split = (Tk + kKeys - 1) / kKeys;
-  if (n_split == 1) return;
-  const float* base = a.part + (long)g * a.part_group_stride + (long)hr * (kHD + 2);
-  const long sstride = (long)a.rep * (kHD + 2);
-  // unconditional loads from clamped (written) splits, masked afterwards
-  float mo[kMergePerWave], mm[kMergePerWave], ml[kMergePerWave];
+// Attention merge fused into o_proj + residual, for caches longer than one
+// 64-key split (src/llm/llm.cpp:254-281).  grid (ceil(hidden / 8)), 512
+// threads; wave w owns o_proj row 8 * blockIdx.x + w.  Every workgroup first
+// merges the partial softmax states of all query heads itself, so no
+// workgroup waits for another and nothing is published: wave w merges heads
+// w, w + 8, ...; lane (split group sg = lane / 16, channel quad c4 = lane % 16)
+// sums splits sg, sg + 4, ... of its head in split order, the (max, sum) of
+// split sg + 4 c4 is read by lane (sg, c4) and reaches the other lanes through a
+// lane shuffle, and the four split groups are added with the two half-wave
+// swaps.  The merged row (n_heads * 64 floats) goes to LDS for the projection.
+// The launch reads the states of splits [0, nrec), nrec = min(4 * SPL,
+// allocated splits); the partial pass wrote every one of them in the same
+// launch order (splits past the keys as empty states), so the merge does not
+// read the position.  The states of the wave's first two heads are requested
+// before the o_proj weights (the first head's only, past 4 splits per group or
+// 16 heads), so waiting for them does not wait for the weight stream (loads
+// retire in order), which stays in flight through the merge.
+// SPL = splits per split group.
+template <int SPL>
+__device__ __forceinline__ void merge_load(const DecAttnArgs& a, int h, int sg, int c4, int smax,
+                                           float4 (&ov)[SPL], float& mv, float& lv) {
+  const int g = h / a.rep, hr = h - g * a.rep;
+  const float* base = a.part + (long)g * a.part_group_stride + (long)hr * kPart;
+  const long ss = (long)a.rep * kPart;
 #pragma unroll
-  for (int i = 0; i < kMergePerWave; ++i) {
-    const float* src = base + min(wave + 4 * i, n_split - 1) * sstride;
-    mo[i] = src[lane];
-    mm[i] = src[kHD];
-    ml[i] = src[kHD + 1];
-  }
+  for (int i = 0; i < SPL; ++i)
+    ov[i] = *reinterpret_cast<const float4*>(base + min(sg + 4 * i, smax) * ss + 4 * c4);
+  const float* st = base + min(sg + 4 * c4, smax) * ss + kHD;
+  mv = st[0];
+  lv = st[1];
+}
+
+template <int SPL>
+__device__ __forceinline__ float4 merge_head(const float4 (&ov)[SPL], float mv, float lv, int sg,
+                                             int c4, int nrec) {
+  const bool own_live = sg + 4 * c4 < nrec;
+  const float M = wave_max(own_live ? mv : -INFINITY);
+  const float w_own = own_live ? expf(mv - M) : 0.0f;
+  const float L = wave_sum(own_live ? w_own * lv : 0.0f);
+  float4 O = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
-  for (int i = 0; i < kMergePerWave; ++i)
-    if (wave + 4 * i >= n_split) {
-      mo[i] = 0.0f;
-      mm[i] = -INFINITY;
-      ml[i] = 0.0f;
+  for (int i = 0; i < SPL; ++i) {
+    const float wi = __shfl(w_own, sg * 16 + i, 64);
+    if (sg + 4 * i < nrec) {
+      O.x += wi * ov[i].x;
+      O.y += wi * ov[i].y;
+      O.z += wi * ov[i].z;
+      O.w += wi * ov[i].w;
     }
-  float M = -INFINITY;
-#pragma unroll
-  for (int i = 0; i < kMergePerWave; ++i) M = fmaxf(M, mm[i]);
-  if (lane == 0) red_m[wave] = M;
-  __syncthreads();
-  M = fmaxf(fmaxf(red_m[0], red_m[1]), fmaxf(red_m[2], red_m[3]));
-  float L = 0.0f, O = 0.0f;
-#pragma unroll
-  for (int i = 0; i < kMergePerWave; ++i) {
-    const float wgt = mm[i] == -INFINITY ? 0.0f : expf(mm[i] - M);
-    L += wgt * ml[i];
-    O += wgt * mo[i];
   }
-  red_o[wave][lane] = O;
-  if (lane == 0) red_l[wave] = L;
-  __syncthreads();
-  if (wave == 0) {
-    const float Ls = (red_l[0] + red_l[1]) + (red_l[2] + red_l[3]);
-    const float Os = (red_o[0][lane] + red_o[1][lane]) + (red_o[2][lane] + red_o[3][lane]);
-    a.out[(long)h * kHD + lane] = Os / Ls;
+  O.x += lane_xor16(O.x);
+  O.y += lane_xor16(O.y);
+  O.z += lane_xor16(O.z);
+  O.w += lane_xor16(O.w);
+  O.x += lane_xor32(O.x);
+  O.y += lane_xor32(O.y);
+  O.z += lane_xor32(O.z);
+  O.w += lane_xor32(O.w);
+  return make_float4(O.x / L, O.y / L, O.z / L, O.w / L);
+}
+
+constexpr int kMergeWaves = 8;  // waves (= o_proj rows) per workgroup
+
+template <int SPL, int NL>
+__global__ __launch_bounds__(64 * kMergeWaves) void dec_merge_o_kernel(DecAttnArgs at,
+                                                                       DecGemvArgs o) {
+  constexpr int HPW = NL / 2;  // heads per wave: 16 heads (hidden <= 1024) or 32
+  // heads whose states are requested ahead of the weights: two while there are
+  // at most 4 splits per group (measured faster), one for more splits or 32
+  // heads (the second head's states then queue behind the weight stream)
+  constexpr int HE = (NL <= 4 && SPL <= 4) ? 2 : 1;
+  __shared__ float4 xs[kMaxHeads * kHD / 4];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int sg = lane >> 4, c4 = lane & 15;
+  const int NH = at.n_heads;
+  const int nrec = min((at.max_rows + kKeys - 1) / kKeys, 4 * SPL);
+  float4 ov[HE][SPL];
+  float mv[HE], lv[HE];
+#pragma unroll
+  for (int e = 0; e < HE; ++e)
+    merge_load<SPL>(at, min(wave + kMergeWaves * e, NH - 1), sg, c4, nrec - 1, ov[e], mv[e],
+                    lv[e]);
+  const long row = (long)blockIdx.x * kMergeWaves + wave;
+  const long rc = min(row, o.N - 1);
+  const int K4 = o.K >> 2;
+  const float4* W4 = reinterpret_cast<const float4*>(o.W) + rc * K4;
+  float4 w[NL];
+#pragma unroll
+  for (int j = 0; j < NL; ++j) w[j] = ld_nt(W4 + min(lane + j * 64, K4 - 1));
+  const float res = o.y[rc];
+#pragma unroll
+  for (int hh = 0; hh < HPW; ++hh) {
+    const int h = wave + kMergeWaves * hh;
+    if (hh >= HE && h < NH)
+      merge_load<SPL>(at, h, sg, c4, nrec - 1, ov[hh % HE], mv[hh % HE], lv[hh % HE]);
+    if (h < NH) {
+      const float4 r = merge_head<SPL>(ov[hh % HE], mv[hh % HE], lv[hh % HE], sg, c4, nrec);
+      if (sg == 0) xs[h * (kHD / 4) + c4] = r;
+    }
   }
+  __syncthreads();
+  float acc = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NL; ++j) {
+    const int k4 = lane + j * 64;
+    if (k4 < K4) acc += dot4(w[j], xs[k4]);
+  }
+  const float v = wave_sum(acc);
+  if (row < o.N && lane == 0) o.y[row] = res + v;
 }
 
 // Writes the position and the token's embedding row (bit-exact copy).
@@ -400,25 +480,85 @@ int dec_gemv(int epi, const DecGemvArgs& a, hipStream_t s) {
   return LX_ERR_ARG;
 }
 
-int dec_attention(const DecAttnArgs& a, int n_kv_heads, bool one_split, hipStream_t s) {
+// Split counts the fused merge + o_proj launches cover (4 * SPL, SPL = 1..16),
+// ascending: each launch reads the partial states of at most 3 splits past
+// the ones in use.
+constexpr int kNumSplitClasses = kMaxSplits / 4;
+constexpr int split_class_cap(int c) { return 4 * (c + 1); }
+static_assert(kNumSplitClasses == kDecAttnClasses, "split classes");
+
+int dec_attention(const DecAttnArgs& a, int n_kv_heads, hipStream_t s) {
+  LX_REQUIRE(a.rep >= 1 && a.rep <= kMaxRep && a.ld % 4 == 0 && a.max_rows >= 1,
+             "dec_attention: bad args");
+  // the caller guarantees position + 1 <= kKeys: the single split's
+  // workgroups write the normalised output
+  hipLaunchKernelGGL(dec_attn_partial_kernel, dim3(1, n_kv_heads), dim3(256), 0, s, a);
+  return check_launch("dec_attn_partial_kernel");
+}
+
+template <int SPL, int NL>
+int launch_merge_o(const DecAttnArgs& a, const DecGemvArgs& o, hipStream_t s) {
+  hipLaunchKernelGGL((dec_merge_o_kernel<SPL, NL>),
+                     dim3((unsigned)((o.N + kMergeWaves - 1) / kMergeWaves)),
+                     dim3(64 * kMergeWaves), 0, s, a, o);
+  return check_launch("dec_merge_o_kernel");
+}
+
+int dec_attention_o(const DecAttnArgs& a, int n_kv_heads, int cls, const DecGemvArgs& o,
+                    hipStream_t s) {
   const int max_splits = dec_attention_splits(a.max_rows);
   LX_REQUIRE(a.rep >= 1 && a.rep <= kMaxRep && a.ld % 4 == 0 && a.max_rows >= 1 &&
-                 max_splits <= 4 * kMergePerWave,
-             "dec_attention: bad args");
-  // one_split: the caller guarantees position + 1 <= kKeys, so the single
-  // split's workgroups write the normalised output and no merge is launched
-  hipLaunchKernelGGL(dec_attn_partial_kernel, dim3(one_split ? 1 : max_splits, n_kv_heads),
-                     dim3(256), 0, s, a);
-  int rc = check_launch("dec_attn_partial_kernel");
-  if (rc || one_split) return rc;
-  hipLaunchKernelGGL(dec_attn_merge_kernel, dim3(n_kv_heads * a.rep), dim3(256), 0, s, a);
-  return check_launch("dec_attn_merge_kernel");
+                 max_splits <= kMaxSplits && cls >= 0 && cls < kNumSplitClasses &&
+                 a.n_heads == n_kv_heads * a.rep && a.n_heads <= kMaxHeads,
+             "dec_attention_o: bad args");
+  LX_REQUIRE(o.W && o.y && o.N > 0 && o.K == a.n_heads * kHD, "dec_attention_o: bad o_proj args");
+  const int cap = split_class_cap(cls);
+  hipLaunchKernelGGL(dec_attn_partial_kernel, dim3(min(max_splits, cap), n_kv_heads), dim3(256),
+                     0, s, a);
+  LX_TRY(check_launch("dec_attn_partial_kernel"));
+  const int nl = dec_nl(o.K);
+  LX_REQUIRE(nl <= 8, "dec_attention_o: hidden %d past 2048", o.K);
+#define LX_MERGE_O(SPL)                                               \
+  case SPL:                                                           \
+    if (nl <= 4) return launch_merge_o<SPL, 4>(a, o, s);              \
+    return launch_merge_o<SPL, 8>(a, o, s);
+  switch (cap / 4) {
+    LX_MERGE_O(1)
+    LX_MERGE_O(2)
+    LX_MERGE_O(3)
+    LX_MERGE_O(4)
+    LX_MERGE_O(5)
+    LX_MERGE_O(6)
+    LX_MERGE_O(7)
+    LX_MERGE_O(8)
+    LX_MERGE_O(9)
+    LX_MERGE_O(10)
+    LX_MERGE_O(11)
+    LX_MERGE_O(12)
+    LX_MERGE_O(13)
+    LX_MERGE_O(14)
+    LX_MERGE_O(15)
+    LX_MERGE_O(16)
+  }
+#undef LX_MERGE_O
+  set_error("dec_attention_o: no launch for %d splits", cap);
+  return LX_ERR_ARG;
+}
+
+int dec_attention_class(int n_split) {
+  for (int c = 0; c < kNumSplitClasses; ++c)
+    if (n_split <= split_class_cap(c)) return c;
+  return -1;
 }
 
 int dec_attention_split_keys() { return kKeys; }
 
 int dec_attention_splits(int max_ctx) { return (max_ctx + kKeys - 1) / kKeys; }
-int dec_attention_max_ctx() { return 4 * kMergePerWave * kKeys; }
+int dec_attention_max_ctx() { return kMaxSplits * kKeys; }
+
+long dec_attention_part_floats(int max_ctx, int rep) {
+  return ((long)dec_attention_splits(max_ctx) * rep * kPart + 31) / 32 * 32;
+}
 
 int dec_begin(const float* table, long row, int D, float* x, int* d_pos, int pos,
               hipStream_t s) {

@@ -160,16 +160,28 @@ struct DecAttnArgs {
   const int* pos = nullptr;  // device
   float scale = 0.0f;
   int rep = 0;               // n_heads / n_kv_heads
+  int n_heads = 0;
   int max_rows = 0;          // cache capacity (rows)
   float* part = nullptr;     // n_kv_heads * part_group_stride floats
   long part_group_stride = 0;
   float* out = nullptr;      // (n_heads * 64)
 };
-// one_split: position + 1 <= dec_attention_split_keys() (one launch, no merge).
-int dec_attention(const DecAttnArgs& a, int n_kv_heads, bool one_split, hipStream_t stream);
+// Position + 1 <= dec_attention_split_keys(): one launch over the single
+// split, writing the normalised output.
+int dec_attention(const DecAttnArgs& a, int n_kv_heads, hipStream_t stream);
+// Longer caches: the split partial pass, then the merge fused into o_proj +
+// residual (o: DEC_RESID arguments, x unused).  Split class `cls` covers up to
+// the cls-th split count; dec_attention_class(n_split) picks it (-1: past
+// dec_attention_max_ctx()).
+int dec_attention_o(const DecAttnArgs& a, int n_kv_heads, int cls, const DecGemvArgs& o,
+                    hipStream_t stream);
+int dec_attention_class(int n_split);
+constexpr int kDecAttnClasses = 16;  // split classes of dec_attention_o
 int dec_attention_split_keys();
 int dec_attention_splits(int max_ctx);
-int dec_attention_max_ctx();  // largest cache the merge pass covers
+int dec_attention_max_ctx();  // largest cache the merge covers
+// floats per kv head of the partial-state buffer
+long dec_attention_part_floats(int max_ctx, int rep);
 // x = table[row]; *d_pos = pos.
 int dec_begin(const float* table, long row, int D, float* x, int* d_pos, int pos,
               hipStream_t stream);

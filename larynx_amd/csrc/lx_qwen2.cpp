@@ -60,7 +60,8 @@ struct lx_qwen2 {
   float* rope_tab = nullptr;  // device copy of the rotary inverse frequencies
   bool use_graph = true;      // replay the layer stack as one HIP graph
   hipStream_t cap_stream = nullptr;
-  hipGraphExec_t graph[2] = {nullptr, nullptr};  // [cache fits one attention split]
+  // [0]: the cache fits one attention split; [1 + c]: split class c
+  hipGraphExec_t graph[1 + kDecAttnClasses] = {};
   ~lx_qwen2() {
     for (hipGraphExec_t g : graph)
       if (g) (void)hipGraphExecDestroy(g);
@@ -146,11 +147,13 @@ int prefill_layer(lx_qwen2* m, Layer& L, int rows, const float* next_norm, hipSt
 }
 
 // One decode layer (src/llm/llm.cpp:254-289): RMSNorm + QKV + rotary + cache
-// append; split-key attention (partial pass, then the merge pass unless the
-// cache fits one split); o_proj + residual; RMSNorm + gate/up + SwiGLU;
-// down_proj + residual: five launches while the cache fits one split, six
-// after.  The position is read from m->d_pos.
-int decode_layer(lx_qwen2* m, Layer& L, bool one_split, hipStream_t s) {
+// append; attention; o_proj + residual; RMSNorm + gate/up + SwiGLU;
+// down_proj + residual.  While the cache fits one split (cls 0) the attention
+// is one launch writing its output and o_proj a launch of its own; past it
+// (cls = 1 + split class) the split partials are merged inside the o_proj
+// launch: five launches per layer either way.  The position is read from
+// m->d_pos.
+int decode_layer(lx_qwen2* m, Layer& L, int cls, hipStream_t s) {
   const int H = m->H, KV = m->KV;
   DecGemvArgs q;
   q.x = m->x;
@@ -177,18 +180,23 @@ int decode_layer(lx_qwen2* m, Layer& L, bool one_split, hipStream_t s) {
   at.pos = m->d_pos;
   at.scale = 1.0f / std::sqrt((float)m->HD);
   at.rep = m->NH / m->NKV;
+  at.n_heads = m->NH;
   at.max_rows = m->max_ctx;
   at.part = m->part;
   at.part_group_stride = m->part_stride;
   at.out = m->att;
-  LX_TRY(dec_attention(at, m->NKV, one_split, s));
   DecGemvArgs o;
   o.x = m->att;
   o.W = L.o_w;
   o.y = m->x;
   o.N = H;
   o.K = H;
-  LX_TRY(dec_gemv(DEC_RESID, o, s));
+  if (cls == 0) {
+    LX_TRY(dec_attention(at, m->NKV, s));
+    LX_TRY(dec_gemv(DEC_RESID, o, s));
+  } else {
+    LX_TRY(dec_attention_o(at, m->NKV, cls - 1, o, s));
+  }
   DecGemvArgs gu;
   gu.x = m->x;
   gu.norm_w = L.post_norm;
@@ -207,15 +215,22 @@ int decode_layer(lx_qwen2* m, Layer& L, bool one_split, hipStream_t s) {
   return dec_gemv(DEC_RESID, d, s);
 }
 
-int decode_stack(lx_qwen2* m, bool one_split, hipStream_t s) {
-  for (auto& L : m->layers) LX_TRY(decode_layer(m, L, one_split, s));
+int decode_stack(lx_qwen2* m, int cls, hipStream_t s) {
+  for (auto& L : m->layers) LX_TRY(decode_layer(m, L, cls, s));
   return LX_OK;
+}
+
+// Launch class of the token decoded at position `pos`: 0 while keys [0, pos]
+// fit one attention split, else 1 + the split class of their split count.
+int decode_class(int pos) {
+  const int n_split = (pos + 1 + dec_attention_split_keys() - 1) / dec_attention_split_keys();
+  return n_split == 1 ? 0 : 1 + dec_attention_class(n_split);
 }
 
 // Captures the decode layer stack into a HIP graph on the library's own
 // stream (capture needs a stream other than the legacy default stream); one
-// graph for caches that fit one attention split, one for longer caches.
-int capture_decode(lx_qwen2* m, bool one_split) {
+// graph per launch class (decode_class).
+int capture_decode(lx_qwen2* m, int cls) {
   if (!m->cap_stream &&
       hipStreamCreateWithFlags(&m->cap_stream, hipStreamNonBlocking) != hipSuccess) {
     set_error("qwen2_decode: stream creation failed");
@@ -225,14 +240,14 @@ int capture_decode(lx_qwen2* m, bool one_split) {
     set_error("qwen2_decode: hipStreamBeginCapture failed");
     return LX_ERR_LAUNCH;
   }
-  int rc = decode_stack(m, one_split, m->cap_stream);
+  int rc = decode_stack(m, cls, m->cap_stream);
   hipGraph_t g = nullptr;
   const hipError_t e = hipStreamEndCapture(m->cap_stream, &g);
   if (rc == LX_OK && (e != hipSuccess || !g)) {
     set_error("qwen2_decode: hipStreamEndCapture failed");
     rc = LX_ERR_LAUNCH;
   }
-  hipGraphExec_t& exec = m->graph[one_split ? 1 : 0];
+  hipGraphExec_t& exec = m->graph[cls];
   if (rc == LX_OK && hipGraphInstantiate(&exec, g, nullptr, nullptr, 0) != hipSuccess) {
     set_error("qwen2_decode: hipGraphInstantiate failed");
     exec = nullptr;
@@ -317,7 +332,7 @@ extern "C" int lx_qwen2_create(const lx_qwen2_weights* w, int max_ctx, lx_qwen2*
   m->arrivals = a.alloc<unsigned>(m->n_arrivals);
   ok = ok && m->arrivals;
   m->max_splits = dec_attention_splits(max_ctx);
-  m->part_stride = ((long)m->max_splits * (m->NH / m->NKV) * (m->HD + 2) + 31) / 32 * 32;
+  m->part_stride = dec_attention_part_floats(max_ctx, m->NH / m->NKV);
   m->part = A((size_t)m->part_stride * m->NKV);
   m->pos = a.alloc<int>(max_ctx);
   m->d_pos = a.alloc<int>(1);
@@ -484,16 +499,17 @@ extern "C" int lx_qwen2_decode(lx_qwen2* m, int token, float* logits, float* fin
   const int H = m->H;
   // speech_embedding row of the token (src/llm/llm.cpp:226-230) and its position
   LX_TRY(dec_begin(m->speech_embedding, token, H, m->x, m->d_pos, m->cache_len, s));
-  // the keys [0, cache_len] of every layer fit one attention split: no merge pass
-  const bool one_split = m->cache_len + 1 <= dec_attention_split_keys();
+  // one captured layer stack per launch class of the position
+  const int cls = decode_class(m->cache_len);
+  LX_REQUIRE(cls >= 0, "qwen2_decode: position %d past the attention merge", m->cache_len);
   if (m->use_graph) {
-    if (!m->graph[one_split]) LX_TRY(capture_decode(m, one_split));
-    if (hipGraphLaunch(m->graph[one_split], s) != hipSuccess) {
+    if (!m->graph[cls]) LX_TRY(capture_decode(m, cls));
+    if (hipGraphLaunch(m->graph[cls], s) != hipSuccess) {
       set_error("qwen2_decode: hipGraphLaunch failed");
       return LX_ERR_LAUNCH;
     }
   } else {
-    LX_TRY(decode_stack(m, one_split, s));
+    LX_TRY(decode_stack(m, cls, s));
   }
   // final norm + llm_decoder head (src/llm/llm.cpp:291-300)
   DecGemvArgs h;
