@@ -316,10 +316,13 @@ __global__ __launch_bounds__(256 * KS) void gemm_pipe_kernel(
   // The empty asm statements keep the two stages' loads in order, so the
   // outstanding-load order at the loop entry matches the one at the back edge
   // and the loop's vmcnt waits count exactly one stage.
+  // slab 1 is requested before slab 0 is waited for, so the first two
+  // slabs' latencies overlap
   LX_GLOAD(sa0, sw0, LX_KC(0));
-  LX_SSTORE(sa0, sw0, 0, LX_KT(0));
   asm volatile("" ::: "memory");
   LX_GLOAD(sa1, sw1, LX_KC(1));
+  asm volatile("" ::: "memory");
+  LX_SSTORE(sa0, sw0, 0, LX_KT(0));
   asm volatile("" ::: "memory");
   LX_GLOAD(sa0, sw0, LX_KC(2));
   asm volatile("" ::: "memory");
