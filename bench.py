@@ -53,6 +53,9 @@ def parse():
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only launch the dominant GEMM (QKV + rotary, T=500) and a plain "
                          "device copy of known size, for rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE")
+    ap.add_argument("--prefill-probe", action="store_true",
+                    help="only run the Qwen2 prefill (L=256, 24 layers) ten times, for "
+                         "rocprofv3 --pmc passes over its kernels")
     return ap.parse_args()
 
 
@@ -529,6 +532,27 @@ def counter_probe(torch, ops, launches=20):
     print(f"counter probe: {launches} x QKV GEMM, FF0 GEMM, attention (B={B} T={T})", flush=True)
 
 
+def prefill_probe(torch, runs=10):
+    """The Qwen2-0.5B prefill at L=256 (full 24-layer model, random N(0, 0.02)
+    weights) `runs` times on its own: the workload of the rocprofv3 --pmc
+    passes whose readings (clock, matrix-core busy, HBM fetch) are summarised
+    per prefill kernel."""
+    from larynx_amd.llm import Qwen2Config, Qwen2LM, qwen2_param_shapes
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(5)
+    cfg = Qwen2Config()
+    params = {n: torch.randn(*sh, device=dev, generator=g) * 0.02
+              for n, sh in qwen2_param_shapes(cfg)}
+    lm = Qwen2LM(params, cfg, max_ctx=2304)
+    lm_in = lm.build_lm_input(list(range(100, 260)), list(range(10, 104)))
+    torch.cuda.synchronize()
+    for _ in range(runs):
+        lm.prefill(lm_in)
+    torch.cuda.synchronize()
+    lm.close()
+    print(f"prefill probe: {runs} x Qwen2 prefill (L={lm_in.shape[0]})", flush=True)
+
+
 def traffic_probe(torch, ops, launches=20):
     """Launch the QKV projection (B*T = 1000, N = 3072, K = 1024, rotary
     epilogue) and a plain 256 MiB device-to-device copy, each `launches` times,
@@ -591,6 +615,9 @@ def main():
         return
     if args.counter_probe:
         counter_probe(torch, ops)
+        return
+    if args.prefill_probe:
+        prefill_probe(torch)
         return
 
     dev = torch.device("cuda:0")
