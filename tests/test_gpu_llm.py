@@ -161,6 +161,53 @@ def test_decode_graph_matches_eager_and_crosses_splits(gpu, qwen):
     graph.close()
 
 
+@pytest.mark.parametrize("max_ctx,n0", [(300, 253), (1100, 1021)])
+def test_decode_crosses_split_classes(gpu, qwen, max_ctx, n0):
+    """Past one split, the attention splits are merged inside the o_proj launch,
+    which reads the split states of its split class (up to 4, 8, 12, ...
+    splits; one captured graph per class): sequential steps across a class
+    boundary (cache 253 -> 258: 4 -> 5 splits; 1021 -> 1026: 16 -> 17) stay
+    bit-identical between graph replay and eager launches and track the oracle.
+    With max_ctx 300 the cache holds 5 splits, fewer than the 8 the second class
+    covers, so the merge clamps to the splits that exist."""
+    import os
+    from larynx_amd.llm import Qwen2LM
+    cfg, params, dparams, _ = qwen
+    announce(f"qwen2 decode across split classes, max_ctx {max_ctx}, cache {n0}..{n0 + 5}")
+    os.environ["LX_DECODE_GRAPH"] = "0"
+    try:
+        eager = Qwen2LM(dparams, cfg, max_ctx=max_ctx)
+    finally:
+        del os.environ["LX_DECODE_GRAPH"]
+    graph = Qwen2LM(dparams, cfg, max_ctx=max_ctx)
+    o = orc.Qwen2(params, cfg, cap=max_ctx)
+    for layer in range(cfg.n_layers):
+        kc = orc.normal((n0, 128), 70 + layer, 1, 0.02)
+        vc = orc.normal((n0, 128), 70 + layer, 2, 0.02)
+        o.k_cache[layer, :n0] = kc
+        o.v_cache[layer, :n0] = vc
+        for lm in (eager, graph):
+            kd, vd = lm.cache_views(layer)
+            kd[:n0].copy_(torch.from_numpy(kc))
+            vd[:n0].copy_(torch.from_numpy(vc))
+    o.cache_len = n0
+    eager.set_cache_len(n0)
+    graph.set_cache_len(n0)
+    torch.cuda.synchronize()
+    for step, tok in enumerate([11, 6562, 4000, 2, 6563]):
+        announce(f"qwen2 decode step {step} at position {n0 + step}")
+        lg_e, fn_e = eager.decode(tok, final_norm=True)
+        lg_g, fn_g = graph.decode(tok, final_norm=True)
+        torch.cuda.synchronize()
+        assert torch.equal(lg_e, lg_g) and torch.equal(fn_e, fn_g), step
+        rlg, rfn = o.decode(tok)
+        assert orc.rel_err(fn_g.cpu().numpy(), rfn) < TOL, step
+        assert orc.rel_err(lg_g.cpu().numpy(), rlg) < TOL, step
+        assert int(np.argmax(lg_g.cpu().numpy())) == int(np.argmax(rlg)), step
+    eager.close()
+    graph.close()
+
+
 @pytest.mark.parametrize("L", [1, 37, 200, 300])
 def test_prefill_ragged_lengths(gpu, qwen, L):
     """Prefill at lengths that leave partial 64-row tiles and change the
