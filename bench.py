@@ -39,7 +39,7 @@ def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--T", type=int, default=500)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
@@ -636,19 +636,29 @@ def main():
     ts = cfm_t_span(cfg.n_timesteps)
     sched = [(float(ts[i]), float(ts[i + 1] - ts[i])) for i in range(cfg.n_timesteps)]
 
+    n_sched = len(sched)
+    z = torch.randn(80, T, device=dev, generator=g)
+
     def step(i):
-        t, dt = sched[i % len(sched)]
+        t, dt = sched[i % n_sched]
         est.cfm_step(x, mu, cond, spks, t, dt)
 
-    for i in range(args.warmup):
-        step(i)
+    def run_steps(k):
+        # k Euler steps as the reference's CFM loop runs them: whole 10-step
+        # solves (one stacked modulation GEMV per solve), the remainder as
+        # single steps
+        for _ in range(k // n_sched):
+            est.cfm_solve(z, mu, cond, spks)
+        for i in range(k % n_sched):
+            step(i)
+
+    run_steps(args.warmup)
     torch.cuda.synchronize()
     s = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     e0.record(s)
-    for i in range(args.steps):
-        step(i)
+    run_steps(args.steps)
     e1.record(s)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
@@ -656,13 +666,18 @@ def main():
     ms_per_step = wall * 1e3 / args.steps
     value = T * args.steps / wall
 
-    # 10-step solve (the reference's whole CFM loop) at the same shape
-    z = torch.randn(80, T, device=dev, generator=g)
+    # one 10-step solve (the reference's whole CFM loop), and 10 single steps
+    # (each with its own time MLP and modulation GEMV), at the same shape
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     est.cfm_solve(z, mu, cond, spks)
     torch.cuda.synchronize()
     solve_ms = (time.perf_counter() - t1) * 1e3
+    t1 = time.perf_counter()
+    for i in range(n_sched):
+        step(i)
+    torch.cuda.synchronize()
+    single_step_ms = (time.perf_counter() - t1) * 1e3 / n_sched
 
     # fused kernels as the step launches them (inputs just written by the
     # producing GEMM, as in the real step), from the runtime's activity records
@@ -713,11 +728,13 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic (random ~N(0,0.02) weights, N(0,1) mel inputs)",
-        "config": {"workload": "CosyVoice3 Flow DiT estimator, one CFG Euler step "
-                               "(22 blocks, dim 1024, 16x64 heads, ff 2048, mel 80)",
+        "config": {"workload": "CosyVoice3 Flow DiT estimator, CFG Euler steps of the "
+                               "10-step CFM solve (22 blocks, dim 1024, 16x64 heads, ff 2048, "
+                               "mel 80)",
                    "B": 2, "T": T, "blocks": 22, "cfg_rate": 0.7},
         "event_ms_per_step": round(ev_ms / args.steps, 4),
         "euler_10step_ms": round(solve_ms, 3),
+        "single_step_ms": round(single_step_ms, 4),
         "step_tflops": round(gemm_flop_step / (ms_per_step * 1e-3) / 1e12, 2),
         "roofline": roofline,
         "kernels": {k: {kk: round(vv, 2) for kk, vv in v.items() if kk in

@@ -53,7 +53,8 @@ const char* lx_last_error(void);
  *   y[b,t,:] = LN_eps(x[b,t,:]) * (1 + scale[b,:]) + shift[b,:]
  * LN: biased variance, no affine.  x, y: (B, T, D).  shift/scale rows are
  * `mod_stride` floats apart, so they may point straight into the chunked AdaLN
- * embedding (B, 6*D) with mod_stride = 6*D (no chunk copies).  y may alias x.
+ * embedding (B, 6*D) with mod_stride = 6*D (no chunk copies); mod_stride 0
+ * gives every batch row the same shift/scale.  y may alias x.
  * Replaces ada_ln (src/flow/ops.cpp:94-104: ggml_norm + add(scale,1) + mul +
  * add) and the view_chunk conts (src/flow/dit.cpp:26-31, 57-62, 134-135).
  * D % 4 == 0, D <= 4096. */
@@ -64,7 +65,7 @@ int lx_adaln_modulate_f32(const float* x, const float* shift, const float* scale
 /* AdaLN modulation embedding (GEMV over the batch rows):
  *   emb[b, :] = W @ silu(c[b, :]) + bias,   W: (n_out, D) row-major.
  * Replaces linear(attn_norm_w, attn_norm_b, ggml_silu(t)) (src/flow/dit.cpp:56)
- * and the norm_out linear (src/flow/dit.cpp:133).  B <= 8. */
+ * and the norm_out linear (src/flow/dit.cpp:133).  B <= 16, B * D * 4 <= 64 KiB. */
 int lx_adaln_emb_f32(const float* c, const float* W, const float* bias, float* emb,
                      int B, int D, int n_out, hipStream_t stream);
 
@@ -83,7 +84,8 @@ int lx_rope_partial_interleaved_f32(float* q, float* k, const int* pos, int B, i
 int lx_gelu_tanh_f32(const float* h, float* y, long n, hipStream_t stream);
 
 /* a5 — gated residual, in place: x[b,t,:] += gate[b,:] * y[b,t,:].
- * gate rows are `gate_stride` floats apart (may point into the AdaLN emb).
+ * gate rows are `gate_stride` floats apart (may point into the AdaLN emb; 0:
+ * one gate row for every batch row).
  * Replaces ggml_add(x, ggml_mul(y, gate)) (src/flow/dit.cpp:71, 77). */
 int lx_gated_residual_f32(float* x, const float* y, const float* gate, long gate_stride,
                           int B, int T, int D, hipStream_t stream);

@@ -14,6 +14,7 @@
 // kernel and the CFG combine + Euler update reads the proj_out rows directly.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <new>
@@ -33,6 +34,7 @@ constexpr float kLnEps = 1e-6f;    // LN_EPS (src/flow/internal.h:34)
 constexpr float kRopeBase = 10000.0f;  // ROPE_FREQ_BASE (src/flow/internal.h:35)
 constexpr int kRotDim = 64;        // ROT_DIM (src/flow/internal.h:25)
 constexpr int kProjSplitMax = 8;   // K slices of the proj_out split-K (the plan's cap)
+constexpr int kSolveChunk = 16;    // solve steps whose modulations one GEMV computes
 
 }  // namespace
 
@@ -53,6 +55,8 @@ struct lx_dit {
 
   // activations (sized for B x max_T)
   float *temb, *tmlp_work, *emb;
+  // A CFM solve's modulations, one row per step for up to kSolveChunk steps
+  float *temb_steps, *tmlp_steps, *emb_steps;
   float *A0, *xe, *c1, *h, *xn, *qkv, *att, *ff, *P;
   float* Pws;          // split-K slices of proj_out (kProjSplitMax x rows x mel)
   int proj_splits = 1; // slices of the last forward's proj_out
@@ -85,16 +89,27 @@ int copy_d2d(float* dst, const float* src, size_t n, hipStream_t s) {
 // host array thost.
 int forward_core(lx_dit* m, const float* x, long x_bstride, const float* mu, const float* cond,
                  const float* spks, int cfg, const float* tdev, const float* thost, int T,
-                 hipStream_t s) {
+                 hipStream_t s, const float* emb_pre = nullptr, long emb_bstride = 0) {
   const int B = m->B, D = m->D, mel = m->mel;
   const int rows = B * T;
-  // Time embedding (a6) and every AdaLN modulation of this step in one GEMV.
-  LX_TRY(time_mlp(tdev, thost, B, m->tm0_w, m->tm0_b, m->tm2_w, m->tm2_b, D, m->tmlp_work, m->temb,
-                  s));
-  LX_TRY(gemv(m->temb, B, D, m->ada_w, m->ada_b, m->emb, m->NA, m->NA, /*silu in*/ 1, 0, s));
-  if (m->cap.time_embed)
-    (void)hipMemcpyAsync(m->cap.time_embed, m->temb, sizeof(float) * B * D,
-                         hipMemcpyDeviceToDevice, s);
+  // The AdaLN modulations of this step: batch row b's at emb + b * NA (NA
+  // floats: 22 blocks x 6 chunks, then norm_out's 2).  emb_pre: computed by
+  // the caller (a CFM solve computes all its steps' at once; both CFG rows
+  // share one, emb_bstride 0); otherwise the time embedding (a6) and every
+  // modulation of this step in one GEMV.
+  const float* emb = m->emb;
+  long NA = m->NA;
+  if (emb_pre) {
+    emb = emb_pre;
+    NA = emb_bstride;
+  } else {
+    LX_TRY(time_mlp(tdev, thost, B, m->tm0_w, m->tm0_b, m->tm2_w, m->tm2_b, D, m->tmlp_work,
+                    m->temb, s));
+    LX_TRY(gemv(m->temb, B, D, m->ada_w, m->ada_b, m->emb, m->NA, m->NA, /*silu in*/ 1, 0, s));
+    if (m->cap.time_embed)
+      (void)hipMemcpyAsync(m->cap.time_embed, m->temb, sizeof(float) * B * D,
+                           hipMemcpyDeviceToDevice, s);
+  }
 
   // InputEmbedding: proj(concat[x, cond, mu, spks]) + conv_pos_embed.
   LX_TRY(dit_pack_input(x, x_bstride, cond, mu, spks, cfg, m->A0, B, T, mel, s));
@@ -118,9 +133,8 @@ int forward_core(lx_dit* m, const float* x, long x_bstride, const float* mu, con
     (void)hipMemcpyAsync(m->cap.input_embed, m->h, sizeof(float) * rows * D,
                          hipMemcpyDeviceToDevice, s);
 
-  const long NA = m->NA;
   for (int i = 0; i < m->depth; ++i) {
-    const float* e = m->emb + (long)i * 6 * D;  // chunk order: shift, scale, gate (msa), (mlp)
+    const float* e = emb + (long)i * 6 * D;  // chunk order: shift, scale, gate (msa), (mlp)
     const float* shift_msa = e;
     const float* scale_msa = e + D;
     const float* gate_msa = e + 2 * D;
@@ -160,7 +174,7 @@ int forward_core(lx_dit* m, const float* x, long x_bstride, const float* mu, con
                            hipMemcpyDeviceToDevice, s);
   }
   // norm_out (AdaLayerNormZero_Final): chunk order scale, shift (src/flow/dit.cpp:134-135).
-  const float* ef = m->emb + (long)m->depth * 6 * D;
+  const float* ef = emb + (long)m->depth * 6 * D;
   LX_TRY(lx_adaln_modulate_f32(m->h, /*shift*/ ef + D, /*scale*/ ef, NA, m->xn, B, T, D, kLnEps, s));
   if (m->cap.norm_out)
     (void)hipMemcpyAsync(m->cap.norm_out, m->xn, sizeof(float) * rows * D, hipMemcpyDeviceToDevice,
@@ -240,6 +254,9 @@ extern "C" int lx_dit_create(const lx_dit_weights* w, int B, int max_T, lx_dit**
   m->temb = A((size_t)B * D);
   m->tmlp_work = A((size_t)B * D);
   m->emb = A((size_t)B * m->NA);
+  m->temb_steps = A((size_t)kSolveChunk * D);
+  m->tmlp_steps = A((size_t)kSolveChunk * D);
+  m->emb_steps = A((size_t)kSolveChunk * m->NA);
   m->A0 = A(rows * 4 * mel);
   m->xe = A(rows * D);
   m->c1 = A(rows * D);
@@ -369,15 +386,39 @@ extern "C" int lx_cfm_solve(lx_dit* m, float* x, const float* mu, const float* c
     float tt = (float)i / (float)n_steps;
     t_span[i] = 1.0f - cosf(tt * 0.5f * PI);
   }
+  // The t and dt of every step, by the recurrence of src/flow/flow.cpp:240-276 (t += dt).
+  std::vector<float> ts(n_steps), dts(n_steps);
   float t = t_span[0];
   float dt = t_span[1] - t_span[0];
   for (int step = 1; step <= n_steps; ++step) {
-    const float tt[2] = {t, t};
-    LX_TRY(forward_core(m, x, 0, mu, cond, spks, 1, nullptr, tt, T, s));
-    LX_TRY(cfm_euler_update(x, m->Pws, m->proj_splits, m->proj_slice, m->proj_b, T, m->mel, dt,
-                            1.0f + cfg_rate, cfg_rate, s));
+    ts[step - 1] = t;
+    dts[step - 1] = dt;
     t += dt;
     if (step < n_steps) dt = t_span[step + 1] - t;
+  }
+  // t does not depend on x, so the time embeddings and AdaLN modulations of up
+  // to kSolveChunk steps come from one time MLP and one stacked GEMV (one
+  // stream of the modulation weights instead of one per step).  Each step's
+  // row is computed with the arithmetic of the per-step GEMV, and both rows of
+  // the CFG pair share it, so the solve matches a sequence of lx_cfm_step.
+  // With a time-embedding capture set, steps run one by one (the capture
+  // records each step's embedding).
+  for (int c0 = 0; c0 < n_steps; c0 += kSolveChunk) {
+    const int nc = std::min(kSolveChunk, n_steps - c0);
+    const bool batched = !m->cap.time_embed;
+    if (batched) {
+      LX_TRY(time_mlp(nullptr, ts.data() + c0, nc, m->tm0_w, m->tm0_b, m->tm2_w, m->tm2_b, m->D,
+                      m->tmlp_steps, m->temb_steps, s));
+      LX_TRY(gemv(m->temb_steps, nc, m->D, m->ada_w, m->ada_b, m->emb_steps, m->NA, m->NA,
+                  /*silu in*/ 1, 0, s));
+    }
+    for (int j = 0; j < nc; ++j) {
+      const float tt[2] = {ts[c0 + j], ts[c0 + j]};
+      LX_TRY(forward_core(m, x, 0, mu, cond, spks, 1, nullptr, tt, T, s,
+                          batched ? m->emb_steps + (long)j * m->NA : nullptr, 0));
+      LX_TRY(cfm_euler_update(x, m->Pws, m->proj_splits, m->proj_slice, m->proj_b, T, m->mel,
+                              dts[c0 + j], 1.0f + cfg_rate, cfg_rate, s));
+    }
   }
   return LX_OK;
 }

@@ -23,12 +23,13 @@ namespace {
 
 constexpr int kGemvWaves = 4;
 constexpr int kGemvRows = 4;
-constexpr int kGemvBMax = 8;
+constexpr int kGemvBMax = 16;   // input rows of one launch
+constexpr int kGemvBSmall = 8;  // below it the lighter instantiation (fewer accumulators)
 
 // Dot products of the staged activations xs (B x K, LDS) with rows of W: each
 // wave owns R output rows at a time (R = 4 streams large W with 4 rows of
 // loads in flight per lane; R = 1 spreads a small W over more workgroups).
-template <int R, int ACT_OUT>
+template <int R, int ACT_OUT, int BM>
 __device__ __forceinline__ void gemv_rows(const float* xs, int B, int K,
                                           const float* __restrict__ W,
                                           const float* __restrict__ bias, float* __restrict__ y,
@@ -43,11 +44,11 @@ __device__ __forceinline__ void gemv_rows(const float* xs, int B, int K,
     float bv[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) bv[r] = (bias && n0 + r < N) ? bias[n0 + r] : 0.0f;
-    float acc[R][kGemvBMax];
+    float acc[R][BM];
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
-      for (int b = 0; b < kGemvBMax; ++b) acc[r][b] = 0.0f;
+      for (int b = 0; b < BM; ++b) acc[r][b] = 0.0f;
 #pragma unroll 4
     for (int k4 = lane; k4 < K4; k4 += kWave) {
       float4 w[R];
@@ -57,7 +58,7 @@ __device__ __forceinline__ void gemv_rows(const float* xs, int B, int K,
         w[r] = (n0 + r < N) ? ld_nt(reinterpret_cast<const float4*>(W + (n0 + r) * K) + k4)
                             : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-      for (int b = 0; b < kGemvBMax; ++b) {
+      for (int b = 0; b < BM; ++b) {
         if (b < B) {
           float4 xv = xs4[b * K4 + k4];
 #pragma unroll
@@ -69,7 +70,7 @@ __device__ __forceinline__ void gemv_rows(const float* xs, int B, int K,
 #pragma unroll
     for (int r = 0; r < R; ++r) {
 #pragma unroll
-      for (int b = 0; b < kGemvBMax; ++b) {
+      for (int b = 0; b < BM; ++b) {
         if (b < B) {
           float s = wave_sum(acc[r][b]);
           if (lane == 0 && n0 + r < N) {
@@ -83,7 +84,7 @@ __device__ __forceinline__ void gemv_rows(const float* xs, int B, int K,
   }
 }
 
-template <int ACT_IN, int ACT_OUT, int R>
+template <int ACT_IN, int ACT_OUT, int R, int BM>
 __global__ __launch_bounds__(kGemvWaves * kWave) void gemv_kernel(
     const float* __restrict__ x, int B, int K, const float* __restrict__ W,
     const float* __restrict__ bias, float* __restrict__ y, long N, long ldy) {
@@ -115,7 +116,7 @@ __global__ __launch_bounds__(kGemvWaves * kWave) void gemv_kernel(
     }
   }
   __syncthreads();
-  gemv_rows<R, ACT_OUT>(xs, B, K, W, bias, y, N, ldy);
+  gemv_rows<R, ACT_OUT, BM>(xs, B, K, W, bias, y, N, ldy);
 }
 
 // First layer of the time MLP with the sinusoidal embedding of t (a6) formed
@@ -127,6 +128,7 @@ struct TimeArgs {
   float t[kGemvBMax];
 };
 
+template <int BM>
 __global__ __launch_bounds__(kGemvWaves * kWave) void time_mlp0_kernel(
     const float* __restrict__ tdev, TimeArgs ta, int B, int half, float scale,
     const float* __restrict__ W, const float* __restrict__ bias, float* __restrict__ y, long N) {
@@ -141,7 +143,7 @@ __global__ __launch_bounds__(kGemvWaves * kWave) void time_mlp0_kernel(
     xs[b * 2 * half + half + j] = cs;
   }
   __syncthreads();
-  gemv_rows<1, 1>(xs, B, 2 * half, W, bias, y, N, N);
+  gemv_rows<1, 1, BM>(xs, B, 2 * half, W, bias, y, N, N);
 }
 
 }  // namespace
@@ -162,13 +164,19 @@ int gemv(const float* x, int B, int K, const float* W, const float* bias, float*
   if (g > 4096) g = 4096;
   dim3 grid((unsigned)g), block(kGemvWaves * kWave);
   size_t lds = (size_t)B * K * sizeof(float);
-#define LX_GEMV_LAUNCH(AI, AO)                                                                  \
-  if (wide)                                                                                     \
-    hipLaunchKernelGGL((gemv_kernel<AI, AO, kGemvRows>), grid, block, lds, stream, x, B, K, W, \
-                       bias, y, N, ldy);                                                        \
-  else                                                                                          \
-    hipLaunchKernelGGL((gemv_kernel<AI, AO, 1>), grid, block, lds, stream, x, B, K, W, bias, y, \
-                       N, ldy);
+#define LX_GEMV_LAUNCH_BM(AI, AO, BM)                                                              \
+  if (wide)                                                                                        \
+    hipLaunchKernelGGL((gemv_kernel<AI, AO, kGemvRows, BM>), grid, block, lds, stream, x, B, K, W, \
+                       bias, y, N, ldy);                                                           \
+  else                                                                                             \
+    hipLaunchKernelGGL((gemv_kernel<AI, AO, 1, BM>), grid, block, lds, stream, x, B, K, W, bias,   \
+                       y, N, ldy);
+#define LX_GEMV_LAUNCH(AI, AO)                    \
+  if (B <= kGemvBSmall) {                         \
+    LX_GEMV_LAUNCH_BM(AI, AO, kGemvBSmall)        \
+  } else {                                        \
+    LX_GEMV_LAUNCH_BM(AI, AO, kGemvBMax)          \
+  }
   if (act_in == 0 && act_out == 0) {
     LX_GEMV_LAUNCH(0, 0)
   } else if (act_in == 1 && act_out == 0) {
@@ -179,6 +187,7 @@ int gemv(const float* x, int B, int K, const float* W, const float* bias, float*
     LX_GEMV_LAUNCH(1, 1)
   }
 #undef LX_GEMV_LAUNCH
+#undef LX_GEMV_LAUNCH_BM
   return check_launch("gemv_kernel");
 }
 
@@ -195,9 +204,14 @@ int time_mlp(const float* tdev, const float* thost, int B, const float* w0, cons
     for (int b = 0; b < B; ++b) ta.t[b] = thost[b];
   const long rows_per_block = kGemvWaves;  // one row per wave
   const long g = (D + rows_per_block - 1) / rows_per_block;
-  hipLaunchKernelGGL(time_mlp0_kernel, dim3((unsigned)g), dim3(kGemvWaves * kWave),
-                     (size_t)B * 2 * half * sizeof(float), stream, tdev, ta, B, half, 1000.0f, w0,
-                     b0, hid, (long)D);
+  if (B <= kGemvBSmall)
+    hipLaunchKernelGGL(time_mlp0_kernel<kGemvBSmall>, dim3((unsigned)g), dim3(kGemvWaves * kWave),
+                       (size_t)B * 2 * half * sizeof(float), stream, tdev, ta, B, half, 1000.0f,
+                       w0, b0, hid, (long)D);
+  else
+    hipLaunchKernelGGL(time_mlp0_kernel<kGemvBMax>, dim3((unsigned)g), dim3(kGemvWaves * kWave),
+                       (size_t)B * 2 * half * sizeof(float), stream, tdev, ta, B, half, 1000.0f,
+                       w0, b0, hid, (long)D);
   LX_TRY(check_launch("time_mlp0_kernel"));
   return gemv(hid, B, D, w2, b2, out, D, D, 0, 0, stream);
 }

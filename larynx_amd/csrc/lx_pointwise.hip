@@ -244,7 +244,8 @@ extern "C" int lx_gated_residual_f32(float* x, const float* y, const float* gate
                                      hipStream_t stream) {
   LX_REQUIRE(x && y && gate, "gated_residual: null pointer");
   LX_REQUIRE(B > 0 && T > 0 && D > 0 && D % 4 == 0, "gated_residual: bad shape");
-  LX_REQUIRE(gate_stride >= D && gate_stride % 4 == 0, "gated_residual: bad gate_stride");
+  LX_REQUIRE((gate_stride == 0 || gate_stride >= D) && gate_stride % 4 == 0,
+             "gated_residual: bad gate_stride");
   LX_REQUIRE(((uintptr_t)x | (uintptr_t)y | (uintptr_t)gate) % 16 == 0,
              "gated_residual: pointers must be 16-byte aligned");
   LX_REQUIRE((long)B * T * (D / 4) < (1L << 31), "gated_residual: too many elements");

@@ -138,7 +138,8 @@ extern "C" int lx_adaln_modulate_f32(const float* x, const float* shift, const f
   LX_REQUIRE(x && shift && scale && y, "adaln: null pointer");
   LX_REQUIRE(B > 0 && T > 0 && D > 0, "adaln: bad shape B=%d T=%d D=%d", B, T, D);
   LX_REQUIRE(D % 4 == 0 && D <= 16 * 256, "adaln: D=%d must be a multiple of 4 and <= 4096", D);
-  LX_REQUIRE(mod_stride >= D && mod_stride % 4 == 0, "adaln: bad mod_stride %ld", mod_stride);
+  LX_REQUIRE((mod_stride == 0 || mod_stride >= D) && mod_stride % 4 == 0,
+             "adaln: bad mod_stride %ld", mod_stride);
   LX_REQUIRE(((uintptr_t)x | (uintptr_t)y | (uintptr_t)shift | (uintptr_t)scale) % 16 == 0,
              "adaln: pointers must be 16-byte aligned");
   const int rows = B * T;

@@ -69,6 +69,25 @@ def test_cfm_solve_golden_T24(gpu, golden_setup):
     assert orc.rel_err(feat.cpu().numpy(), c["feat"][0]) < TOL_22
 
 
+@pytest.mark.parametrize("n_steps", [10, 20])
+def test_cfm_solve_batched_modulation(gpu, golden_setup, n_steps):
+    """The solve computes the modulations of up to 16 steps in one stacked
+    GEMV; with a time-embedding capture set it runs every step's own GEMV
+    instead.  Both must give the same bits (20 steps: two chunks)."""
+    _, _, _, est = golden_setup
+    announce(f"cfm solve batched modulation n_steps={n_steps}")
+    T = 100
+    z, mu, cond = (torch.from_numpy(orc.normal((80, T), 41, s)).to(gpu) for s in (1, 2, 3))
+    spks = torch.from_numpy(orc.normal((80,), 41, 4, 0.1)).to(gpu)
+    a = est.cfm_solve(z, mu, cond, spks, n_steps=n_steps, cfg_rate=0.7)
+    est.set_capture({"time_embed": torch.empty(2, 1024, device=gpu)})
+    b = est.cfm_solve(z, mu, cond, spks, n_steps=n_steps, cfg_rate=0.7)
+    torch.cuda.synchronize()
+    est.set_capture(None)
+    assert torch.isfinite(a).all()
+    assert torch.equal(a, b)
+
+
 def test_dit_forward_T500_vs_oracle(gpu, golden_setup):
     _, params, _, est = golden_setup
     announce("dit forward T=500 (22 blocks) vs oracle")

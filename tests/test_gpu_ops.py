@@ -54,9 +54,10 @@ def test_adaln_final_chunk_order(gpu, ops):
     assert orc.rel_err(y, orc.adaln(x, emb[:, :D], emb[:, D:])) < TOL
 
 
-def test_adaln_emb_gemv(gpu, ops):
-    announce("adaln_emb gemv")
-    B, D, N = 2, 1024, 6144
+@pytest.mark.parametrize("B", [2, 10, 16])
+def test_adaln_emb_gemv(gpu, ops, B):
+    announce(f"adaln_emb gemv B={B}")
+    D, N = 1024, 6144
     c = rnd((B, D), 1)
     W, b = rnd((N, D), 2, 0.02), rnd((N,), 3, 0.02)
     e = ops.adaln_emb(dev(c, gpu), dev(W, gpu), dev(b, gpu)).cpu().numpy()
@@ -140,12 +141,13 @@ def test_timestep_golden(gpu, ops):
     assert np.abs(out - orc.timestep_embed(s["t"])).max() < 2e-6
 
 
-def test_time_mlp(gpu, ops):
-    announce("time_mlp")
+@pytest.mark.parametrize("nt", [3, 10])
+def test_time_mlp(gpu, ops, nt):
+    announce(f"time_mlp B={nt}")
     D = 1024
     w0, b0 = rnd((D, 256), 1, 0.02), rnd((D,), 2, 0.02)
     w2, b2 = rnd((D, D), 3, 0.02), rnd((D,), 4, 0.02)
-    t = np.array([0.0, 0.31, 0.99], np.float32)
+    t = np.array([0.0, 0.31, 0.99], np.float32) if nt == 3 else np.linspace(0, 1, nt, dtype=np.float32)
     out = ops.time_mlp(*(dev(a, gpu) for a in (t, w0, b0, w2, b2))).cpu().numpy()
     assert orc.rel_err(out, orc.time_mlp(t, w0, b0, w2, b2)) < TOL
 
