@@ -441,6 +441,433 @@ __global__ __launch_bounds__(64 * QS * KS) void attn_flash_kernel(
   }
 }
 
+
+// ---- fp32 attention on the bf16 matrix cores (split operands) ----
+//
+// Every fp32 operand x is split into three bf16 parts, x = x0 + x1 + x2
+// (x0 = bf16(x), x1 = bf16(x - x0), x2 = bf16(x - x0 - x1)), exact for
+// normal values: the three parts carry 24 significant bits.  A product
+// a * b is then sum_ij a_i b_j; each a_i b_j is exact in the fp32
+// accumulator of v_mfma_f32_32x32x16_bf16, and the six terms with
+// i + j <= 2 are kept (the dropped a1 b2, a2 b1, a2 b2 are below 2^-23 |ab|,
+// under fp32's own rounding of the product).  Sums accumulate in fp32.  Six
+// bf16 MFMAs of 32 cycles replace eight fp32 32x32x2 MFMAs of 64 cycles for
+// the same 32 x 32 x 16 block, and the VALU work of the split runs beside the
+// matrix pipe.
+//
+// Same work split, merge and output as attn_flash_kernel; S^T = K Q^T and
+// O^T += V^T P^T keep the accumulator layouts of the fp32 kernel.  Operands of
+// v_mfma_f32_32x32x16_bf16: lane l supplies row (column) l % 32 and the eight k
+// values of its half h = l / 32.  For S^T the k index is the head channel
+// (K and Q rows, channels s*16 + h*8 + j).  For O^T it is the key: lane half
+// h's register j of P^T (S^T register 8u + j) holds key 16u + key16(h, j),
+// key16 = (j/4)*8 + h*4 + j%4, so V^T is staged in LDS with the keys of each
+// 16-key group permuted to that order (positions h*8 + j), and each lane
+// reads its eight keys as one 16-byte vector.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float floatx8 __attribute__((ext_vector_type(8)));
+
+template <typename F, typename H>
+__device__ __forceinline__ void split3(F v, H& x0, H& x1, H& x2) {
+  x0 = __builtin_convertvector(v, H);
+  const F r = v - __builtin_convertvector(x0, F);
+  x1 = __builtin_convertvector(r, H);
+  x2 = __builtin_convertvector(r - __builtin_convertvector(x1, F), H);
+}
+
+// acc += sum of the six split products a_i b_j, i + j <= 2 (smallest first)
+__device__ __forceinline__ floatx16 mfma_split6(const bf16x8* a, const bf16x8* b, floatx16 acc) {
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[2], b[0], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], b[1], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[2], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], b[0], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[1], acc, 0, 0, 0);
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[0], acc, 0, 0, 0);
+}
+
+// LDS of the split kernel, two buffers each of K planes [3][KT keys][kKP]
+// and V^T planes [3][64 channels][KT + 8] (bf16); the merge reuses it.
+constexpr int kKP = kHD + 8;  // bf16 per K plane row (144 bytes: conflict-free 16-byte reads)
+template <int QS, int KS>
+constexpr size_t bx_lds() {
+  constexpr int KT = 32 * KS;
+  constexpr size_t planes = (size_t)2 * 2 * 3 * (KT * kKP + kHD * (KT + 8));
+  constexpr size_t merge = KS == 2 ? (size_t)QS * 2 * 18 * 64 * 4
+                                   : (size_t)(QS * (KS - 1) * 64 * 34 + QS * 32 * kLD) * 4;
+  return planes > merge ? planes : merge;
+}
+
+// position of key k (within a tile) in the permuted V^T rows
+__device__ __forceinline__ int vt_pos(int k) {
+  return (k & ~15) + ((k >> 2) & 1) * 8 + ((k >> 3) & 1) * 4 + (k & 3);
+}
+
+// Software pipelined over the key tiles: iteration t issues the score MFMAs
+// of tile t + 1 first, then runs the softmax of tile t (VALU, beside those
+// MFMAs), splits P and issues O^T += V^T P^T of tile t, then splits and stores
+// the tiles fetched during the iteration (K of tile t + 2, V of tile t + 1)
+// beside the PV MFMAs.  K and V rotate through two LDS buffers each: K of
+// tile t + 2 replaces K of tile t (its scores were formed in iteration t - 1),
+// V of tile t + 1 replaces V of tile t - 1, so one barrier per tile suffices.
+template <int QS, int KS, bool BUF>
+__global__ __launch_bounds__(64 * QS * KS) void attn_bx_kernel(
+    const float* __restrict__ q, int ldq, const float* __restrict__ k, int ldk,
+    const float* __restrict__ v, int ldv, float* __restrict__ o, int ldo, int Tq, int Tk,
+    int n_heads, int rep, float qscale, int causal, int q_offset) {
+  constexpr int kQT = 32 * QS;
+  constexpr int KT = 32 * KS;
+  constexpr int NT = 64 * QS * KS;
+  constexpr int LPT = KT * 16 / NT;  // K float4 per thread per tile
+  constexpr int LPV = LPT / 2;       // V key pairs (two float4) per thread per tile
+  constexpr int VP = KT + 8;         // bf16 per V^T plane row
+  constexpr int KBUF = 3 * KT * kKP;  // bf16 per K buffer
+  constexpr int VBUF = 3 * kHD * VP;  // bf16 per V buffer
+  static_assert(LPT * NT == KT * 16 && LPV * 2 == LPT, "operand tile must split evenly");
+  static_assert(bx_lds<QS, KS>() <= 160 * 1024, "LDS of one CU");
+  extern __shared__ __attribute__((aligned(16))) float lds[];
+  __bf16* Kp = reinterpret_cast<__bf16*>(lds);  // [2][3][KT][kKP]
+  __bf16* Vt = Kp + 2 * KBUF;                    // [2][3][64][VP]
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int qs = wave % QS, ks = wave / QS;
+  const int lane = tid & 63, r = lane & 31, h = lane >> 5;
+  const int nq = (Tq + kQT - 1) / kQT;
+  int work;
+  {
+    const int n = gridDim.x, x = blockIdx.x & 7, per = n >> 3, rem = n & 7;
+    work = x * per + min(x, rem) + (blockIdx.x >> 3);
+  }
+  const int qtile = work % nq, bh = work / nq;
+  const int head = bh % n_heads, b = bh / n_heads, g = head / rep;
+  const int qt0 = qtile * kQT;
+  const int q0 = qt0 + qs * 32;
+
+  // Q^T operand, split: qb[s][p] holds part p of Q[q0 + r][s*16 + h*8 + j] *
+  // scale * log2(e), j = 0..7.
+  bf16x8 qb[4][3];
+  {
+    const float* qrow = q + ((long)b * Tq + min(q0 + r, Tq - 1)) * ldq + head * kHD + h * 8;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const floatx4 lo4 = *reinterpret_cast<const floatx4*>(qrow + s * 16) * qscale;
+      const floatx4 hi4 = *reinterpret_cast<const floatx4*>(qrow + s * 16 + 4) * qscale;
+      floatx8 x;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        x[e] = lo4[e];
+        x[4 + e] = hi4[e];
+      }
+      split3(x, qb[s][0], qb[s][1], qb[s][2]);
+    }
+  }
+  const int my_q = q_offset + q0 + r;
+  const int kend = causal ? min(Tk, q_offset + min(qt0 + kQT - 1, Tq - 1) + 1) : Tk;
+  const int ntiles = (kend + KT - 1) / KT;
+
+  // K/V tile loaders (as attn_flash_kernel).  K: float4 (row, c) per step;
+  // V: two float4 of keys (2 pi, 2 pi + 1) at channels c..c+3, so that each
+  // V^T row receives the key pair as one 4-byte store.
+  const float* kbase = k + (long)b * Tk * ldk + g * kHD;
+  const float* vbase = v + (long)b * Tk * ldv + g * kHD;
+  const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)kbase, (short)0, BUF ? (int)(((long)(Tk - 1) * ldk + kHD) * 4) : 0, 0x00020000);
+  const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)vbase, (short)0, BUF ? (int)(((long)(Tk - 1) * ldv + kHD) * 4) : 0, 0x00020000);
+  floatx4 rk[LPT], rv[LPV][2];
+  auto gload_k = [&](int t) {
+#pragma unroll
+    for (int j = 0; j < LPT; ++j) {
+      const int idx = tid + NT * j;
+      const int row = idx >> 4, c = (idx & 15) * 4;
+      if (BUF) {
+        rk[j] = __builtin_amdgcn_raw_buffer_load_b128(krs, (row * ldk + c) * 4, t * KT * ldk * 4, 0);
+      } else {
+        const int key = min(t * KT + row, Tk - 1);
+        rk[j] = *reinterpret_cast<const floatx4*>(kbase + (long)key * ldk + c);
+      }
+    }
+  };
+  // V key pair pr, channels c..c+3 of step idx: a wave's 64 steps cover 16
+  // consecutive pairs x 16 channels, so its V^T stores (rows c+e, 16 key
+  // pairs per row, rows 4 apart) fall on 64 distinct LDS banks.
+  auto v_map = [](int idx, int& pr, int& c) {
+    constexpr int PG = KT / 32;  // groups of 16 pairs
+    const int hi = idx >> 6;
+    pr = (idx & 15) + 16 * (hi % PG);
+    c = 4 * (((idx >> 4) & 3) + 4 * (hi / PG));
+  };
+  auto gload_v = [&](int t) {
+#pragma unroll
+    for (int j = 0; j < LPV; ++j) {
+      const int idx = tid + NT * j;
+      int pr, c;
+      v_map(idx, pr, c);
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int row = 2 * pr + e;
+        if (BUF) {
+          rv[j][e] = __builtin_amdgcn_raw_buffer_load_b128(vrs, (row * ldv + c) * 4,
+                                                           t * KT * ldv * 4, 0);
+        } else {
+          const int key = min(t * KT + row, Tk - 1);
+          rv[j][e] = *reinterpret_cast<const floatx4*>(vbase + (long)key * ldv + c);
+        }
+      }
+    }
+  };
+  // split a loaded tile and store its parts into LDS buffer `buf`
+  auto stage_k = [&](int buf) {
+    __bf16* dst = Kp + buf * KBUF;
+#pragma unroll
+    for (int j = 0; j < LPT; ++j) {
+      const int idx = tid + NT * j;
+      const int row = idx >> 4, c = (idx & 15) * 4;
+      bf16x4 x[3];
+      split3(rk[j], x[0], x[1], x[2]);
+#pragma unroll
+      for (int p = 0; p < 3; ++p)
+        *reinterpret_cast<bf16x4*>(dst + (p * KT + row) * kKP + c) = x[p];
+    }
+  };
+  auto stage_v = [&](int buf) {
+    __bf16* dst = Vt + buf * VBUF;
+#pragma unroll
+    for (int j = 0; j < LPV; ++j) {
+      const int idx = tid + NT * j;
+      int pr, c;
+      v_map(idx, pr, c);
+      const int pos = vt_pos(2 * pr);
+      bf16x4 x0[3], x1[3];
+      split3(rv[j][0], x0[0], x0[1], x0[2]);
+      split3(rv[j][1], x1[0], x1[1], x1[2]);
+#pragma unroll
+      for (int p = 0; p < 3; ++p)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          bf16x2 pair;
+          pair[0] = x0[p][e];
+          pair[1] = x1[p][e];
+          *reinterpret_cast<bf16x2*>(dst + (p * kHD + c + e) * VP + pos) = pair;
+        }
+    }
+  };
+  // S^T of this wave's 32 keys of the tile in K buffer `buf`
+  const __bf16* kfrag = Kp + (ks * 32 + r) * kKP + h * 8;
+  auto scores = [&](int buf) {
+    floatx16 s;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) s[i] = 0.0f;
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      bf16x8 ka[3];
+#pragma unroll
+      for (int p = 0; p < 3; ++p)
+        ka[p] = *reinterpret_cast<const bf16x8*>(kfrag + buf * KBUF + p * KT * kKP + st * 16);
+      s = mfma_split6(ka, qb[st], s);
+    }
+    return s;
+  };
+
+  floatx16 o0, o1;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    o0[i] = 0.0f;
+    o1[i] = 0.0f;
+  }
+  float m_run = -INFINITY, l_run = 0.0f;
+  const __bf16* vfrag = Vt + r * VP + ks * 32 + h * 8;
+
+  if (ntiles > 0) {
+    gload_k(0);
+    gload_v(0);
+    stage_k(0);
+    stage_v(0);
+  }
+  if (ntiles > 1) {
+    gload_k(1);
+    stage_k(1);
+  }
+  __syncthreads();
+  // iteration t: s_in holds the scores of tile t, s_out receives tile t + 1's
+  auto iter = [&](int t, const floatx16& s_in, floatx16& s_out) {
+    const bool ld_k = t + 2 < ntiles, ld_v = t + 1 < ntiles;
+    if (ld_k) gload_k(t + 2);
+    if (ld_v) gload_v(t + 1);
+    const int kb = t * KT + ks * 32;  // first key of this wave's part of tile t
+    if (t + 1 < ntiles && kb + KT < kend) s_out = scores((t + 1) & 1);
+    if (kb < kend) {
+      floatx16 s = s_in;
+      // S^T register i of lane half h is key kb + (i/4)*8 + h*4 + i%4 for query r.
+      if (kb + 32 > Tk || (causal && kb + 31 > q_offset + q0)) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int key = kb + (i >> 2) * 8 + h * 4 + (i & 3);
+          const bool ok = key < Tk && (!causal || key <= my_q);
+          s[i] = ok ? s[i] : -INFINITY;
+        }
+      }
+      float mloc = s[0];
+#pragma unroll
+      for (int i = 1; i < 16; ++i) mloc = fmaxf(mloc, s[i]);
+      mloc = fmaxf(mloc, lane_xor32(mloc));
+      // Lazy rescaling, as attn_flash_kernel: the reference moves only when a
+      // query's maximum exceeds it by more than kLazy (log2 units).
+      const bool move = mloc > m_run + kLazy;  // false while the lane is fully masked
+      if (__builtin_amdgcn_read_exec() & __ballot(move)) {
+        const float m_new = move ? mloc : m_run;
+        const float alpha = move ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
+        l_run *= alpha;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          o0[i] *= alpha;
+          o1[i] *= alpha;
+        }
+        m_run = m_new;
+      }
+      const float m_use = m_run == -INFINITY ? 0.0f : m_run;  // fully masked so far
+      float psum = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        s[i] = __builtin_amdgcn_exp2f(s[i] - m_use);
+        psum += s[i];
+      }
+      l_run += psum;
+      // O^T += V^T P^T over the two 16-key steps of the block
+      const __bf16* vb = vfrag + (t & 1) * VBUF;
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        floatx8 pv;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) pv[j] = s[8 * u + j];
+        bf16x8 pb[3];
+        split3(pv, pb[0], pb[1], pb[2]);
+        bf16x8 va[3], vc[3];
+#pragma unroll
+        for (int p = 0; p < 3; ++p) {
+          va[p] = *reinterpret_cast<const bf16x8*>(vb + p * kHD * VP + u * 16);
+          vc[p] = *reinterpret_cast<const bf16x8*>(vb + (p * kHD + 32) * VP + u * 16);
+        }
+        o0 = mfma_split6(va, pb, o0);
+        o1 = mfma_split6(vc, pb, o1);
+      }
+    }
+    if (ld_k) stage_k(t & 1);
+    if (ld_v) stage_v((t + 1) & 1);
+    __syncthreads();
+  };
+  floatx16 sa, sb;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    sa[i] = 0.0f;
+    sb[i] = 0.0f;
+  }
+  if (ntiles > 0 && ks * 32 < kend) sa = scores(0);
+  for (int t = 0; t < ntiles; t += 2) {
+    iter(t, sa, sb);
+    if (t + 1 < ntiles) iter(t + 1, sb, sa);
+  }
+  const float l_tot = l_run + lane_xor32(l_run);
+  if constexpr (KS == 2) {
+    // Two key parts: each wave finalises one half of the 64 channels (part 0
+    // channels 0-31, part 1 channels 32-63).  Both publish (m, l) and the
+    // half they do not own, then combine their own half with the partner's
+    // in part order (part 0's terms first) and store it straight from the
+    // registers: register i of lane (r, h) holds channels (i/4)*8 + h*4 +
+    // i%4 of query r, four consecutive channels per float4.
+    static_assert(QS * 2 * 18 * 64 * 4 <= bx_lds<QS, KS>(), "exchange space");
+    float* pub = lds + (qs * 2 + ks) * (18 * 64);
+    const floatx16& give = ks == 0 ? o1 : o0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) pub[i * 64 + lane] = give[i];
+    pub[16 * 64 + lane] = m_run;
+    pub[17 * 64 + lane] = l_tot;
+    __syncthreads();
+    const float* part = lds + (qs * 2 + (ks ^ 1)) * (18 * 64);
+    const float m_o = part[16 * 64 + lane], l_o = part[17 * 64 + lane];
+    const float m = fmaxf(m_run, m_o);
+    const float a_s = exp2f(m_run - m), a_o = exp2f(m_o - m);
+    const float l = ks == 0 ? l_tot * a_s + l_o * a_o : l_o * a_o + l_tot * a_s;
+    const float inv = 1.0f / l;
+    const floatx16& keep = ks == 0 ? o0 : o1;
+    const int qi = q0 + r;
+    if (qi < Tq) {
+      float* orow = o + ((long)b * Tq + qi) * ldo + head * kHD + ks * 32 + h * 4;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        floatx4 w;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int i = g * 4 + e;
+          const float mine = keep[i] * a_s, other = part[i * 64 + lane] * a_o;
+          w[e] = (ks == 0 ? mine + other : other + mine) * inv;
+        }
+        *reinterpret_cast<floatx4*>(orow + g * 8) = w;
+      }
+    }
+    return;
+  }
+  // Merge the key parts: ks > 0 publish (m, l, O^T) per lane, ks = 0 combines
+  // them in part order.
+  float* xch = lds + qs * ((KS - 1) * 64 * 34);  // per query sub-tile (QS of them)
+  if (ks > 0) {
+    float* mine = xch + (ks - 1) * (64 * 34);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      mine[i * 64 + lane] = o0[i];
+      mine[(16 + i) * 64 + lane] = o1[i];
+    }
+    mine[32 * 64 + lane] = m_run;
+    mine[33 * 64 + lane] = l_tot;
+  }
+  __syncthreads();
+  float* otile = lds + QS * (KS - 1) * 64 * 34;   // transposed output tiles [QS][32 q][kLD]
+  float* ot = otile + qs * (32 * kLD);
+  if (ks == 0) {
+    float m = m_run;
+#pragma unroll
+    for (int p = 0; p < KS - 1; ++p) m = fmaxf(m, xch[p * (64 * 34) + 32 * 64 + lane]);
+    const float a0 = exp2f(m_run - m);
+    float l = l_tot * a0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      o0[i] *= a0;
+      o1[i] *= a0;
+    }
+#pragma unroll
+    for (int p = 0; p < KS - 1; ++p) {
+      const float* other = xch + p * (64 * 34);
+      const float ap = exp2f(other[32 * 64 + lane] - m);
+      l += other[33 * 64 + lane] * ap;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        o0[i] += other[i * 64 + lane] * ap;
+        o1[i] += other[(16 + i) * 64 + lane] * ap;
+      }
+    }
+    const float inv = 1.0f / l;
+    // register i of tile t is channel t*32 + (i/4)*8 + h*4 + i%4 of query r
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int d = (i >> 2) * 8 + h * 4 + (i & 3);
+      ot[r * kLD + d] = o0[i] * inv;
+      ot[r * kLD + 32 + d] = o1[i] * inv;
+    }
+  }
+  __syncthreads();
+  // coalesced store of the sub-tiles: kQT queries x 16 float4
+  for (int idx = tid; idx < kQT * 16; idx += NT) {
+    const int row = idx >> 4, c = (idx & 15) * 4;  // row = qs*32 + local row
+    const int qi = qt0 + row;
+    if (qi < Tq) {
+      const float* src = otile + (row >> 5) * (32 * kLD) + (row & 31) * kLD + c;
+      *reinterpret_cast<floatx4*>(o + ((long)b * Tq + qi) * ldo + head * kHD + c) =
+          *reinterpret_cast<const floatx4*>(src);
+    }
+  }
+}
+
 }  // namespace
 }  // namespace lx
 
@@ -479,29 +906,40 @@ extern "C" int lx_attention_f32(const float* q, int ldq, const float* k, int ldk
   // layout is slower (27.8 us: the 4-part merge and two barriers per tile
   // cost more than the second resident workgroup per CU returns).
   // The third, 128-query workgroups of 4 query sub-tiles x 2 key parts (512
-  // threads, 70 KB: every K/V tile feeds twice the queries), replaces the
-  // 64-query layout when its grid is a whole number of workgroups per CU: T = 3000 (768 workgroups)
-  // 612 -> 571 us, T = 2000 283 -> 262, T = 1000 75.9 -> 73.8.  Grids that
+  // threads: every K/V tile feeds twice the queries), replaces the
+  // 64-query layout when its grid is a whole number of workgroups per CU (fp32
+  // kernel: T = 3000, 768 workgroups, 612 -> 571 us; T = 2000 283 -> 262; T = 1000
+  // 75.9 -> 73.8).  Grids that
   // leave a partial round (T = 1500: 384 workgroups; 2500: 640) run slower
   // than the 64-query layout and keep it.
   const long wg64 = (long)((Tq + 63) / 64) * n_heads * B;
   const long wg128 = (long)((Tq + 127) / 128) * n_heads * B;
   const int layout = wg64 < 256 ? 0 : (wg128 % 256 == 0 ? 2 : 1);  // small / 64-query / wide
+  // The split-operand kernel (attn_bx_kernel) runs the 128-query layout and
+  // the 64-query layout when its grid fits the CUs in one round (T = 500: 23.6
+  // vs 26.2 us; T = 1000: 59.7 vs 81.2; T = 2000: 210 vs 275; T = 3000: 450
+  // vs 571).  With 108 KB of LDS it keeps one workgroup per CU, so a 64-query
+  // grid of several rounds (T = 1500: 181 vs 170 us) and the small grids stay
+  // on the fp32 kernel, whose 70 KB (or single-buffered) LDS lets two
+  // workgroups share a CU.
+  const bool split = layout == 2 || (layout == 1 && wg64 <= 256);
   auto pick = [&]() {
+    if (split) {
+      if (layout == 2) return buf ? attn_bx_kernel<4, 2, true> : attn_bx_kernel<4, 2, false>;
+      return buf ? attn_bx_kernel<2, 2, true> : attn_bx_kernel<2, 2, false>;
+    }
     if (layout == 0)
       return buf ? attn_flash_kernel<1, 4, false, true> : attn_flash_kernel<1, 4, false, false>;
-    if (layout == 2)
-      return buf ? attn_flash_kernel<4, 2, true, true> : attn_flash_kernel<4, 2, true, false>;
     return buf ? attn_flash_kernel<2, 2, true, true> : attn_flash_kernel<2, 2, true, false>;
   };
   auto kern = pick();
   const int qt = layout == 0 ? 32 : layout == 1 ? 64 : 128;
   const int threads = layout == 2 ? 512 : 256;
-  const size_t lds = layout == 0   ? flash_lds<1, 4, false>()
-                     : layout == 1 ? flash_lds<2, 2, true>()
-                                   : flash_lds<4, 2, true>();
-  static LdsLimit once[3][2];  // [layout][buf]
-  const int rc = raise_lds_limit((const void*)kern, lds, once[layout][buf], "attention");
+  const size_t lds = split ? (layout == 2 ? bx_lds<4, 2>() : bx_lds<2, 2>())
+                           : (layout == 0 ? flash_lds<1, 4, false>() : flash_lds<2, 2, true>());
+  const int variant = split ? 2 + (layout == 2) : layout;
+  static LdsLimit once[4][2];  // [kernel variant][buf]
+  const int rc = raise_lds_limit((const void*)kern, lds, once[variant][buf], "attention");
   if (rc) return rc;
   const long nwg = (long)((Tq + qt - 1) / qt) * n_heads * B;
   LX_REQUIRE(nwg < (1L << 31), "attention: %ld workgroups exceed the grid limit", nwg);

@@ -352,6 +352,30 @@ def test_attention_dit(gpu, ops, B, T):
     assert orc.rel_err(o, ref) < TOL
 
 
+@pytest.mark.parametrize("T", [500, 1000, 1500])
+def test_attention_fp32_level_error(gpu, ops, T):
+    """T = 500 (64-query layout, one round) and T = 1000 (128-query layout) run the
+    split-operand kernel, which forms Q K^T and P V from three-part bf16 splits of
+    the fp32 operands; T = 1500 runs the fp32 kernel.  Against a float64
+    softmax(q k^T) v both stay at fp32 level, the maximum error below 2e-6 of the
+    output's largest magnitude (measured: split kernel 1.0e-6 at T = 500 and 8.9e-7
+    at T = 1000, fp32 kernel 1.1e-6 at T = 1500)."""
+    B, D = 2, 1024
+    qkv = rnd((B, T, 3 * D), 21)
+    qd = dev(qkv, gpu)
+    o = ops.attention(qd[..., :D], qd[..., D:2 * D], qd[..., 2 * D:], 16).double().cpu()
+    x = torch.from_numpy(qkv).double()
+    worst = 0.0
+    for hh in (0, 5, 15):
+        c = slice(hh * 64, hh * 64 + 64)
+        qh, kh = x[:, :, c] * 0.125, x[:, :, D + hh * 64:D + hh * 64 + 64]
+        vh = x[:, :, 2 * D + hh * 64:2 * D + hh * 64 + 64]
+        ref = torch.softmax(qh @ kh.transpose(1, 2), dim=-1) @ vh
+        worst = max(worst, float((o[:, :, c] - ref).abs().max() / ref.abs().max()))
+    announce(f"attention T={T} max error vs float64: {worst:.2e}")
+    assert worst < 2e-6
+
+
 @pytest.mark.parametrize("Tq", [64, 2500, 2048])
 def test_attention_kv_past_2gib(gpu, ops, Tq):
     """K and V rows of a fused (180000, 3072) buffer (2.2 GB, row stride 3072): byte
