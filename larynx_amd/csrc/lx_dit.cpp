@@ -35,6 +35,8 @@ constexpr float kRopeBase = 10000.0f;  // ROPE_FREQ_BASE (src/flow/internal.h:35
 constexpr int kRotDim = 64;        // ROT_DIM (src/flow/internal.h:25)
 constexpr int kProjSplitMax = 8;   // K slices of the proj_out split-K (the plan's cap)
 constexpr int kSolveChunk = 16;    // solve steps whose modulations one GEMV computes
+constexpr int kSplitGemmRows = 2048;  // B * T from which a projection may take the split GEMM
+constexpr int kCUs = 256;             // compute units of the MI355X
 
 }  // namespace
 
@@ -50,6 +52,9 @@ struct lx_dit {
   float *conv1_wp, *conv1_b, *conv2_wp, *conv2_b;
   float *ada_w, *ada_b;                 // (NA, D), (NA)
   std::vector<float*> qkv_w, qkv_b;     // (3D, D), (3D)
+  // the four projections' weights as three bf16 planes each (split_planes),
+  // for the split-operand GEMM at large B * T
+  std::vector<void*> qkv_wp, out_wp, ff0_wp, ff2_wp;
   std::vector<float*> out_w, out_b, ff0_w, ff0_b, ff2_w, ff2_b;
   float *proj_w, *proj_b;
 
@@ -133,6 +138,23 @@ int forward_core(lx_dit* m, const float* x, long x_bstride, const float* mu, con
     (void)hipMemcpyAsync(m->cap.input_embed, m->h, sizeof(float) * rows * D,
                          hipMemcpyDeviceToDevice, s);
 
+  // A block projection takes the split-operand bf16 GEMM (128 x 128 tiles)
+  // from kSplitGemmRows rows on when its tiles fill the CUs' rounds to at least
+  // 85% (T = 2000, B = 2: every projection, step 15.9 -> 14.1 ms; T = 3000:
+  // QKV 276 -> 245 us and FF0 185 -> 154 us, while out / FF2, 376 tiles = 1.47
+  // rounds, keep the fp32 kernel's 64 x 64 tiles), else the fp32 GEMM.
+  const bool split_ok = rows >= kSplitGemmRows && D % 128 == 0 && m->F % 128 == 0;
+  auto proj = [&](const float* x, int ldx, const float* W, const void* Wp, const float* bias,
+                  float* y, int ldy, int N, int K, const lx_epilogue* epi) {
+    bool split = split_ok;
+    if (split) {
+      const long tiles = (long)((rows + 127) / 128) * (N / 128);
+      const long rounds = (tiles + kCUs - 1) / kCUs;
+      split = tiles * 100 >= rounds * kCUs * 85;
+    }
+    return split ? linear_split(x, ldx, Wp, bias, y, ldy, rows, N, K, epi, s)
+                 : lx_linear_f32(x, ldx, W, bias, y, ldy, rows, N, K, epi, s);
+  };
   for (int i = 0; i < m->depth; ++i) {
     const float* e = emb + (long)i * 6 * D;  // chunk order: shift, scale, gate (msa), (mlp)
     const float* shift_msa = e;
@@ -151,8 +173,7 @@ int forward_core(lx_dit* m, const float* x, long x_bstride, const float* mu, con
     rope.rope_section = D;   // q occupies columns [0, D), k [D, 2D)
     rope.rope_sections = 2;
     rope.rope_base = kRopeBase;
-    LX_TRY(lx_linear_f32(m->xn, D, m->qkv_w[i], m->qkv_b[i], m->qkv, 3 * D, rows, 3 * D, D, &rope,
-                         s));
+    LX_TRY(proj(m->xn, D, m->qkv_w[i], m->qkv_wp[i], m->qkv_b[i], m->qkv, 3 * D, 3 * D, D, &rope));
     LX_TRY(lx_attention_f32(m->qkv, 3 * D, m->qkv + D, 3 * D, m->qkv + 2 * D, 3 * D, m->att, D, B,
                             T, T, m->heads, m->heads, m->hd, 1.0f / std::sqrt((float)m->hd), 0, 0,
                             s));
@@ -161,14 +182,14 @@ int forward_core(lx_dit* m, const float* x, long x_bstride, const float* mu, con
     gated.rows_per_batch = T;
     gated.gate = gate_msa;
     gated.gate_stride = NA;
-    LX_TRY(lx_linear_f32(m->att, D, m->out_w[i], m->out_b[i], m->h, D, rows, D, D, &gated, s));
+    LX_TRY(proj(m->att, D, m->out_w[i], m->out_wp[i], m->out_b[i], m->h, D, D, D, &gated));
 
     LX_TRY(lx_adaln_modulate_f32(m->h, shift_mlp, scale_mlp, NA, m->xn, B, T, D, kLnEps, s));
     lx_epilogue gelu{};
     gelu.kind = LX_EPI_GELU_TANH;
-    LX_TRY(lx_linear_f32(m->xn, D, m->ff0_w[i], m->ff0_b[i], m->ff, m->F, rows, m->F, D, &gelu, s));
+    LX_TRY(proj(m->xn, D, m->ff0_w[i], m->ff0_wp[i], m->ff0_b[i], m->ff, m->F, m->F, D, &gelu));
     gated.gate = gate_mlp;
-    LX_TRY(lx_linear_f32(m->ff, m->F, m->ff2_w[i], m->ff2_b[i], m->h, D, rows, D, m->F, &gated, s));
+    LX_TRY(proj(m->ff, m->F, m->ff2_w[i], m->ff2_wp[i], m->ff2_b[i], m->h, D, D, m->F, &gated));
     if (m->cap.blocks)
       (void)hipMemcpyAsync(m->cap.blocks + (long)i * rows * D, m->h, sizeof(float) * rows * D,
                            hipMemcpyDeviceToDevice, s);
@@ -239,6 +260,11 @@ extern "C" int lx_dit_create(const lx_dit_weights* w, int B, int max_T, lx_dit**
   m->ada_w = A((size_t)m->NA * D);
   m->ada_b = A(m->NA);
   for (int i = 0; i < depth; ++i) {
+    m->qkv_wp.push_back(a.alloc<unsigned short>((size_t)3 * 3 * D * D));
+    m->out_wp.push_back(a.alloc<unsigned short>((size_t)3 * D * D));
+    m->ff0_wp.push_back(a.alloc<unsigned short>((size_t)3 * F * D));
+    m->ff2_wp.push_back(a.alloc<unsigned short>((size_t)3 * D * F));
+    ok = ok && m->qkv_wp.back() && m->out_wp.back() && m->ff0_wp.back() && m->ff2_wp.back();
     m->qkv_w.push_back(A((size_t)3 * D * D));
     m->qkv_b.push_back(A((size_t)3 * D));
     m->out_w.push_back(A((size_t)D * D));
@@ -312,6 +338,10 @@ extern "C" int lx_dit_create(const lx_dit_weights* w, int B, int max_T, lx_dit**
     C(m->ff0_b[i], bw.ff0_b, F);
     C(m->ff2_w[i], bw.ff2_w, (size_t)D * F);
     C(m->ff2_b[i], bw.ff2_b, D);
+    if (rc == LX_OK) rc = split_planes(m->qkv_w[i], m->qkv_wp[i], (long)3 * D * D, s);
+    if (rc == LX_OK) rc = split_planes(m->out_w[i], m->out_wp[i], (long)D * D, s);
+    if (rc == LX_OK) rc = split_planes(m->ff0_w[i], m->ff0_wp[i], (long)F * D, s);
+    if (rc == LX_OK) rc = split_planes(m->ff2_w[i], m->ff2_wp[i], (long)D * F, s);
   }
   C(m->ada_w + (size_t)depth * 6 * D * D, w->norm_out_w, (size_t)2 * D * D);
   C(m->ada_b + (size_t)depth * 6 * D, w->norm_out_b, (size_t)2 * D);

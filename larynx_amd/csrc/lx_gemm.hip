@@ -36,6 +36,9 @@ struct EpiArgs {
   float inv_freq[64];
 };
 
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned uintx2_t __attribute__((ext_vector_type(2)));
+
 // Split tail: when a launch's tiles leave a partial last round over the CUs,
 // the first n_full tiles run whole and each of the remaining tiles runs as
 // `splits` K slices of `ksplit` columns (workgroups n_full + tile * splits +
@@ -782,6 +785,215 @@ int make_epi(const lx_epilogue* e, int N, EpiArgs* out) {
   return LX_OK;
 }
 
+
+// ---- fp32 GEMM on the bf16 matrix cores (split operands), for large M ----
+//
+// y = epi(x @ W^T + bias) with every product formed from three-part bf16
+// splits: x = x0 + x1 + x2 (x0 = bf16(x), x1 = bf16(x - x0), x2 = bf16(x - x0 -
+// x1), exact for normal values), the six products a_i b_j with i + j <= 2 on
+// v_mfma_f32_32x32x16_bf16, fp32 accumulation.  W arrives pre-split (three
+// planes of (N, K) bf16, made once by split_planes); x is split as it is
+// staged into LDS.  128 x 128 workgroup tiles of 8 waves (2 x 4, each 64 x 32:
+// two 32 x 32 accumulators), K in 32-wide slabs, LDS double buffered (three
+// planes per operand, 80-byte rows: conflict-free 16-byte fragment reads), the
+// next two slabs' global loads in flight.  The epilogue stages the tile in LDS
+// and runs the fp32 kernel's float4 epilogue.  N must be a multiple of 128, K
+// of 32, all epilogue pointers 16-byte aligned.
+typedef __bf16 sbf16x8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ floatx16 mfma_split6x(const sbf16x8* a, const sbf16x8* b, floatx16 acc) {
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[2], b[0], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], b[1], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[2], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], b[0], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[1], acc, 0, 0, 0);
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[0], acc, 0, 0, 0);
+}
+
+__device__ __forceinline__ floatx4 bf16x4_back(bf16x4_t h) {
+  const uintx2_t u = __builtin_bit_cast(uintx2_t, h);
+  floatx4 f;
+  f[0] = __uint_as_float(u[0] << 16);
+  f[1] = __uint_as_float(u[0] & 0xffff0000u);
+  f[2] = __uint_as_float(u[1] << 16);
+  f[3] = __uint_as_float(u[1] & 0xffff0000u);
+  return f;
+}
+
+constexpr int kSplitBM = 128, kSplitBN = 128, kSplitBK = 32, kSplitThreads = 512;
+constexpr int kSplitRS = kSplitBK + 8;  // bf16 per LDS row
+constexpr size_t kSplitLds = (size_t)2 * 3 * (kSplitBM + kSplitBN) * kSplitRS * 2;
+
+template <int EPI>
+__global__ __launch_bounds__(kSplitThreads) void gemm_split_kernel(
+    const float* __restrict__ X, int ldx, const __bf16* __restrict__ Wp, long wplane,
+    const float* __restrict__ bias, float* Y, int ldy, int M, int N, int K, EpiArgs ep) {
+  constexpr int WN = 4, BI = 2;
+  constexpr int NT = kSplitThreads, BM = kSplitBM, BN = kSplitBN, BK = kSplitBK;
+  constexpr int RS = kSplitRS;
+  constexpr int APL = BM * RS, WPL = BN * RS;  // bf16 per plane
+  constexpr int BUFSZ = 3 * APL + 3 * WPL;     // bf16 per buffer
+  constexpr int LA = BM * BK / 4 / NT;         // x float4 per thread per slab
+  constexpr int LW = 3 * BN * BK / 8 / NT;     // W 16-byte chunks per thread per slab
+  static_assert(LA * NT * 4 == BM * BK && LW * NT * 8 == 3 * BN * BK, "slab split");
+  static_assert((size_t)BM * (BN + 4) * 4 <= kSplitLds, "epilogue tile");
+  extern __shared__ __attribute__((aligned(16))) __bf16 sm[];
+  const int tiles_m = (M + BM - 1) / BM, tiles_n = N / BN;
+  const int nwg = tiles_m * tiles_n;
+  int id = blockIdx.x;
+  {
+    const int full = (nwg / 8) * 8;
+    if (id < full) id = (id % 8) * (full / 8) + id / 8;
+  }
+  // runs of 8 M-tiles with N fastest across a run (as gemm_pipe_kernel)
+  int mt, nt;
+  {
+    const int grp = id / (8 * tiles_n);
+    const int gs = min(8, tiles_m - grp * 8);
+    const int in = id - grp * 8 * tiles_n;
+    mt = grp * 8 + in % gs;
+    nt = in / gs;
+  }
+  const int m0 = mt * BM, n0 = nt * BN;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WN, wn = wave % WN;
+  const int nk = K / BK;
+  // x: float4 (row, c); rows past M repeat the last row (never stored)
+  const float* pa[LA];
+  int sa[LA];
+#pragma unroll
+  for (int i = 0; i < LA; ++i) {
+    const int idx = tid + NT * i;
+    const int row = idx / (BK / 4), c = (idx % (BK / 4)) * 4;
+    pa[i] = X + (long)min(m0 + row, M - 1) * ldx + c;
+    sa[i] = row * RS + c;
+  }
+  // W: 16-byte chunk (plane, row, c)
+  const __bf16* pw[LW];
+  int sw[LW];
+#pragma unroll
+  for (int i = 0; i < LW; ++i) {
+    const int idx = tid + NT * i;
+    const int p = idx / (BN * BK / 8), rem = idx % (BN * BK / 8);
+    const int row = rem / (BK / 8), c = (rem % (BK / 8)) * 8;
+    pw[i] = Wp + p * wplane + (long)(n0 + row) * K + c;
+    sw[i] = 3 * APL + p * WPL + row * RS + c;
+  }
+  floatx4 ga0[LA], gw0[LW], ga1[LA], gw1[LW];
+#define LX_SGL(GA, GW, KT)                                                                    \
+  {                                                                                           \
+    const int kk = min(KT, nk - 1) * BK;                                                      \
+    _Pragma("unroll") for (int i = 0; i < LA; ++i)                                            \
+      GA[i] = *reinterpret_cast<const floatx4*>(pa[i] + kk);                                  \
+    _Pragma("unroll") for (int i = 0; i < LW; ++i)                                            \
+      GW[i] = *reinterpret_cast<const floatx4*>(pw[i] + kk);                                  \
+  }
+#define LX_SST(GA, GW, B)                                                                     \
+  {                                                                                           \
+    __bf16* base = sm + (B) * BUFSZ;                                                          \
+    _Pragma("unroll") for (int i = 0; i < LA; ++i) {                                          \
+      const bf16x4_t x0 = __builtin_convertvector(GA[i], bf16x4_t);                           \
+      const floatx4 r = GA[i] - bf16x4_back(x0);                                              \
+      const bf16x4_t x1 = __builtin_convertvector(r, bf16x4_t);                               \
+      const bf16x4_t x2 = __builtin_convertvector(r - bf16x4_back(x1), bf16x4_t);             \
+      *reinterpret_cast<bf16x4_t*>(base + sa[i]) = x0;                                        \
+      *reinterpret_cast<bf16x4_t*>(base + APL + sa[i]) = x1;                                  \
+      *reinterpret_cast<bf16x4_t*>(base + 2 * APL + sa[i]) = x2;                              \
+    }                                                                                         \
+    _Pragma("unroll") for (int i = 0; i < LW; ++i)                                            \
+      *reinterpret_cast<floatx4*>(base + sw[i]) = GW[i];                                      \
+  }
+  floatx16 acc[BI];
+#pragma unroll
+  for (int i = 0; i < BI; ++i)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[i][e] = 0.0f;
+  const int fr = lane & 31, fh = lane >> 5;
+  const int aoff = (wm * 32 * BI + fr) * RS + fh * 8;
+  const int woff = 3 * APL + (wn * 32 + fr) * RS + fh * 8;
+#define LX_SMM(B)                                                                             \
+  {                                                                                           \
+    const __bf16* base = sm + (B) * BUFSZ;                                                    \
+    _Pragma("unroll") for (int st = 0; st < 2; ++st) {                                        \
+      sbf16x8 fa[BI][3], fb[3];                                                               \
+      _Pragma("unroll") for (int i = 0; i < BI; ++i)                                          \
+        _Pragma("unroll") for (int p = 0; p < 3; ++p)                                         \
+          fa[i][p] = *reinterpret_cast<const sbf16x8*>(base + aoff + p * APL + i * 32 * RS +  \
+                                                        st * 16);                             \
+      _Pragma("unroll") for (int p = 0; p < 3; ++p)                                           \
+        fb[p] = *reinterpret_cast<const sbf16x8*>(base + woff + p * WPL + st * 16);           \
+      _Pragma("unroll") for (int i = 0; i < BI; ++i) acc[i] = mfma_split6x(fa[i], fb, acc[i]); \
+    }                                                                                         \
+  }
+  LX_SGL(ga0, gw0, 0);
+  LX_SGL(ga1, gw1, 1);
+  LX_SST(ga0, gw0, 0);
+  LX_SGL(ga0, gw0, 2);
+  __syncthreads();
+  // slab kt in buffer 0 and kt + 1 in ga1 on entry; an odd slab count runs a
+  // surplus slab of the last one's repeat into buffer 1, never multiplied
+  for (int kt = 0; kt < nk; kt += 2) {
+    LX_SMM(0);
+    LX_SST(ga1, gw1, 1);
+    LX_SGL(ga1, gw1, kt + 3);
+    __syncthreads();
+    if (kt + 1 < nk) LX_SMM(1);
+    LX_SST(ga0, gw0, 0);
+    LX_SGL(ga0, gw0, kt + 4);
+    __syncthreads();
+  }
+#undef LX_SGL
+#undef LX_SST
+#undef LX_SMM
+  // epilogue: the tile through LDS, then float4 slots with the fp32 kernel's
+  // epilogue operations
+  constexpr int LDC = BN + 4;
+  float* Cs = reinterpret_cast<float*>(sm);
+#pragma unroll
+  for (int i = 0; i < BI; ++i)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int row = wm * 32 * BI + i * 32 + (e >> 2) * 8 + fh * 4 + (e & 3);
+      Cs[row * LDC + wn * 32 + fr] = acc[i][e];
+    }
+  __syncthreads();
+  const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int j = 0; j < BM * BN / 4 / NT; ++j) {
+    const int idx = tid + j * NT;
+    const int row = idx / (BN / 4), c = (idx % (BN / 4)) * 4;
+    const int m = m0 + row, n = n0 + c;
+    if (m < M) {
+      const float4 v = *reinterpret_cast<const float4*>(Cs + row * LDC + c);
+      const float4 b = bias ? *reinterpret_cast<const float4*>(bias + n) : z4;
+      float4 g = z4, yo = z4;
+      int posm = 0;
+      if (EPI == LX_EPI_GATED_RESID)
+        g = *reinterpret_cast<const float4*>(ep.gate + (long)(m / ep.rows_per_batch) *
+                                                           ep.gate_stride + n);
+      if (EPI == LX_EPI_GATED_RESID || EPI == LX_EPI_RESID)
+        yo = *reinterpret_cast<const float4*>(Y + (long)m * ldy + n);
+      if (EPI == LX_EPI_ROPE_PARTIAL) posm = ep.pos[m % ep.rows_per_batch];
+      epilogue4v<EPI>(Y, ldy, m, n, v, b, g, yo, posm, ep);
+    }
+  }
+}
+
+__global__ void split_planes_kernel(const float* __restrict__ w, __bf16* __restrict__ out,
+                                    long n4) {
+  const long i = blockIdx.x * (long)blockDim.x + threadIdx.x;
+  if (i >= n4) return;
+  const floatx4 x = reinterpret_cast<const floatx4*>(w)[i];
+  const bf16x4_t x0 = __builtin_convertvector(x, bf16x4_t);
+  const floatx4 r = x - bf16x4_back(x0);
+  const bf16x4_t x1 = __builtin_convertvector(r, bf16x4_t);
+  const bf16x4_t x2 = __builtin_convertvector(r - bf16x4_back(x1), bf16x4_t);
+  reinterpret_cast<bf16x4_t*>(out)[i] = x0;
+  reinterpret_cast<bf16x4_t*>(out + 4 * n4)[i] = x1;
+  reinterpret_cast<bf16x4_t*>(out + 8 * n4)[i] = x2;
+}
+
 }  // namespace
 
 int gemv_epi(const float* x, int ldx, const float* W, const float* bias, float* y, int ldy,
@@ -987,6 +1199,56 @@ int linear_impl(const float* x, int ldx, const float* W, const float* bias, floa
   }
   return dispatch_gemm(kind, pick_config(M, N, K), x, ldx, W, bias, y, ldy, M, N, K, ep, stream,
                        sp);
+}
+
+int split_planes(const float* w, void* planes, long n, hipStream_t stream) {
+  LX_REQUIRE(w && planes && n > 0 && n % 4 == 0, "split_planes: bad arguments");
+  LX_REQUIRE(((uintptr_t)w | (uintptr_t)planes) % 16 == 0, "split_planes: unaligned");
+  const long n4 = n / 4;
+  hipLaunchKernelGGL(split_planes_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, stream,
+                     w, static_cast<__bf16*>(planes), n4);
+  return check_launch("split_planes_kernel");
+}
+
+int linear_split(const float* x, int ldx, const void* Wp, const float* bias, float* y, int ldy,
+                 int M, int N, int K, const lx_epilogue* epi, hipStream_t stream) {
+  LX_REQUIRE(x && Wp && y, "linear_split: null pointer");
+  LX_REQUIRE(M > 0 && N > 0 && N % kSplitBN == 0 && K > 0 && K % kSplitBK == 0 && ldx % 4 == 0 &&
+                 ldx >= K,
+             "linear_split: bad shape M=%d N=%d K=%d", M, N, K);
+  const int kind = epi ? epi->kind : LX_EPI_NONE;
+  LX_REQUIRE(kind != LX_EPI_SWIGLU_PAIRED && ldy >= N, "linear_split: unsupported epilogue");
+  LX_REQUIRE(((uintptr_t)x | (uintptr_t)Wp) % 16 == 0, "linear_split: x and W must be aligned");
+  EpiArgs ep;
+  int rc = make_epi(epi, N, &ep);
+  if (rc) return rc;
+  ep.vec = epi_vec_ok(ep, y, ldy, bias);
+  LX_REQUIRE(ep.vec, "linear_split: y, bias and gate must be 16-byte aligned");
+  const long tiles = (long)((M + kSplitBM - 1) / kSplitBM) * (N / kSplitBN);
+  LX_REQUIRE(tiles < (1L << 31), "linear_split: too many tiles");
+  const long wplane = (long)N * K;
+#define LX_SPLIT_CASE(E)                                                                        \
+  case E: {                                                                                     \
+    static LdsLimit once;                                                                       \
+    rc = raise_lds_limit((const void*)gemm_split_kernel<E>, kSplitLds, once, "linear_split");   \
+    if (rc) return rc;                                                                          \
+    hipLaunchKernelGGL(gemm_split_kernel<E>, dim3((unsigned)tiles), dim3(kSplitThreads),        \
+                       kSplitLds, stream, x, ldx, static_cast<const __bf16*>(Wp), wplane, bias, \
+                       y, ldy, M, N, K, ep);                                                    \
+    break;                                                                                      \
+  }
+  switch (kind) {
+    LX_SPLIT_CASE(LX_EPI_NONE)
+    LX_SPLIT_CASE(LX_EPI_GELU_TANH)
+    LX_SPLIT_CASE(LX_EPI_GATED_RESID)
+    LX_SPLIT_CASE(LX_EPI_ROPE_PARTIAL)
+    LX_SPLIT_CASE(LX_EPI_RESID)
+    default:
+      set_error("linear_split: unknown epilogue kind %d", kind);
+      return LX_ERR_ARG;
+  }
+#undef LX_SPLIT_CASE
+  return check_launch("gemm_split_kernel");
 }
 
 int linear_split_tail(const float* x, int ldx, const float* W, const float* bias, float* y,

@@ -8,7 +8,9 @@
 - a 2-block estimator with large AdaLN weights (gates O(1), so every branch
   carries weight in the residual stream) against the oracle;
 - size-independent properties at T=3000: run-to-run bit identity and CFG-row
-  independence.
+  independence;
+- 2-block estimators at T=3000 and T=2000 (the latter with every projection on
+  the split-operand bf16 GEMM) against the oracle.
 """
 import os
 
@@ -180,6 +182,27 @@ def test_dit_T3000_two_blocks_vs_oracle(gpu):
     x, mu, cond = (orc.normal((2, 80, T), 9, s) for s in (1, 2, 3))
     spks = orc.normal((2, 80), 9, 4, 1.0 / np.sqrt(80.0))
     t = np.array([0.35, 0.35], np.float32)
+    dphi = est.forward(*(torch.from_numpy(a).to(gpu) for a in (x, mu, cond, spks, t)))
+    torch.cuda.synchronize()
+    est.close()
+    ref = orc.Dit(params, depth=2).forward(x, mu, cond, spks, t)
+    assert orc.rel_err(dphi.cpu().numpy(), ref) < 1e-4
+
+
+def test_dit_T2000_two_blocks_split_gemm_vs_oracle(gpu):
+    """B=2, T=2000 (4000 rows): every block projection (QKV + rotary, out and FF2
+    with the gated residual, FF0 + GELU) runs the split-operand bf16 GEMM
+    (its tiles fill whole rounds of the CUs); the result matches the oracle at
+    the per-op tolerance."""
+    from larynx_amd.flow import DiTConfig, DiTEstimator, dit_param_shapes
+    announce("dit T=2000 depth=2 split GEMMs vs oracle")
+    cfg = DiTConfig(depth=2)
+    params = orc.make_params(dit_param_shapes(cfg), 13)
+    est = DiTEstimator(to_dev(params, gpu), cfg, B=2, max_T=2000)
+    T = 2000
+    x, mu, cond = (orc.normal((2, 80, T), 10, s) for s in (1, 2, 3))
+    spks = orc.normal((2, 80), 10, 4, 1.0 / np.sqrt(80.0))
+    t = np.array([0.6, 0.6], np.float32)
     dphi = est.forward(*(torch.from_numpy(a).to(gpu) for a in (x, mu, cond, spks, t)))
     torch.cuda.synchronize()
     est.close()
