@@ -100,8 +100,8 @@ int lx_timestep_embed_f32(const float* t, int B, int half_dim, float scale, floa
 
 /* a6 — full TimestepEmbedding: sinusoid(256, scale 1000) -> Linear(256->D) ->
  * SiLU -> Linear(D->D).  w0: (D, 256), w2: (D, D).  work: device scratch of at
- * least B*(256 + D) floats.  Replaces time_embed_host
- * (src/flow/flow_matching.cpp:10-42) on the device. */
+ * least B*(256 + D) floats.  B <= 16, B * D * 4 <= 64 KiB.  Replaces
+ * time_embed_host (src/flow/flow_matching.cpp:10-42) on the device. */
 int lx_time_mlp_f32(const float* t, int B, const float* w0, const float* b0,
                     const float* w2, const float* b2, int D, float* work, float* out,
                     hipStream_t stream);

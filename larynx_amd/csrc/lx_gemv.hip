@@ -1,5 +1,5 @@
 // Skinny products y = act_out(W @ act_in(x) + bias) for a handful of rows
-// (B <= 8): the AdaLN modulation linears and the time-embedding MLP.  These
+// (B <= 16): the AdaLN modulation linears and the time-embedding MLP.  These
 // are weight-streaming (HBM-bound on W), so each wave owns R output rows at a
 // time, keeps R float4 weight loads in flight per lane, and reduces with
 // wave64 shuffles.  The activations are staged in LDS with act_in applied.
