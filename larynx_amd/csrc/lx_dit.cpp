@@ -138,22 +138,25 @@ int forward_core(lx_dit* m, const float* x, long x_bstride, const float* mu, con
     (void)hipMemcpyAsync(m->cap.input_embed, m->h, sizeof(float) * rows * D,
                          hipMemcpyDeviceToDevice, s);
 
-  // A block projection takes the split-operand bf16 GEMM (128 x 128 tiles)
-  // from kSplitGemmRows rows on when its tiles fill the CUs' rounds to at least
-  // 85% (T = 2000, B = 2: every projection, step 15.9 -> 14.1 ms; T = 3000:
-  // QKV 276 -> 245 us and FF0 185 -> 154 us, while out / FF2, 376 tiles = 1.47
-  // rounds, keep the fp32 kernel's 64 x 64 tiles), else the fp32 GEMM.
+  // A block projection takes the split-operand bf16 GEMM from kSplitGemmRows
+  // rows on when its tiles fill the CUs' rounds to at least 85%: 128 x 128
+  // tiles if those do, else 128 x 64 (T = 2000, B = 2: every projection on
+  // 128 x 128, step 15.9 -> 14.1 ms; T = 3000: QKV 276 -> 245 us and FF0 185 ->
+  // 154 us on 128 x 128, out / FF2 on 128 x 64 (128 x 128 would be 1.47
+  // rounds), step 23.94 -> 23.63 ms for the latter; T = 1500: QKV and FF0 on
+  // 128 x 64, step 12.55 -> 12.24 ms), else the fp32 GEMM.
   const bool split_ok = rows >= kSplitGemmRows && D % 128 == 0 && m->F % 128 == 0;
   auto proj = [&](const float* x, int ldx, const float* W, const void* Wp, const float* bias,
                   float* y, int ldy, int N, int K, const lx_epilogue* epi) {
-    bool split = split_ok;
-    if (split) {
-      const long tiles = (long)((rows + 127) / 128) * (N / 128);
+    auto fills = [&](int bn) {
+      const long tiles = (long)((rows + 127) / 128) * (N / bn);
       const long rounds = (tiles + kCUs - 1) / kCUs;
-      split = tiles * 100 >= rounds * kCUs * 85;
-    }
-    return split ? linear_split(x, ldx, Wp, bias, y, ldy, rows, N, K, epi, s)
-                 : lx_linear_f32(x, ldx, W, bias, y, ldy, rows, N, K, epi, s);
+      return tiles * 100 >= rounds * kCUs * 85;
+    };
+    if (split_ok && fills(128)) return linear_split(x, ldx, Wp, bias, y, ldy, rows, N, K, epi, 0, s);
+    if (split_ok && fills(64))
+      return linear_split(x, ldx, Wp, bias, y, ldy, rows, N, K, epi, 1, s);
+    return lx_linear_f32(x, ldx, W, bias, y, ldy, rows, N, K, epi, s);
   };
   for (int i = 0; i < m->depth; ++i) {
     const float* e = emb + (long)i * 6 * D;  // chunk order: shift, scale, gate (msa), (mlp)

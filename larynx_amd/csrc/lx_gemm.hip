@@ -820,23 +820,30 @@ __device__ __forceinline__ floatx4 bf16x4_back(bf16x4_t h) {
   return f;
 }
 
-constexpr int kSplitBM = 128, kSplitBN = 128, kSplitBK = 32, kSplitThreads = 512;
+constexpr int kSplitBK = 32;
 constexpr int kSplitRS = kSplitBK + 8;  // bf16 per LDS row
-constexpr size_t kSplitLds = (size_t)2 * 3 * (kSplitBM + kSplitBN) * kSplitRS * 2;
 
-template <int EPI>
-__global__ __launch_bounds__(kSplitThreads) void gemm_split_kernel(
+// WM x WN waves, each (32 BI) x 32 outputs: workgroup tile (32 BI WM) x (32 WN).
+template <int WM, int WN, int BI>
+struct SplitCfg {
+  static constexpr int NT = 64 * WM * WN, BM = 32 * BI * WM, BN = 32 * WN;
+  static constexpr size_t lds = (size_t)2 * 3 * (BM + BN) * kSplitRS * 2;
+};
+
+template <int EPI, int WM, int WN, int BI>
+__global__ __launch_bounds__(64 * WM * WN) void gemm_split_kernel(
     const float* __restrict__ X, int ldx, const __bf16* __restrict__ Wp, long wplane,
     const float* __restrict__ bias, float* Y, int ldy, int M, int N, int K, EpiArgs ep) {
-  constexpr int WN = 4, BI = 2;
-  constexpr int NT = kSplitThreads, BM = kSplitBM, BN = kSplitBN, BK = kSplitBK;
+  using Cfg = SplitCfg<WM, WN, BI>;
+  constexpr int NT = Cfg::NT, BM = Cfg::BM, BN = Cfg::BN, BK = kSplitBK;
   constexpr int RS = kSplitRS;
   constexpr int APL = BM * RS, WPL = BN * RS;  // bf16 per plane
   constexpr int BUFSZ = 3 * APL + 3 * WPL;     // bf16 per buffer
-  constexpr int LA = BM * BK / 4 / NT;         // x float4 per thread per slab
-  constexpr int LW = 3 * BN * BK / 8 / NT;     // W 16-byte chunks per thread per slab
-  static_assert(LA * NT * 4 == BM * BK && LW * NT * 8 == 3 * BN * BK, "slab split");
-  static_assert((size_t)BM * (BN + 4) * 4 <= kSplitLds, "epilogue tile");
+  constexpr int LAT = BM * BK / 4, LWT = 3 * BN * BK / 8;  // x float4, W chunks per slab
+  constexpr int LA = (LAT + NT - 1) / NT;      // per thread (a surplus step repeats the
+  constexpr int LW = (LWT + NT - 1) / NT;      // last one: same value to the same place)
+  static_assert((size_t)BM * (BN + 4) * 4 <= Cfg::lds, "epilogue tile");
+  static_assert(BM * BN / 4 % NT == 0, "epilogue slots");
   extern __shared__ __attribute__((aligned(16))) __bf16 sm[];
   const int tiles_m = (M + BM - 1) / BM, tiles_n = N / BN;
   const int nwg = tiles_m * tiles_n;
@@ -864,7 +871,7 @@ __global__ __launch_bounds__(kSplitThreads) void gemm_split_kernel(
   int sa[LA];
 #pragma unroll
   for (int i = 0; i < LA; ++i) {
-    const int idx = tid + NT * i;
+    const int idx = min(tid + NT * i, LAT - 1);
     const int row = idx / (BK / 4), c = (idx % (BK / 4)) * 4;
     pa[i] = X + (long)min(m0 + row, M - 1) * ldx + c;
     sa[i] = row * RS + c;
@@ -874,7 +881,7 @@ __global__ __launch_bounds__(kSplitThreads) void gemm_split_kernel(
   int sw[LW];
 #pragma unroll
   for (int i = 0; i < LW; ++i) {
-    const int idx = tid + NT * i;
+    const int idx = min(tid + NT * i, LWT - 1);
     const int p = idx / (BN * BK / 8), rem = idx % (BN * BK / 8);
     const int row = rem / (BK / 8), c = (rem % (BK / 8)) * 8;
     pw[i] = Wp + p * wplane + (long)(n0 + row) * K + c;
@@ -1211,9 +1218,11 @@ int split_planes(const float* w, void* planes, long n, hipStream_t stream) {
 }
 
 int linear_split(const float* x, int ldx, const void* Wp, const float* bias, float* y, int ldy,
-                 int M, int N, int K, const lx_epilogue* epi, hipStream_t stream) {
+                 int M, int N, int K, const lx_epilogue* epi, int narrow, hipStream_t stream) {
+  const int BN = narrow ? SplitCfg<4, 2, 1>::BN : SplitCfg<2, 4, 2>::BN;
+  const int BM = narrow ? SplitCfg<4, 2, 1>::BM : SplitCfg<2, 4, 2>::BM;
   LX_REQUIRE(x && Wp && y, "linear_split: null pointer");
-  LX_REQUIRE(M > 0 && N > 0 && N % kSplitBN == 0 && K > 0 && K % kSplitBK == 0 && ldx % 4 == 0 &&
+  LX_REQUIRE(M > 0 && N > 0 && N % BN == 0 && K > 0 && K % kSplitBK == 0 && ldx % 4 == 0 &&
                  ldx >= K,
              "linear_split: bad shape M=%d N=%d K=%d", M, N, K);
   const int kind = epi ? epi->kind : LX_EPI_NONE;
@@ -1224,18 +1233,24 @@ int linear_split(const float* x, int ldx, const void* Wp, const float* bias, flo
   if (rc) return rc;
   ep.vec = epi_vec_ok(ep, y, ldy, bias);
   LX_REQUIRE(ep.vec, "linear_split: y, bias and gate must be 16-byte aligned");
-  const long tiles = (long)((M + kSplitBM - 1) / kSplitBM) * (N / kSplitBN);
+  const long tiles = (long)((M + BM - 1) / BM) * (N / BN);
   LX_REQUIRE(tiles < (1L << 31), "linear_split: too many tiles");
   const long wplane = (long)N * K;
-#define LX_SPLIT_CASE(E)                                                                        \
-  case E: {                                                                                     \
-    static LdsLimit once;                                                                       \
-    rc = raise_lds_limit((const void*)gemm_split_kernel<E>, kSplitLds, once, "linear_split");   \
-    if (rc) return rc;                                                                          \
-    hipLaunchKernelGGL(gemm_split_kernel<E>, dim3((unsigned)tiles), dim3(kSplitThreads),        \
-                       kSplitLds, stream, x, ldx, static_cast<const __bf16*>(Wp), wplane, bias, \
-                       y, ldy, M, N, K, ep);                                                    \
-    break;                                                                                      \
+  auto launch = [&](auto kern, size_t lds, int threads, LdsLimit& once) {
+    int r = raise_lds_limit((const void*)kern, lds, once, "linear_split");
+    if (r) return r;
+    hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(threads), lds, stream, x, ldx,
+                       static_cast<const __bf16*>(Wp), wplane, bias, y, ldy, M, N, K, ep);
+    return check_launch("gemm_split_kernel");
+  };
+#define LX_SPLIT_CASE(E)                                                                   \
+  case E: {                                                                                \
+    static LdsLimit once_w, once_n;                                                        \
+    if (narrow)                                                                            \
+      return launch(gemm_split_kernel<E, 4, 2, 1>, SplitCfg<4, 2, 1>::lds,                 \
+                    SplitCfg<4, 2, 1>::NT, once_n);                                        \
+    return launch(gemm_split_kernel<E, 2, 4, 2>, SplitCfg<2, 4, 2>::lds,                   \
+                  SplitCfg<2, 4, 2>::NT, once_w);                                          \
   }
   switch (kind) {
     LX_SPLIT_CASE(LX_EPI_NONE)
@@ -1244,11 +1259,11 @@ int linear_split(const float* x, int ldx, const void* Wp, const float* bias, flo
     LX_SPLIT_CASE(LX_EPI_ROPE_PARTIAL)
     LX_SPLIT_CASE(LX_EPI_RESID)
     default:
-      set_error("linear_split: unknown epilogue kind %d", kind);
-      return LX_ERR_ARG;
+      break;
   }
 #undef LX_SPLIT_CASE
-  return check_launch("gemm_split_kernel");
+  set_error("linear_split: unknown epilogue kind %d", kind);
+  return LX_ERR_ARG;
 }
 
 int linear_split_tail(const float* x, int ldx, const float* W, const float* bias, float* y,

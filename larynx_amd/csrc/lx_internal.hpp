@@ -110,10 +110,12 @@ int linear_split_tail(const float* x, int ldx, const float* W, const float* bias
 int split_planes(const float* w, void* planes, long n, hipStream_t stream);
 // lx_linear_f32 on the bf16 matrix cores with split operands: W given as the
 // three planes of split_planes over its (N, K) values, x split in the kernel,
-// six products per element pair, fp32 accumulation.  N % 128 == 0, K % 32 ==
-// 0; every epilogue but SWIGLU_PAIRED; y, bias and gate 16-byte aligned.
+// six products per element pair, fp32 accumulation.  Tiles of 128 x 128
+// (narrow: 128 x 64, for N that leaves the wide tiles a partial round);
+// N % 128 (narrow: 64) == 0, K % 32 == 0; every epilogue but SWIGLU_PAIRED;
+// y, bias and gate 16-byte aligned.
 int linear_split(const float* x, int ldx, const void* Wp, const float* bias, float* y, int ldy,
-                 int M, int N, int K, const lx_epilogue* epi, hipStream_t stream);
+                 int M, int N, int K, const lx_epilogue* epi, int narrow, hipStream_t stream);
 // Scratch floats a split tail of this shape uses (0: none) and its tail tiles.
 size_t split_tail_ws_floats(int M, int N, int K, int* tail_tiles);
 // x[m, :] += sum_s ws[s][m, :] (+ bias); then, if norm_w, hn[m, :] =
