@@ -1226,7 +1226,7 @@ int linear_split(const float* x, int ldx, const void* Wp, const float* bias, flo
                  ldx >= K,
              "linear_split: bad shape M=%d N=%d K=%d", M, N, K);
   const int kind = epi ? epi->kind : LX_EPI_NONE;
-  LX_REQUIRE(kind != LX_EPI_SWIGLU_PAIRED && ldy >= N, "linear_split: unsupported epilogue");
+  LX_REQUIRE(ldy >= (kind == LX_EPI_SWIGLU_PAIRED ? N / 2 : N), "linear_split: ldy too small");
   LX_REQUIRE(((uintptr_t)x | (uintptr_t)Wp) % 16 == 0, "linear_split: x and W must be aligned");
   EpiArgs ep;
   int rc = make_epi(epi, N, &ep);
@@ -1258,6 +1258,7 @@ int linear_split(const float* x, int ldx, const void* Wp, const float* bias, flo
     LX_SPLIT_CASE(LX_EPI_GATED_RESID)
     LX_SPLIT_CASE(LX_EPI_ROPE_PARTIAL)
     LX_SPLIT_CASE(LX_EPI_RESID)
+    LX_SPLIT_CASE(LX_EPI_SWIGLU_PAIRED)
     default:
       break;
   }

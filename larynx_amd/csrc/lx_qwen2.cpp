@@ -13,7 +13,6 @@
 #include <hip/hip_runtime.h>
 
 #include <cmath>
-#include <cstdlib>
 #include <new>
 #include <vector>
 
@@ -30,6 +29,7 @@ constexpr int kTaskIdToken = 6563;  // TASK_ID_TOKEN (src/llm/internal.h:34)
 struct Layer {
   float *qkv_w, *qkv_b, *o_w, *gu_w, *down_w, *in_norm, *post_norm;
   float *k_cache, *v_cache;  // (max_ctx, KV)
+  void* gu_wp;  // gate/up rows as three bf16 planes (split_planes), for long prefills
 };
 
 }  // namespace
@@ -124,6 +124,19 @@ size_t splitk_ws_floats(int max_ctx, int H, int QKV, int I, int* tails) {
 //   o_proj: split-K partials, then residual + post_attention_layernorm;
 //   gate/up with the SwiGLU epilogue;
 //   down_proj: split-K partials, then residual + next_norm.
+// gate/up + SwiGLU on the split-operand bf16 GEMM (128 x 128 tiles) when its
+// tiles fill one round of the 256 CUs at least half or several rounds to at
+// least 75%; else the fp32 GEMM with its split tail.  Prefill at L = 128 /
+// 256 / 384 / 512 / 1024 / 2048: 1.92 / 2.68 / 3.60 / 4.29 / 7.61 / 15.22 ms
+// with the fp32 GEMM, 2.13 / 2.64 / 3.24 / 4.54 / 7.30 / 14.00 with the split
+// one (76 / 152 / 228 / 304 / 608 / 1216 tiles).
+bool gateup_split(int rows, int N, int K) {
+  if (rows < 128 || N % 128 != 0 || K % 32 != 0) return false;
+  const long tiles = (long)((rows + 127) / 128) * (N / 128);
+  const long rounds = (tiles + 255) / 256;
+  return rounds == 1 ? tiles >= 128 : tiles * 100 >= rounds * 256 * 75;
+}
+
 int prefill_layer(lx_qwen2* m, Layer& L, int rows, const float* next_norm, hipStream_t s) {
   const int H = m->H, KV = m->KV, QKV = m->QKV;
   int ks = 0;
@@ -139,8 +152,12 @@ int prefill_layer(lx_qwen2* m, Layer& L, int rows, const float* next_norm, hipSt
   LX_TRY(splitk_resid_rmsnorm(m->ws, sp, rows, H, nullptr, m->x, L.post_norm, m->eps, m->hn, s));
   lx_epilogue swiglu{};
   swiglu.kind = LX_EPI_SWIGLU_PAIRED;
-  LX_TRY(linear_split_tail(m->hn, H, L.gu_w, nullptr, m->act, m->I, rows, 2 * m->I, H, &swiglu,
-                           m->ws, m->ws_floats, m->arrivals, m->n_arrivals, s));
+  if (gateup_split(rows, 2 * m->I, H))
+    LX_TRY(linear_split(m->hn, H, L.gu_wp, nullptr, m->act, m->I, rows, 2 * m->I, H, &swiglu,
+                        /*narrow*/ 0, s));
+  else
+    LX_TRY(linear_split_tail(m->hn, H, L.gu_w, nullptr, m->act, m->I, rows, 2 * m->I, H,
+                             &swiglu, m->ws, m->ws_floats, m->arrivals, m->n_arrivals, s));
   sp = gemm_splitk_plan(rows, H, m->I, &ks);
   LX_TRY(gemm_splitk_partials(m->act, m->I, L.down_w, m->I, m->ws, rows, H, m->I, sp, ks, s));
   return splitk_resid_rmsnorm(m->ws, sp, rows, H, nullptr, m->x, next_norm, m->eps, m->hn, s);
@@ -313,6 +330,8 @@ extern "C" int lx_qwen2_create(const lx_qwen2_weights* w, int max_ctx, lx_qwen2*
     L.qkv_b = A(QKV);
     L.o_w = A((size_t)H * H);
     L.gu_w = A((size_t)2 * I * H);
+    L.gu_wp = a.alloc<unsigned short>((size_t)3 * 2 * I * H);
+    ok = ok && L.gu_wp;
     L.down_w = A((size_t)H * I);
     L.in_norm = A(H);
     L.post_norm = A(H);
@@ -381,6 +400,7 @@ extern "C" int lx_qwen2_create(const lx_qwen2_weights* w, int max_ctx, lx_qwen2*
     C(L.post_norm, lw.post_norm, H);
     if (rc == LX_OK) rc = (lw.gate_w && lw.up_w) ? LX_OK : LX_ERR_ARG;
     if (rc == LX_OK) rc = interleave_rows(lw.gate_w, lw.up_w, L.gu_w, I, H, s);
+    if (rc == LX_OK) rc = split_planes(L.gu_w, L.gu_wp, (long)2 * I * H, s);
   }
   if (rc == LX_OK) rc = iota_i32(m->pos, max_ctx, s);
   // the split tail's arrival counters start at zero; every launch leaves them so
