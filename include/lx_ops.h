@@ -190,7 +190,10 @@ int lx_linear_f32(const float* x, int ldx, const float* W, const float* bias, fl
                   int ldy, int M, int N, int K, const lx_epilogue* epi,
                   hipStream_t stream);
 
-/* Scaled-dot-product attention (flash-style, fp32 MFMA, scores never stored):
+/* Scaled-dot-product attention (flash-style, scores never stored; fp32
+ * arithmetic, on the fp32 matrix cores or, for grids that fill the CUs in whole
+ * rounds, on the bf16 ones with every operand split into three bf16 parts and
+ * six exact partial products accumulated in fp32):
  *   o[b, t, h*hd:(h+1)*hd] = softmax(scale * q_h k_g^T [+ causal mask]) v_g
  * with g = h / (n_heads / n_kv_heads) (GQA, consecutive like HF repeat_kv).
  * q: (B, Tq, *) row stride ldq, head h at column h*hd; k, v: (B, Tk, *) row
