@@ -821,7 +821,14 @@ __device__ __forceinline__ floatx4 bf16x4_back(bf16x4_t h) {
 }
 
 constexpr int kSplitBK = 32;
-constexpr int kSplitRS = kSplitBK + 8;  // bf16 per LDS row
+// LDS rows of 32 bf16 (64 bytes, unpadded) whose four 16-byte chunks are
+// XOR-swizzled by (row / 8) % 4: the staging stores (four rows per 256-byte
+// pass) and the fragment reads (32 rows, one chunk each) both hit distinct
+// banks.
+constexpr int kSplitRS = kSplitBK;  // bf16 per LDS row
+__device__ __forceinline__ int split_col(int row, int c) {
+  return ((((c >> 3) ^ (row >> 3)) & 3) << 3) | (c & 7);
+}
 
 // WM x WN waves, each (32 BI) x 32 outputs: workgroup tile (32 BI WM) x (32 WN).
 template <int WM, int WN, int BI>
@@ -874,7 +881,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_split_kernel(
     const int idx = min(tid + NT * i, LAT - 1);
     const int row = idx / (BK / 4), c = (idx % (BK / 4)) * 4;
     pa[i] = X + (long)min(m0 + row, M - 1) * ldx + c;
-    sa[i] = row * RS + c;
+    sa[i] = row * RS + split_col(row, c);
   }
   // W: 16-byte chunk (plane, row, c)
   const __bf16* pw[LW];
@@ -885,7 +892,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_split_kernel(
     const int p = idx / (BN * BK / 8), rem = idx % (BN * BK / 8);
     const int row = rem / (BK / 8), c = (rem % (BK / 8)) * 8;
     pw[i] = Wp + p * wplane + (long)(n0 + row) * K + c;
-    sw[i] = 3 * APL + p * WPL + row * RS + c;
+    sw[i] = 3 * APL + p * WPL + row * RS + split_col(row, c);
   }
   floatx4 ga0[LA], gw0[LW], ga1[LA], gw1[LW];
 #define LX_SGL(GA, GW, KT)                                                                    \
@@ -917,8 +924,11 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_split_kernel(
 #pragma unroll
     for (int e = 0; e < 16; ++e) acc[i][e] = 0.0f;
   const int fr = lane & 31, fh = lane >> 5;
-  const int aoff = (wm * 32 * BI + fr) * RS + fh * 8;
-  const int woff = 3 * APL + (wn * 32 + fr) * RS + fh * 8;
+  // fragment rows are wm * 32 BI + i * 32 + fr (A) and wn * 32 + fr (W): their
+  // chunk swizzle is (fr / 8) % 4, the same for every block
+  const int aoff = (wm * 32 * BI + fr) * RS;
+  const int woff = 3 * APL + (wn * 32 + fr) * RS;
+  const int fc[2] = {split_col(fr, fh * 8), split_col(fr, 16 + fh * 8)};
 #define LX_SMM(B)                                                                             \
   {                                                                                           \
     const __bf16* base = sm + (B) * BUFSZ;                                                    \
@@ -927,9 +937,9 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_split_kernel(
       _Pragma("unroll") for (int i = 0; i < BI; ++i)                                          \
         _Pragma("unroll") for (int p = 0; p < 3; ++p)                                         \
           fa[i][p] = *reinterpret_cast<const sbf16x8*>(base + aoff + p * APL + i * 32 * RS +  \
-                                                        st * 16);                             \
+                                                        fc[st]);                              \
       _Pragma("unroll") for (int p = 0; p < 3; ++p)                                           \
-        fb[p] = *reinterpret_cast<const sbf16x8*>(base + woff + p * WPL + st * 16);           \
+        fb[p] = *reinterpret_cast<const sbf16x8*>(base + woff + p * WPL + fc[st]);            \
       _Pragma("unroll") for (int i = 0; i < BI; ++i) acc[i] = mfma_split6x(fa[i], fb, acc[i]); \
     }                                                                                         \
   }
