@@ -35,7 +35,7 @@ constexpr float kRopeBase = 10000.0f;  // ROPE_FREQ_BASE (src/flow/internal.h:35
 constexpr int kRotDim = 64;        // ROT_DIM (src/flow/internal.h:25)
 constexpr int kProjSplitMax = 8;   // K slices of the proj_out split-K (the plan's cap)
 constexpr int kSolveChunk = 16;    // solve steps whose modulations one GEMV computes
-constexpr int kSplitGemmRows = 2048;  // B * T from which a projection may take the split GEMM
+constexpr int kSplitGemmRows = 1536;  // B * T from which a projection may take the split GEMM
 constexpr int kCUs = 256;             // compute units of the MI355X
 
 }  // namespace
@@ -144,7 +144,10 @@ int forward_core(lx_dit* m, const float* x, long x_bstride, const float* mu, con
   // 128 x 128, step 15.9 -> 14.1 ms; T = 3000: QKV 276 -> 245 us and FF0 185 ->
   // 154 us on 128 x 128, out / FF2 on 128 x 64 (128 x 128 would be 1.47
   // rounds), step 23.94 -> 23.63 ms for the latter; T = 1500: QKV and FF0 on
-  // 128 x 64, step 12.55 -> 12.24 ms), else the fp32 GEMM.
+  // 128 x 64, step 12.55 -> 12.24 ms; T = 1000: QKV, out and FF2 on 128 x 64,
+  // FF0 on 128 x 128, step 8.36 -> 7.06 ms), else the fp32 GEMM.  At
+  // T = 500 (1000 rows) FF0's one round of 128 x 64 tiles is no faster than
+  // the fp32 GEMM (step 4.14 vs 4.17 ms).
   const bool split_ok = rows >= kSplitGemmRows && D % 128 == 0 && m->F % 128 == 0;
   auto proj = [&](const float* x, int ldx, const float* W, const void* Wp, const float* bias,
                   float* y, int ldy, int N, int K, const lx_epilogue* epi) {
