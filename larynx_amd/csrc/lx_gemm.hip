@@ -795,8 +795,9 @@ int make_epi(const lx_epilogue* e, int N, EpiArgs* out) {
 // planes of (N, K) bf16, made once by split_planes); x is split as it is
 // staged into LDS.  128 x 128 workgroup tiles of 8 waves (2 x 4, each 64 x 32:
 // two 32 x 32 accumulators), K in 32-wide slabs, LDS double buffered (three
-// planes per operand, 80-byte rows: conflict-free 16-byte fragment reads), the
-// next two slabs' global loads in flight.  The epilogue stages the tile in LDS
+// planes per operand, 64-byte rows with an XOR chunk swizzle: conflict-free
+// staging stores and 16-byte fragment reads), the next two slabs' global loads
+// in flight.  The epilogue stages the tile in LDS
 // and runs the fp32 kernel's float4 epilogue.  N must be a multiple of 128, K
 // of 32, all epilogue pointers 16-byte aligned.
 typedef __bf16 sbf16x8 __attribute__((ext_vector_type(8)));
@@ -929,39 +930,81 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_split_kernel(
   const int aoff = (wm * 32 * BI + fr) * RS;
   const int woff = 3 * APL + (wn * 32 + fr) * RS;
   const int fc[2] = {split_col(fr, fh * 8), split_col(fr, 16 + fh * 8)};
-#define LX_SMM(B)                                                                             \
+  // The six products of mfma_split6x as (A part, W part), in its order.
+  constexpr int kPa[6] = {2, 1, 0, 1, 0, 0}, kPw[6] = {0, 1, 2, 0, 1, 0};
+#define LX_SRD(FA, FB, B, ST)                                                                 \
   {                                                                                           \
     const __bf16* base = sm + (B) * BUFSZ;                                                    \
-    _Pragma("unroll") for (int st = 0; st < 2; ++st) {                                        \
-      sbf16x8 fa[BI][3], fb[3];                                                               \
-      _Pragma("unroll") for (int i = 0; i < BI; ++i)                                          \
-        _Pragma("unroll") for (int p = 0; p < 3; ++p)                                         \
-          fa[i][p] = *reinterpret_cast<const sbf16x8*>(base + aoff + p * APL + i * 32 * RS +  \
-                                                        fc[st]);                              \
+    _Pragma("unroll") for (int i = 0; i < BI; ++i)                                            \
       _Pragma("unroll") for (int p = 0; p < 3; ++p)                                           \
-        fb[p] = *reinterpret_cast<const sbf16x8*>(base + woff + p * WPL + fc[st]);            \
-      _Pragma("unroll") for (int i = 0; i < BI; ++i) acc[i] = mfma_split6x(fa[i], fb, acc[i]); \
-    }                                                                                         \
+        FA[i][p] = *reinterpret_cast<const sbf16x8*>(base + aoff + p * APL + i * 32 * RS +    \
+                                                     fc[ST]);                                 \
+    _Pragma("unroll") for (int p = 0; p < 3; ++p)                                             \
+      FB[p] = *reinterpret_cast<const sbf16x8*>(base + woff + p * WPL + fc[ST]);              \
+  }
+#define LX_SMUL(FA, FB, P0, P1)                                                               \
+  _Pragma("unroll") for (int q = P0; q < P1; ++q)                                             \
+    _Pragma("unroll") for (int i = 0; i < BI; ++i)                                            \
+      acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(FA[i][kPa[q]], FB[kPw[q]], acc[i], 0, 0, 0);
+  // Each slab is two 16-wide k steps, fragment sets F0 and F1.  Two
+  // accumulators per wave (BI = 2) pipeline across the barrier: F1's reads
+  // issue under F0's MFMAs, the next slab's staging and global loads under F0's
+  // and the first four of F1's six products, and after the barrier the next
+  // slab's F0 reads issue under F1's last two products, so the matrix pipe
+  // does not drain at each barrier (QKV at 6000 rows 255 -> 242 us).  With one
+  // accumulator (BI = 1) the two live fragment sets would take the kernel past
+  // 128 VGPRs and one of its two workgroups per CU (out / FF2 at 6000 rows
+  // 127 -> 136 us), so it multiplies each slab between the barriers.
+#define LX_HALF(B, GA, GW, KT)                                                                \
+  {                                                                                           \
+    LX_SRD(fa1, fb1, B, 1);                                                                   \
+    LX_SMUL(fa0, fb0, 0, 6);                                                                  \
+    LX_SST(GA, GW, 1 - (B));                                                                  \
+    LX_SGL(GA, GW, (KT) + 3);                                                                 \
+    LX_SMUL(fa1, fb1, 0, 4);                                                                  \
+    __syncthreads();                                                                          \
+    if ((KT) + 1 < nk) LX_SRD(fa0, fb0, 1 - (B), 0);                                          \
+    LX_SMUL(fa1, fb1, 4, 6);                                                                  \
+  }
+#define LX_SMM(B)                                                                             \
+  _Pragma("unroll") for (int st = 0; st < 2; ++st) {                                          \
+    sbf16x8 fa[BI][3], fb[3];                                                                 \
+    LX_SRD(fa, fb, B, st);                                                                    \
+    LX_SMUL(fa, fb, 0, 6);                                                                    \
   }
   LX_SGL(ga0, gw0, 0);
   LX_SGL(ga1, gw1, 1);
   LX_SST(ga0, gw0, 0);
   LX_SGL(ga0, gw0, 2);
   __syncthreads();
-  // slab kt in buffer 0 and kt + 1 in ga1 on entry; an odd slab count runs a
-  // surplus slab of the last one's repeat into buffer 1, never multiplied
-  for (int kt = 0; kt < nk; kt += 2) {
-    LX_SMM(0);
-    LX_SST(ga1, gw1, 1);
-    LX_SGL(ga1, gw1, kt + 3);
-    __syncthreads();
-    if (kt + 1 < nk) LX_SMM(1);
-    LX_SST(ga0, gw0, 0);
-    LX_SGL(ga0, gw0, kt + 4);
-    __syncthreads();
+  if constexpr (BI >= 2) {
+    sbf16x8 fa0[BI][3], fb0[3], fa1[BI][3], fb1[3];
+    LX_SRD(fa0, fb0, 0, 0);
+    // slab kt in buffer 0 (its F0 in registers) and kt + 1 in ga1 on entry;
+    // the last slab stages a repeat of itself, never multiplied
+    for (int kt = 0; kt < nk; kt += 2) {
+      LX_HALF(0, ga1, gw1, kt);
+      if (kt + 1 < nk) LX_HALF(1, ga0, gw0, kt + 1);
+    }
+  } else {
+    // slab kt in buffer 0 and kt + 1 in ga1 on entry; an odd slab count runs
+    // a surplus slab of the last one's repeat into buffer 1, never multiplied
+    for (int kt = 0; kt < nk; kt += 2) {
+      LX_SMM(0);
+      LX_SST(ga1, gw1, 1);
+      LX_SGL(ga1, gw1, kt + 3);
+      __syncthreads();
+      if (kt + 1 < nk) LX_SMM(1);
+      LX_SST(ga0, gw0, 0);
+      LX_SGL(ga0, gw0, kt + 4);
+      __syncthreads();
+    }
   }
 #undef LX_SGL
 #undef LX_SST
+#undef LX_SRD
+#undef LX_SMUL
+#undef LX_HALF
 #undef LX_SMM
   // epilogue: the tile through LDS, then float4 slots with the fp32 kernel's
   // epilogue operations
