@@ -9,9 +9,13 @@ value = T * steps / wall time of the timed region (mel frames per second).
 Also reported on the same JSON line:
   roofline      the dominant kernel's achieved FLOP/s (HIP events around graph
                 replays of its launches under continuous load, on the replay stream)
-                vs the 157.3 TFLOP/s fp32 MFMA peak, and its HBM traffic per launch
-                from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary;
-  kernels       per-kernel-class timings of one step's launches (same method);
+                vs its matrix-core peak (157.3 TFLOP/s fp32; for the split-operand
+                GEMM, which forms each fp32 product from six bf16 MFMA products, the
+                bf16 MFMA flops executed vs the 2.5 PFLOP/s dense bf16 peak), and its
+                HBM traffic per launch from the committed rocprofv3 FETCH_SIZE /
+                WRITE_SIZE summary;
+  kernels       per-kernel-class timings of one step's launches (same method), each
+                class on the kernel the estimator runs for it;
   fused_ops     achieved HBM GB/s of every fused op at the configs' shapes, with
                 each launch on a distinct buffer set (> 256 MB rotation, so the
                 MALL does not serve the reads);
@@ -33,6 +37,8 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 MFMA_F32_PEAK_TFLOPS = 157.3
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+SPLIT_PRODUCTS = 6  # bf16 MFMA products per fp32 product in the split-operand kernels
 
 
 def parse():
@@ -183,9 +189,32 @@ def graph_time_ms(fn, n, torch, reps=3):
         return None
 
 
+def dit_split_tile(rows, N, D=1024, F=2048, cus=256):
+    """The estimator's choice of GEMM for a block projection (lx_dit.cpp,
+    forward_core): 0 / 1 = split-operand kernel with 128 x 128 / 128 x 64
+    tiles, None = fp32 kernel."""
+    if D % 128 or F % 128:
+        return None
+    mt = (rows + 127) // 128
+
+    def fills(bn):
+        tiles = mt * (N // bn)
+        rounds = (tiles + cus - 1) // cus
+        return tiles * 100 >= rounds * cus * 85
+    if rows >= 1536:
+        if fills(128):
+            return 0
+        if fills(64):
+            return 1
+        return None
+    t128 = mt * (N // 128)
+    return 0 if t128 <= cus and t128 * 100 >= cus * 70 else None
+
+
 def gemm_kernels(torch, ops, T, dev):
     """Per-class timings of the estimator's projection GEMMs and attention at
-    the step's shapes (each class is one kernel instantiation)."""
+    the step's shapes, each class on the kernel the step runs for it (the fp32
+    or the split-operand GEMM, as the estimator chooses by tile count)."""
     D, F, B = 1024, 2048, 2
     M = B * T
     g = torch.Generator(device=dev).manual_seed(3)
@@ -211,13 +240,22 @@ def gemm_kernels(torch, ops, T, dev):
                          gate_stride=D)
     out = {}
     qv = qkv.view(B, T, 3 * D)
+
+    def proj(x, W, b, ep, y):
+        tile = dit_split_tile(M, W.shape[0])
+        if tile is None:
+            return (lambda: ops.linear(x, W, b, ep, out=y)), "gemm_pipe_kernel", None
+        planes = ops.split_planes(W)
+        kern = "gemm_split_kernel " + ("128x128" if tile == 0 else "128x64")
+        return ((lambda: ops.linear_split(x, planes, b, ep, out=y, tile=tile)), kern,
+                (lambda: ops.linear(x, W, b, ep, out=y)))
     cases = {
-        "gemm_qkv_rope": (lambda: ops.linear(xd, wq, bq, rope, out=qkv), 2 * M * 3 * D * D, 1),
-        "gemm_out_gated": (lambda: ops.linear(xd, wo, bd, gated, out=h), 2 * M * D * D, 1),
-        "gemm_ff0_gelu": (lambda: ops.linear(xd, w1, b1, gelu, out=ff), 2 * M * F * D, 1),
-        "gemm_ff2_gated": (lambda: ops.linear(xf, w2, bd, gated, out=h), 2 * M * D * F, 1),
-        "attention": (lambda: ops.attention(qv[..., :D], qv[..., D:2 * D], qv[..., 2 * D:], 16,
-                                            out=att),
+        "gemm_qkv_rope": (proj(xd, wq, bq, rope, qkv), 2 * M * 3 * D * D, 1),
+        "gemm_out_gated": (proj(xd, wo, bd, gated, h), 2 * M * D * D, 1),
+        "gemm_ff0_gelu": (proj(xd, w1, b1, gelu, ff), 2 * M * F * D, 1),
+        "gemm_ff2_gated": (proj(xf, w2, bd, gated, h), 2 * M * D * F, 1),
+        "attention": ((lambda: ops.attention(qv[..., :D], qv[..., D:2 * D], qv[..., 2 * D:], 16,
+                                             out=att), "attn", None),
                       4 * B * 16 * T * T * 64, 1),
     }
     # hipBLASLt (torch.mm, fp32) on the same plain-GEMM shapes, as a library reference point
@@ -227,10 +265,12 @@ def gemm_kernels(torch, ops, T, dev):
         "gemm_ff0_gelu": lambda: torch.mm(xd, w1.T),
         "gemm_ff2_gated": lambda: torch.mm(xf, w2.T),
     }
-    for name, (fn, flops, per_block) in cases.items():
+    for name, ((fn, kern, fp32_fn), flops, per_block) in cases.items():
         ms = steady_launch_ms(fn, torch)
         out[name] = {"avg_us": ms * 1e3, "flop": flops, "tflops": flops / (ms * 1e-3) / 1e12,
-                     "per_block": per_block}
+                     "per_block": per_block, "kernel": kern}
+        if fp32_fn is not None:  # the fp32 kernel on the same class, for comparison
+            out[name]["fp32_kernel_us"] = steady_launch_ms(fp32_fn, torch) * 1e3
         if name in lib_ref:
             try:
                 out[name]["hipblaslt_us"] = steady_launch_ms(lib_ref[name], torch) * 1e3
@@ -494,13 +534,14 @@ def cpu_baseline(T, seconds):
                       f"{ggml_cpu.threads()} OpenMP threads"}
 
 
-TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemm_qkv_rope_T500_traffic.md")
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemm_split_qkv_rope_T500_traffic.md")
 COPY_PROBE_BYTES = 256 << 20
 
 
 def counter_probe(torch, ops, launches=20):
     """The DiT step's three largest MFMA kernels at T=500, each `launches` times
-    on its own: the QKV projection with the rotary epilogue (M=1000, N=3072,
+    on its own: the QKV projection with the rotary epilogue on the split-operand
+    GEMM (128 x 128 tiles, as the step runs it; M=1000, N=3072,
     K=1024), FF0 with the GELU epilogue (N=2048) and the 16-head attention
     (B=2, T=500): the workload of the rocprofv3 --pmc passes whose readings
     (matrix-core busy, VALU and LDS activity) are summarised per kernel."""
@@ -521,9 +562,10 @@ def counter_probe(torch, ops, launches=20):
                         rot_dim=64, rope_section=D, rope_sections=2, rope_base=10000.0)
     gelu = ops.Epilogue(kind=ops.LX_EPI_GELU_TANH)
     q3 = qkv.view(B, T, 3 * D)
+    pq = ops.split_planes(wq)
     torch.cuda.synchronize()
     for _ in range(launches):
-        ops.linear(xd, wq, bq, rope, out=qkv)
+        ops.linear_split(xd, pq, bq, rope, out=qkv, tile=0)
     for _ in range(launches):
         ops.linear(xd, w0, b0, gelu, out=ff)
     for _ in range(launches):
@@ -554,9 +596,10 @@ def prefill_probe(torch, runs=10):
 
 
 def traffic_probe(torch, ops, launches=20):
-    """Launch the QKV projection (B*T = 1000, N = 3072, K = 1024, rotary
-    epilogue) and a plain 256 MiB device-to-device copy, each `launches` times,
-    with nothing else on the device: the workload of the two rocprofv3 --pmc
+    """Launch the QKV projection as the step runs it (split-operand GEMM, 128 x
+    128 tiles; B*T = 1000, N = 3072, K = 1024, rotary epilogue) and a plain
+    256 MiB device-to-device copy, each `launches` times, with nothing else on
+    the device: the workload of the two rocprofv3 --pmc
     runs (FETCH_SIZE, then WRITE_SIZE) whose per-dispatch readings give the
     dominant kernel's HBM traffic, scaled by the copy's reading for its known
     size."""
@@ -573,9 +616,10 @@ def traffic_probe(torch, ops, launches=20):
                         rot_dim=64, rope_section=D, rope_sections=2, rope_base=10000.0)
     src = torch.randn(COPY_PROBE_BYTES // 4, device=dev, generator=g)
     dst = torch.empty_like(src)
+    pq = ops.split_planes(wq)
     torch.cuda.synchronize()
     for _ in range(launches):
-        ops.linear(xd, wq, bq, rope, out=qkv)
+        ops.linear_split(xd, pq, bq, rope, out=qkv, tile=0)
     torch.cuda.synchronize()
     for _ in range(launches):
         dst.copy_(src)
@@ -696,12 +740,19 @@ def main():
     kernels = gemm_kernels(torch, ops, T, dev)
     # dominant kernel: largest share of a step (22 blocks, one launch each)
     dom_name, dom = max(kernels.items(), key=lambda kv: kv[1]["avg_us"] * kv[1]["per_block"])
-    roofline = {"kernel": dom_name, "bound": "mfma", "achieved": round(dom["tflops"], 3),
-                "peak": MFMA_F32_PEAK_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(dom["tflops"] / MFMA_F32_PEAK_TFLOPS, 4),
+    if dom["kernel"].startswith("gemm_split_kernel"):
+        # fp32 arithmetic as six bf16 MFMA products per element pair: priced
+        # against the dense bf16 peak with the MFMA flops executed
+        achieved, peak = SPLIT_PRODUCTS * dom["tflops"], MFMA_BF16_PEAK_TFLOPS
+    else:
+        achieved, peak = dom["tflops"], MFMA_F32_PEAK_TFLOPS
+    roofline = {"kernel": dom_name, "impl": dom["kernel"], "bound": "mfma",
+                "achieved": round(achieved, 3), "peak": peak, "unit": "TFLOP/s",
+                "frac": round(achieved / peak, 4),
                 "traffic": (committed_traffic()
                             if dom_name == "gemm_qkv_rope" and T == 500 else None),
-                "avg_us": round(dom["avg_us"], 2), "flop_per_launch": dom["flop"]}
+                "avg_us": round(dom["avg_us"], 2), "flop_per_launch": dom["flop"],
+                "fp32_equivalent_tflops": round(dom["tflops"], 3)}
     gemm_flop_step = 22 * sum(k["flop"] for k in kernels.values())
     long_t = long_utterance(torch, est, dev, g)
     flow = None if args.no_flow else flow_infer(torch, dev, g, dit_params)
@@ -737,8 +788,10 @@ def main():
         "single_step_ms": round(single_step_ms, 4),
         "step_tflops": round(gemm_flop_step / (ms_per_step * 1e-3) / 1e12, 2),
         "roofline": roofline,
-        "kernels": {k: {kk: round(vv, 2) for kk, vv in v.items() if kk in
-                        ("avg_us", "tflops", "hipblaslt_us")} for k, v in kernels.items()},
+        "kernels": {k: {kk: (round(vv, 2) if kk != "kernel" else vv)
+                        for kk, vv in v.items() if kk in
+                        ("avg_us", "tflops", "hipblaslt_us", "kernel", "fp32_kernel_us")}
+                    for k, v in kernels.items()},
         "long_utterance": long_t,
         "flow_infer": flow,
         "qwen2": qwen,

@@ -190,6 +190,24 @@ int lx_linear_f32(const float* x, int ldx, const float* W, const float* bias, fl
                   int ldy, int M, int N, int K, const lx_epilogue* epi,
                   hipStream_t stream);
 
+/* Split-operand linear, fp32 arithmetic on the bf16 matrix cores: every
+ * operand is split into three bf16 parts (w = w0 + w1 + w2, exact for normal
+ * values) and each product is formed from the six parts a_i * w_j with
+ * i + j <= 2, accumulated in fp32 (error at the fp32 level, about 1e-6 of the
+ * result's magnitude).  lx_split_planes_f32 writes the planes of an (N, K)
+ * weight once (3 * N * K bf16: plane p at p * N * K; n = N * K, a multiple of
+ * 4); lx_linear_split_f32 then computes y = epi(x @ W^T + bias) from them, as
+ * lx_linear_f32 does from W.  tile 0: 128 x 128 output tiles (N a multiple of
+ * 128), tile 1: 128 x 64 (N a multiple of 64); K a multiple of 32, ldx of 4;
+ * x, planes, y, bias and the gate 16-byte aligned.  Replaces the same
+ * linear() = ggml_mul_mat + ggml_add (src/flow/ops.cpp:20-26) as
+ * lx_linear_f32; the planes have no counterpart in the reference (its weights
+ * stay fp32), they are what the estimator keeps for its projections. */
+int lx_split_planes_f32(const float* W, void* planes, long n, hipStream_t stream);
+int lx_linear_split_f32(const float* x, int ldx, const void* planes, const float* bias,
+                        float* y, int ldy, int M, int N, int K, const lx_epilogue* epi,
+                        int tile, hipStream_t stream);
+
 /* Scaled-dot-product attention (flash-style, scores never stored; fp32
  * arithmetic, on the fp32 matrix cores or, for grids that fill the CUs in whole
  * rounds, on the bf16 ones with every operand split into three bf16 parts and

@@ -131,6 +131,10 @@ SIGNATURES = [
     ("lx_linear_f32", C.c_int,
      [fp, C.c_int, fp, fp, fp, C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(Epilogue),
       stream_t]),
+    ("lx_split_planes_f32", C.c_int, [fp, C.c_void_p, C.c_long, stream_t]),
+    ("lx_linear_split_f32", C.c_int,
+     [fp, C.c_int, C.c_void_p, fp, fp, C.c_int, C.c_int, C.c_int, C.c_int,
+      C.POINTER(Epilogue), C.c_int, stream_t]),
     ("lx_attention_f32", C.c_int,
      [fp, C.c_int, fp, C.c_int, fp, C.c_int, fp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
       C.c_int, C.c_int, C.c_float, C.c_int, C.c_int, stream_t]),

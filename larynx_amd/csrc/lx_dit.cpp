@@ -147,8 +147,11 @@ int forward_core(lx_dit* m, const float* x, long x_bstride, const float* mu, con
   // 128 x 64, step 12.55 -> 12.24 ms; T = 1000: QKV, out and FF2 on 128 x 64,
   // FF0 on 128 x 128, step 8.36 -> 7.06 ms), else the fp32 GEMM.  At
   // T = 500 (1000 rows) FF0's one round of 128 x 64 tiles is no faster than
-  // the fp32 GEMM (step 4.14 vs 4.17 ms).
+  // the fp32 GEMM (step 4.14 vs 4.17 ms).  Below kSplitGemmRows a projection
+  // whose 128 x 128 tiles make one round over at least 70% of the CUs takes
+  // them: T = 500 QKV (192 tiles), step 4.035 -> 3.987 ms.
   const bool split_ok = rows >= kSplitGemmRows && D % 128 == 0 && m->F % 128 == 0;
+  const bool split_small = rows < kSplitGemmRows && D % 128 == 0 && m->F % 128 == 0;
   auto proj = [&](const float* x, int ldx, const float* W, const void* Wp, const float* bias,
                   float* y, int ldy, int N, int K, const lx_epilogue* epi) {
     auto fills = [&](int bn) {
@@ -159,6 +162,9 @@ int forward_core(lx_dit* m, const float* x, long x_bstride, const float* mu, con
     if (split_ok && fills(128)) return linear_split(x, ldx, Wp, bias, y, ldy, rows, N, K, epi, 0, s);
     if (split_ok && fills(64))
       return linear_split(x, ldx, Wp, bias, y, ldy, rows, N, K, epi, 1, s);
+    const long tiles128 = (long)((rows + 127) / 128) * (N / 128);
+    if (split_small && tiles128 <= kCUs && tiles128 * 100 >= kCUs * 70)
+      return linear_split(x, ldx, Wp, bias, y, ldy, rows, N, K, epi, 0, s);
     return lx_linear_f32(x, ldx, W, bias, y, ldy, rows, N, K, epi, s);
   };
   for (int i = 0; i < m->depth; ++i) {

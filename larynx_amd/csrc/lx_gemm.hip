@@ -1329,6 +1329,17 @@ int linear_split_tail(const float* x, int ldx, const float* W, const float* bias
 
 }  // namespace lx
 
+extern "C" int lx_split_planes_f32(const float* W, void* planes, long n, hipStream_t stream) {
+  return split_planes(W, planes, n, stream);
+}
+
+extern "C" int lx_linear_split_f32(const float* x, int ldx, const void* planes,
+                                   const float* bias, float* y, int ldy, int M, int N, int K,
+                                   const lx_epilogue* epi, int tile, hipStream_t stream) {
+  LX_REQUIRE(tile == 0 || tile == 1, "linear_split: tile must be 0 or 1, got %d", tile);
+  return linear_split(x, ldx, planes, bias, y, ldy, M, N, K, epi, tile, stream);
+}
+
 extern "C" int lx_linear_f32(const float* x, int ldx, const float* W, const float* bias,
                              float* y, int ldy, int M, int N, int K, const lx_epilogue* epi,
                              hipStream_t stream) {

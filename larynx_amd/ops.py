@@ -158,6 +158,34 @@ def linear(x, W, b=None, epilogue=None, out=None):
     return out
 
 
+def split_planes(W):
+    """The three bf16 planes (3, N, K) of an fp32 weight W (N, K), w = w0 + w1 + w2,
+    that linear_split reads."""
+    N, K = W.shape
+    planes = torch.empty(3, N, K, device=W.device, dtype=torch.bfloat16)
+    check(lib.lx_split_planes_f32(_p(W), planes.data_ptr(), N * K, stream()))
+    return planes
+
+
+def linear_split(x, planes, b=None, epilogue=None, out=None, tile=0):
+    """epi(x @ W^T + b) with fp32 arithmetic on the bf16 matrix cores (six exact
+    bf16 partial products per element pair), W given as split_planes(W); tile 0:
+    128 x 128 output tiles, 1: 128 x 64.  src/flow/ops.cpp:20-26."""
+    M, K = x.shape
+    N = planes.shape[1]
+    kind = epilogue.kind if epilogue is not None else LX_EPI_NONE
+    if out is None:
+        if kind in (LX_EPI_GATED_RESID, LX_EPI_RESID):
+            raise ValueError("residual epilogues need out= (the residual stream)")
+        ncol = N // 2 if kind == LX_EPI_SWIGLU_PAIRED else N
+        out = torch.empty(M, ncol, device=x.device, dtype=torch.float32)
+    check(lib.lx_linear_split_f32(_p(x), x.stride(0), planes.data_ptr(), _p(b), _p(out),
+                                  out.stride(0), M, N, K,
+                                  C.byref(epilogue) if epilogue is not None else None, tile,
+                                  stream()))
+    return out
+
+
 def attention(q, k, v, n_heads, n_kv_heads=None, scale=None, causal=False, q_offset=0,
               out=None, head_dim=64):
     """softmax(scale q k^T) v per head; q (B, Tq, *), k/v (B, Tk, *) with heads packed from

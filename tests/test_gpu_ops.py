@@ -340,6 +340,71 @@ def test_linear_swiglu_and_resid_epilogues(gpu, ops, M):
     assert orc.rel_err(rd.cpu().numpy(), ref) < TOL
 
 
+@pytest.mark.parametrize("M,N,K,tile", [(1000, 3072, 1024, 0), (300, 256, 96, 1),
+                                        (37, 128, 32, 0), (1000, 1024, 2048, 1)])
+def test_linear_split_fp32_level(gpu, ops, M, N, K, tile):
+    """The split-operand GEMM (three bf16 planes per operand, six exact products,
+    fp32 accumulation) against float64 products on the host: the error is at the
+    fp32 level, as for the fp32 matrix-core kernel (bound 4e-6 of the output's
+    largest magnitude; bf16 arithmetic alone would give about 4e-3)."""
+    announce(f"linear_split M={M} N={N} K={K} tile={tile}")
+    x, W, b = rnd((M, K), 1), rnd((N, K), 2, 0.03), rnd((N,), 3)
+    Wd = dev(W, gpu)
+    planes = ops.split_planes(Wd)
+    assert planes.shape == (3, N, K)
+    # the planes sum back to W exactly
+    assert torch.equal((planes[0].float() + planes[1].float()) + planes[2].float(), Wd)
+    y = ops.linear_split(dev(x, gpu), planes, dev(b, gpu), tile=tile).cpu().numpy()
+    ref = x.astype(np.float64) @ W.astype(np.float64).T + b.astype(np.float64)
+    assert np.abs(y - ref).max() / np.abs(ref).max() < 4e-6
+    y32 = ops.linear(dev(x, gpu), Wd, dev(b, gpu)).cpu().numpy()
+    assert np.abs(y32 - ref).max() / np.abs(ref).max() < 4e-6
+
+
+@pytest.mark.parametrize("T,tile", [(500, 0), (77, 1)])
+def test_linear_split_epilogues(gpu, ops, T, tile):
+    """QKV + partial rotary (the T=500 step's QKV launch: 192 tiles of 128 x 128)
+    and the gated residual through the split-operand GEMM, against the oracle."""
+    announce(f"linear_split epilogues T={T} tile={tile}")
+    B, D = 2, 1024
+    x, W, b = rnd((B * T, D), 1), rnd((3 * D, D), 2, 0.03), rnd((3 * D,), 3)
+    pos = torch.arange(T, dtype=torch.int32, device=gpu)
+    ep = ops.Epilogue(kind=ops.LX_EPI_ROPE_PARTIAL, rows_per_batch=T, pos=pos.data_ptr(),
+                      rot_dim=64, rope_section=D, rope_sections=2, rope_base=10000.0)
+    y = ops.linear_split(dev(x, gpu), ops.split_planes(dev(W, gpu)), dev(b, gpu), ep,
+                         tile=tile).cpu().numpy()
+    ref = orc.linear(x, W, b).reshape(B, T, 3 * D)
+    p = np.arange(T, dtype=np.int32)
+    q = orc.rope_partial(np.ascontiguousarray(ref[..., :D]), p)
+    k = orc.rope_partial(np.ascontiguousarray(ref[..., D:2 * D]), p)
+    ref = np.concatenate([q, k, ref[..., 2 * D:]], -1).reshape(B * T, 3 * D)
+    assert orc.rel_err(y, ref) < TOL
+    Wo, bo = rnd((D, D), 4, 0.03), rnd((D,), 5)
+    h = rnd((B, T, D), 6)
+    emb = rnd((B, 6 * D), 7, 0.3)
+    hd, ed = dev(h, gpu), dev(emb, gpu)
+    gate = ed[:, 2 * D:]
+    epg = ops.Epilogue(kind=ops.LX_EPI_GATED_RESID, rows_per_batch=T, gate=gate.data_ptr(),
+                       gate_stride=6 * D)
+    ops.linear_split(dev(x, gpu), ops.split_planes(dev(Wo, gpu)), dev(bo, gpu), epg,
+                     out=hd.view(B * T, D), tile=tile)
+    refg = orc.gated_residual(h, orc.linear(x, Wo, bo).reshape(B, T, D), emb[:, 2 * D:3 * D])
+    assert orc.rel_err(hd.cpu().numpy(), refg) < TOL
+
+
+def test_linear_split_rejects_bad_arguments(gpu, ops):
+    from larynx_amd import LxError
+    announce("linear_split bad arguments")
+    x = torch.zeros(64, 64, device=gpu)
+    planes = ops.split_planes(torch.zeros(192, 64, device=gpu))
+    with pytest.raises(LxError):
+        ops.linear_split(x, planes, tile=0)  # N = 192 not a multiple of 128
+    with pytest.raises(LxError):
+        ops.linear_split(x, planes, tile=2)
+    with pytest.raises(LxError):
+        ops.linear_split(x[:, :48], planes[:, :, :48], tile=1)  # K = 48 not a multiple of 32
+
+
 @pytest.mark.parametrize("B,T", [(2, 500), (2, 45), (1, 1), (2, 3000), (2, 1000), (2, 1020),
                                  (1, 2000), (2, 1500)])
 def test_attention_dit(gpu, ops, B, T):
