@@ -255,7 +255,8 @@ def gemm_kernels(torch, ops, T, dev):
         "gemm_ff0_gelu": (proj(xd, w1, b1, gelu, ff), 2 * M * F * D, 1),
         "gemm_ff2_gated": (proj(xf, w2, bd, gated, h), 2 * M * D * F, 1),
         "attention": ((lambda: ops.attention(qv[..., :D], qv[..., D:2 * D], qv[..., 2 * D:], 16,
-                                             out=att), "attn", None),
+                                             out=att), "attn_bx_kernel / attn_flash_kernel",
+                       None),
                       4 * B * 16 * T * T * 64, 1),
     }
     # hipBLASLt (torch.mm, fp32) on the same plain-GEMM shapes, as a library reference point
