@@ -754,6 +754,12 @@ def main():
                             if dom_name == "gemm_qkv_rope" and T == 500 else None),
                 "avg_us": round(dom["avg_us"], 2), "flop_per_launch": dom["flop"],
                 "fp32_equivalent_tflops": round(dom["tflops"], 3)}
+    if "fp32_kernel_us" in dom:  # the fp32 matrix-core GEMM on the same class, for reference
+        f32 = dom["flop"] / (dom["fp32_kernel_us"] * 1e-6) / 1e12
+        roofline["fp32_kernel"] = {"impl": "gemm_pipe_kernel",
+                                   "avg_us": round(dom["fp32_kernel_us"], 2),
+                                   "achieved": round(f32, 3), "peak": MFMA_F32_PEAK_TFLOPS,
+                                   "frac": round(f32 / MFMA_F32_PEAK_TFLOPS, 4)}
     gemm_flop_step = 22 * sum(k["flop"] for k in kernels.values())
     long_t = long_utterance(torch, est, dev, g)
     flow = None if args.no_flow else flow_infer(torch, dev, g, dit_params)
