@@ -386,10 +386,10 @@ def copy_ceiling_gbs(torch, dev, mib=512, reps=10):
             "frac": round(gbs / HBM_PEAK_GBS, 4), "kernel": "torch copy_, device to device"}
 
 
-def long_utterance(torch, est, dev, g, steps=3):
-    """ms per CFG Euler step at T=3000 (the long-utterance config), same estimator."""
+def long_utterance(torch, est, dev, g, steps=3, T=3000):
+    """ms per CFG Euler step at T=3000 (the long-utterance config; T=1000 for the
+    medium one), same estimator."""
     from larynx_amd.flow import cfm_t_span
-    T = 3000
     x = torch.randn(80, T, device=dev, generator=g)
     mu = torch.randn(80, T, device=dev, generator=g)
     cond = torch.randn(80, T, device=dev, generator=g)
@@ -762,6 +762,7 @@ def main():
                                    "frac": round(f32 / MFMA_F32_PEAK_TFLOPS, 4)}
     gemm_flop_step = 22 * sum(k["flop"] for k in kernels.values())
     long_t = long_utterance(torch, est, dev, g)
+    long_t["T1000"] = long_utterance(torch, est, dev, g, steps=5, T=1000)
     flow = None if args.no_flow else flow_infer(torch, dev, g, dit_params)
     del dit_params, params
     fused = {} if args.no_fused else fused_ops_gbs(torch, ops, dev)
