@@ -62,6 +62,21 @@ int lx_adaln_modulate_f32(const float* x, const float* shift, const float* scale
                           long mod_stride, float* y, int B, int T, int D, float eps,
                           hipStream_t stream);
 
+/* The gated residual of a projection computed as `splits` K slices, folded into
+ * the next modulated LayerNorm (one pass over the row):
+ *   h = h + gate_b * ((partials[0] + ... + partials[splits-1]) + bias)
+ *   y = LayerNorm_eps(h) * (1 + scale_b) + shift_b        (when y != NULL)
+ * h: (B, T, D) updated in place; partials: `splits` (<= 4) slices of (B*T, D),
+ * partial_stride floats apart, summed in slice order (splits 0: h is only
+ * normalised); bias (D) or NULL; gate / shift / scale: per-batch rows as in
+ * lx_gated_residual_f32 / lx_adaln_modulate_f32.  All pointers 16-byte aligned.
+ * Replaces the gated residual x + gate * (to_out / ff output) of
+ * src/flow/dit.cpp:71,77 plus the next ada_ln (src/flow/ops.cpp:94-104). */
+int lx_adaln_resid_f32(float* h, const float* partials, int splits, long partial_stride,
+                       const float* bias, const float* gate, long gate_stride,
+                       const float* shift, const float* scale, long mod_stride, float* y,
+                       int B, int T, int D, float eps, hipStream_t stream);
+
 /* AdaLN modulation embedding (GEMV over the batch rows):
  *   emb[b, :] = W @ silu(c[b, :]) + bias,   W: (n_out, D) row-major.
  * Replaces linear(attn_norm_w, attn_norm_b, ggml_silu(t)) (src/flow/dit.cpp:56)
@@ -207,6 +222,49 @@ int lx_split_planes_f32(const float* W, void* planes, long n, hipStream_t stream
 int lx_linear_split_f32(const float* x, int ldx, const void* planes, const float* bias,
                         float* y, int ldy, int M, int N, int K, const lx_epilogue* epi,
                         int tile, hipStream_t stream);
+
+/* Split-operand linear with the weight in MFMA fragment order: the same fp32
+ * arithmetic on the bf16 matrix cores as lx_linear_split_f32 (three-part
+ * operand splits, six products, fp32 accumulation), in the layout the
+ * estimator runs its projections in.  lx_wfrag_pack_f32 writes an (N, K)
+ * weight once in fragment order (3 * N * K bf16; N a multiple of 32, K of 16).
+ * A is fp32 (M, K) with row stride lda.  Outputs:
+ *   LX_BX_OUT_F32      Y = epi(A @ W^T + bias) (row stride ldy), every
+ *                      lx_epilogue kind but SWIGLU_PAIRED;
+ *   LX_BX_OUT_PARTIAL  the raw products of `slices` equal K slices, slice s
+ *                      into Y + s * slice_stride (no bias, no epilogue): the
+ *                      consumer sums the slices in slice order.
+ * Tiles of bm (128 or 64) rows x 128 columns: N a multiple of 128, K / slices
+ * a multiple of 64; A, Wf, Y, bias and the gate 16-byte aligned.
+ * Optional stream-K scratch (OUT_F32): with ws (at least 2 * CUs * bm * 128
+ * floats, CUs = 256 on MI355X) and counters (one per output tile, zeroed once
+ * by the caller and left zeroed by every call), one workgroup per compute unit
+ * takes an equal share of the tiles' k range; a tile shared by several
+ * workgroups is summed by the last to finish, in k order (deterministic, no
+ * waiting).  Calls sharing one ws / counters pair must not overlap.
+ * Replaces linear() = ggml_mul_mat + ggml_add (src/flow/ops.cpp:20-26) with the
+ * node its epilogue absorbs; the fragment-ordered weight has no counterpart
+ * in the reference (its weights stay fp32). */
+enum { LX_BX_OUT_F32 = 0, LX_BX_OUT_PARTIAL = 1 };
+typedef struct lx_linear_bx {
+  const float* A;
+  long lda;
+  const void* Wf;
+  const float* bias;
+  const lx_epilogue* epi;
+  int out;
+  float* Y;
+  long ldy, slice_stride;
+  int M, N, K;
+  int bm;
+  int slices;
+  float* ws;
+  size_t ws_floats;
+  unsigned* counters;
+  int n_counters;
+} lx_linear_bx;
+int lx_wfrag_pack_f32(const float* W, void* Wf, int N, int K, hipStream_t stream);
+int lx_linear_bx_f32(const lx_linear_bx* g, hipStream_t stream);
 
 /* Scaled-dot-product attention (flash-style, scores never stored; fp32
  * arithmetic, on the fp32 matrix cores or, for grids that fill the CUs in whole

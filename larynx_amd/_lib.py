@@ -26,6 +26,9 @@ LX_EPI_ROPE_PARTIAL = 3
 LX_EPI_RESID = 4
 LX_EPI_SWIGLU_PAIRED = 5
 
+LX_BX_OUT_F32 = 0
+LX_BX_OUT_PARTIAL = 1
+
 fp = C.c_void_p  # device pointer
 ip = C.c_void_p
 stream_t = C.c_void_p
@@ -48,6 +51,16 @@ class Epilogue(C.Structure):
         ("rope_section", C.c_int),
         ("rope_sections", C.c_int),
         ("rope_base", C.c_float),
+    ]
+
+
+class LinearBx(C.Structure):
+    _fields_ = [
+        ("A", fp), ("lda", C.c_long), ("Wf", C.c_void_p), ("bias", fp),
+        ("epi", C.POINTER(Epilogue)), ("out", C.c_int), ("Y", fp), ("ldy", C.c_long),
+        ("slice_stride", C.c_long), ("M", C.c_int), ("N", C.c_int), ("K", C.c_int),
+        ("bm", C.c_int), ("slices", C.c_int), ("ws", fp), ("ws_floats", C.c_size_t),
+        ("counters", C.c_void_p), ("n_counters", C.c_int),
     ]
 
 
@@ -113,6 +126,9 @@ SIGNATURES = [
     ("lx_last_error", C.c_char_p, []),
     ("lx_adaln_modulate_f32", C.c_int,
      [fp, fp, fp, C.c_long, fp, C.c_int, C.c_int, C.c_int, C.c_float, stream_t]),
+    ("lx_adaln_resid_f32", C.c_int,
+     [fp, fp, C.c_int, C.c_long, fp, fp, C.c_long, fp, fp, C.c_long, fp, C.c_int, C.c_int,
+      C.c_int, C.c_float, stream_t]),
     ("lx_adaln_emb_f32", C.c_int, [fp, fp, fp, fp, C.c_int, C.c_int, C.c_int, stream_t]),
     ("lx_rope_partial_interleaved_f32", C.c_int,
      [fp, fp, ip, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, stream_t]),
@@ -135,6 +151,8 @@ SIGNATURES = [
     ("lx_linear_split_f32", C.c_int,
      [fp, C.c_int, C.c_void_p, fp, fp, C.c_int, C.c_int, C.c_int, C.c_int,
       C.POINTER(Epilogue), C.c_int, stream_t]),
+    ("lx_wfrag_pack_f32", C.c_int, [fp, C.c_void_p, C.c_int, C.c_int, stream_t]),
+    ("lx_linear_bx_f32", C.c_int, [C.POINTER(LinearBx), stream_t]),
     ("lx_attention_f32", C.c_int,
      [fp, C.c_int, fp, C.c_int, fp, C.c_int, fp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
       C.c_int, C.c_int, C.c_float, C.c_int, C.c_int, stream_t]),

@@ -33,10 +33,12 @@ constexpr int kConvG = 16;         // CONV_POS_GROUPS (src/flow/internal.h:33)
 constexpr float kLnEps = 1e-6f;    // LN_EPS (src/flow/internal.h:34)
 constexpr float kRopeBase = 10000.0f;  // ROPE_FREQ_BASE (src/flow/internal.h:35)
 constexpr int kRotDim = 64;        // ROT_DIM (src/flow/internal.h:25)
-constexpr int kProjSplitMax = 8;   // K slices of the proj_out split-K (the plan's cap)
+constexpr int kProjSplitMax = 9;   // K slices of the proj_out split-K (gemm_splitk_plan's cap)
 constexpr int kSolveChunk = 16;    // solve steps whose modulations one GEMV computes
-constexpr int kSplitGemmRows = 1536;  // B * T from which a projection may take the split GEMM
-constexpr int kCUs = 256;             // compute units of the MI355X
+// Up to this many rows (B * T) the out and FF2 projections run as two K slices
+// whose sum is folded into the next modulated LayerNorm: at B * T = 1000 their
+// 64-row tiles number 128, half the CUs.
+constexpr int kPartialRows = 1024;
 
 }  // namespace
 
@@ -51,11 +53,14 @@ struct lx_dit {
   float *in_w, *in_b;
   float *conv1_wp, *conv1_b, *conv2_wp, *conv2_b;
   float *ada_w, *ada_b;                 // (NA, D), (NA)
-  std::vector<float*> qkv_w, qkv_b;     // (3D, D), (3D)
-  // the four projections' weights as three bf16 planes each (split_planes),
-  // for the split-operand GEMM at large B * T
-  std::vector<void*> qkv_wp, out_wp, ff0_wp, ff2_wp;
-  std::vector<float*> out_w, out_b, ff0_w, ff0_b, ff2_w, ff2_b;
+  // Block projections: with `frag` the weights are kept only in MFMA
+  // fragment order (wfrag_pack: three bf16 parts, 3 * N * K bf16) for the
+  // split-operand GEMM; otherwise (a width the fragment tiles do not cover)
+  // as fp32 for lx_linear_f32.  QKV is fused into one (3D, D) matrix.
+  bool frag = false;
+  std::vector<void*> qkv_wf, out_wf, ff0_wf, ff2_wf;
+  std::vector<float*> qkv_w, out_w, ff0_w, ff2_w;
+  std::vector<float*> qkv_b, out_b, ff0_b, ff2_b;
   float *proj_w, *proj_b;
 
   // activations (sized for B x max_T)
@@ -64,6 +69,7 @@ struct lx_dit {
   float *temb_steps, *tmlp_steps, *emb_steps;
   float *A0, *xe, *c1, *h, *xn, *qkv, *att, *ff, *P;
   float* Pws;          // split-K slices of proj_out (kProjSplitMax x rows x mel)
+  float* Rws;          // K slices of the out / FF2 projections (2 x kPartialRows x D)
   int proj_splits = 1; // slices of the last forward's proj_out
   long proj_slice = 0; // floats between slices
   int* pos;
@@ -138,34 +144,72 @@ int forward_core(lx_dit* m, const float* x, long x_bstride, const float* mu, con
     (void)hipMemcpyAsync(m->cap.input_embed, m->h, sizeof(float) * rows * D,
                          hipMemcpyDeviceToDevice, s);
 
-  // A block projection takes the split-operand bf16 GEMM from kSplitGemmRows
-  // rows on when its tiles fill the CUs' rounds to at least 85%: 128 x 128
-  // tiles if those do, else 128 x 64 (T = 2000, B = 2: every projection on
-  // 128 x 128, step 15.9 -> 14.1 ms; T = 3000: QKV 276 -> 245 us and FF0 185 ->
-  // 154 us on 128 x 128, out / FF2 on 128 x 64 (128 x 128 would be 1.47
-  // rounds), step 23.94 -> 23.63 ms for the latter; T = 1500: QKV and FF0 on
-  // 128 x 64, step 12.55 -> 12.24 ms; T = 1000: QKV, out and FF2 on 128 x 64,
-  // FF0 on 128 x 128, step 8.36 -> 7.06 ms), else the fp32 GEMM.  At
-  // T = 500 (1000 rows) FF0's one round of 128 x 64 tiles is no faster than
-  // the fp32 GEMM (step 4.14 vs 4.17 ms).  Below kSplitGemmRows a projection
-  // whose 128 x 128 tiles make one round over at least 70% of the CUs takes
-  // them: T = 500 QKV (192 tiles), step 4.035 -> 3.987 ms.
-  const bool split_ok = rows >= kSplitGemmRows && D % 128 == 0 && m->F % 128 == 0;
-  const bool split_small = rows < kSplitGemmRows && D % 128 == 0 && m->F % 128 == 0;
-  auto proj = [&](const float* x, int ldx, const float* W, const void* Wp, const float* bias,
-                  float* y, int ldy, int N, int K, const lx_epilogue* epi) {
-    auto fills = [&](int bn) {
-      const long tiles = (long)((rows + 127) / 128) * (N / bn);
-      const long rounds = (tiles + kCUs - 1) / kCUs;
-      return tiles * 100 >= rounds * kCUs * 85;
-    };
-    if (split_ok && fills(128)) return linear_split(x, ldx, Wp, bias, y, ldy, rows, N, K, epi, 0, s);
-    if (split_ok && fills(64))
-      return linear_split(x, ldx, Wp, bias, y, ldy, rows, N, K, epi, 1, s);
-    const long tiles128 = (long)((rows + 127) / 128) * (N / 128);
-    if (split_small && tiles128 <= kCUs && tiles128 * 100 >= kCUs * 70)
-      return linear_split(x, ldx, Wp, bias, y, ldy, rows, N, K, epi, 0, s);
-    return lx_linear_f32(x, ldx, W, bias, y, ldy, rows, N, K, epi, s);
+  // Block projections on the split-operand GEMM with fragment-order weights
+  // (64-row tiles, two workgroups per CU).  Up to kPartialRows rows the out
+  // and FF2 projections (N = D: 128 tiles at B * T = 1000, half the CUs) run
+  // as two K slices of 64-row tiles; their sum, bias and gate go into the
+  // residual stream inside the next modulated LayerNorm (lx_adaln_resid_f32),
+  // which replaces the gated-residual epilogue.
+  struct Pending {
+    const float* bias = nullptr;
+    const float* gate = nullptr;
+  } pend;
+  bool pending = false;
+  const bool partial = m->frag && rows <= kPartialRows && D % 128 == 0 && m->F % 128 == 0;
+  auto adaln = [&](const float* shift, const float* scale, float* y) -> int {
+    if (!pending) return lx_adaln_modulate_f32(m->h, shift, scale, NA, y, B, T, D, kLnEps, s);
+    pending = false;
+    return lx_adaln_resid_f32(m->h, m->Rws, 2, (long)rows * D, pend.bias, pend.gate, NA, shift,
+                              scale, NA, y, B, T, D, kLnEps, s);
+  };
+  auto proj = [&](const float* x, int ldx, const void* Wf, const float* W, const float* bias,
+                  float* y, int ldy, int N, int K, const lx_epilogue* epi) -> int {
+    if (!m->frag) return lx_linear_f32(x, ldx, W, bias, y, ldy, rows, N, K, epi, s);
+    lx_linear_bx g{};
+    g.A = x;
+    g.lda = ldx;
+    g.Wf = Wf;
+    g.bias = bias;
+    g.epi = epi;
+    g.out = LX_BX_OUT_F32;
+    g.Y = y;
+    g.ldy = ldy;
+    g.M = rows;
+    g.N = N;
+    g.K = K;
+    g.bm = 64;
+    g.slices = 1;
+    return linear_bx(g, s);
+  };
+  // y (the residual stream h) += gate * (x W^T + bias), directly or as pending K slices
+  auto proj_gated = [&](const float* x, int ldx, const void* Wf, const float* W, const float* bias,
+                        const float* gate, int K) -> int {
+    if (!partial) {
+      lx_epilogue gated{};
+      gated.kind = LX_EPI_GATED_RESID;
+      gated.rows_per_batch = T;
+      gated.gate = gate;
+      gated.gate_stride = NA;
+      return proj(x, ldx, Wf, W, bias, m->h, D, D, K, &gated);
+    }
+    lx_linear_bx g{};
+    g.A = x;
+    g.lda = ldx;
+    g.Wf = Wf;
+    g.out = LX_BX_OUT_PARTIAL;
+    g.Y = m->Rws;
+    g.ldy = D;
+    g.slice_stride = (long)rows * D;
+    g.M = rows;
+    g.N = D;
+    g.K = K;
+    g.bm = 64;
+    g.slices = 2;
+    LX_TRY(linear_bx(g, s));
+    pend.bias = bias;
+    pend.gate = gate;
+    pending = true;
+    return LX_OK;
   };
   for (int i = 0; i < m->depth; ++i) {
     const float* e = emb + (long)i * 6 * D;  // chunk order: shift, scale, gate (msa), (mlp)
@@ -175,8 +219,16 @@ int forward_core(lx_dit* m, const float* x, long x_bstride, const float* mu, con
     const float* shift_mlp = e + 3 * D;
     const float* scale_mlp = e + 4 * D;
     const float* gate_mlp = e + 5 * D;
+    const void* wf0 = m->frag ? m->qkv_wf[i] : nullptr;
+    const void* wf1 = m->frag ? m->out_wf[i] : nullptr;
+    const void* wf2 = m->frag ? m->ff0_wf[i] : nullptr;
+    const void* wf3 = m->frag ? m->ff2_wf[i] : nullptr;
+    const float* w0 = m->frag ? nullptr : m->qkv_w[i];
+    const float* w1 = m->frag ? nullptr : m->out_w[i];
+    const float* w2 = m->frag ? nullptr : m->ff0_w[i];
+    const float* w3 = m->frag ? nullptr : m->ff2_w[i];
 
-    LX_TRY(lx_adaln_modulate_f32(m->h, shift_msa, scale_msa, NA, m->xn, B, T, D, kLnEps, s));
+    LX_TRY(adaln(shift_msa, scale_msa, m->xn));
     lx_epilogue rope{};
     rope.kind = LX_EPI_ROPE_PARTIAL;
     rope.rows_per_batch = T;
@@ -185,30 +237,30 @@ int forward_core(lx_dit* m, const float* x, long x_bstride, const float* mu, con
     rope.rope_section = D;   // q occupies columns [0, D), k [D, 2D)
     rope.rope_sections = 2;
     rope.rope_base = kRopeBase;
-    LX_TRY(proj(m->xn, D, m->qkv_w[i], m->qkv_wp[i], m->qkv_b[i], m->qkv, 3 * D, 3 * D, D, &rope));
+    LX_TRY(proj(m->xn, D, wf0, w0, m->qkv_b[i], m->qkv, 3 * D, 3 * D, D, &rope));
     LX_TRY(lx_attention_f32(m->qkv, 3 * D, m->qkv + D, 3 * D, m->qkv + 2 * D, 3 * D, m->att, D, B,
                             T, T, m->heads, m->heads, m->hd, 1.0f / std::sqrt((float)m->hd), 0, 0,
                             s));
-    lx_epilogue gated{};
-    gated.kind = LX_EPI_GATED_RESID;
-    gated.rows_per_batch = T;
-    gated.gate = gate_msa;
-    gated.gate_stride = NA;
-    LX_TRY(proj(m->att, D, m->out_w[i], m->out_wp[i], m->out_b[i], m->h, D, D, D, &gated));
+    LX_TRY(proj_gated(m->att, D, wf1, w1, m->out_b[i], gate_msa, D));
 
-    LX_TRY(lx_adaln_modulate_f32(m->h, shift_mlp, scale_mlp, NA, m->xn, B, T, D, kLnEps, s));
+    LX_TRY(adaln(shift_mlp, scale_mlp, m->xn));
     lx_epilogue gelu{};
     gelu.kind = LX_EPI_GELU_TANH;
-    LX_TRY(proj(m->xn, D, m->ff0_w[i], m->ff0_wp[i], m->ff0_b[i], m->ff, m->F, m->F, D, &gelu));
-    gated.gate = gate_mlp;
-    LX_TRY(proj(m->ff, m->F, m->ff2_w[i], m->ff2_wp[i], m->ff2_b[i], m->h, D, D, m->F, &gated));
-    if (m->cap.blocks)
+    LX_TRY(proj(m->xn, D, wf2, w2, m->ff0_b[i], m->ff, m->F, m->F, D, &gelu));
+    LX_TRY(proj_gated(m->ff, m->F, wf3, w3, m->ff2_b[i], gate_mlp, m->F));
+    if (m->cap.blocks) {
+      if (pending) {  // the block's output: fold the FF2 slices into h now
+        pending = false;
+        LX_TRY(lx_adaln_resid_f32(m->h, m->Rws, 2, (long)rows * D, pend.bias, pend.gate, NA,
+                                  emb, emb, NA, nullptr, B, T, D, kLnEps, s));
+      }
       (void)hipMemcpyAsync(m->cap.blocks + (long)i * rows * D, m->h, sizeof(float) * rows * D,
                            hipMemcpyDeviceToDevice, s);
+    }
   }
   // norm_out (AdaLayerNormZero_Final): chunk order scale, shift (src/flow/dit.cpp:134-135).
   const float* ef = emb + (long)m->depth * 6 * D;
-  LX_TRY(lx_adaln_modulate_f32(m->h, /*shift*/ ef + D, /*scale*/ ef, NA, m->xn, B, T, D, kLnEps, s));
+  LX_TRY(adaln(/*shift*/ ef + D, /*scale*/ ef, m->xn));
   if (m->cap.norm_out)
     (void)hipMemcpyAsync(m->cap.norm_out, m->xn, sizeof(float) * rows * D, hipMemcpyDeviceToDevice,
                          s);
@@ -216,6 +268,7 @@ int forward_core(lx_dit* m, const float* x, long x_bstride, const float* mu, con
   // fill the device; the slice sum + bias is fused into the consumer.
   int ks = 0;
   const int splits = gemm_splitk_plan(rows, mel, D, &ks);
+  LX_REQUIRE(splits <= kProjSplitMax, "dit_forward: proj_out plan of %d slices", splits);
   LX_TRY(gemm_splitk_partials(m->xn, D, m->proj_w, D, m->Pws, rows, mel, D, splits, ks, s));
   m->proj_splits = splits;
   m->proj_slice = (long)rows * mel;
@@ -271,24 +324,29 @@ extern "C" int lx_dit_create(const lx_dit_weights* w, int B, int max_T, lx_dit**
   m->conv2_b = A(D);
   m->ada_w = A((size_t)m->NA * D);
   m->ada_b = A(m->NA);
+  const size_t rows = (size_t)B * max_T;
+  // the fragment-order GEMM needs N % 128, K % 64 and each activation below 2 GiB
+  m->frag = D % 128 == 0 && F % 128 == 0 && rows * F * 4 < (1ull << 31);
   for (int i = 0; i < depth; ++i) {
-    m->qkv_wp.push_back(a.alloc<unsigned short>((size_t)3 * 3 * D * D));
-    m->out_wp.push_back(a.alloc<unsigned short>((size_t)3 * D * D));
-    m->ff0_wp.push_back(a.alloc<unsigned short>((size_t)3 * F * D));
-    m->ff2_wp.push_back(a.alloc<unsigned short>((size_t)3 * D * F));
-    ok = ok && m->qkv_wp.back() && m->out_wp.back() && m->ff0_wp.back() && m->ff2_wp.back();
-    m->qkv_w.push_back(A((size_t)3 * D * D));
+    if (m->frag) {
+      m->qkv_wf.push_back(a.alloc<unsigned short>((size_t)3 * 3 * D * D));
+      m->out_wf.push_back(a.alloc<unsigned short>((size_t)3 * D * D));
+      m->ff0_wf.push_back(a.alloc<unsigned short>((size_t)3 * F * D));
+      m->ff2_wf.push_back(a.alloc<unsigned short>((size_t)3 * D * F));
+      ok = ok && m->qkv_wf.back() && m->out_wf.back() && m->ff0_wf.back() && m->ff2_wf.back();
+    } else {
+      m->qkv_w.push_back(A((size_t)3 * D * D));
+      m->out_w.push_back(A((size_t)D * D));
+      m->ff0_w.push_back(A((size_t)F * D));
+      m->ff2_w.push_back(A((size_t)D * F));
+    }
     m->qkv_b.push_back(A((size_t)3 * D));
-    m->out_w.push_back(A((size_t)D * D));
     m->out_b.push_back(A(D));
-    m->ff0_w.push_back(A((size_t)F * D));
     m->ff0_b.push_back(A(F));
-    m->ff2_w.push_back(A((size_t)D * F));
     m->ff2_b.push_back(A(D));
   }
   m->proj_w = A((size_t)mel * D);
   m->proj_b = A(mel);
-  const size_t rows = (size_t)B * max_T;
   m->temb = A((size_t)B * D);
   m->tmlp_work = A((size_t)B * D);
   m->emb = A((size_t)B * m->NA);
@@ -305,6 +363,7 @@ extern "C" int lx_dit_create(const lx_dit_weights* w, int B, int max_T, lx_dit**
   m->ff = A(rows * F);
   m->P = A(rows * mel);
   m->Pws = A(rows * mel * kProjSplitMax);
+  m->Rws = m->frag ? A((size_t)2 * std::min<size_t>(rows, kPartialRows) * D) : nullptr;
   m->pos = a.alloc<int>(max_T);
   ok = ok && m->pos;
   if (!ok) {
@@ -323,6 +382,26 @@ extern "C" int lx_dit_create(const lx_dit_weights* w, int B, int max_T, lx_dit**
   auto C = [&](float* dst, const float* src, size_t n) {
     if (rc == LX_OK) rc = copy_d2d(dst, src, n, s);
   };
+  // fragment-order packing straight from the caller's (N, K) weight; a source
+  // that is not 16-byte aligned goes through an aligned staging copy first
+  float* stage = nullptr;
+  auto P = [&](const float* src, void* dst, int N, int K) {
+    if (rc != LX_OK) return;
+    if (!src) {
+      rc = LX_ERR_ARG;
+      return;
+    }
+    if ((uintptr_t)src % 16) {
+      if (!stage && hipMalloc(&stage, sizeof(float) * (size_t)std::max(D, F) * std::max(D, F)) !=
+                        hipSuccess) {
+        rc = LX_ERR_ALLOC;
+        return;
+      }
+      rc = copy_d2d(stage, src, (size_t)N * K, s);
+      src = stage;
+    }
+    if (rc == LX_OK) rc = wfrag_pack(src, dst, N, K, s);
+  };
   C(m->tm0_w, w->time_mlp_0_w, (size_t)D * kFreqDim);
   C(m->tm0_b, w->time_mlp_0_b, D);
   C(m->tm2_w, w->time_mlp_2_w, (size_t)D * D);
@@ -338,22 +417,30 @@ extern "C" int lx_dit_create(const lx_dit_weights* w, int B, int max_T, lx_dit**
     const lx_dit_block_weights& bw = w->blocks[i];
     C(m->ada_w + (size_t)i * 6 * D * D, bw.attn_norm_w, (size_t)6 * D * D);
     C(m->ada_b + (size_t)i * 6 * D, bw.attn_norm_b, (size_t)6 * D);
-    C(m->qkv_w[i], bw.to_q_w, (size_t)D * D);
-    C(m->qkv_w[i] + (size_t)D * D, bw.to_k_w, (size_t)D * D);
-    C(m->qkv_w[i] + (size_t)2 * D * D, bw.to_v_w, (size_t)D * D);
     C(m->qkv_b[i], bw.to_q_b, D);
     C(m->qkv_b[i] + D, bw.to_k_b, D);
     C(m->qkv_b[i] + 2 * D, bw.to_v_b, D);
-    C(m->out_w[i], bw.to_out_w, (size_t)D * D);
     C(m->out_b[i], bw.to_out_b, D);
-    C(m->ff0_w[i], bw.ff0_w, (size_t)F * D);
     C(m->ff0_b[i], bw.ff0_b, F);
-    C(m->ff2_w[i], bw.ff2_w, (size_t)D * F);
     C(m->ff2_b[i], bw.ff2_b, D);
-    if (rc == LX_OK) rc = split_planes(m->qkv_w[i], m->qkv_wp[i], (long)3 * D * D, s);
-    if (rc == LX_OK) rc = split_planes(m->out_w[i], m->out_wp[i], (long)D * D, s);
-    if (rc == LX_OK) rc = split_planes(m->ff0_w[i], m->ff0_wp[i], (long)F * D, s);
-    if (rc == LX_OK) rc = split_planes(m->ff2_w[i], m->ff2_wp[i], (long)D * F, s);
+    if (m->frag) {
+      // the fused QKV matrix in fragment order: q, k and v are whole 32-row
+      // blocks of it, 3 D D bf16 apart
+      unsigned short* q = static_cast<unsigned short*>(m->qkv_wf[i]);
+      P(bw.to_q_w, q, D, D);
+      P(bw.to_k_w, q + (size_t)3 * D * D, D, D);
+      P(bw.to_v_w, q + (size_t)6 * D * D, D, D);
+      P(bw.to_out_w, m->out_wf[i], D, D);
+      P(bw.ff0_w, m->ff0_wf[i], F, D);
+      P(bw.ff2_w, m->ff2_wf[i], D, F);
+    } else {
+      C(m->qkv_w[i], bw.to_q_w, (size_t)D * D);
+      C(m->qkv_w[i] + (size_t)D * D, bw.to_k_w, (size_t)D * D);
+      C(m->qkv_w[i] + (size_t)2 * D * D, bw.to_v_w, (size_t)D * D);
+      C(m->out_w[i], bw.to_out_w, (size_t)D * D);
+      C(m->ff0_w[i], bw.ff0_w, (size_t)F * D);
+      C(m->ff2_w[i], bw.ff2_w, (size_t)D * F);
+    }
   }
   C(m->ada_w + (size_t)depth * 6 * D * D, w->norm_out_w, (size_t)2 * D * D);
   C(m->ada_b + (size_t)depth * 6 * D, w->norm_out_b, (size_t)2 * D);
@@ -365,6 +452,7 @@ extern "C" int lx_dit_create(const lx_dit_weights* w, int B, int max_T, lx_dit**
     rc = LX_ERR_LAUNCH;
   }
   (void)hipStreamDestroy(s);
+  if (stage) (void)hipFree(stage);
   if (rc != LX_OK) {
     if (rc == LX_ERR_ARG) set_error("dit_create: missing weight tensor");
     delete m;

@@ -20,24 +20,12 @@
 #include <cstring>
 
 #include "lx_common.hpp"
+#include "lx_gemm_common.hpp"
 #include "lx_internal.hpp"
 
 namespace lx {
 namespace {
 
-struct EpiArgs {
-  int kind;
-  int vec;  // y, bias, gate rows 16-byte aligned: float4 epilogue path
-  int rows_per_batch;
-  const float* gate;
-  long gate_stride;
-  const int* pos;
-  int rot_dim, section, sections;
-  float inv_freq[64];
-};
-
-typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
-typedef unsigned uintx2_t __attribute__((ext_vector_type(2)));
 
 // Split tail: when a launch's tiles leave a partial last round over the CUs,
 // the first n_full tiles run whole and each of the remaining tiles runs as
@@ -55,14 +43,6 @@ struct TailArgs {
   unsigned* arrivals = nullptr;
 };
 
-__device__ __forceinline__ void rotate_pair(float& x0, float& x1, float ang) {
-  float s, c;
-  sincosf(ang, &s, &c);
-  float a = x0 * c - x1 * s;
-  float b = x1 * c + x0 * s;
-  x0 = a;
-  x1 = b;
-}
 
 // Shared epilogue of the tiled kernels: 4 consecutive columns n..n+3 of row m.
 template <int EPI>
@@ -115,40 +95,6 @@ __device__ __forceinline__ void epilogue4(float* Y, int ldy, int m, int n, int N
   }
 }
 
-// float4 epilogue of 4 columns n..n+3 (all < N) of row m with its operands
-// already loaded: b = bias[n..n+3], g = gate row segment, yo = the residual.
-// Same per-component operations as epilogue4.
-template <int EPI>
-__device__ __forceinline__ void epilogue4v(float* Y, int ldy, int m, int n, float4 v, float4 b,
-                                           float4 g, float4 yo, int posm, const EpiArgs& ep) {
-  float vv[4] = {v.x + b.x, v.y + b.y, v.z + b.z, v.w + b.w};
-  if (EPI == LX_EPI_SWIGLU_PAIRED) {
-    float2 o;
-    o.x = (vv[0] / (1.0f + expf(-vv[0]))) * vv[1];
-    o.y = (vv[2] / (1.0f + expf(-vv[2]))) * vv[3];
-    *reinterpret_cast<float2*>(Y + (long)m * ldy + (n >> 1)) = o;
-    return;
-  }
-  if (EPI == LX_EPI_GELU_TANH) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) vv[e] = gelu_tanh(vv[e]);
-  }
-  if (EPI == LX_EPI_ROPE_PARTIAL) {
-    const int cs = n % ep.section;
-    if (n < ep.sections * ep.section && cs < ep.rot_dim) {
-      const float p = (float)posm;
-      const int i0 = cs >> 1;
-      rotate_pair(vv[0], vv[1], p * ep.inv_freq[i0]);
-      rotate_pair(vv[2], vv[3], p * ep.inv_freq[i0 + 1]);
-    }
-  }
-  float4 o = make_float4(vv[0], vv[1], vv[2], vv[3]);
-  if (EPI == LX_EPI_GATED_RESID)
-    o = make_float4(yo.x + vv[0] * g.x, yo.y + vv[1] * g.y, yo.z + vv[2] * g.z, yo.w + vv[3] * g.w);
-  else if (EPI == LX_EPI_RESID)
-    o = make_float4(yo.x + vv[0], yo.y + vv[1], yo.z + vv[2], yo.w + vv[3]);
-  *reinterpret_cast<float4*>(Y + (long)m * ldy + n) = o;
-}
 
 // Pipelined NT GEMM for 64 x 64 output tiles, 4 waves (2 x 2) per k-group
 // (KS k-groups split the K slabs of one tile between them and are reduced
@@ -732,6 +678,8 @@ __global__ __launch_bounds__(256) void gemv_epi_kernel(const float* __restrict__
   }
 }
 
+}  // namespace
+
 // float4 epilogue: output rows, bias and gate rows 16-byte aligned (the
 // paired SwiGLU output stores float2: 8-byte alignment suffices for it, and
 // 16 bytes is asked anyway).
@@ -785,6 +733,8 @@ int make_epi(const lx_epilogue* e, int N, EpiArgs* out) {
   return LX_OK;
 }
 
+namespace {
+
 
 // ---- fp32 GEMM on the bf16 matrix cores (split operands), for large M ----
 //
@@ -800,36 +750,6 @@ int make_epi(const lx_epilogue* e, int N, EpiArgs* out) {
 // in flight.  The epilogue stages the tile in LDS
 // and runs the fp32 kernel's float4 epilogue.  N must be a multiple of 128, K
 // of 32, all epilogue pointers 16-byte aligned.
-typedef __bf16 sbf16x8 __attribute__((ext_vector_type(8)));
-
-__device__ __forceinline__ floatx16 mfma_split6x(const sbf16x8* a, const sbf16x8* b, floatx16 acc) {
-  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[2], b[0], acc, 0, 0, 0);
-  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], b[1], acc, 0, 0, 0);
-  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[2], acc, 0, 0, 0);
-  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], b[0], acc, 0, 0, 0);
-  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[1], acc, 0, 0, 0);
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[0], acc, 0, 0, 0);
-}
-
-__device__ __forceinline__ floatx4 bf16x4_back(bf16x4_t h) {
-  const uintx2_t u = __builtin_bit_cast(uintx2_t, h);
-  floatx4 f;
-  f[0] = __uint_as_float(u[0] << 16);
-  f[1] = __uint_as_float(u[0] & 0xffff0000u);
-  f[2] = __uint_as_float(u[1] << 16);
-  f[3] = __uint_as_float(u[1] & 0xffff0000u);
-  return f;
-}
-
-constexpr int kSplitBK = 32;
-// LDS rows of 32 bf16 (64 bytes, unpadded) whose four 16-byte chunks are
-// XOR-swizzled by (row / 8) % 4: the staging stores (four rows per 256-byte
-// pass) and the fragment reads (32 rows, one chunk each) both hit distinct
-// banks.
-constexpr int kSplitRS = kSplitBK;  // bf16 per LDS row
-__device__ __forceinline__ int split_col(int row, int c) {
-  return ((((c >> 3) ^ (row >> 3)) & 3) << 3) | (c & 7);
-}
 
 // WM x WN waves, each (32 BI) x 32 outputs: workgroup tile (32 BI WM) x (32 WN).
 template <int WM, int WN, int BI>

@@ -1,0 +1,619 @@
+// Split-operand GEMM with the weights in MFMA fragment order.
+//
+// y = epi(x @ W^T + bias) as fp32 arithmetic on the bf16 matrix cores: every
+// operand is three bf16 parts (x = x0 + x1 + x2, x0 = bf16(x), x1 = bf16(x -
+// x0), x2 = bf16(x - x0 - x1)), each element pair is the six products a_i b_j
+// with i + j <= 2 on v_mfma_f32_32x32x16_bf16, accumulated in fp32 (the same
+// arithmetic as gemm_split_kernel).  The layout halves the per-CU LDS traffic
+// of a tile:
+//   - 4 waves per workgroup split the tile's 128 columns: wave w owns columns
+//     n0 + 32 w .. n0 + 32 w + 31 for all BM rows (BM / 32 accumulators of
+//     32 x 32).
+//   - The A tile (BM rows x 32 k per slab) is split into its three bf16 planes
+//     as it is staged, once, in LDS, and read by all four waves.  LDS rows are
+//     64 bytes with the four 16-byte chunks XOR-swizzled by (row / 8) % 4
+//     (conflict-free staging stores and fragment reads), four slab buffers.
+//   - W is re-packed once (wfrag_pack) into fragment order: for each 32-row
+//     block of W, 16-wide k step and plane, the 64 lanes' 16-byte B fragments
+//     are one contiguous 1 KB.  Each wave streams its own columns' fragments
+//     straight into registers three slabs ahead with coalesced loads; W never
+//     passes through LDS.
+//   - One barrier per slab, between its two k steps; the fragment reads,
+//     staging stores and global loads are interleaved one per MFMA.
+// Outputs: the fp32 epilogues of lx_linear_f32 (through an LDS tile, float4
+// stores), or raw fp32 partial tiles of K slices (the consumer sums the slices
+// in order).  With stream-K scratch, one workgroup per CU takes an equal share
+// of the (tile, slab pair) work, so launches whose tiles do not fill the CUs
+// in whole rounds still use all of them.
+#include <algorithm>
+
+#include "lx_common.hpp"
+#include "lx_gemm_common.hpp"
+#include "lx_internal.hpp"
+
+namespace lx {
+namespace {
+
+constexpr int kBxWaves = 4;
+constexpr int kBxThreads = 64 * kBxWaves;
+constexpr int kBxBN = 32 * kBxWaves;  // columns per workgroup
+constexpr int kBxBK = 32;             // k per slab: two 16-wide MFMA k steps
+constexpr int kBxBufs = 4;            // A slab buffers
+
+template <int BMB>
+struct BxCfg {
+  static constexpr int BM = 32 * BMB;
+  static constexpr int ABUF = 3 * BM * kBxBK;  // bf16 per A slab buffer (three planes)
+  static constexpr size_t lds_k = (size_t)kBxBufs * ABUF * 2;
+  static constexpr size_t lds_c = (size_t)BM * (kBxBN + 4) * 4;
+  static constexpr size_t lds = lds_k > lds_c ? lds_k : lds_c;
+};
+
+struct BxArgs {
+  const float* A;  // (M, lda)
+  long lda;
+  const __bf16* Wf;  // W (N, K) in fragment order (wfrag_pack)
+  const float* bias;
+  float* Y;  // fp32 output rows (ldy), or partial slices slice_stride floats apart
+  long ldy;
+  long slice_stride;
+  int M, N, K, kslice, tiles_m, tiles_n, slices;
+  int streamk;          // 1: stream-K over `grid` workgroups (ws and counters set)
+  int grid;
+  float* ws;            // stream-K partial tiles: 2 per workgroup, BM * 128 floats each
+  int ws_bytes;
+  unsigned* counters;   // stream-K arrival counts, one per tile, zero between launches
+};
+
+enum { BX_OUT_F32 = LX_BX_OUT_F32, BX_OUT_PARTIAL = LX_BX_OUT_PARTIAL };
+
+// Fragments are held as 32-bit vectors and reinterpreted as bf16 only at the
+// MFMA (loop-carried bf16 vectors are otherwise rebuilt element by element).
+typedef unsigned uintx4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ sbf16x8 as_bf16x8(uintx4_t v) { return __builtin_bit_cast(sbf16x8, v); }
+
+// Three bf16 parts of four fp32 values.
+__device__ __forceinline__ void split3(floatx4 v, bf16x4_t& x0, bf16x4_t& x1, bf16x4_t& x2) {
+  x0 = __builtin_convertvector(v, bf16x4_t);
+  const floatx4 r = v - bf16x4_back(x0);
+  x1 = __builtin_convertvector(r, bf16x4_t);
+  x2 = __builtin_convertvector(r - bf16x4_back(x1), bf16x4_t);
+}
+
+// Stream-K partial tiles: a launch of G workgroups over `tiles` output tiles
+// of npt slab pairs each gives workgroup w the units [w U / G, (w + 1) U / G)
+// of the U = tiles * npt (tile, pair) units.  A tile that several workgroups
+// share is finished by the last one to arrive: each publishes its partial
+// tile (slot 2 w for its first segment, 2 w + 1 for its last) and counts its
+// arrival; the last sums the contributors' partials in k order (workgroup
+// order), adds the epilogue, and clears the count for the next launch.  No
+// workgroup waits for another.
+__device__ __forceinline__ int bx_owner(long p, long U, int G) {
+  return (int)(((p + 1) * G - 1) / U);
+}
+
+// 128-row tiles run one wave per SIMD: the register budget holds two k steps
+// of A fragments and four slabs of W fragments, so the scheduler must not
+// trade them away for a second wave.  64-row tiles fit two waves per SIMD (two
+// workgroups per CU), which cover each other's waits.
+#ifndef LX_BX_WAVES64
+#define LX_BX_WAVES64 2
+#endif
+template <int EPI, int BMB, int OUT>
+__global__ __launch_bounds__(kBxThreads) __attribute__((amdgpu_waves_per_eu(
+    BMB == 2 ? LX_BX_WAVES64 : 1, BMB == 2 ? LX_BX_WAVES64 : 1))) void
+gemm_bx_kernel(BxArgs a, EpiArgs ep) {
+  using Cfg = BxCfg<BMB>;
+  constexpr int BM = Cfg::BM, ABUF = Cfg::ABUF;
+  constexpr int LA = 8 * BM / kBxThreads;  // A float4 per thread per slab
+  static_assert(LA * kBxThreads == 8 * BM, "staging slots");
+  constexpr int SLOTS = BM * kBxBN / 4 / kBxThreads;  // epilogue float4 slots per thread
+  extern __shared__ __attribute__((aligned(16))) __bf16 sm[];
+  __shared__ int s_last;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int fr = lane & 31, fh = lane >> 5;
+  const int tiles = a.tiles_m * a.tiles_n * a.slices;
+  const int npt = a.kslice / (2 * kBxBK);  // slab pairs per tile
+  const int G = gridDim.x;
+  int w = blockIdx.x;
+  {
+    // the dispatcher deals workgroups round-robin over the 8 XCDs: give each
+    // XCD a contiguous run of work (tiles ordered (slice, N tile, M tile)) so
+    // that its L2 holds a few W column blocks and the A rows they meet
+    const int full = G / 8 * 8;
+    if (w < full) w = (w % 8) * (full / 8) + w / 8;
+  }
+  const long U = (long)tiles * npt;
+  const long u0 = a.streamk ? (long)w * U / G : (long)w * npt;
+  const long u1 = a.streamk ? (long)(w + 1) * U / G : u0 + npt;
+  constexpr int SLAB_BYTES = kBxBK * 4;  // A bytes per row per slab
+  // A fragments: row block i, plane p, k step st of a slab buffer
+  const int aoff = fr * kBxBK;
+  const int fc0 = split_col(fr, fh * 8), fc1 = split_col(fr, 16 + fh * 8);
+  // The six products (A part, W part) in the order of mfma_split6x: the small
+  // terms first.
+  constexpr int kPa[6] = {2, 1, 0, 1, 0, 0}, kPw[6] = {0, 1, 2, 0, 1, 0};
+  const __amdgpu_buffer_rsrc_t prs =
+      __builtin_amdgcn_make_buffer_rsrc(a.ws, (short)0, a.ws_bytes, 0x00020000);
+  constexpr int kSc1 = 16;  // cache-policy bits: sc1 = device scope
+  floatx16 acc[BMB];
+  bool first_seg = true;
+  for (long u = u0; u < u1;) {
+    const int t = (int)(u / npt);
+    const int q0 = (int)(u - (long)t * npt);
+    const long uend = min(u1, (long)(t + 1) * npt);
+    const int q1 = (int)(uend - (long)t * npt);
+    u = uend;
+    const int slot = first_seg ? 2 * w : 2 * w + 1;
+    if (!first_seg) __syncthreads();  // the last segment's epilogue is done with the LDS
+    first_seg = false;
+    const int mt = t % a.tiles_m;
+    const int rest = t / a.tiles_m;
+    const int nt = rest % a.tiles_n;
+    const int slice = rest / a.tiles_n;
+    const int m0 = mt * BM, n0 = nt * kBxBN;
+    const int kb = slice * a.kslice + q0 * 2 * kBxBK;
+    const int nk = (q1 - q0) * 2;
+
+    // A staging sources and LDS destinations (bf16 units)
+    // (rows past M repeat the last row; they only reach unstored outputs).
+    // Byte offsets from a workgroup-uniform base: A stays below 2 GiB.
+    const char* abase = reinterpret_cast<const char*>(a.A + kb);
+    int pa[LA], sa[LA];
+#pragma unroll
+    for (int i = 0; i < LA; ++i) {
+      const int idx = tid + kBxThreads * i;
+      const int row = idx / 8, c = (idx % 8) * 4;
+      pa[i] = (min(m0 + row, a.M - 1) * (int)a.lda + c) * 4;
+      sa[i] = row * kBxBK + split_col(row, c);
+    }
+    auto load_a = [&](floatx4* g, int s) {
+#pragma unroll
+      for (int i = 0; i < LA; ++i)
+        g[i] = *reinterpret_cast<const floatx4*>(abase + pa[i] + s * SLAB_BYTES);
+    };
+    auto store_a = [&](const floatx4* g, int buf) {
+      __bf16* base = sm + buf * ABUF;
+#pragma unroll
+      for (int i = 0; i < LA; ++i) {
+        bf16x4_t x0, x1, x2;
+        split3(g[i], x0, x1, x2);
+        *reinterpret_cast<bf16x4_t*>(base + sa[i]) = x0;
+        *reinterpret_cast<bf16x4_t*>(base + BM * kBxBK + sa[i]) = x1;
+        *reinterpret_cast<bf16x4_t*>(base + 2 * BM * kBxBK + sa[i]) = x2;
+      }
+    };
+    // W fragments of this wave's 32 columns: k step ks, plane p at wf + (ks * 3 + p) * 512;
+    // the three planes of k step st of slab s
+    const int nks = a.K / 16;
+    const char* wf = reinterpret_cast<const char*>(
+        a.Wf + ((long)(n0 / 32 + wave) * nks + kb / 16) * 3 * 512);  // wave-uniform
+    const int wl = lane * 16;
+    auto load_w = [&](uintx4_t* wv, int s, int st) {
+#pragma unroll
+      for (int j = 0; j < 3; ++j)
+        wv[j] = *reinterpret_cast<const uintx4_t*>(wf + wl + (s * 6 + st * 3 + j) * 1024);
+    };
+    auto read_a = [&](uintx4_t (*f)[3], int buf, int st) {
+      const __bf16* base = sm + buf * ABUF + aoff + (st ? fc1 : fc0);
+#pragma unroll
+      for (int i = 0; i < BMB; ++i)
+#pragma unroll
+        for (int p = 0; p < 3; ++p)
+          f[i][p] = *reinterpret_cast<const uintx4_t*>(base + p * BM * kBxBK + i * 32 * kBxBK);
+    };
+#pragma unroll
+    for (int i = 0; i < BMB; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][e] = 0.0f;
+    auto mul = [&](uintx4_t (*f)[3], const uintx4_t* wv) {
+#pragma unroll
+      for (int q = 0; q < 6; ++q)
+#pragma unroll
+        for (int i = 0; i < BMB; ++i)
+          acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(f[i][kPa[q]]),
+                                                           as_bf16x8(wv[kPw[q]]), acc[i], 0, 0, 0);
+    };
+    // Registers: A fragments of the two k steps (fa0, fa1); the W fragments of
+    // four slabs (slab s in set s % 4: k step 0's three planes, then k step
+    // 1's); two A staging sets (gy for even slabs, gx for odd ones).  LDS: four
+    // slab buffers (slab s in buffer s % 4).  Prefetch distances: W three
+    // slabs, A two slabs from load to LDS store and three from store to use,
+    // so a load has about two slabs of MFMAs (2-3 us) to arrive.
+    uintx4_t fa0[BMB][3], fa1[BMB][3];
+    uintx4_t wv0[6], wv1[6], wv2[6], wv3[6];
+    floatx4 gx[LA], gy[LA];
+    auto load_ws = [&](uintx4_t* wv, int s) {
+      load_w(wv, s, 0);
+      load_w(wv + 3, s, 1);
+    };
+    // Every prefetch is unconditional (indices clamped to the last slab; the
+    // surplus slabs go to buffers nobody reads), so each body issues its
+    // global loads in one fixed order: at the top of slab s the loads in
+    // flight are A(s + 3), W(s + 1), A(s + 4), W(s + 2), oldest first.  The
+    // prologue ends in that same order, so the waits the compiler derives
+    // (from the merge of both paths into the loop) never stall on a recent
+    // load; it issues slabs 0-2 together (one memory latency).
+    const int last = nk - 1;
+    {
+      floatx4 gz[LA];
+      load_a(gx, 0);
+      load_a(gy, min(1, last));
+      load_a(gz, min(2, last));
+      load_ws(wv0, 0);
+      store_a(gx, 0);
+      store_a(gy, 1);
+      store_a(gz, 2);
+      load_a(gy, min(3, last));
+      load_ws(wv1, min(1, last));
+      load_a(gx, min(4, last));
+      load_ws(wv2, min(2, last));
+    }
+    __syncthreads();
+    read_a(fa0, 0, 0);
+    // Slab s.  k step 0: its MFMAs, beside them the fragment reads of k step
+    // 1, the staging of slab s + 3 (into slab s - 1's buffer) and the loads of
+    // slab s + 5 (into the staging set just stored).  Then the barrier (k step
+    // 1's fragments and slab s + 3 are in LDS; every wave is past its reads of
+    // slab s - 1's buffer).  k step 1: its MFMAs, beside them the next slab's
+    // k step 0 fragment reads and the W of slab s + 3 (into slab s - 1's
+    // register set).  The group barriers interleave one memory instruction per
+    // MFMA so that the matrix pipe keeps issuing while they go out.
+    constexpr int NM = 6 * BMB;            // MFMAs per k step
+    constexpr int NR = 3 * BMB;            // fragment reads per k step
+    constexpr int NW = 3 * LA;             // staging LDS stores
+    auto body = [&](int s, int b, uintx4_t* wc, uintx4_t* wn, floatx4* g) {
+      read_a(fa1, b, 1);
+      store_a(g, (b + 3) & 3);
+      load_a(g, min(s + 5, last));
+      mul(fa0, wc);
+#pragma unroll
+      for (int i = 0; i < NR; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+      }
+#pragma unroll
+      for (int i = 0; i < NW; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // DS write
+      }
+#pragma unroll
+      for (int i = 0; i < LA; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read (A)
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, NM, 0);
+      __builtin_amdgcn_sched_barrier(0);  // k step 1's MFMAs stay below the barrier
+      __syncthreads();
+      __builtin_amdgcn_sched_barrier(0);
+      read_a(fa0, (b + 1) & 3, 0);
+      load_ws(wn, min(s + 3, last));
+      mul(fa1, wc + 3);
+#pragma unroll
+      for (int i = 0; i < NR; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
+      }
+#pragma unroll
+      for (int i = 0; i < 6; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 1);  // VMEM read (W)
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, NM, 1);
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    int s = 0;
+    for (; s + 4 <= nk; s += 4) {
+      body(s, 0, wv0, wv3, gy);
+      body(s + 1, 1, wv1, wv0, gx);
+      body(s + 2, 2, wv2, wv1, gy);
+      body(s + 3, 3, wv3, wv2, gx);
+    }
+    if (s < nk) {  // nk % 4 == 2
+      body(s, 0, wv0, wv3, gy);
+      body(s + 1, 1, wv1, wv0, gx);
+    }
+    __syncthreads();
+
+    // Accumulator element e of lane l in row block i is row 32 i + (e / 4) * 8
+    // + (l / 32) * 4 + e % 4, column 32 wave + l % 32.
+    if (OUT == BX_OUT_PARTIAL) {
+      float* P = a.Y + slice * a.slice_stride + n0 + 32 * wave + fr;
+#pragma unroll
+      for (int i = 0; i < BMB; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int m = m0 + 32 * i + (e >> 2) * 8 + fh * 4 + (e & 3);
+          if (m < a.M) P[(long)m * a.ldy] = acc[i][e];
+        }
+      continue;
+    }
+    if (q0 != 0 || q1 != npt) {
+      // Shared tile: publish this segment's partial products (fragment order,
+      // 1 KB per store instruction, device-scope stores: the contributors run
+      // on different XCDs) and count the arrival.
+      const int pbase = slot * (BM * kBxBN) * 4 + ((wave * BMB) * 4 * 64 + lane) * 16;
+#pragma unroll
+      for (int i = 0; i < BMB; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const floatx4 v = {acc[i][4 * q], acc[i][4 * q + 1], acc[i][4 * q + 2],
+                             acc[i][4 * q + 3]};
+          __builtin_amdgcn_raw_buffer_store_b128(v, prs, pbase + (i * 4 + q) * 64 * 16, 0, kSc1);
+        }
+      __builtin_amdgcn_s_waitcnt(0);  // the stores are performed before the count
+      const long tu0 = (long)t * npt;
+      const int cf = bx_owner(tu0, U, G), cl = bx_owner(tu0 + npt - 1, U, G);
+      __syncthreads();
+      if (tid == 0)
+        s_last = __hip_atomic_fetch_add(a.counters + t, 1u, __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(cl - cf);
+      __syncthreads();
+      if (!s_last) continue;
+      // Last to arrive: the contributors' partials in workgroup (= k) order,
+      // two contributors' loads in flight at a time.
+      floatx16 tot[BMB];
+      auto part = [&](floatx16* pv, int c) {
+        if (c == w) {
+#pragma unroll
+          for (int i = 0; i < BMB; ++i) pv[i] = acc[i];
+          return;
+        }
+        // c's first segment starts inside this tile, else this tile is its last
+        const int cs = (long)c * U / G >= tu0 ? 2 * c : 2 * c + 1;
+        const int cb = cs * (BM * kBxBN) * 4 + ((wave * BMB) * 4 * 64 + lane) * 16;
+#pragma unroll
+        for (int i = 0; i < BMB; ++i)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const floatx4 v =
+                __builtin_amdgcn_raw_buffer_load_b128(prs, cb + (i * 4 + q) * 64 * 16, 0, kSc1);
+            pv[i][4 * q] = v[0];
+            pv[i][4 * q + 1] = v[1];
+            pv[i][4 * q + 2] = v[2];
+            pv[i][4 * q + 3] = v[3];
+          }
+      };
+      for (int c = cf; c <= cl; c += 2) {
+        floatx16 p0[BMB], p1[BMB];
+        part(p0, c);
+        if (c + 1 <= cl) part(p1, c + 1);
+#pragma unroll
+        for (int i = 0; i < BMB; ++i) {
+          tot[i] = c == cf ? p0[i] : tot[i] + p0[i];
+          if (c + 1 <= cl) tot[i] += p1[i];
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < BMB; ++i) acc[i] = tot[i];
+      if (tid == 0)
+        __hip_atomic_store(a.counters + t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+
+    // Epilogue: its per-row global operands (residual, gate, position) are
+    // loaded first, then the tile goes through LDS into row-contiguous float4
+    // slots.  The bias (one 512-byte row per tile) is read where it is used.
+    // (64-row tiles, two waves per SIMD, load them in the slot loop instead:
+    // the prefetch would not fit their register budget.)
+    const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    constexpr bool PRE = BMB == 4;
+    float4 eg[SLOTS], ey[SLOTS];
+    int epos[SLOTS];
+#pragma unroll
+    for (int j = 0; j < SLOTS; ++j) {
+      if (!PRE) break;
+      const int idx = tid + j * kBxThreads;
+      const int row = idx / (kBxBN / 4), c = (idx % (kBxBN / 4)) * 4;
+      const int m = min(m0 + row, a.M - 1), n = n0 + c;
+      eg[j] = ey[j] = z4;
+      epos[j] = 0;
+      if (OUT == BX_OUT_F32) {
+        if (EPI == LX_EPI_GATED_RESID)
+          eg[j] = *reinterpret_cast<const float4*>(ep.gate + (long)(m / ep.rows_per_batch) *
+                                                                 ep.gate_stride + n);
+        if (EPI == LX_EPI_GATED_RESID || EPI == LX_EPI_RESID)
+          ey[j] = *reinterpret_cast<const float4*>(a.Y + (long)m * a.ldy + n);
+        if (EPI == LX_EPI_ROPE_PARTIAL) epos[j] = ep.pos[m % ep.rows_per_batch];
+      }
+    }
+    constexpr int LDC = kBxBN + 4;
+    float* Cs = reinterpret_cast<float*>(sm);
+#pragma unroll
+    for (int i = 0; i < BMB; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int row = 32 * i + (e >> 2) * 8 + fh * 4 + (e & 3);
+        Cs[row * LDC + 32 * wave + fr] = acc[i][e];
+      }
+    __syncthreads();
+    // The slot addresses are formed here from an opaque copy of the thread
+    // id: hoisted to the kernel's entry they would stay live through the main
+    // loop, past the register budget of the 64-row tiles.
+    int etid = tid;
+    asm volatile("" : "+v"(etid));
+#pragma unroll
+    for (int j = 0; j < SLOTS; ++j) {
+      const int idx = etid + j * kBxThreads;
+      const int row = idx / (kBxBN / 4), c = (idx % (kBxBN / 4)) * 4;
+      const int m = m0 + row, n = n0 + c;
+      if (m >= a.M) continue;
+      const float4 v = *reinterpret_cast<const float4*>(Cs + row * LDC + c);
+      const float4 eb = a.bias ? *reinterpret_cast<const float4*>(a.bias + n) : z4;
+      if (!PRE) {
+        eg[j] = ey[j] = z4;
+        epos[j] = 0;
+        if (EPI == LX_EPI_GATED_RESID)
+          eg[j] = *reinterpret_cast<const float4*>(ep.gate + (long)(m / ep.rows_per_batch) *
+                                                                 ep.gate_stride + n);
+        if (EPI == LX_EPI_GATED_RESID || EPI == LX_EPI_RESID)
+          ey[j] = *reinterpret_cast<const float4*>(a.Y + (long)m * a.ldy + n);
+        if (EPI == LX_EPI_ROPE_PARTIAL) epos[j] = ep.pos[m % ep.rows_per_batch];
+      }
+      epilogue4v<EPI>(a.Y, (int)a.ldy, m, n, v, eb, eg[j], ey[j], epos[j], ep);
+    }
+  }
+}
+
+// W (N, K) fp32 -> fragment order: Wf[((nb * nks + ks) * 3 + p) * 512 + l * 8 + j]
+// = part p of W[nb * 32 + l % 32][ks * 16 + (l / 32) * 8 + j] (nks = K / 16),
+// the B operand of v_mfma_f32_32x32x16_bf16 for lane l.  The parts are the
+// rounding of split_planes.
+__global__ void wfrag_pack_kernel(const float* __restrict__ W, __bf16* __restrict__ Wf, int N,
+                                  int K) {
+  const int nks = K / 16;
+  const long total = (long)(N / 32) * nks * 64;
+  const long t = blockIdx.x * 256L + threadIdx.x;
+  if (t >= total) return;
+  const int l = (int)(t % 64);
+  const long r = t / 64;
+  const int ks = (int)(r % nks);
+  const long nb = r / nks;
+  const float* src = W + (nb * 32 + l % 32) * (long)K + ks * 16 + (l / 32) * 8;
+  __bf16* dst = Wf + (nb * nks + ks) * 3 * 512 + l * 8;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const floatx4 v = *reinterpret_cast<const floatx4*>(src + 4 * h);
+    bf16x4_t x0, x1, x2;
+    split3(v, x0, x1, x2);
+    *reinterpret_cast<bf16x4_t*>(dst + 4 * h) = x0;
+    *reinterpret_cast<bf16x4_t*>(dst + 512 + 4 * h) = x1;
+    *reinterpret_cast<bf16x4_t*>(dst + 1024 + 4 * h) = x2;
+  }
+}
+
+// Compute units of the current device (cached per device).
+int device_cus() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cus[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
+template <int EPI, int BMB, int OUT>
+int launch_bx(const BxArgs& a, const EpiArgs& ep, hipStream_t stream) {
+  auto kern = gemm_bx_kernel<EPI, BMB, OUT>;
+  static LdsLimit once;
+  const size_t lds = BxCfg<BMB>::lds;
+  int rc = raise_lds_limit((const void*)kern, lds, once, "linear_bx");
+  if (rc) return rc;
+  const long nwg = a.streamk ? a.grid : (long)a.tiles_m * a.tiles_n * a.slices;
+  hipLaunchKernelGGL(kern, dim3((unsigned)nwg), dim3(kBxThreads), lds, stream, a, ep);
+  return check_launch("gemm_bx_kernel");
+}
+
+template <int BMB>
+int dispatch_bx(const BxArgs& a, int out, const EpiArgs& ep, hipStream_t s) {
+  if (out == BX_OUT_PARTIAL) return launch_bx<LX_EPI_NONE, BMB, BX_OUT_PARTIAL>(a, ep, s);
+  switch (ep.kind) {
+    case LX_EPI_NONE: return launch_bx<LX_EPI_NONE, BMB, BX_OUT_F32>(a, ep, s);
+    case LX_EPI_GELU_TANH: return launch_bx<LX_EPI_GELU_TANH, BMB, BX_OUT_F32>(a, ep, s);
+    case LX_EPI_GATED_RESID: return launch_bx<LX_EPI_GATED_RESID, BMB, BX_OUT_F32>(a, ep, s);
+    case LX_EPI_ROPE_PARTIAL: return launch_bx<LX_EPI_ROPE_PARTIAL, BMB, BX_OUT_F32>(a, ep, s);
+    case LX_EPI_RESID: return launch_bx<LX_EPI_RESID, BMB, BX_OUT_F32>(a, ep, s);
+    default: break;
+  }
+  set_error("linear_bx: epilogue kind %d not available", ep.kind);
+  return LX_ERR_ARG;
+}
+
+}  // namespace
+
+int wfrag_pack(const float* W, void* Wf, int N, int K, hipStream_t stream) {
+  LX_REQUIRE(W && Wf && N > 0 && K > 0 && N % 32 == 0 && K % 16 == 0,
+             "wfrag_pack: bad shape N=%d K=%d", N, K);
+  LX_REQUIRE(((uintptr_t)W | (uintptr_t)Wf) % 16 == 0, "wfrag_pack: unaligned");
+  const long total = (long)(N / 32) * (K / 16) * 64;
+  hipLaunchKernelGGL(wfrag_pack_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                     stream, W, static_cast<__bf16*>(Wf), N, K);
+  return check_launch("wfrag_pack_kernel");
+}
+
+int linear_bx(const lx_linear_bx& g, hipStream_t stream) {
+  LX_REQUIRE(g.A && g.Wf, "linear_bx: null operand");
+  LX_REQUIRE(g.M > 0 && g.N > 0 && g.K > 0 && g.N % kBxBN == 0 && g.K % (2 * kBxBK) == 0,
+             "linear_bx: bad shape M=%d N=%d K=%d (N %% 128, K %% 64)", g.M, g.N, g.K);
+  LX_REQUIRE(g.bm == 64 || g.bm == 128, "linear_bx: bm=%d must be 64 or 128", g.bm);
+  LX_REQUIRE(g.lda >= g.K && g.lda % 4 == 0 && (long)g.M * g.lda * 4 < (1L << 31),
+             "linear_bx: lda=%ld (K=%d), A must stay below 2 GiB", g.lda, g.K);
+  LX_REQUIRE(((uintptr_t)g.A | (uintptr_t)g.Wf) % 16 == 0,
+             "linear_bx: operands must be 16-byte aligned");
+  LX_REQUIRE(g.out == BX_OUT_F32 || g.out == BX_OUT_PARTIAL, "linear_bx: unknown output %d",
+             g.out);
+  const int slices = g.slices < 1 ? 1 : g.slices;
+  int kslice = g.K;
+  if (slices > 1) {
+    LX_REQUIRE(g.out == BX_OUT_PARTIAL, "linear_bx: K slices need the partial output");
+    LX_REQUIRE(g.K % (slices * 2 * kBxBK) == 0,
+               "linear_bx: K=%d is not %d slices of an even number of 32-wide slabs", g.K, slices);
+    kslice = g.K / slices;
+  }
+  EpiArgs ep;
+  int rc = make_epi(g.epi, g.N, &ep);
+  if (rc) return rc;
+  if (g.out == BX_OUT_PARTIAL) {
+    LX_REQUIRE(g.Y && g.ldy >= g.N && (slices == 1 || g.slice_stride >= (long)g.M * g.ldy),
+               "linear_bx: bad partial output");
+  } else {
+    LX_REQUIRE(g.Y && g.ldy >= g.N && g.ldy < (1L << 31), "linear_bx: bad output");
+    ep.vec = epi_vec_ok(ep, g.Y, (int)g.ldy, g.bias);
+    LX_REQUIRE(ep.vec, "linear_bx: y, bias and gate must be 16-byte aligned");
+  }
+  BxArgs a;
+  a.A = g.A;
+  a.lda = g.lda;
+  a.Wf = static_cast<const __bf16*>(g.Wf);
+  a.bias = g.bias;
+  a.Y = g.Y;
+  a.ldy = g.ldy;
+  a.slice_stride = g.slice_stride;
+  a.M = g.M;
+  a.N = g.N;
+  a.K = g.K;
+  a.kslice = kslice;
+  a.tiles_m = (g.M + g.bm - 1) / g.bm;
+  a.tiles_n = g.N / kBxBN;
+  a.slices = slices;
+  LX_REQUIRE((long)a.tiles_m * a.tiles_n * slices < (1L << 31), "linear_bx: too many tiles");
+  a.streamk = 0;
+  a.grid = 0;
+  a.ws = nullptr;
+  a.ws_bytes = 0;
+  a.counters = nullptr;
+  if (g.ws && g.counters && g.out != BX_OUT_PARTIAL) {
+    // Stream-K over one workgroup per CU (at most one per slab pair of work):
+    // every CU gets the same number of slab pairs whatever the tile count.
+    const int tiles = a.tiles_m * a.tiles_n;
+    const long units = (long)tiles * (g.K / (2 * kBxBK));
+    const int G = (int)std::min<long>(device_cus(), units);
+    const size_t need = (size_t)2 * G * g.bm * kBxBN;
+    if (tiles <= g.n_counters && need <= g.ws_floats && need * 4 < (1u << 31)) {
+      a.streamk = 1;
+      a.grid = G;
+      a.ws = g.ws;
+      a.ws_bytes = (int)(need * 4);
+      a.counters = g.counters;
+    }
+  }
+  return g.bm == 128 ? dispatch_bx<4>(a, g.out, ep, stream) : dispatch_bx<2>(a, g.out, ep, stream);
+}
+
+}  // namespace lx
+
+using namespace lx;
+
+extern "C" int lx_wfrag_pack_f32(const float* W, void* Wf, int N, int K, hipStream_t stream) {
+  return wfrag_pack(W, Wf, N, K, stream);
+}
+
+extern "C" int lx_linear_bx_f32(const lx_linear_bx* g, hipStream_t stream) {
+  LX_REQUIRE(g, "linear_bx: null argument");
+  return linear_bx(*g, stream);
+}

@@ -130,6 +130,12 @@ int splitk_qkv_rope_cache(const float* ws, int splits, int M, const float* bias,
                           int n_kv_heads, const int* pos, const float* inv_freq, float* q_out,
                           int ldq, float* k_cache, float* v_cache, int row0, hipStream_t stream);
 
+// ---- split-operand GEMM with W in fragment order (lx_gemm_bx.hip) ----
+// lx_linear_bx_f32 (arguments and outputs as declared in lx_ops.h).
+int linear_bx(const lx_linear_bx& g, hipStream_t stream);
+// W (N, K) -> fragment order (3 * N * K bf16); N % 32 == 0, K % 16 == 0.
+int wfrag_pack(const float* W, void* Wf, int N, int K, hipStream_t stream);
+
 // ---- single-token decode (lx_decode.hip) ----
 enum { DEC_QKV_ROPE = 0, DEC_SWIGLU = 1, DEC_RESID = 2, DEC_HEAD = 3 };
 

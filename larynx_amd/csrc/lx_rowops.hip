@@ -85,6 +85,124 @@ __global__ __launch_bounds__(kRowsPerBlock * kWave) void adaln_kernel(
   }
 }
 
+// The gated residual of a K-split projection folded into the next modulated
+// LayerNorm, one wave per row:
+//   h[r] = h[r] + gate_b * ((P_0[r] + ... + P_{S-1}[r]) + bias)   (S >= 1)
+//   y[r] = LN(h[r]) * (1 + scale_b) + shift_b                     (y != null)
+// The partial products are summed in slice order; the residual update is the
+// projection epilogue's own expression (h + (acc + bias) * gate).  The
+// (1 + scale), shift and gate rows of the batches a block touches and the bias
+// are staged in LDS.
+template <int NV, int SMAX>
+__global__ __launch_bounds__(kRowsPerBlock * kWave) void adaln_resid_kernel(
+    float* h, const float* P, int S, long pstride, const float* __restrict__ bias,
+    const float* __restrict__ gate, long gate_stride, const float* __restrict__ shift,
+    const float* __restrict__ scale, long mod_stride, float* y, int rows, int T, int D,
+    float eps) {
+  extern __shared__ float smem[];
+  const int D4 = D >> 2;
+  const int row0 = blockIdx.x * kRowsPerBlock;
+  const int wave = threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave;
+  const int row = min(row0 + wave, rows - 1);
+  const bool live = row0 + wave < rows;
+  // this wave's row and its partial rows, every load in flight first
+  float4* hr = reinterpret_cast<float4*>(h + (long)row * D);
+  float4 v[NV], pv[SMAX > 0 ? SMAX : 1][NV];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int i = lane + j * kWave;
+    v[j] = i < D4 ? hr[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+#pragma unroll
+  for (int sl = 0; sl < SMAX; ++sl)
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int i = lane + j * kWave;
+      pv[sl][j] = sl < S && i < D4
+                      ? ld_nt(reinterpret_cast<const float4*>(P + sl * pstride + (long)row * D) + i)
+                      : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  const int b_first = row0 / T;
+  const int last_row = min(row0 + kRowsPerBlock, rows) - 1;
+  const int nb = last_row / T - b_first + 1;
+  // LDS: per batch (1 + scale), shift, gate; then the bias
+  float* sb = smem + 3 * nb * D;
+  for (int bi = 0; bi < nb; ++bi) {
+    const float4* sc = reinterpret_cast<const float4*>(scale + (long)(b_first + bi) * mod_stride);
+    const float4* sh = reinterpret_cast<const float4*>(shift + (long)(b_first + bi) * mod_stride);
+    const float4* ga = reinterpret_cast<const float4*>(gate + (long)(b_first + bi) * gate_stride);
+    float4* s1 = reinterpret_cast<float4*>(smem + (3 * bi) * D);
+    float4* s2 = reinterpret_cast<float4*>(smem + (3 * bi + 1) * D);
+    float4* s3 = reinterpret_cast<float4*>(smem + (3 * bi + 2) * D);
+    for (int i = threadIdx.x; i < D4; i += blockDim.x) {
+      if (y) {
+        const float4 a = sc[i];
+        s1[i] = make_float4(1.0f + a.x, 1.0f + a.y, 1.0f + a.z, 1.0f + a.w);
+        s2[i] = sh[i];
+      }
+      if (S > 0) s3[i] = ga[i];
+    }
+  }
+  if (S > 0)
+    for (int i = threadIdx.x; i < D4; i += blockDim.x)
+      reinterpret_cast<float4*>(sb)[i] =
+          bias ? reinterpret_cast<const float4*>(bias)[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+  __syncthreads();
+  const int bi = row / T - b_first;
+  if (SMAX > 0 && S > 0) {
+    const float4* g4 = reinterpret_cast<const float4*>(smem + (3 * bi + 2) * D);
+    const float4* b4 = reinterpret_cast<const float4*>(sb);
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int i = lane + j * kWave;
+      if (i >= D4) continue;
+      float4 a = pv[0][j];
+#pragma unroll
+      for (int sl = 1; sl < SMAX; ++sl)
+        if (sl < S) a = make_float4(a.x + pv[sl][j].x, a.y + pv[sl][j].y, a.z + pv[sl][j].z,
+                                    a.w + pv[sl][j].w);
+      const float4 b = b4[i], g = g4[i];
+      v[j] = make_float4(v[j].x + (a.x + b.x) * g.x, v[j].y + (a.y + b.y) * g.y,
+                         v[j].z + (a.z + b.z) * g.z, v[j].w + (a.w + b.w) * g.w);
+      if (live) hr[i] = v[j];
+    }
+  }
+  if (!y) return;
+  float sm = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) sm += (v[j].x + v[j].y) + (v[j].z + v[j].w);
+  const float mean = wave_sum(sm) / (float)D;
+  float q = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int i = lane + j * kWave;
+    if (i < D4) {
+      const float a = v[j].x - mean, b = v[j].y - mean, c = v[j].z - mean, d = v[j].w - mean;
+      q += (a * a + b * b) + (c * c + d * d);
+    }
+  }
+  const float var = wave_sum(q) / (float)D;  // biased, as ggml_norm / nn.LayerNorm
+  const float rstd = 1.0f / sqrtf(var + eps);
+  if (!live) return;
+  const float4* s1 = reinterpret_cast<const float4*>(smem + (3 * bi) * D);
+  const float4* s2 = reinterpret_cast<const float4*>(smem + (3 * bi + 1) * D);
+  float4* yr = reinterpret_cast<float4*>(y + (long)row * D);
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int i = lane + j * kWave;
+    if (i < D4) {
+      const float4 m = s1[i], sh = s2[i];
+      float4 o;
+      o.x = ((v[j].x - mean) * rstd) * m.x + sh.x;
+      o.y = ((v[j].y - mean) * rstd) * m.y + sh.y;
+      o.z = ((v[j].z - mean) * rstd) * m.z + sh.z;
+      o.w = ((v[j].w - mean) * rstd) * m.w + sh.w;
+      yr[i] = o;
+    }
+  }
+}
+
 template <int NV>
 __global__ __launch_bounds__(kRowsPerBlock * kWave) void rmsnorm_kernel(
     const float* x, const float* __restrict__ w, float* y, int rows, int D, float eps) {
@@ -160,6 +278,48 @@ extern "C" int lx_adaln_modulate_f32(const float* x, const float* shift, const f
     hipLaunchKernelGGL(adaln_kernel<16>, dim3(nblk), dim3(kRowsPerBlock * kWave), lds, stream,
                        x, shift, scale, mod_stride, y, rows, T, D, eps);
   return check_launch("adaln_kernel");
+}
+
+extern "C" int lx_adaln_resid_f32(float* h, const float* partials, int splits,
+                                  long partial_stride, const float* bias, const float* gate,
+                                  long gate_stride, const float* shift, const float* scale,
+                                  long mod_stride, float* y, int B, int T, int D, float eps,
+                                  hipStream_t stream) {
+  LX_REQUIRE(h && shift && scale, "adaln_resid: null pointer");
+  LX_REQUIRE(B > 0 && T > 0 && D > 0, "adaln_resid: bad shape B=%d T=%d D=%d", B, T, D);
+  LX_REQUIRE(D % 4 == 0 && D <= 16 * 256, "adaln_resid: D=%d must be a multiple of 4, <= 4096",
+             D);
+  LX_REQUIRE(splits >= 0 && splits <= 4, "adaln_resid: %d partial slices (at most 4)", splits);
+  LX_REQUIRE(splits == 0 || (partials && gate && partial_stride >= (long)B * T * D &&
+                             partial_stride % 4 == 0 && (gate_stride == 0 || gate_stride >= D) &&
+                             gate_stride % 4 == 0),
+             "adaln_resid: bad partials / gate");
+  LX_REQUIRE(splits > 0 || y, "adaln_resid: nothing to do");
+  LX_REQUIRE((mod_stride == 0 || mod_stride >= D) && mod_stride % 4 == 0,
+             "adaln_resid: bad mod_stride %ld", mod_stride);
+  LX_REQUIRE(((uintptr_t)h | (uintptr_t)y | (uintptr_t)shift | (uintptr_t)scale |
+              (uintptr_t)partials | (uintptr_t)gate | (uintptr_t)bias) % 16 == 0,
+             "adaln_resid: pointers must be 16-byte aligned");
+  const int rows = B * T;
+  const int nblk = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
+  const int span = (T >= kRowsPerBlock) ? 2 : (kRowsPerBlock / T + 2);
+  const int max_b = span < B ? span : B;
+  const size_t lds = ((size_t)3 * max_b + 1) * D * sizeof(float);
+  LX_REQUIRE(lds <= 64 * 1024, "adaln_resid: T=%d too small for D=%d", T, D);
+  LX_REQUIRE(splits == 0 || D <= 8 * 256, "adaln_resid: D=%d above 2048 with partials", D);
+  const int nv = (D / 4 + kWave - 1) / kWave;
+#define LX_AR(NVV, SM)                                                                          \
+  hipLaunchKernelGGL((adaln_resid_kernel<NVV, SM>), dim3(nblk), dim3(kRowsPerBlock * kWave), lds,     \
+                     stream, h, partials, splits, partial_stride, bias, gate, gate_stride, shift, \
+                     scale, mod_stride, y, rows, T, D, eps)
+  if (nv <= 4)
+    LX_AR(4, 4);
+  else if (nv <= 8)
+    LX_AR(8, 4);
+  else
+    LX_AR(16, 0);  // splits == 0 here
+#undef LX_AR
+  return check_launch("adaln_resid_kernel");
 }
 
 extern "C" int lx_rmsnorm_f32(const float* x, const float* w, float* y, int rows, int D,

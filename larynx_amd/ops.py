@@ -10,15 +10,17 @@ import ctypes as C
 
 import torch
 
-from ._lib import (LX_EPI_GATED_RESID, LX_EPI_GELU_TANH, LX_EPI_NONE, LX_EPI_RESID,
-                   LX_EPI_ROPE_PARTIAL, LX_EPI_SWIGLU_PAIRED, Epilogue, check, lib)
+from ._lib import (LX_BX_OUT_F32, LX_BX_OUT_PARTIAL, LX_EPI_GATED_RESID,
+                   LX_EPI_GELU_TANH, LX_EPI_NONE, LX_EPI_RESID, LX_EPI_ROPE_PARTIAL,
+                   LX_EPI_SWIGLU_PAIRED, Epilogue, LinearBx, check, lib)
 
 __all__ = [
-    "stream", "ada_ln", "adaln_emb", "rope_partial", "gelu_tanh", "gated_residual",
+    "stream", "ada_ln", "adaln_resid", "adaln_emb", "rope_partial", "gelu_tanh", "gated_residual",
     "timestep_embed", "time_mlp", "rms_norm", "rope_full", "swiglu", "embed_gather", "linear",
-    "attention", "conv_pos_mish", "conv_pack_weight", "Epilogue",
+    "attention", "conv_pos_mish", "conv_pack_weight", "Epilogue", "split_planes",
+    "linear_split", "wfrag_pack", "linear_bx", "bx_scratch",
     "LX_EPI_NONE", "LX_EPI_GELU_TANH", "LX_EPI_GATED_RESID", "LX_EPI_ROPE_PARTIAL",
-    "LX_EPI_RESID", "LX_EPI_SWIGLU_PAIRED",
+    "LX_EPI_RESID", "LX_EPI_SWIGLU_PAIRED", "LX_BX_OUT_F32", "LX_BX_OUT_PARTIAL",
 ]
 
 
@@ -50,6 +52,23 @@ def ada_ln(x, scale, shift, eps=1e-6, out=None):
     y = torch.empty_like(x) if out is None else out
     check(lib.lx_adaln_modulate_f32(_p(x), _p(shift), _p(scale), scale.stride(0), _p(y), B, T, D,
                                     eps, stream()))
+    return y
+
+
+def adaln_resid(h, partials, bias, gate, shift, scale, out=None, eps=1e-6):
+    """h += gate * (sum of the K-slice partials (S, B*T, D) + bias), in place; then,
+    unless out is False, LN(h) * (1 + scale) + shift into out (B, T, D).
+    gate/shift/scale: (B, D) views (row stride = their stride(0)).
+    src/flow/dit.cpp:71,77 + src/flow/ops.cpp:94-104."""
+    B, T, D = h.shape
+    S = 0 if partials is None else partials.shape[0]
+    y = None
+    if out is not False:
+        y = torch.empty_like(h) if out is None else out
+    check(lib.lx_adaln_resid_f32(_p(h), _p(partials), S,
+                                 partials.stride(0) if S else 0, _p(bias), _p(gate),
+                                 gate.stride(0) if gate is not None else 0, _p(shift), _p(scale),
+                                 shift.stride(0), _p(y), B, T, D, eps, stream()))
     return y
 
 
@@ -184,6 +203,56 @@ def linear_split(x, planes, b=None, epilogue=None, out=None, tile=0):
                                   C.byref(epilogue) if epilogue is not None else None, tile,
                                   stream()))
     return out
+
+
+def wfrag_pack(W):
+    """W (N, K) fp32 in MFMA fragment order (3 * N * K bf16) for linear_bx."""
+    N, K = W.shape
+    wf = torch.empty(3 * N * K, device=W.device, dtype=torch.bfloat16)
+    check(lib.lx_wfrag_pack_f32(_p(W), wf.data_ptr(), N, K, stream()))
+    return wf
+
+
+def linear_bx(a, wf, N, b=None, epilogue=None, out=None, out_kind=LX_BX_OUT_F32, bm=128,
+              slices=1, scratch=None):
+    """epi(a @ W^T + b) with fp32 arithmetic on the bf16 matrix cores, W given as
+    wfrag_pack(W) (N rows), a fp32 (M, K).  out_kind LX_BX_OUT_F32: (M, N) (out= the
+    residual stream for residual epilogues); LX_BX_OUT_PARTIAL: (slices, M, N) raw
+    K-slice products.  scratch = bx_scratch(): the launch runs stream-K over the
+    CUs.  src/flow/ops.cpp:20-26."""
+    M, K = a.shape
+    g = LinearBx()
+    g.A, g.lda = a.data_ptr(), a.stride(0)
+    g.Wf = wf.data_ptr()
+    g.bias = _p(b)
+    if epilogue is not None:
+        g.epi = C.pointer(epilogue)
+    g.out = out_kind
+    g.M, g.N, g.K, g.bm, g.slices = M, N, K, bm, slices
+    if out_kind == LX_BX_OUT_PARTIAL:
+        if out is None:
+            out = torch.empty(slices, M, N, device=a.device, dtype=torch.float32)
+        g.Y, g.ldy, g.slice_stride = out.data_ptr(), out.stride(1), out.stride(0)
+    else:
+        kind = epilogue.kind if epilogue is not None else LX_EPI_NONE
+        if out is None:
+            if kind in (LX_EPI_GATED_RESID, LX_EPI_RESID):
+                raise ValueError("residual epilogues need out= (the residual stream)")
+            out = torch.empty(M, N, device=a.device, dtype=torch.float32)
+        g.Y, g.ldy = out.data_ptr(), out.stride(0)
+    if scratch is not None:
+        ws, cnt = scratch
+        g.ws, g.ws_floats = ws.data_ptr(), ws.numel()
+        g.counters, g.n_counters = cnt.data_ptr(), cnt.numel()
+    check(lib.lx_linear_bx_f32(C.byref(g), stream()))
+    return out
+
+
+def bx_scratch(device, bm=128, max_tiles=4096):
+    """Stream-K scratch for linear_bx: partial tiles and zeroed arrival counters."""
+    ws = torch.empty(2 * 256 * bm * 128, device=device, dtype=torch.float32)
+    cnt = torch.zeros(max_tiles, device=device, dtype=torch.int32)
+    return ws, cnt
 
 
 def attention(q, k, v, n_heads, n_kv_heads=None, scale=None, causal=False, q_offset=0,

@@ -64,6 +64,20 @@ def test_argument_errors_need_no_device():
     assert lib.lx_linear_f32(fake, 6, fake, None, fake, 6, 8, 8, 6, None, None) == LX_ERR_ARG
     assert lib.lx_conv_pos_mish_f32(fake, fake, fake, None, fake, 1, 8, 1024, 8, 31,
                                     None) == LX_ERR_ARG  # 128 channels per group
+    # fragment-order GEMM: N not a multiple of 128, K slices of odd slab counts
+    from larynx_amd._lib import LX_BX_OUT_PARTIAL, LinearBx
+    g = LinearBx()
+    g.A, g.lda, g.Wf, g.Y, g.ldy, g.M, g.N, g.K, g.bm, g.slices = (16, 1024, 16, 16, 1000,
+                                                                   8, 1000, 1024, 64, 1)
+    assert lib.lx_linear_bx_f32(C.byref(g), None) == LX_ERR_ARG
+    assert b"N %" in lib.lx_last_error() or b"bad shape" in lib.lx_last_error()
+    g.N, g.ldy, g.out, g.slices, g.K, g.lda = 1024, 1024, LX_BX_OUT_PARTIAL, 3, 1152, 1152
+    assert lib.lx_linear_bx_f32(C.byref(g), None) == LX_ERR_ARG
+    g.bm, g.slices = 96, 1
+    assert lib.lx_linear_bx_f32(C.byref(g), None) == LX_ERR_ARG
+    # the folded residual takes at most four partial slices
+    assert lib.lx_adaln_resid_f32(fake, fake, 5, 1 << 20, None, fake, 1024, fake, fake, 1024,
+                                  fake, 2, 8, 1024, 1e-6, None) == LX_ERR_ARG
     # composite objects: null handles and empty token lists are refused on the host
     assert lib.lx_flow_infer(None, None, 0, None, 0, None, 0, None, None, None,
                              None) == LX_ERR_ARG
@@ -105,7 +119,8 @@ def _c_layout(struct, fields):
     ("lx_epilogue", "Epilogue"), ("lx_dit_block_weights", "DitBlockWeights"),
     ("lx_dit_weights", "DitWeights"), ("lx_dit_capture", "DitCapture"),
     ("lx_qwen2_layer_weights", "Qwen2LayerWeights"), ("lx_qwen2_weights", "Qwen2Weights"),
-    ("lx_flow_frontend_weights", "FlowFrontendWeights"), ("lx_flow_capture", "FlowCapture")])
+    ("lx_flow_frontend_weights", "FlowFrontendWeights"), ("lx_flow_capture", "FlowCapture"),
+    ("lx_linear_bx", "LinearBx")])
 def test_struct_layouts_match_header(struct, cls):
     import larynx_amd._lib as L
     py = getattr(L, cls)

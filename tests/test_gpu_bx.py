@@ -1,0 +1,198 @@
+"""Parity of the fragment-order split-operand GEMM (lx_linear_bx_f32) and of the
+gated residual folded into the modulated LayerNorm (lx_adaln_resid_f32).
+
+The GEMM forms every fp32 product from three bf16 parts per operand (six exact
+partial products, fp32 accumulation), so its error against float64 products is
+at the fp32 level: the bound 4e-6 of the output's largest magnitude is the one
+the fp32 matrix-core kernel meets (bf16 arithmetic alone would give ~4e-3).
+Epilogues and the fused LayerNorm are checked against the oracle at the per-op
+bar (1e-4).
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import announce
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-4
+FP32_LEVEL = 4e-6
+
+
+def rnd(shape, stream, std=1.0, seed=23):
+    return orc.normal(shape, seed, stream, std)
+
+
+def dev(a, gpu):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(gpu)
+
+
+@pytest.fixture(scope="module")
+def ops(gpu):
+    from larynx_amd import ops as o
+    return o
+
+
+def unpack_wfrag(wf, N, K):
+    """W rebuilt on the host from its fragment order: part p of W[nb*32 + l % 32,
+    ks*16 + (l // 32)*8 + j] sits at ((nb*(K/16) + ks)*3 + p)*512 + l*8 + j."""
+    parts = wf.view(torch.int16).cpu().numpy().astype(np.int32)
+    f = (parts.astype(np.uint32) << 16).view(np.float32).reshape(N // 32, K // 16, 3, 2, 32, 8)
+    # axes: nb, ks, part, lane half h, row r, j  ->  W[nb*32 + r, ks*16 + h*8 + j]
+    tot = (f[:, :, 0].astype(np.float64) + f[:, :, 1]) + f[:, :, 2]
+    return tot.transpose(0, 3, 1, 2, 4).reshape(N, K)
+
+
+def test_wfrag_layout_and_parts_exact(gpu, ops):
+    """The fragment order places every weight where the MFMA B operand expects
+    it, and its three bf16 parts sum back to the fp32 weight exactly."""
+    announce("wfrag layout")
+    N, K = 256, 192
+    W = rnd((N, K), 1, 0.05)
+    wf = ops.wfrag_pack(dev(W, gpu))
+    assert wf.numel() == 3 * N * K
+    assert np.array_equal(unpack_wfrag(wf, N, K), W.astype(np.float64))
+
+
+@pytest.mark.parametrize("M,N,K,bm,sk", [
+    (1000, 3072, 1024, 128, False), (1000, 1024, 1024, 64, False), (1000, 2048, 1024, 64, True),
+    (37, 128, 64, 64, False), (6000, 1024, 2048, 64, False), (6000, 3072, 1024, 128, True),
+    (300, 256, 192, 128, True), (48, 3072, 1024, 64, False)])
+def test_linear_bx_fp32_level(gpu, ops, M, N, K, bm, sk):
+    announce(f"linear_bx M={M} N={N} K={K} bm={bm} streamk={sk}")
+    x, W, b = rnd((M, K), 2), rnd((N, K), 3, 0.03), rnd((N,), 4)
+    scr = ops.bx_scratch(gpu, bm=bm) if sk else None
+    y = ops.linear_bx(dev(x, gpu), ops.wfrag_pack(dev(W, gpu)), N, dev(b, gpu), bm=bm,
+                      scratch=scr).cpu().numpy()
+    ref = x.astype(np.float64) @ W.astype(np.float64).T + b.astype(np.float64)
+    assert np.abs(y - ref).max() / np.abs(ref).max() < FP32_LEVEL
+    if sk:  # every arrival count is left at zero for the next call
+        assert int(scr[1].abs().sum()) == 0
+
+
+@pytest.mark.parametrize("T,bm,sk", [(500, 64, False), (500, 128, True), (24, 64, False),
+                                     (3, 128, False), (1500, 64, True)])
+def test_linear_bx_epilogues(gpu, ops, T, bm, sk):
+    """QKV + partial rotary, FF0 + GELU and out / FF2 + gated residual at the
+    estimator's shapes, against the oracle."""
+    announce(f"linear_bx epilogues T={T} bm={bm} streamk={sk}")
+    B, D, F = 2, 1024, 2048
+    scr = ops.bx_scratch(gpu, bm=bm) if sk else None
+    x, W, b = rnd((B * T, D), 5), rnd((3 * D, D), 6, 0.03), rnd((3 * D,), 7)
+    pos = torch.arange(T, dtype=torch.int32, device=gpu)
+    ep = ops.Epilogue(kind=ops.LX_EPI_ROPE_PARTIAL, rows_per_batch=T, pos=pos.data_ptr(),
+                      rot_dim=64, rope_section=D, rope_sections=2, rope_base=10000.0)
+    y = ops.linear_bx(dev(x, gpu), ops.wfrag_pack(dev(W, gpu)), 3 * D, dev(b, gpu), ep, bm=bm,
+                      scratch=scr).cpu().numpy()
+    ref = orc.linear(x, W, b).reshape(B, T, 3 * D)
+    p = np.arange(T, dtype=np.int32)
+    q = orc.rope_partial(np.ascontiguousarray(ref[..., :D]), p)
+    k = orc.rope_partial(np.ascontiguousarray(ref[..., D:2 * D]), p)
+    ref = np.concatenate([q, k, ref[..., 2 * D:]], -1).reshape(B * T, 3 * D)
+    assert orc.rel_err(y, ref) < TOL
+
+    W1, b1 = rnd((F, D), 8, 0.03), rnd((F,), 9)
+    g = ops.Epilogue(kind=ops.LX_EPI_GELU_TANH)
+    y1 = ops.linear_bx(dev(x, gpu), ops.wfrag_pack(dev(W1, gpu)), F, dev(b1, gpu), g, bm=bm,
+                       scratch=scr).cpu().numpy()
+    assert orc.rel_err(y1, orc.gelu_tanh(orc.linear(x, W1, b1))) < TOL
+
+    xf, W2, b2 = rnd((B * T, F), 10), rnd((D, F), 11, 0.03), rnd((D,), 12)
+    h = rnd((B, T, D), 13)
+    emb = rnd((B, 6 * D), 14, 0.3)
+    hd, ed = dev(h, gpu), dev(emb, gpu)
+    gate = ed[:, 5 * D:]
+    epg = ops.Epilogue(kind=ops.LX_EPI_GATED_RESID, rows_per_batch=T, gate=gate.data_ptr(),
+                       gate_stride=6 * D)
+    ops.linear_bx(dev(xf, gpu), ops.wfrag_pack(dev(W2, gpu)), D, dev(b2, gpu), epg,
+                  out=hd.view(B * T, D), bm=bm, scratch=scr)
+    refg = orc.gated_residual(h, orc.linear(xf, W2, b2).reshape(B, T, D), emb[:, 5 * D:])
+    assert orc.rel_err(hd.cpu().numpy(), refg) < TOL
+
+
+@pytest.mark.parametrize("M,K,slices,bm", [(1000, 1024, 2, 64), (1000, 2048, 2, 64),
+                                           (1000, 2048, 4, 128), (45, 1024, 2, 64)])
+def test_linear_bx_partial_slices(gpu, ops, M, K, slices, bm):
+    """K slices written as raw partial products: each slice is its own K range's
+    product, and their sum is the whole one."""
+    announce(f"linear_bx partial M={M} K={K} slices={slices} bm={bm}")
+    N = 1024
+    x, W = rnd((M, K), 15), rnd((N, K), 16, 0.03)
+    P = ops.linear_bx(dev(x, gpu), ops.wfrag_pack(dev(W, gpu)), N,
+                      out_kind=ops.LX_BX_OUT_PARTIAL, slices=slices, bm=bm).cpu().numpy()
+    ks = K // slices
+    x64, W64 = x.astype(np.float64), W.astype(np.float64)
+    for s in range(slices):
+        ref = x64[:, s * ks:(s + 1) * ks] @ W64[:, s * ks:(s + 1) * ks].T
+        assert np.abs(P[s] - ref).max() / np.abs(ref).max() < FP32_LEVEL
+    ref = x64 @ W64.T
+    assert np.abs(P.astype(np.float64).sum(0) - ref).max() / np.abs(ref).max() < FP32_LEVEL
+
+
+def test_linear_bx_streamk_is_deterministic(gpu, ops):
+    """Stream-K sums a shared tile's partials in k order whatever the arrival
+    order: repeated calls are bit-identical (QKV at T=500: 192 tiles over 256
+    workgroups, every tile shared by two)."""
+    announce("linear_bx stream-K determinism")
+    x, W = dev(rnd((1000, 1024), 17), gpu), dev(rnd((3072, 1024), 18, 0.03), gpu)
+    wf = ops.wfrag_pack(W)
+    scr = ops.bx_scratch(gpu)
+    y0 = ops.linear_bx(x, wf, 3072, scratch=scr)
+    for _ in range(4):
+        assert torch.equal(ops.linear_bx(x, wf, 3072, scratch=scr), y0)
+
+
+def test_linear_bx_rejects_bad_arguments(gpu, ops):
+    from larynx_amd import LxError
+    announce("linear_bx bad arguments")
+    x = torch.zeros(64, 128, device=gpu)
+    wf = ops.wfrag_pack(torch.zeros(192, 128, device=gpu))
+    with pytest.raises(LxError):
+        ops.linear_bx(x, wf, 192)  # N not a multiple of 128
+    wf = ops.wfrag_pack(torch.zeros(128, 128, device=gpu))
+    with pytest.raises(LxError):
+        ops.linear_bx(x, wf, 128, bm=32)
+    with pytest.raises(LxError):
+        ops.linear_bx(x, wf, 128, out_kind=ops.LX_BX_OUT_PARTIAL, slices=3)
+    with pytest.raises(LxError):  # K slices only with the partial output
+        ops.linear_bx(x, wf, 128, slices=2)
+    with pytest.raises(LxError):
+        ops.linear_bx(x[:, :96], ops.wfrag_pack(torch.zeros(128, 96, device=gpu)), 128)
+
+
+@pytest.mark.parametrize("B,T,S", [(2, 500, 2), (2, 500, 0), (2, 24, 4), (2, 3, 1), (1, 7, 2)])
+def test_adaln_resid(gpu, ops, B, T, S):
+    """h += gate * (sum of the K-slice partials + bias), then the modulated
+    LayerNorm of the updated h, against the oracle (gated residual, then ada_ln)."""
+    announce(f"adaln_resid B={B} T={T} S={S}")
+    D = 1024
+    h = rnd((B, T, D), 19) * 2 + 0.1
+    P = rnd((max(S, 1), B * T, D), 20)
+    bias = rnd((D,), 21, 0.1)
+    emb = rnd((B, 6 * D), 22, 0.2)
+    hd, ed = dev(h, gpu), dev(emb, gpu)
+    Pd = dev(P[:S], gpu) if S else None
+    y = ops.adaln_resid(hd, Pd, dev(bias, gpu), ed[:, 2 * D:3 * D], ed[:, :D], ed[:, D:2 * D])
+    if S:
+        acc = P[:S].astype(np.float64).sum(0).reshape(B, T, D) + bias
+        h_ref = orc.gated_residual(h, acc.astype(np.float32), emb[:, 2 * D:3 * D])
+    else:
+        h_ref = h
+    assert orc.rel_err(hd.cpu().numpy(), h_ref) < TOL
+    ref = orc.adaln(h_ref, emb[:, D:2 * D], emb[:, :D])
+    assert orc.rel_err(y.cpu().numpy(), ref) < TOL
+
+
+def test_adaln_resid_reduce_only_matches_fused(gpu, ops):
+    """The reduce-only form (no LayerNorm output) leaves h bit-identical to the
+    fused one: the estimator uses it for block captures."""
+    announce("adaln_resid reduce-only")
+    B, T, D = 2, 500, 1024
+    h = dev(rnd((B, T, D), 23), gpu)
+    P = dev(rnd((2, B * T, D), 24), gpu)
+    bias, emb = dev(rnd((D,), 25), gpu), dev(rnd((B, 6 * D), 26, 0.2), gpu)
+    h1, h2 = h.clone(), h.clone()
+    ops.adaln_resid(h1, P, bias, emb[:, 2 * D:3 * D], emb[:, :D], emb[:, D:2 * D])
+    ops.adaln_resid(h2, P, bias, emb[:, 2 * D:3 * D], emb[:, :D], emb[:, D:2 * D], out=False)
+    assert torch.equal(h1, h2)
