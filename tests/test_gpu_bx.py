@@ -196,3 +196,45 @@ def test_adaln_resid_reduce_only_matches_fused(gpu, ops):
     ops.adaln_resid(h1, P, bias, emb[:, 2 * D:3 * D], emb[:, :D], emb[:, D:2 * D])
     ops.adaln_resid(h2, P, bias, emb[:, 2 * D:3 * D], emb[:, :D], emb[:, D:2 * D], out=False)
     assert torch.equal(h1, h2)
+
+
+def test_split_operand_nonfinite_inputs(gpu, ops):
+    """The contract of the split-operand kernels for non-finite operands: an
+    infinite element, a NaN, or a finite value above the largest bf16 magnitude
+    (3.3895e38; its leading part rounds to infinity) turns every output it
+    reaches into NaN (the parts x - bf16(x) of an infinity are NaN), where the
+    fp32 kernel gives +-inf or a finite product; every other output is
+    unaffected.  GEMM: the rows of A holding such an element.  Attention: the
+    query row of such a q element, and every query of the (batch, head) whose
+    keys hold one."""
+    announce("split-operand kernels: non-finite inputs")
+    M, N, K = 1000, 1024, 1024
+    x = rnd((M, K), 40)
+    W = rnd((N, K), 41, 0.02)
+    bad = {3: np.inf, 5: np.nan, 7: 3.3999e38, 9: -np.inf}
+    for r, v in bad.items():
+        x[r, 17] = v
+    xd, Wd = dev(x, gpu), dev(W, gpu)
+    clean = np.ones(M, bool)
+    clean[list(bad)] = False
+    ref = x[clean].astype(np.float64) @ W.astype(np.float64).T
+    for y in (ops.linear_bx(xd, ops.wfrag_pack(Wd), N, bm=64).cpu().numpy(),
+              ops.linear_split(xd, ops.split_planes(Wd), tile=0).cpu().numpy()):
+        for r in bad:
+            assert np.isnan(y[r]).all(), r
+        assert np.abs(y[clean] - ref).max() / np.abs(ref).max() < FP32_LEVEL
+    y32 = ops.linear(xd, Wd).cpu().numpy()  # the fp32 kernel, for contrast
+    assert np.isfinite(y32[7]).all() and not np.isfinite(y32[3]).any()
+
+    B, T, D = 2, 500, 1024  # 64-query split-operand layout
+    qkv = rnd((B, T, 3 * D), 42, 0.5)
+    qkv[0, 10, 3 * 64 + 5] = np.nan         # q of batch 0, query 10, head 3
+    qkv[1, 20, D + 5 * 64 + 7] = np.inf     # k of batch 1, key 20, head 5
+    qd = dev(qkv, gpu)
+    o = ops.attention(qd[..., :D], qd[..., D:2 * D], qd[..., 2 * D:], 16).cpu().numpy()
+    hit = np.zeros((B, T, 16), bool)
+    hit[0, 10, 3] = True
+    hit[1, :, 5] = True
+    oh = o.reshape(B, T, 16, 64)
+    assert np.isnan(oh[hit]).all()
+    assert np.isfinite(oh[~hit]).all()

@@ -172,3 +172,32 @@ def test_dit_T3000_22_blocks_vs_oracle(gpu):
     print(f"norm_out {e_norm:.2e} dphi {e_dphi:.2e}", flush=True)
     assert max(errs) < TOL_22, errs
     assert e_norm < TOL_22 and e_dphi < TOL_22
+
+
+@pytest.mark.timeout(900)
+def test_cfm_solve_T3000_vs_oracle(gpu):
+    """The long-utterance workload's whole CFM solve (src/flow/flow.cpp:240-274 at
+    T = 3000): 10 CFG Euler steps on the cosine t-schedule, CFG rate 0.7, the CFG
+    pair as B = 2, through a 2-block estimator, against the oracle's solve at the
+    per-op bar."""
+    from larynx_amd.flow import DiTConfig, DiTEstimator, dit_param_shapes
+    cfg = DiTConfig(depth=2)
+    T = 3000
+    announce("cfm solve T=3000 2 blocks: weights")
+    params = orc.make_params(dit_param_shapes(cfg), 3010)
+    est = DiTEstimator({k: torch.from_numpy(v).to(gpu) for k, v in params.items()}, cfg, B=2,
+                       max_T=T)
+    z = orc.normal((80, T), 3011, 1)
+    mu = orc.normal((80, T), 3011, 2)
+    cond = orc.normal((80, T), 3011, 3)
+    spks = orc.normal((80,), 3011, 4, 1.0 / np.sqrt(80.0))
+    announce("cfm solve T=3000 2 blocks: device solve")
+    feat = est.cfm_solve(*(torch.from_numpy(a).to(gpu) for a in (z, mu, cond, spks)),
+                         n_steps=10, cfg_rate=0.7)
+    torch.cuda.synchronize()
+    est.close()
+    announce("cfm solve T=3000 2 blocks: oracle solve")
+    ref = orc.Dit(params, depth=2).cfm_solve(z, mu, cond, spks, n_steps=10, cfg_rate=0.7)
+    err = orc.rel_err(feat.cpu().numpy(), ref)
+    print(f"solve rel err {err:.2e}", flush=True)
+    assert err < TOL

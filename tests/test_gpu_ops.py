@@ -495,6 +495,22 @@ def test_attention_wide_layout_causal(gpu, ops, B, T):
     assert orc.rel_err(o, ref) < TOL
 
 
+@pytest.mark.parametrize("kvh,causal,off", [(16, True, 0), (16, True, 48), (4, False, 0),
+                                           (4, True, 0)])
+def test_attention_64query_layout_causal_gqa(gpu, ops, kvh, causal, off):
+    """The 64-query split-operand layout (B=2, T=500, 16 query heads: 256
+    workgroups, one round) with causal masks, a query offset and 16:4 grouped
+    heads, against the oracle."""
+    announce(f"attention 64-query layout kv_heads={kvh} causal={causal} q_offset={off}")
+    B, T, D = 2, 500, 1024
+    q = rnd((B, T, D), 31)
+    k, v = rnd((B, T + off, kvh * 64), 32), rnd((B, T + off, kvh * 64), 33)
+    o = ops.attention(dev(q, gpu), dev(k, gpu), dev(v, gpu), 16, kvh, causal=causal,
+                      q_offset=off).cpu().numpy()
+    ref = orc.attention(q, k, v, 16, kvh, causal=causal, q_offset=off)
+    assert orc.rel_err(o, ref) < TOL
+
+
 @pytest.mark.parametrize("slope,causal", [(0.05, False), (0.15, False), (0.15, True),
                                           (-0.15, False)])
 def test_attention_reference_moves(gpu, ops, slope, causal):
