@@ -230,7 +230,7 @@ int lx_linear_split_f32(const float* x, int ldx, const void* planes, const float
  * weight once in fragment order (3 * N * K bf16; N a multiple of 32, K of 16).
  * A is fp32 (M, K) with row stride lda.  Outputs:
  *   LX_BX_OUT_F32      Y = epi(A @ W^T + bias) (row stride ldy), every
- *                      lx_epilogue kind but SWIGLU_PAIRED;
+ *                      lx_epilogue kind (SWIGLU_PAIRED: N / 2 columns);
  *   LX_BX_OUT_PARTIAL  the raw products of `slices` equal K slices, slice s
  *                      into Y + s * slice_stride (no bias, no epilogue): the
  *                      consumer sums the slices in slice order.
@@ -491,11 +491,17 @@ int lx_qwen2_prefill(lx_qwen2* m, const float* lm_input, int L, float* logits,
  * logits: device (speech_vocab); final_norm: device (H) or NULL.
  * The position lives in device memory, so the layer stack is captured into a
  * HIP graph on the first decode (on a stream of the object's own) and
- * replayed on `stream` for every later token; with LX_DECODE_GRAPH=0 in the
- * environment at create time it is launched eagerly instead.  Calls on one
- * object must not overlap. */
+ * replayed on `stream` for every later token (see lx_qwen2_set_decode_graph).
+ * Calls on one object must not overlap. */
 int lx_qwen2_decode(lx_qwen2* m, int token, float* logits, float* final_norm,
                     hipStream_t stream);
+
+/* Decode launch mode: enable != 0 (the default) replays the captured layer
+ * stack as a HIP graph; 0 launches the same kernels eagerly on `stream` (for
+ * callers that capture decode into graphs of their own, and for checking the
+ * two bit for bit).  No counterpart in the reference, which rebuilds its ggml
+ * graph every step (src/llm/llm.cpp:232-275). */
+int lx_qwen2_set_decode_graph(lx_qwen2* m, int enable);
 
 /* LLM::cache_len / cache_key / cache_value (include/larynx/llm/llm.h:77-84).
  * The cache of layer l is (cache_len, n_kv_heads * head_dim) roped keys /

@@ -198,6 +198,7 @@ SIGNATURES = [
     ("lx_qwen2_cache_key", C.c_void_p, [C.c_void_p, C.c_int]),
     ("lx_qwen2_cache_value", C.c_void_p, [C.c_void_p, C.c_int]),
     ("lx_qwen2_set_cache_len", C.c_int, [C.c_void_p, C.c_int]),
+    ("lx_qwen2_set_decode_graph", C.c_int, [C.c_void_p, C.c_int]),
 ]
 
 

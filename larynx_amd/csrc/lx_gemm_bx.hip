@@ -518,6 +518,8 @@ int dispatch_bx(const BxArgs& a, int out, const EpiArgs& ep, hipStream_t s) {
     case LX_EPI_GATED_RESID: return launch_bx<LX_EPI_GATED_RESID, BMB, BX_OUT_F32>(a, ep, s);
     case LX_EPI_ROPE_PARTIAL: return launch_bx<LX_EPI_ROPE_PARTIAL, BMB, BX_OUT_F32>(a, ep, s);
     case LX_EPI_RESID: return launch_bx<LX_EPI_RESID, BMB, BX_OUT_F32>(a, ep, s);
+    case LX_EPI_SWIGLU_PAIRED:
+      return launch_bx<LX_EPI_SWIGLU_PAIRED, BMB, BX_OUT_F32>(a, ep, s);
     default: break;
   }
   set_error("linear_bx: epilogue kind %d not available", ep.kind);
@@ -562,7 +564,9 @@ int linear_bx(const lx_linear_bx& g, hipStream_t stream) {
     LX_REQUIRE(g.Y && g.ldy >= g.N && (slices == 1 || g.slice_stride >= (long)g.M * g.ldy),
                "linear_bx: bad partial output");
   } else {
-    LX_REQUIRE(g.Y && g.ldy >= g.N && g.ldy < (1L << 31), "linear_bx: bad output");
+    LX_REQUIRE(g.Y && g.ldy >= (ep.kind == LX_EPI_SWIGLU_PAIRED ? g.N / 2 : g.N) &&
+                   g.ldy < (1L << 31),
+               "linear_bx: bad output");
     ep.vec = epi_vec_ok(ep, g.Y, (int)g.ldy, g.bias);
     LX_REQUIRE(ep.vec, "linear_bx: y, bias and gate must be 16-byte aligned");
   }

@@ -29,8 +29,23 @@ constexpr int kTaskIdToken = 6563;  // TASK_ID_TOKEN (src/llm/internal.h:34)
 struct Layer {
   float *qkv_w, *qkv_b, *o_w, *gu_w, *down_w, *in_norm, *post_norm;
   float *k_cache, *v_cache;  // (max_ctx, KV)
-  void* gu_wp;  // gate/up rows as three bf16 planes (split_planes), for long prefills
+  // the prefill projections' weights in MFMA fragment order (wfrag_pack), for
+  // the split-operand GEMM; decode streams the fp32 copies above
+  void *qkv_wf = nullptr, *o_wf = nullptr, *gu_wf = nullptr, *down_wf = nullptr;
 };
+
+// K slices of a prefill projection on the fragment-order GEMM (64-row tiles):
+// the largest divisor of its 64-wide K steps, at most 9 (the reduce passes' bound),
+// whose tiles times slices stay within one workgroup per CU.  L = 256: q|k|v and
+// o_proj 7 slices (252 / 196 workgroups), down_proj 4 (112); L = 1024: 1 / 2 / 2.
+int prefill_bx_slices(int rows, int N, int K) {
+  const int steps = K / 64;
+  const long tiles = (long)((rows + 63) / 64) * (N / 128);
+  int best = 1;
+  for (int d = 1; d <= 9 && d <= steps; ++d)
+    if (steps % d == 0 && tiles * d <= 256) best = d;
+  return best;
+}
 
 }  // namespace
 
@@ -49,6 +64,7 @@ struct lx_qwen2 {
   float *x, *hn, *qkv, *att, *act;
   float* ws = nullptr;  // split-K partial sums, and the gate/up split tail's partial tiles
   size_t ws_floats = 0;
+  bool frag = false;    // prefill projections on the fragment-order split-operand GEMM
   unsigned* arrivals = nullptr;  // split-tail arrival counters (zeroed at creation)
   int n_arrivals = 0;
   int* pos;     // pos[i] = i
@@ -104,7 +120,8 @@ size_t splitk_ws_floats(int max_ctx, int H, int QKV, int I, int* tails) {
     for (const auto& sh : shapes) {
       int ks = 0;
       const int splits = gemm_splitk_plan(rows, sh[0], sh[1], &ks);
-      const size_t n = (size_t)splits * rows * sh[0];
+      const int bx = prefill_bx_slices(rows, sh[0], sh[1]);
+      const size_t n = (size_t)std::max(splits, bx) * rows * sh[0];
       if (n > best) best = n;
     }
     int t = 0;
@@ -116,50 +133,78 @@ size_t splitk_ws_floats(int max_ctx, int H, int QKV, int I, int* tails) {
   return best;
 }
 
+// q|k|v, o_proj or down_proj as K-slice partial products into m->ws; returns the
+// slice count through *splits.
+int prefill_partials(lx_qwen2* m, const float* x, int ldx, const void* wf, const float* w,
+                     int rows, int N, int K, int* splits, hipStream_t s) {
+  if (m->frag) {
+    const int sl = prefill_bx_slices(rows, N, K);
+    lx_linear_bx g{};
+    g.A = x;
+    g.lda = ldx;
+    g.Wf = wf;
+    g.out = LX_BX_OUT_PARTIAL;
+    g.Y = m->ws;
+    g.ldy = N;
+    g.slice_stride = (long)rows * N;
+    g.M = rows;
+    g.N = N;
+    g.K = K;
+    g.bm = 64;
+    g.slices = sl;
+    *splits = sl;
+    return linear_bx(g, s);
+  }
+  int ks = 0;
+  *splits = gemm_splitk_plan(rows, N, K, &ks);
+  return gemm_splitk_partials(x, ldx, w, K, m->ws, rows, N, K, *splits, ks, s);
+}
+
 // Prefill layer (src/llm/llm.cpp:141-173) over L rows at positions m->pos[0..L).
 // On entry m->hn holds input_layernorm(x); on exit x is the layer output and
 // m->hn holds next_norm(x) (the next layer's input_layernorm or the final norm).
-//   q/k/v: split-K partials, then bias + NEOX rotary + cache append in one pass;
+//   q/k/v: K-slice partials, then bias + NEOX rotary + cache append in one pass;
 //   attention (causal, GQA) reads q and the cache;
-//   o_proj: split-K partials, then residual + post_attention_layernorm;
+//   o_proj: K-slice partials, then residual + post_attention_layernorm;
 //   gate/up with the SwiGLU epilogue;
-//   down_proj: split-K partials, then residual + next_norm.
-// gate/up + SwiGLU on the split-operand bf16 GEMM (128 x 128 tiles) when its
-// tiles fill one round of the 256 CUs at least half or several rounds to at
-// least 75%; else the fp32 GEMM with its split tail.  Prefill at L = 128 /
-// 256 / 384 / 512 / 1024 / 2048: 1.92 / 2.68 / 3.60 / 4.29 / 7.61 / 15.22 ms
-// with the fp32 GEMM, 2.13 / 2.64 / 3.24 / 4.54 / 7.30 / 14.00 with the split
-// one (76 / 152 / 228 / 304 / 608 / 1216 tiles).
-bool gateup_split(int rows, int N, int K) {
-  if (rows < 128 || N % 128 != 0 || K % 32 != 0) return false;
-  const long tiles = (long)((rows + 127) / 128) * (N / 128);
-  const long rounds = (tiles + 255) / 256;
-  return rounds == 1 ? tiles >= 128 : tiles * 100 >= rounds * 256 * 75;
-}
-
+//   down_proj: K-slice partials, then residual + next_norm.
+// Every projection runs on the fragment-order split-operand GEMM when the
+// geometry allows (m->frag: N multiples of 128, K of 64), else on the fp32 GEMMs.
 int prefill_layer(lx_qwen2* m, Layer& L, int rows, const float* next_norm, hipStream_t s) {
   const int H = m->H, KV = m->KV, QKV = m->QKV;
-  int ks = 0;
-  int sp = gemm_splitk_plan(rows, QKV, H, &ks);
-  LX_TRY(gemm_splitk_partials(m->hn, H, L.qkv_w, H, m->ws, rows, QKV, H, sp, ks, s));
+  int sp = 0;
+  LX_TRY(prefill_partials(m, m->hn, H, L.qkv_wf, L.qkv_w, rows, QKV, H, &sp, s));
   LX_TRY(splitk_qkv_rope_cache(m->ws, sp, rows, L.qkv_b, m->NH, m->NKV, m->pos, m->rope_tab,
                                m->qkv, QKV, L.k_cache, L.v_cache, 0, s));
   const float scale = 1.0f / std::sqrt((float)m->HD);
   LX_TRY(lx_attention_f32(m->qkv, QKV, L.k_cache, KV, L.v_cache, KV, m->att, H, 1, rows, rows,
                           m->NH, m->NKV, m->HD, scale, /*causal*/ 1, /*q_offset*/ 0, s));
-  sp = gemm_splitk_plan(rows, H, H, &ks);
-  LX_TRY(gemm_splitk_partials(m->att, H, L.o_w, H, m->ws, rows, H, H, sp, ks, s));
+  LX_TRY(prefill_partials(m, m->att, H, L.o_wf, L.o_w, rows, H, H, &sp, s));
   LX_TRY(splitk_resid_rmsnorm(m->ws, sp, rows, H, nullptr, m->x, L.post_norm, m->eps, m->hn, s));
   lx_epilogue swiglu{};
   swiglu.kind = LX_EPI_SWIGLU_PAIRED;
-  if (gateup_split(rows, 2 * m->I, H))
-    LX_TRY(linear_split(m->hn, H, L.gu_wp, nullptr, m->act, m->I, rows, 2 * m->I, H, &swiglu,
-                        /*narrow*/ 0, s));
-  else
+  if (m->frag) {
+    // gate/up + SwiGLU: 128-row tiles while they fit one round over the CUs
+    // (L = 256: 152 tiles, 33 vs 35 us), else 64-row tiles (L = 1024: 95 vs 116 us)
+    lx_linear_bx g{};
+    g.A = m->hn;
+    g.lda = H;
+    g.Wf = L.gu_wf;
+    g.epi = &swiglu;
+    g.out = LX_BX_OUT_F32;
+    g.Y = m->act;
+    g.ldy = m->I;
+    g.M = rows;
+    g.N = 2 * m->I;
+    g.K = H;
+    g.bm = (long)((rows + 127) / 128) * (2 * m->I / 128) <= 256 ? 128 : 64;
+    g.slices = 1;
+    LX_TRY(linear_bx(g, s));
+  } else {
     LX_TRY(linear_split_tail(m->hn, H, L.gu_w, nullptr, m->act, m->I, rows, 2 * m->I, H,
                              &swiglu, m->ws, m->ws_floats, m->arrivals, m->n_arrivals, s));
-  sp = gemm_splitk_plan(rows, H, m->I, &ks);
-  LX_TRY(gemm_splitk_partials(m->act, m->I, L.down_w, m->I, m->ws, rows, H, m->I, sp, ks, s));
+  }
+  LX_TRY(prefill_partials(m, m->act, m->I, L.down_wf, L.down_w, rows, H, m->I, &sp, s));
   return splitk_resid_rmsnorm(m->ws, sp, rows, H, nullptr, m->x, next_norm, m->eps, m->hn, s);
 }
 
@@ -315,6 +360,10 @@ extern "C" int lx_qwen2_create(const lx_qwen2_weights* w, int max_ctx, lx_qwen2*
   m->embed_tokens = w->embed_tokens;
   m->speech_embedding = w->speech_embedding;
   const int H = m->H, I = m->I, KV = m->KV, QKV = m->QKV;
+  // the fragment-order GEMM needs N multiples of 128 and K of 64 in every
+  // prefill projection, and each activation below 2 GiB
+  m->frag = QKV % 128 == 0 && H % 128 == 0 && (2 * I) % 128 == 0 && I % 64 == 0 &&
+            (size_t)max_ctx * I * 4 < (1ull << 31);
   Arena& a = m->arena;
   bool ok = true;
   auto A = [&](size_t n) {
@@ -330,9 +379,14 @@ extern "C" int lx_qwen2_create(const lx_qwen2_weights* w, int max_ctx, lx_qwen2*
     L.qkv_b = A(QKV);
     L.o_w = A((size_t)H * H);
     L.gu_w = A((size_t)2 * I * H);
-    L.gu_wp = a.alloc<unsigned short>((size_t)3 * 2 * I * H);
-    ok = ok && L.gu_wp;
     L.down_w = A((size_t)H * I);
+    if (m->frag) {
+      L.qkv_wf = a.alloc<unsigned short>((size_t)3 * QKV * H);
+      L.o_wf = a.alloc<unsigned short>((size_t)3 * H * H);
+      L.gu_wf = a.alloc<unsigned short>((size_t)3 * 2 * I * H);
+      L.down_wf = a.alloc<unsigned short>((size_t)3 * H * I);
+      ok = ok && L.qkv_wf && L.o_wf && L.gu_wf && L.down_wf;
+    }
     L.in_norm = A(H);
     L.post_norm = A(H);
     L.k_cache = A((size_t)max_ctx * KV);
@@ -357,8 +411,6 @@ extern "C" int lx_qwen2_create(const lx_qwen2_weights* w, int max_ctx, lx_qwen2*
   m->d_pos = a.alloc<int>(1);
   m->rope_tab = A(m->HD / 2);
   ok = ok && m->pos && m->d_pos;
-  const char* env = std::getenv("LX_DECODE_GRAPH");
-  m->use_graph = !(env && env[0] == '0');
   if (!ok) {
     delete m;
     set_error("qwen2_create: device allocation failed");
@@ -400,7 +452,12 @@ extern "C" int lx_qwen2_create(const lx_qwen2_weights* w, int max_ctx, lx_qwen2*
     C(L.post_norm, lw.post_norm, H);
     if (rc == LX_OK) rc = (lw.gate_w && lw.up_w) ? LX_OK : LX_ERR_ARG;
     if (rc == LX_OK) rc = interleave_rows(lw.gate_w, lw.up_w, L.gu_w, I, H, s);
-    if (rc == LX_OK) rc = split_planes(L.gu_w, L.gu_wp, (long)2 * I * H, s);
+    if (m->frag) {
+      if (rc == LX_OK) rc = wfrag_pack(L.qkv_w, L.qkv_wf, QKV, H, s);
+      if (rc == LX_OK) rc = wfrag_pack(L.o_w, L.o_wf, H, H, s);
+      if (rc == LX_OK) rc = wfrag_pack(L.gu_w, L.gu_wf, 2 * I, H, s);
+      if (rc == LX_OK) rc = wfrag_pack(L.down_w, L.down_wf, H, I, s);
+    }
   }
   if (rc == LX_OK) rc = iota_i32(m->pos, max_ctx, s);
   // the split tail's arrival counters start at zero; every launch leaves them so
@@ -556,6 +613,12 @@ extern "C" const float* lx_qwen2_cache_key(const lx_qwen2* m, int layer) {
 extern "C" const float* lx_qwen2_cache_value(const lx_qwen2* m, int layer) {
   if (!m || layer < 0 || layer >= m->NL) return nullptr;
   return m->layers[layer].v_cache;
+}
+
+extern "C" int lx_qwen2_set_decode_graph(lx_qwen2* m, int enable) {
+  LX_REQUIRE(m, "qwen2_set_decode_graph: null model");
+  m->use_graph = enable != 0;  // graphs already captured are kept for a later switch back
+  return LX_OK;
 }
 
 extern "C" int lx_qwen2_set_cache_len(lx_qwen2* m, int len) {

@@ -192,6 +192,11 @@ class Qwen2LM:
     def set_cache_len(self, n):
         check(lib.lx_qwen2_set_cache_len(self._h, int(n)))
 
+    def set_decode_graph(self, enable):
+        """Replay decode as a captured HIP graph (True, the default) or launch it
+        eagerly (False)."""
+        check(lib.lx_qwen2_set_decode_graph(self._h, 1 if enable else 0))
+
     def cache_views(self, layer):
         """(k, v) device views (max_ctx, KV) of the layer's cache (roped keys, raw values)."""
         KV = self.cfg.n_kv_heads * self.cfg.head_dim

@@ -238,7 +238,8 @@ def linear_bx(a, wf, N, b=None, epilogue=None, out=None, out_kind=LX_BX_OUT_F32,
         if out is None:
             if kind in (LX_EPI_GATED_RESID, LX_EPI_RESID):
                 raise ValueError("residual epilogues need out= (the residual stream)")
-            out = torch.empty(M, N, device=a.device, dtype=torch.float32)
+            ncol = N // 2 if kind == LX_EPI_SWIGLU_PAIRED else N
+            out = torch.empty(M, ncol, device=a.device, dtype=torch.float32)
         g.Y, g.ldy = out.data_ptr(), out.stride(0)
     if scratch is not None:
         ws, cnt = scratch

@@ -115,18 +115,14 @@ def test_errors(gpu, qwen):
 
 def test_decode_graph_matches_eager_and_crosses_splits(gpu, qwen):
     """The decode layer stack replayed as a HIP graph and launched eagerly
-    (LX_DECODE_GRAPH=0) give bit-identical logits; sequential decode steps
+    (set_decode_graph(False)) give bit-identical logits; sequential decode steps
     across the 64-key attention split boundary (cache 62 -> 67) track the
     oracle, including its device-side position and split counters."""
-    import os
     from larynx_amd.llm import Qwen2LM
     cfg, params, dparams, _ = qwen
     announce("qwen2 decode graph vs eager, cache 62..67")
-    os.environ["LX_DECODE_GRAPH"] = "0"
-    try:
-        eager = Qwen2LM(dparams, cfg, max_ctx=128)
-    finally:
-        del os.environ["LX_DECODE_GRAPH"]
+    eager = Qwen2LM(dparams, cfg, max_ctx=128)
+    eager.set_decode_graph(False)
     graph = Qwen2LM(dparams, cfg, max_ctx=128)
     o = orc.Qwen2(params, cfg, cap=128)
     n0 = 62
@@ -170,15 +166,11 @@ def test_decode_crosses_split_classes(gpu, qwen, max_ctx, n0):
     bit-identical between graph replay and eager launches and track the oracle.
     With max_ctx 300 the cache holds 5 splits, fewer than the 8 the second class
     covers, so the merge clamps to the splits that exist."""
-    import os
     from larynx_amd.llm import Qwen2LM
     cfg, params, dparams, _ = qwen
     announce(f"qwen2 decode across split classes, max_ctx {max_ctx}, cache {n0}..{n0 + 5}")
-    os.environ["LX_DECODE_GRAPH"] = "0"
-    try:
-        eager = Qwen2LM(dparams, cfg, max_ctx=max_ctx)
-    finally:
-        del os.environ["LX_DECODE_GRAPH"]
+    eager = Qwen2LM(dparams, cfg, max_ctx=max_ctx)
+    eager.set_decode_graph(False)
     graph = Qwen2LM(dparams, cfg, max_ctx=max_ctx)
     o = orc.Qwen2(params, cfg, cap=max_ctx)
     for layer in range(cfg.n_layers):
