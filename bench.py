@@ -111,6 +111,17 @@ def splitk_slices(M, N, K, target_wgs=512, max_slices=8):
     return (K + ks - 1) // ks
 
 
+def prefill_bx_slices(rows, N, K):
+    """K slices of a Qwen2 prefill projection on the fragment-order GEMM
+    (prefill_bx_slices in larynx_amd/csrc/lx_qwen2.cpp): at most 9 and at most
+    256 / (64-row tiles), then the fewest with the same longest slice."""
+    steps = K // 64
+    tiles = ((rows + 63) // 64) * (N // 128)
+    most = min(9, steps, max(1, 256 // tiles))
+    per = -(-steps // most)
+    return -(-steps // per)
+
+
 def event_time_ms(fn, n, torch):
     """Average ms per call of fn over n calls, HIP events on torch's current
     stream (the stream every liblxops call of this script is enqueued on)."""
@@ -504,9 +515,9 @@ def qwen2_lm(torch, dev, g):
     L, H, KVW = lm_in.shape[0], cfg.hidden, cfg.n_kv_heads * cfg.head_dim
     NQKV = H + 2 * KVW
     rec = profiled_kernels(torch, lambda: lm.prefill(lm_in))
-    s_o = splitk_slices(L, H, H)
-    s_d = splitk_slices(L, H, cfg.intermediate)
-    s_q = splitk_slices(L, NQKV, H)
+    s_o = prefill_bx_slices(L, H, H)
+    s_d = prefill_bx_slices(L, H, cfg.intermediate)
+    s_q = prefill_bx_slices(L, NQKV, H)
     # o_proj and down_proj reduce passes alternate within a layer
     rr = [(s + 3) * L * H * 4 + H * 4 for s in (s_o, s_d)]
     out["in_path"] = {

@@ -231,11 +231,13 @@ int lx_linear_split_f32(const float* x, int ldx, const void* planes, const float
  * A is fp32 (M, K) with row stride lda.  Outputs:
  *   LX_BX_OUT_F32      Y = epi(A @ W^T + bias) (row stride ldy), every
  *                      lx_epilogue kind (SWIGLU_PAIRED: N / 2 columns);
- *   LX_BX_OUT_PARTIAL  the raw products of `slices` equal K slices, slice s
- *                      into Y + s * slice_stride (no bias, no epilogue): the
- *                      consumer sums the slices in slice order.
- * Tiles of bm (128 or 64) rows x 128 columns: N a multiple of 128, K / slices
- * a multiple of 64; A, Wf, Y, bias and the gate 16-byte aligned.
+ *   LX_BX_OUT_PARTIAL  the raw products of `slices` K slices, slice s into
+ *                      Y + s * slice_stride (no bias, no epilogue): the
+ *                      consumer sums the slices in slice order.  Each slice
+ *                      spans ceil(K / 64 / slices) 64-wide steps, the last
+ *                      the remainder, which must not be empty.
+ * Tiles of bm (128 or 64) rows x 128 columns: N a multiple of 128, K of 64;
+ * A, Wf, Y, bias and the gate 16-byte aligned.
  * Optional stream-K scratch (OUT_F32): with ws (at least 2 * CUs * bm * 128
  * floats, CUs = 256 on MI355X) and counters (one per output tile, zeroed once
  * by the caller and left zeroed by every call), one workgroup per compute unit

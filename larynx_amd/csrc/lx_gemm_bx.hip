@@ -125,8 +125,12 @@ gemm_bx_kernel(BxArgs a, EpiArgs ep) {
     if (w < full) w = (w % 8) * (full / 8) + w / 8;
   }
   const long U = (long)tiles * npt;
+  // data-parallel: one tile per workgroup, its slice's slab pairs (the last
+  // slice may hold fewer); stream-K (one slice): an equal share of all of them
+  const int tile_pairs =
+      min(npt, a.K / (2 * kBxBK) - (w / (a.tiles_m * a.tiles_n)) * npt);
   const long u0 = a.streamk ? (long)w * U / G : (long)w * npt;
-  const long u1 = a.streamk ? (long)(w + 1) * U / G : u0 + npt;
+  const long u1 = a.streamk ? (long)(w + 1) * U / G : u0 + tile_pairs;
   constexpr int SLAB_BYTES = kBxBK * 4;  // A bytes per row per slab
   // A fragments: row block i, plane p, k step st of a slab buffer
   const int aoff = fr * kBxBK;
@@ -553,9 +557,12 @@ int linear_bx(const lx_linear_bx& g, hipStream_t stream) {
   int kslice = g.K;
   if (slices > 1) {
     LX_REQUIRE(g.out == BX_OUT_PARTIAL, "linear_bx: K slices need the partial output");
-    LX_REQUIRE(g.K % (slices * 2 * kBxBK) == 0,
-               "linear_bx: K=%d is not %d slices of an even number of 32-wide slabs", g.K, slices);
-    kslice = g.K / slices;
+    // slices of ceil(pairs / slices) 64-wide steps, the last one the rest
+    const int pairs = g.K / (2 * kBxBK), per = (pairs + slices - 1) / slices;
+    LX_REQUIRE((slices - 1) * per < pairs,
+               "linear_bx: K=%d leaves slice %d of %d empty (slices of %d 64-wide steps)", g.K,
+               slices - 1, slices, per);
+    kslice = per * 2 * kBxBK;
   }
   EpiArgs ep;
   int rc = make_epi(g.epi, g.N, &ep);

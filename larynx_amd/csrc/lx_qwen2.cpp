@@ -35,16 +35,17 @@ struct Layer {
 };
 
 // K slices of a prefill projection on the fragment-order GEMM (64-row tiles):
-// the largest divisor of its 64-wide K steps, at most 9 (the reduce passes' bound),
-// whose tiles times slices stay within one workgroup per CU.  L = 256: q|k|v and
-// o_proj 7 slices (252 / 196 workgroups), down_proj 4 (112); L = 1024: 1 / 2 / 2.
+// as many as the reduce passes take (9) while tiles x slices stay within one
+// workgroup per CU, then the fewest that keep the same longest slice (slices
+// of ceil(steps / slices) 64-wide steps).  L = 256: q|k|v 7 slices of 2 steps
+// (252 workgroups), o_proj 7 of 2 (196), down_proj 9 of 9 (252); L = 1024:
+// 1 / 2 / 2.
 int prefill_bx_slices(int rows, int N, int K) {
   const int steps = K / 64;
   const long tiles = (long)((rows + 63) / 64) * (N / 128);
-  int best = 1;
-  for (int d = 1; d <= 9 && d <= steps; ++d)
-    if (steps % d == 0 && tiles * d <= 256) best = d;
-  return best;
+  int most = (int)std::min<long>(std::min(9, steps), std::max<long>(1, 256 / tiles));
+  const int per = (steps + most - 1) / most;
+  return (steps + per - 1) / per;
 }
 
 }  // namespace

@@ -111,20 +111,25 @@ def test_linear_bx_epilogues(gpu, ops, T, bm, sk):
     assert orc.rel_err(hd.cpu().numpy(), refg) < TOL
 
 
-@pytest.mark.parametrize("M,K,slices,bm", [(1000, 1024, 2, 64), (1000, 2048, 2, 64),
-                                           (1000, 2048, 4, 128), (45, 1024, 2, 64)])
-def test_linear_bx_partial_slices(gpu, ops, M, K, slices, bm):
-    """K slices written as raw partial products: each slice is its own K range's
-    product, and their sum is the whole one."""
-    announce(f"linear_bx partial M={M} K={K} slices={slices} bm={bm}")
-    N = 1024
+@pytest.mark.parametrize("M,N,K,slices,bm", [
+    (1000, 1024, 1024, 2, 64), (1000, 1024, 2048, 2, 64), (1000, 1024, 2048, 4, 128),
+    (45, 1024, 1024, 2, 64),
+    # the Qwen2 L=256 prefill plans: o_proj 14 steps as 7 x 2, down_proj 76 steps
+    # as 8 x 9 + 4 (ragged last slice), and 3 steps over 2 slices
+    (256, 896, 896, 7, 64), (256, 896, 4864, 9, 64), (70, 128, 192, 2, 128)])
+def test_linear_bx_partial_slices(gpu, ops, M, N, K, slices, bm):
+    """K slices written as raw partial products: slice s is the product over its
+    K range (ceil(K / 64 / slices) 64-wide steps each, the last the rest), and
+    their sum is the whole one."""
+    announce(f"linear_bx partial M={M} N={N} K={K} slices={slices} bm={bm}")
     x, W = rnd((M, K), 15), rnd((N, K), 16, 0.03)
     P = ops.linear_bx(dev(x, gpu), ops.wfrag_pack(dev(W, gpu)), N,
                       out_kind=ops.LX_BX_OUT_PARTIAL, slices=slices, bm=bm).cpu().numpy()
-    ks = K // slices
+    ks = -(-(K // 64) // slices) * 64
+    assert (slices - 1) * ks < K
     x64, W64 = x.astype(np.float64), W.astype(np.float64)
     for s in range(slices):
-        ref = x64[:, s * ks:(s + 1) * ks] @ W64[:, s * ks:(s + 1) * ks].T
+        ref = x64[:, s * ks:min(K, (s + 1) * ks)] @ W64[:, s * ks:min(K, (s + 1) * ks)].T
         assert np.abs(P[s] - ref).max() / np.abs(ref).max() < FP32_LEVEL
     ref = x64 @ W64.T
     assert np.abs(P.astype(np.float64).sum(0) - ref).max() / np.abs(ref).max() < FP32_LEVEL
@@ -153,7 +158,7 @@ def test_linear_bx_rejects_bad_arguments(gpu, ops):
     wf = ops.wfrag_pack(torch.zeros(128, 128, device=gpu))
     with pytest.raises(LxError):
         ops.linear_bx(x, wf, 128, bm=32)
-    with pytest.raises(LxError):
+    with pytest.raises(LxError):  # 2 steps of 64 leave a third slice empty
         ops.linear_bx(x, wf, 128, out_kind=ops.LX_BX_OUT_PARTIAL, slices=3)
     with pytest.raises(LxError):  # K slices only with the partial output
         ops.linear_bx(x, wf, 128, slices=2)
