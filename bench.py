@@ -10,10 +10,13 @@ Also reported on the same JSON line:
   roofline      the dominant kernel's achieved fp32 FLOP/s (HIP events around graph
                 replays of its launches under continuous load, on the replay stream)
                 vs the 157.3 TFLOP/s fp32 matrix peak (for a split-operand kernel,
-                which forms each fp32 product from six bf16 MFMA products, also the
-                bf16 MFMA flops executed vs the 2.5 PFLOP/s dense bf16 peak, as
+                which forms each fp32 product from three (projections, the
+                estimator's default) or six (attention) bf16 MFMA products, also
+                the bf16 MFMA flops executed vs the 2.5 PFLOP/s dense bf16 peak, as
                 bf16_pipe), and its HBM traffic per launch from the committed
                 rocprofv3 FETCH_SIZE / WRITE_SIZE summary;
+  six_products  the same timed steps with the block projections on the six-product
+                split (fp32-GEMM error level; lx_dit_set_products(dit, 6));
   kernels       per-kernel-class timings of one step's launches (same method), each
                 class on the kernel the estimator runs for it;
   fused_ops     achieved HBM GB/s of every fused op at the configs' shapes, with
@@ -39,7 +42,10 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0
 MFMA_F32_PEAK_TFLOPS = 157.3
 MFMA_BF16_PEAK_TFLOPS = 2500.0
-SPLIT_PRODUCTS = 6  # bf16 MFMA products per fp32 product in the split-operand kernels
+# bf16 MFMA products per fp32 product: the estimator's projections (its default,
+# lx_dit.cpp `products`) and the split-operand attention
+DIT_PRODUCTS = 3
+ATTN_PRODUCTS = 6
 
 
 def parse():
@@ -256,12 +262,15 @@ def gemm_kernels(torch, ops, T, dev):
         wf = ops.wfrag_pack(W)
         kind, sl = dit_projection_plan(M, N)
         fp32 = (lambda: ops.linear(x, W, b, ep, out=y))
-        if kind == "partial":
-            return ((lambda: ops.linear_bx(x, wf, N, out=part, out_kind=ops.LX_BX_OUT_PARTIAL,
-                                           bm=64, slices=sl)),
-                    f"gemm_bx_kernel 64x128, {sl} K slices (sum folded into adaln_resid)", fp32)
-        return ((lambda: ops.linear_bx(x, wf, N, b, ep, out=y, bm=64)), "gemm_bx_kernel 64x128",
-                fp32)
+
+        def bx(products):
+            if kind == "partial":
+                return lambda: ops.linear_bx(x, wf, N, out=part, out_kind=ops.LX_BX_OUT_PARTIAL,
+                                             bm=64, slices=sl, products=products)
+            return lambda: ops.linear_bx(x, wf, N, b, ep, out=y, bm=64, products=products)
+        kern = (f"gemm_bx_kernel 64x128, {DIT_PRODUCTS} products"
+                + (f", {sl} K slices (sum folded into adaln_resid)" if kind == "partial" else ""))
+        return bx(DIT_PRODUCTS), kern, fp32, bx(6)
     cases = {
         "gemm_qkv_rope": (proj(xd, wq, bq, rope, qkv), 2 * M * 3 * D * D, 1),
         "gemm_out_gated": (proj(xd, wo, bd, gated, hv), 2 * M * D * D, 1),
@@ -269,7 +278,7 @@ def gemm_kernels(torch, ops, T, dev):
         "gemm_ff2_gated": (proj(xf, w2, bd, gated, hv), 2 * M * D * F, 1),
         "attention": ((lambda: ops.attention(qv[..., :D], qv[..., D:2 * D], qv[..., 2 * D:], 16,
                                              out=att), "attn_bx_kernel / attn_flash_kernel",
-                       None),
+                       None, None),
                       4 * B * 16 * T * T * 64, 1),
     }
     # hipBLASLt (torch.mm, fp32) on the same plain-GEMM shapes, as a library reference point
@@ -279,12 +288,14 @@ def gemm_kernels(torch, ops, T, dev):
         "gemm_ff0_gelu": lambda: torch.mm(xd, w1.T),
         "gemm_ff2_gated": lambda: torch.mm(xf, w2.T),
     }
-    for name, ((fn, kern, fp32_fn), flops, per_block) in cases.items():
+    for name, ((fn, kern, fp32_fn, six_fn), flops, per_block) in cases.items():
         ms = steady_launch_ms(fn, torch)
         out[name] = {"avg_us": ms * 1e3, "flop": flops, "tflops": flops / (ms * 1e-3) / 1e12,
                      "per_block": per_block, "kernel": kern}
         if fp32_fn is not None:  # the fp32 kernel on the same class, for comparison
             out[name]["fp32_kernel_us"] = steady_launch_ms(fp32_fn, torch) * 1e3
+        if six_fn is not None:  # the six-product split on the same class
+            out[name]["six_products_us"] = steady_launch_ms(six_fn, torch) * 1e3
         if name in lib_ref:
             try:
                 out[name]["hipblaslt_us"] = steady_launch_ms(lib_ref[name], torch) * 1e3
@@ -511,7 +522,17 @@ def qwen2_lm(torch, dev, g):
         lm.prefill(lm_in)
     torch.cuda.synchronize()
     prefill_ms = (time.perf_counter() - t0) * 1e3 / 3
-    out = {"prefill_L256_ms": round(prefill_ms, 3), "decode_ms_per_token": {}}
+    lm.set_products(6)  # the six-product split on the same prefill, for comparison
+    lm.prefill(lm_in)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(3):
+        lm.prefill(lm_in)
+    torch.cuda.synchronize()
+    six_ms = (time.perf_counter() - t0) * 1e3 / 3
+    lm.set_products(3)
+    out = {"prefill_L256_ms": round(prefill_ms, 3), "prefill_products": 3,
+           "prefill_L256_ms_six_products": round(six_ms, 3), "decode_ms_per_token": {}}
     L, H, KVW = lm_in.shape[0], cfg.hidden, cfg.n_kv_heads * cfg.head_dim
     NQKV = H + 2 * KVW
     rec = profiled_kernels(torch, lambda: lm.prefill(lm_in))
@@ -629,13 +650,15 @@ def counter_probe(torch, ops, launches=20):
     part = torch.empty(2, M, D, device=dev)
     torch.cuda.synchronize()
     for _ in range(launches):
-        ops.linear_bx(xd, fq, 3 * D, bq, rope, out=qkv, bm=64)
+        ops.linear_bx(xd, fq, 3 * D, bq, rope, out=qkv, bm=64, products=DIT_PRODUCTS)
     for _ in range(launches):
-        ops.linear_bx(xd, f0, F, b0, gelu, out=ff, bm=64)
+        ops.linear_bx(xd, f0, F, b0, gelu, out=ff, bm=64, products=DIT_PRODUCTS)
     for _ in range(launches):
-        ops.linear_bx(xd, fo, D, out=part, out_kind=ops.LX_BX_OUT_PARTIAL, bm=64, slices=2)
+        ops.linear_bx(xd, fo, D, out=part, out_kind=ops.LX_BX_OUT_PARTIAL, bm=64, slices=2,
+                      products=DIT_PRODUCTS)
     for _ in range(launches):
-        ops.linear_bx(ff, f2, D, out=part, out_kind=ops.LX_BX_OUT_PARTIAL, bm=64, slices=2)
+        ops.linear_bx(ff, f2, D, out=part, out_kind=ops.LX_BX_OUT_PARTIAL, bm=64, slices=2,
+                      products=DIT_PRODUCTS)
     for _ in range(launches):
         ops.attention(q3[..., :D], q3[..., D:2 * D], q3[..., 2 * D:], 16, 16, out=att)
     torch.cuda.synchronize()
@@ -689,7 +712,7 @@ def traffic_probe(torch, ops, launches=20):
     fq = ops.wfrag_pack(wq)
     torch.cuda.synchronize()
     for _ in range(launches):
-        ops.linear_bx(xd, fq, 3 * D, bq, rope, out=qkv, bm=64)
+        ops.linear_bx(xd, fq, 3 * D, bq, rope, out=qkv, bm=64, products=DIT_PRODUCTS)
     torch.cuda.synchronize()
     for _ in range(launches):
         dst.copy_(src)
@@ -780,6 +803,16 @@ def main():
     ms_per_step = wall * 1e3 / args.steps
     value = T * args.steps / wall
 
+    # the same timed steps with the six-product projections (fp32-GEMM error level)
+    est.set_products(6)
+    run_steps(args.warmup)
+    torch.cuda.synchronize()
+    t6 = time.perf_counter()
+    run_steps(args.steps)
+    torch.cuda.synchronize()
+    six_ms_per_step = (time.perf_counter() - t6) * 1e3 / args.steps
+    est.set_products(DIT_PRODUCTS)
+
     # one 10-step solve (the reference's whole CFM loop), and 10 single steps
     # (each with its own time MLP and modulation GEMV), at the same shape
     torch.cuda.synchronize()
@@ -824,13 +857,14 @@ def main():
                 "traffic": (committed_traffic()
                             if dom_name == "gemm_qkv_rope" and T == 500 else None),
                 "avg_us": round(dom["avg_us"], 2), "flop_per_launch": dom["flop"]}
-    if dom["kernel"].startswith(("gemm_bx_kernel", "gemm_split_kernel", "attn_bx_kernel")):
-        # the same work as executed: six bf16 MFMA products per fp32 product,
-        # against the dense bf16 peak
-        bf = SPLIT_PRODUCTS * dom["tflops"]
+    if dom["kernel"].startswith(("gemm_bx_kernel", "attn_bx_kernel")):
+        # the same work as executed: bf16 MFMA products per fp32 product, against
+        # the dense bf16 peak
+        npr = DIT_PRODUCTS if dom["kernel"].startswith("gemm_bx_kernel") else ATTN_PRODUCTS
+        bf = npr * dom["tflops"]
         roofline["bf16_pipe"] = {"achieved": round(bf, 3), "peak": MFMA_BF16_PEAK_TFLOPS,
                                  "frac": round(bf / MFMA_BF16_PEAK_TFLOPS, 4),
-                                 "note": "six bf16 MFMA products per fp32 product"}
+                                 "note": f"{npr} bf16 MFMA products per fp32 product"}
     if "fp32_kernel_us" in dom:  # the fp32 matrix-core GEMM on the same class, for reference
         f32 = dom["flop"] / (dom["fp32_kernel_us"] * 1e-6) / 1e12
         roofline["fp32_kernel"] = {"impl": "gemm_pipe_kernel",
@@ -874,9 +908,15 @@ def main():
         "single_step_ms": round(single_step_ms, 4),
         "step_tflops": round(gemm_flop_step / (ms_per_step * 1e-3) / 1e12, 2),
         "roofline": roofline,
+        "products": DIT_PRODUCTS,
+        "six_products": {"ms_per_step": round(six_ms_per_step, 4),
+                         "value": round(T / (six_ms_per_step * 1e-3), 1),
+                         "note": "same steps, block projections as six bf16 products per "
+                                 "fp32 product (fp32-GEMM error level)"},
         "kernels": {k: {kk: (round(vv, 2) if kk != "kernel" else vv)
                         for kk, vv in v.items() if kk in
-                        ("avg_us", "tflops", "hipblaslt_us", "kernel", "fp32_kernel_us", "gbs")}
+                        ("avg_us", "tflops", "hipblaslt_us", "kernel", "fp32_kernel_us", "gbs",
+                         "six_products_us")}
                     for k, v in kernels.items()},
         "long_utterance": long_t,
         "flow_infer": flow,

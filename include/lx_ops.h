@@ -244,6 +244,11 @@ int lx_linear_split_f32(const float* x, int ldx, const void* planes, const float
  * takes an equal share of the tiles' k range; a tile shared by several
  * workgroups is summed by the last to finish, in k order (deterministic, no
  * waiting).  Calls sharing one ws / counters pair must not overlap.
+ * products: 6 (or 0) forms each element pair as the six products of the
+ * three-part splits (fp32-level error, the default); 3 uses two-part splits
+ * (x0 + x1, 16 significant bits each) and the three products a0 b0 + a0 b1 +
+ * a1 b0: half the matrix-core work and two thirds of the W traffic, each
+ * product within about 2^-16 of a * b (the packed weight is the same).
  * Replaces linear() = ggml_mul_mat + ggml_add (src/flow/ops.cpp:20-26) with the
  * node its epilogue absorbs; the fragment-ordered weight has no counterpart
  * in the reference (its weights stay fp32). */
@@ -264,6 +269,7 @@ typedef struct lx_linear_bx {
   size_t ws_floats;
   unsigned* counters;
   int n_counters;
+  int products;
 } lx_linear_bx;
 int lx_wfrag_pack_f32(const float* W, void* Wf, int N, int K, hipStream_t stream);
 int lx_linear_bx_f32(const lx_linear_bx* g, hipStream_t stream);
@@ -362,6 +368,15 @@ typedef struct lx_dit_capture {
   float* blocks; float* norm_out;
 } lx_dit_capture;
 int lx_dit_set_capture(lx_dit* dit, const lx_dit_capture* cap);
+
+/* Arithmetic of the block projections (q|k|v, out, FF0, FF2) on the
+ * fragment-order split-operand GEMM (lx_linear_bx): products = 3 (the default:
+ * two bf16 parts per operand, a0 b0 + a0 b1 + a1 b0; max relative error about
+ * 5e-6 per projection at B = 2, T = 500) or 6 (three parts, i + j <= 2: about
+ * 1.3e-6, the level of an fp32 GEMM, at 1.4-1.55x the projection time).
+ * Attention keeps its six-product split either way.  No counterpart in the
+ * reference, whose ggml projections are fp32 SGEMM (src/flow/ops.cpp:20-26). */
+int lx_dit_set_products(lx_dit* dit, int products);
 
 /* Full CFM Euler solve with classifier-free guidance, device resident
  * (CausalConditionalCFM.solve_euler; src/flow/flow.cpp:202-274):
@@ -504,6 +519,11 @@ int lx_qwen2_decode(lx_qwen2* m, int token, float* logits, float* final_norm,
  * two bit for bit).  No counterpart in the reference, which rebuilds its ggml
  * graph every step (src/llm/llm.cpp:232-275). */
 int lx_qwen2_set_decode_graph(lx_qwen2* m, int enable);
+
+/* Prefill projections' split-operand products, 3 (the default) or 6, as
+ * lx_dit_set_products (decode's GEMVs are fp32 either way).  No counterpart
+ * in the reference (src/llm/llm.cpp:141-173 runs fp32 ggml_mul_mat). */
+int lx_qwen2_set_products(lx_qwen2* m, int products);
 
 /* LLM::cache_len / cache_key / cache_value (include/larynx/llm/llm.h:77-84).
  * The cache of layer l is (cache_len, n_kv_heads * head_dim) roped keys /

@@ -60,7 +60,7 @@ class LinearBx(C.Structure):
         ("epi", C.POINTER(Epilogue)), ("out", C.c_int), ("Y", fp), ("ldy", C.c_long),
         ("slice_stride", C.c_long), ("M", C.c_int), ("N", C.c_int), ("K", C.c_int),
         ("bm", C.c_int), ("slices", C.c_int), ("ws", fp), ("ws_floats", C.c_size_t),
-        ("counters", C.c_void_p), ("n_counters", C.c_int),
+        ("counters", C.c_void_p), ("n_counters", C.c_int), ("products", C.c_int),
     ]
 
 
@@ -164,6 +164,7 @@ SIGNATURES = [
     ("lx_dit_destroy", None, [C.c_void_p]),
     ("lx_dit_forward", C.c_int, [C.c_void_p, fp, fp, fp, fp, fp, fp, C.c_int, stream_t]),
     ("lx_dit_set_capture", C.c_int, [C.c_void_p, C.POINTER(DitCapture)]),
+    ("lx_dit_set_products", C.c_int, [C.c_void_p, C.c_int]),
     ("lx_cfm_solve", C.c_int,
      [C.c_void_p, fp, fp, fp, fp, C.c_int, C.c_int, C.c_float, stream_t]),
     ("lx_cfm_step", C.c_int,
@@ -199,6 +200,7 @@ SIGNATURES = [
     ("lx_qwen2_cache_value", C.c_void_p, [C.c_void_p, C.c_int]),
     ("lx_qwen2_set_cache_len", C.c_int, [C.c_void_p, C.c_int]),
     ("lx_qwen2_set_decode_graph", C.c_int, [C.c_void_p, C.c_int]),
+    ("lx_qwen2_set_products", C.c_int, [C.c_void_p, C.c_int]),
 ]
 
 

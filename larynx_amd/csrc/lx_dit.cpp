@@ -58,6 +58,7 @@ struct lx_dit {
   // split-operand GEMM; otherwise (a width the fragment tiles do not cover)
   // as fp32 for lx_linear_f32.  QKV is fused into one (3D, D) matrix.
   bool frag = false;
+  int products = 3;  // split-operand products per element pair (3 or 6)
   std::vector<void*> qkv_wf, out_wf, ff0_wf, ff2_wf;
   std::vector<float*> qkv_w, out_w, ff0_w, ff2_w;
   std::vector<float*> qkv_b, out_b, ff0_b, ff2_b;
@@ -179,6 +180,7 @@ int forward_core(lx_dit* m, const float* x, long x_bstride, const float* mu, con
     g.K = K;
     g.bm = 64;
     g.slices = 1;
+    g.products = m->products;
     return linear_bx(g, s);
   };
   // y (the residual stream h) += gate * (x W^T + bias), directly or as pending K slices
@@ -205,6 +207,7 @@ int forward_core(lx_dit* m, const float* x, long x_bstride, const float* mu, con
     g.K = K;
     g.bm = 64;
     g.slices = 2;
+    g.products = m->products;
     LX_TRY(linear_bx(g, s));
     pend.bias = bias;
     pend.gate = gate;
@@ -474,6 +477,13 @@ extern "C" int lx_dit_set_capture(lx_dit* dit, const lx_dit_capture* cap) {
     dit->cap = *cap;
   else
     dit->cap = lx_dit_capture{};
+  return LX_OK;
+}
+
+extern "C" int lx_dit_set_products(lx_dit* dit, int products) {
+  LX_REQUIRE(dit, "dit_set_products: null estimator");
+  LX_REQUIRE(products == 3 || products == 6, "dit_set_products: %d products (3 or 6)", products);
+  dit->products = products;
   return LX_OK;
 }
 

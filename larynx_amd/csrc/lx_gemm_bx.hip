@@ -40,10 +40,13 @@ constexpr int kBxBN = 32 * kBxWaves;  // columns per workgroup
 constexpr int kBxBK = 32;             // k per slab: two 16-wide MFMA k steps
 constexpr int kBxBufs = 4;            // A slab buffers
 
-template <int BMB>
+// NP products per element pair: 6 (three parts each, i + j <= 2) or 3 (two
+// parts each: a0 b0 + a0 b1 + a1 b0); NP / 2 + 1 bf16 planes per operand.
+template <int BMB, int NP>
 struct BxCfg {
   static constexpr int BM = 32 * BMB;
-  static constexpr int ABUF = 3 * BM * kBxBK;  // bf16 per A slab buffer (three planes)
+  static constexpr int NPL = NP == 6 ? 3 : 2;
+  static constexpr int ABUF = NPL * BM * kBxBK;  // bf16 per A slab buffer (NPL planes)
   static constexpr size_t lds_k = (size_t)kBxBufs * ABUF * 2;
   static constexpr size_t lds_c = (size_t)BM * (kBxBN + 4) * 4;
   static constexpr size_t lds = lds_k > lds_c ? lds_k : lds_c;
@@ -99,12 +102,12 @@ __device__ __forceinline__ int bx_owner(long p, long U, int G) {
 #ifndef LX_BX_WAVES64
 #define LX_BX_WAVES64 2
 #endif
-template <int EPI, int BMB, int OUT>
+template <int EPI, int BMB, int OUT, int NP>
 __global__ __launch_bounds__(kBxThreads) __attribute__((amdgpu_waves_per_eu(
     BMB == 2 ? LX_BX_WAVES64 : 1, BMB == 2 ? LX_BX_WAVES64 : 1))) void
 gemm_bx_kernel(BxArgs a, EpiArgs ep) {
-  using Cfg = BxCfg<BMB>;
-  constexpr int BM = Cfg::BM, ABUF = Cfg::ABUF;
+  using Cfg = BxCfg<BMB, NP>;
+  constexpr int BM = Cfg::BM, ABUF = Cfg::ABUF, NPL = Cfg::NPL;
   constexpr int LA = 8 * BM / kBxThreads;  // A float4 per thread per slab
   static_assert(LA * kBxThreads == 8 * BM, "staging slots");
   constexpr int SLOTS = BM * kBxBN / 4 / kBxThreads;  // epilogue float4 slots per thread
@@ -135,9 +138,10 @@ gemm_bx_kernel(BxArgs a, EpiArgs ep) {
   // A fragments: row block i, plane p, k step st of a slab buffer
   const int aoff = fr * kBxBK;
   const int fc0 = split_col(fr, fh * 8), fc1 = split_col(fr, 16 + fh * 8);
-  // The six products (A part, W part) in the order of mfma_split6x: the small
-  // terms first.
-  constexpr int kPa[6] = {2, 1, 0, 1, 0, 0}, kPw[6] = {0, 1, 2, 0, 1, 0};
+  // The products (A part, W part), the small terms first: six as in
+  // mfma_split6x, or the three of the two-part splits.
+  constexpr int kPa6[6] = {2, 1, 0, 1, 0, 0}, kPw6[6] = {0, 1, 2, 0, 1, 0};
+  constexpr int kPa3[3] = {1, 0, 0}, kPw3[3] = {0, 1, 0};
   const __amdgpu_buffer_rsrc_t prs =
       __builtin_amdgcn_make_buffer_rsrc(a.ws, (short)0, a.ws_bytes, 0x00020000);
   constexpr int kSc1 = 16;  // cache-policy bits: sc1 = device scope
@@ -182,10 +186,10 @@ gemm_bx_kernel(BxArgs a, EpiArgs ep) {
 #pragma unroll
       for (int i = 0; i < LA; ++i) {
         bf16x4_t x0, x1, x2;
-        split3(g[i], x0, x1, x2);
+        split3(g[i], x0, x1, x2);  // (x2 is dead code with two planes)
         *reinterpret_cast<bf16x4_t*>(base + sa[i]) = x0;
         *reinterpret_cast<bf16x4_t*>(base + BM * kBxBK + sa[i]) = x1;
-        *reinterpret_cast<bf16x4_t*>(base + 2 * BM * kBxBK + sa[i]) = x2;
+        if (NPL == 3) *reinterpret_cast<bf16x4_t*>(base + 2 * BM * kBxBK + sa[i]) = x2;
       }
     };
     // W fragments of this wave's 32 columns: k step ks, plane p at wf + (ks * 3 + p) * 512;
@@ -196,7 +200,7 @@ gemm_bx_kernel(BxArgs a, EpiArgs ep) {
     const int wl = lane * 16;
     auto load_w = [&](uintx4_t* wv, int s, int st) {
 #pragma unroll
-      for (int j = 0; j < 3; ++j)
+      for (int j = 0; j < NPL; ++j)
         wv[j] = *reinterpret_cast<const uintx4_t*>(wf + wl + (s * 6 + st * 3 + j) * 1024);
     };
     auto read_a = [&](uintx4_t (*f)[3], int buf, int st) {
@@ -204,7 +208,7 @@ gemm_bx_kernel(BxArgs a, EpiArgs ep) {
 #pragma unroll
       for (int i = 0; i < BMB; ++i)
 #pragma unroll
-        for (int p = 0; p < 3; ++p)
+        for (int p = 0; p < NPL; ++p)
           f[i][p] = *reinterpret_cast<const uintx4_t*>(base + p * BM * kBxBK + i * 32 * kBxBK);
     };
 #pragma unroll
@@ -213,11 +217,12 @@ gemm_bx_kernel(BxArgs a, EpiArgs ep) {
       for (int e = 0; e < 16; ++e) acc[i][e] = 0.0f;
     auto mul = [&](uintx4_t (*f)[3], const uintx4_t* wv) {
 #pragma unroll
-      for (int q = 0; q < 6; ++q)
+      for (int q = 0; q < NP; ++q)
 #pragma unroll
         for (int i = 0; i < BMB; ++i)
-          acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(f[i][kPa[q]]),
-                                                           as_bf16x8(wv[kPw[q]]), acc[i], 0, 0, 0);
+          acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+              as_bf16x8(f[i][NP == 6 ? kPa6[q] : kPa3[q]]),
+              as_bf16x8(wv[NP == 6 ? kPw6[q] : kPw3[q]]), acc[i], 0, 0, 0);
     };
     // Registers: A fragments of the two k steps (fa0, fa1); the W fragments of
     // four slabs (slab s in set s % 4: k step 0's three planes, then k step
@@ -264,9 +269,9 @@ gemm_bx_kernel(BxArgs a, EpiArgs ep) {
     // k step 0 fragment reads and the W of slab s + 3 (into slab s - 1's
     // register set).  The group barriers interleave one memory instruction per
     // MFMA so that the matrix pipe keeps issuing while they go out.
-    constexpr int NM = 6 * BMB;            // MFMAs per k step
-    constexpr int NR = 3 * BMB;            // fragment reads per k step
-    constexpr int NW = 3 * LA;             // staging LDS stores
+    constexpr int NM = NP * BMB;           // MFMAs per k step
+    constexpr int NR = NPL * BMB;          // fragment reads per k step
+    constexpr int NW = NPL * LA;           // staging LDS stores
     auto body = [&](int s, int b, uintx4_t* wc, uintx4_t* wn, floatx4* g) {
       read_a(fa1, b, 1);
       store_a(g, (b + 3) & 3);
@@ -300,7 +305,7 @@ gemm_bx_kernel(BxArgs a, EpiArgs ep) {
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
       }
 #pragma unroll
-      for (int i = 0; i < 6; ++i) {
+      for (int i = 0; i < 2 * NPL; ++i) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
         __builtin_amdgcn_sched_group_barrier(0x020, 1, 1);  // VMEM read (W)
       }
@@ -501,11 +506,11 @@ int device_cus() {
   return cus[dev];
 }
 
-template <int EPI, int BMB, int OUT>
+template <int EPI, int BMB, int OUT, int NP>
 int launch_bx(const BxArgs& a, const EpiArgs& ep, hipStream_t stream) {
-  auto kern = gemm_bx_kernel<EPI, BMB, OUT>;
+  auto kern = gemm_bx_kernel<EPI, BMB, OUT, NP>;
   static LdsLimit once;
-  const size_t lds = BxCfg<BMB>::lds;
+  const size_t lds = BxCfg<BMB, NP>::lds;
   int rc = raise_lds_limit((const void*)kern, lds, once, "linear_bx");
   if (rc) return rc;
   const long nwg = a.streamk ? a.grid : (long)a.tiles_m * a.tiles_n * a.slices;
@@ -513,17 +518,18 @@ int launch_bx(const BxArgs& a, const EpiArgs& ep, hipStream_t stream) {
   return check_launch("gemm_bx_kernel");
 }
 
-template <int BMB>
+template <int BMB, int NP>
 int dispatch_bx(const BxArgs& a, int out, const EpiArgs& ep, hipStream_t s) {
-  if (out == BX_OUT_PARTIAL) return launch_bx<LX_EPI_NONE, BMB, BX_OUT_PARTIAL>(a, ep, s);
+  if (out == BX_OUT_PARTIAL) return launch_bx<LX_EPI_NONE, BMB, BX_OUT_PARTIAL, NP>(a, ep, s);
   switch (ep.kind) {
-    case LX_EPI_NONE: return launch_bx<LX_EPI_NONE, BMB, BX_OUT_F32>(a, ep, s);
-    case LX_EPI_GELU_TANH: return launch_bx<LX_EPI_GELU_TANH, BMB, BX_OUT_F32>(a, ep, s);
-    case LX_EPI_GATED_RESID: return launch_bx<LX_EPI_GATED_RESID, BMB, BX_OUT_F32>(a, ep, s);
-    case LX_EPI_ROPE_PARTIAL: return launch_bx<LX_EPI_ROPE_PARTIAL, BMB, BX_OUT_F32>(a, ep, s);
-    case LX_EPI_RESID: return launch_bx<LX_EPI_RESID, BMB, BX_OUT_F32>(a, ep, s);
+    case LX_EPI_NONE: return launch_bx<LX_EPI_NONE, BMB, BX_OUT_F32, NP>(a, ep, s);
+    case LX_EPI_GELU_TANH: return launch_bx<LX_EPI_GELU_TANH, BMB, BX_OUT_F32, NP>(a, ep, s);
+    case LX_EPI_GATED_RESID: return launch_bx<LX_EPI_GATED_RESID, BMB, BX_OUT_F32, NP>(a, ep, s);
+    case LX_EPI_ROPE_PARTIAL:
+      return launch_bx<LX_EPI_ROPE_PARTIAL, BMB, BX_OUT_F32, NP>(a, ep, s);
+    case LX_EPI_RESID: return launch_bx<LX_EPI_RESID, BMB, BX_OUT_F32, NP>(a, ep, s);
     case LX_EPI_SWIGLU_PAIRED:
-      return launch_bx<LX_EPI_SWIGLU_PAIRED, BMB, BX_OUT_F32>(a, ep, s);
+      return launch_bx<LX_EPI_SWIGLU_PAIRED, BMB, BX_OUT_F32, NP>(a, ep, s);
     default: break;
   }
   set_error("linear_bx: epilogue kind %d not available", ep.kind);
@@ -547,6 +553,8 @@ int linear_bx(const lx_linear_bx& g, hipStream_t stream) {
   LX_REQUIRE(g.M > 0 && g.N > 0 && g.K > 0 && g.N % kBxBN == 0 && g.K % (2 * kBxBK) == 0,
              "linear_bx: bad shape M=%d N=%d K=%d (N %% 128, K %% 64)", g.M, g.N, g.K);
   LX_REQUIRE(g.bm == 64 || g.bm == 128, "linear_bx: bm=%d must be 64 or 128", g.bm);
+  LX_REQUIRE(g.products == 0 || g.products == 3 || g.products == 6,
+             "linear_bx: products=%d must be 3 or 6 (0: 6)", g.products);
   LX_REQUIRE(g.lda >= g.K && g.lda % 4 == 0 && (long)g.M * g.lda * 4 < (1L << 31),
              "linear_bx: lda=%ld (K=%d), A must stay below 2 GiB", g.lda, g.K);
   LX_REQUIRE(((uintptr_t)g.A | (uintptr_t)g.Wf) % 16 == 0,
@@ -613,7 +621,11 @@ int linear_bx(const lx_linear_bx& g, hipStream_t stream) {
       a.counters = g.counters;
     }
   }
-  return g.bm == 128 ? dispatch_bx<4>(a, g.out, ep, stream) : dispatch_bx<2>(a, g.out, ep, stream);
+  if (g.products == 3)
+    return g.bm == 128 ? dispatch_bx<4, 3>(a, g.out, ep, stream)
+                       : dispatch_bx<2, 3>(a, g.out, ep, stream);
+  return g.bm == 128 ? dispatch_bx<4, 6>(a, g.out, ep, stream)
+                     : dispatch_bx<2, 6>(a, g.out, ep, stream);
 }
 
 }  // namespace lx

@@ -66,6 +66,7 @@ struct lx_qwen2 {
   float* ws = nullptr;  // split-K partial sums, and the gate/up split tail's partial tiles
   size_t ws_floats = 0;
   bool frag = false;    // prefill projections on the fragment-order split-operand GEMM
+  int products = 3;     // its products per element pair (3 or 6)
   unsigned* arrivals = nullptr;  // split-tail arrival counters (zeroed at creation)
   int n_arrivals = 0;
   int* pos;     // pos[i] = i
@@ -153,6 +154,7 @@ int prefill_partials(lx_qwen2* m, const float* x, int ldx, const void* wf, const
     g.K = K;
     g.bm = 64;
     g.slices = sl;
+    g.products = m->products;
     *splits = sl;
     return linear_bx(g, s);
   }
@@ -200,6 +202,7 @@ int prefill_layer(lx_qwen2* m, Layer& L, int rows, const float* next_norm, hipSt
     g.K = H;
     g.bm = (long)((rows + 127) / 128) * (2 * m->I / 128) <= 256 ? 128 : 64;
     g.slices = 1;
+    g.products = m->products;
     LX_TRY(linear_bx(g, s));
   } else {
     LX_TRY(linear_split_tail(m->hn, H, L.gu_w, nullptr, m->act, m->I, rows, 2 * m->I, H,
@@ -614,6 +617,14 @@ extern "C" const float* lx_qwen2_cache_key(const lx_qwen2* m, int layer) {
 extern "C" const float* lx_qwen2_cache_value(const lx_qwen2* m, int layer) {
   if (!m || layer < 0 || layer >= m->NL) return nullptr;
   return m->layers[layer].v_cache;
+}
+
+extern "C" int lx_qwen2_set_products(lx_qwen2* m, int products) {
+  LX_REQUIRE(m, "qwen2_set_products: null model");
+  LX_REQUIRE(products == 3 || products == 6, "qwen2_set_products: %d products (3 or 6)",
+             products);
+  m->products = products;
+  return LX_OK;
 }
 
 extern "C" int lx_qwen2_set_decode_graph(lx_qwen2* m, int enable) {

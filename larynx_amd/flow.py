@@ -168,6 +168,11 @@ class DiTEstimator:
         self._capture = capture
         check(lib.lx_dit_set_capture(self._h, C.byref(cap)))
 
+    def set_products(self, products):
+        """Split-operand products of the block projections: 3 (the default, about
+        5e-6 relative error per projection) or 6 (fp32-GEMM level, slower)."""
+        check(lib.lx_dit_set_products(self._h, int(products)))
+
     def forward(self, x, mu, cond, spks, t):
         """dphi = DiT(x, mu, t, spks, cond); x/mu/cond (B, mel, T), spks (B, mel), t (B)."""
         B, mel, T = x.shape
@@ -303,6 +308,10 @@ class FlowDecoder:
                 setattr(cap, k, C.c_void_p(v.data_ptr()))
         self._capture = capture
         check(lib.lx_flow_set_capture(self._h, C.byref(cap)))
+
+    def set_products(self, products):
+        """Split-operand products of the estimator's block projections (3 or 6)."""
+        check(lib.lx_dit_set_products(lib.lx_flow_estimator(self._h), int(products)))
 
     def infer(self, prompt_tokens, tokens, prompt_feat, spk_embedding, noise_z):
         """Speech tokens -> mel frames past the prompt, (mel, MEL_T - mel_len1).

@@ -197,6 +197,10 @@ class Qwen2LM:
         eagerly (False)."""
         check(lib.lx_qwen2_set_decode_graph(self._h, 1 if enable else 0))
 
+    def set_products(self, products):
+        """Split-operand products of the prefill projections: 3 (the default) or 6."""
+        check(lib.lx_qwen2_set_products(self._h, int(products)))
+
     def cache_views(self, layer):
         """(k, v) device views (max_ctx, KV) of the layer's cache (roped keys, raw values)."""
         KV = self.cfg.n_kv_heads * self.cfg.head_dim

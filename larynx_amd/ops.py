@@ -214,7 +214,7 @@ def wfrag_pack(W):
 
 
 def linear_bx(a, wf, N, b=None, epilogue=None, out=None, out_kind=LX_BX_OUT_F32, bm=128,
-              slices=1, scratch=None):
+              slices=1, scratch=None, products=6):
     """epi(a @ W^T + b) with fp32 arithmetic on the bf16 matrix cores, W given as
     wfrag_pack(W) (N rows), a fp32 (M, K).  out_kind LX_BX_OUT_F32: (M, N) (out= the
     residual stream for residual epilogues); LX_BX_OUT_PARTIAL: (slices, M, N) raw
@@ -228,7 +228,7 @@ def linear_bx(a, wf, N, b=None, epilogue=None, out=None, out_kind=LX_BX_OUT_F32,
     if epilogue is not None:
         g.epi = C.pointer(epilogue)
     g.out = out_kind
-    g.M, g.N, g.K, g.bm, g.slices = M, N, K, bm, slices
+    g.M, g.N, g.K, g.bm, g.slices, g.products = M, N, K, bm, slices, products
     if out_kind == LX_BX_OUT_PARTIAL:
         if out is None:
             out = torch.empty(slices, M, N, device=a.device, dtype=torch.float32)

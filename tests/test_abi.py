@@ -64,17 +64,23 @@ def test_argument_errors_need_no_device():
     assert lib.lx_linear_f32(fake, 6, fake, None, fake, 6, 8, 8, 6, None, None) == LX_ERR_ARG
     assert lib.lx_conv_pos_mish_f32(fake, fake, fake, None, fake, 1, 8, 1024, 8, 31,
                                     None) == LX_ERR_ARG  # 128 channels per group
-    # fragment-order GEMM: N not a multiple of 128, K slices of odd slab counts
+    # fragment-order GEMM: N not a multiple of 128, an empty last K slice (18
+    # steps of 64 as 7 slices of 3), a tile height other than 64 / 128, a
+    # product count other than 3 / 6
     from larynx_amd._lib import LX_BX_OUT_PARTIAL, LinearBx
     g = LinearBx()
     g.A, g.lda, g.Wf, g.Y, g.ldy, g.M, g.N, g.K, g.bm, g.slices = (16, 1024, 16, 16, 1000,
                                                                    8, 1000, 1024, 64, 1)
     assert lib.lx_linear_bx_f32(C.byref(g), None) == LX_ERR_ARG
     assert b"N %" in lib.lx_last_error() or b"bad shape" in lib.lx_last_error()
-    g.N, g.ldy, g.out, g.slices, g.K, g.lda = 1024, 1024, LX_BX_OUT_PARTIAL, 3, 1152, 1152
+    g.N, g.ldy, g.out, g.slices, g.K, g.lda = 1024, 1024, LX_BX_OUT_PARTIAL, 7, 1152, 1152
     assert lib.lx_linear_bx_f32(C.byref(g), None) == LX_ERR_ARG
+    assert b"empty" in lib.lx_last_error()
     g.bm, g.slices = 96, 1
     assert lib.lx_linear_bx_f32(C.byref(g), None) == LX_ERR_ARG
+    g.bm, g.products = 64, 4
+    assert lib.lx_linear_bx_f32(C.byref(g), None) == LX_ERR_ARG
+    assert b"products" in lib.lx_last_error()
     # the folded residual takes at most four partial slices
     assert lib.lx_adaln_resid_f32(fake, fake, 5, 1 << 20, None, fake, 1024, fake, fake, 1024,
                                   fake, 2, 8, 1024, 1e-6, None) == LX_ERR_ARG

@@ -18,6 +18,9 @@ from oracle import oracle as orc
 pytestmark = pytest.mark.gpu
 TOL = 1e-4
 FP32_LEVEL = 4e-6
+# Three products of two-part splits: each product within about 2^-16 of a * b;
+# measured 3.5e-6 - 5.6e-6 over the estimator's and the Qwen2 prefill's shapes.
+THREE_PRODUCT_LEVEL = 2e-5
 
 
 def rnd(shape, stream, std=1.0, seed=23):
@@ -55,28 +58,31 @@ def test_wfrag_layout_and_parts_exact(gpu, ops):
     assert np.array_equal(unpack_wfrag(wf, N, K), W.astype(np.float64))
 
 
+@pytest.mark.parametrize("products", [6, 3])
 @pytest.mark.parametrize("M,N,K,bm,sk", [
     (1000, 3072, 1024, 128, False), (1000, 1024, 1024, 64, False), (1000, 2048, 1024, 64, True),
     (37, 128, 64, 64, False), (6000, 1024, 2048, 64, False), (6000, 3072, 1024, 128, True),
     (300, 256, 192, 128, True), (48, 3072, 1024, 64, False)])
-def test_linear_bx_fp32_level(gpu, ops, M, N, K, bm, sk):
-    announce(f"linear_bx M={M} N={N} K={K} bm={bm} streamk={sk}")
+def test_linear_bx_fp32_level(gpu, ops, M, N, K, bm, sk, products):
+    announce(f"linear_bx M={M} N={N} K={K} bm={bm} streamk={sk} products={products}")
     x, W, b = rnd((M, K), 2), rnd((N, K), 3, 0.03), rnd((N,), 4)
     scr = ops.bx_scratch(gpu, bm=bm) if sk else None
     y = ops.linear_bx(dev(x, gpu), ops.wfrag_pack(dev(W, gpu)), N, dev(b, gpu), bm=bm,
-                      scratch=scr).cpu().numpy()
+                      scratch=scr, products=products).cpu().numpy()
     ref = x.astype(np.float64) @ W.astype(np.float64).T + b.astype(np.float64)
-    assert np.abs(y - ref).max() / np.abs(ref).max() < FP32_LEVEL
+    err = np.abs(y - ref).max() / np.abs(ref).max()
+    assert err < (FP32_LEVEL if products == 6 else THREE_PRODUCT_LEVEL), err
     if sk:  # every arrival count is left at zero for the next call
         assert int(scr[1].abs().sum()) == 0
 
 
-@pytest.mark.parametrize("T,bm,sk", [(500, 64, False), (500, 128, True), (24, 64, False),
-                                     (3, 128, False), (1500, 64, True)])
-def test_linear_bx_epilogues(gpu, ops, T, bm, sk):
+@pytest.mark.parametrize("T,bm,sk,products", [
+    (500, 64, False, 3), (500, 64, False, 6), (500, 128, True, 3), (24, 64, False, 3),
+    (3, 128, False, 6), (1500, 64, True, 6)])
+def test_linear_bx_epilogues(gpu, ops, T, bm, sk, products):
     """QKV + partial rotary, FF0 + GELU and out / FF2 + gated residual at the
     estimator's shapes, against the oracle."""
-    announce(f"linear_bx epilogues T={T} bm={bm} streamk={sk}")
+    announce(f"linear_bx epilogues T={T} bm={bm} streamk={sk} products={products}")
     B, D, F = 2, 1024, 2048
     scr = ops.bx_scratch(gpu, bm=bm) if sk else None
     x, W, b = rnd((B * T, D), 5), rnd((3 * D, D), 6, 0.03), rnd((3 * D,), 7)
@@ -84,7 +90,7 @@ def test_linear_bx_epilogues(gpu, ops, T, bm, sk):
     ep = ops.Epilogue(kind=ops.LX_EPI_ROPE_PARTIAL, rows_per_batch=T, pos=pos.data_ptr(),
                       rot_dim=64, rope_section=D, rope_sections=2, rope_base=10000.0)
     y = ops.linear_bx(dev(x, gpu), ops.wfrag_pack(dev(W, gpu)), 3 * D, dev(b, gpu), ep, bm=bm,
-                      scratch=scr).cpu().numpy()
+                      scratch=scr, products=products).cpu().numpy()
     ref = orc.linear(x, W, b).reshape(B, T, 3 * D)
     p = np.arange(T, dtype=np.int32)
     q = orc.rope_partial(np.ascontiguousarray(ref[..., :D]), p)
@@ -95,7 +101,7 @@ def test_linear_bx_epilogues(gpu, ops, T, bm, sk):
     W1, b1 = rnd((F, D), 8, 0.03), rnd((F,), 9)
     g = ops.Epilogue(kind=ops.LX_EPI_GELU_TANH)
     y1 = ops.linear_bx(dev(x, gpu), ops.wfrag_pack(dev(W1, gpu)), F, dev(b1, gpu), g, bm=bm,
-                       scratch=scr).cpu().numpy()
+                       scratch=scr, products=products).cpu().numpy()
     assert orc.rel_err(y1, orc.gelu_tanh(orc.linear(x, W1, b1))) < TOL
 
     xf, W2, b2 = rnd((B * T, F), 10), rnd((D, F), 11, 0.03), rnd((D,), 12)
@@ -106,7 +112,7 @@ def test_linear_bx_epilogues(gpu, ops, T, bm, sk):
     epg = ops.Epilogue(kind=ops.LX_EPI_GATED_RESID, rows_per_batch=T, gate=gate.data_ptr(),
                        gate_stride=6 * D)
     ops.linear_bx(dev(xf, gpu), ops.wfrag_pack(dev(W2, gpu)), D, dev(b2, gpu), epg,
-                  out=hd.view(B * T, D), bm=bm, scratch=scr)
+                  out=hd.view(B * T, D), bm=bm, scratch=scr, products=products)
     refg = orc.gated_residual(h, orc.linear(xf, W2, b2).reshape(B, T, D), emb[:, 5 * D:])
     assert orc.rel_err(hd.cpu().numpy(), refg) < TOL
 
@@ -223,11 +229,13 @@ def test_split_operand_nonfinite_inputs(gpu, ops):
     clean = np.ones(M, bool)
     clean[list(bad)] = False
     ref = x[clean].astype(np.float64) @ W.astype(np.float64).T
-    for y in (ops.linear_bx(xd, ops.wfrag_pack(Wd), N, bm=64).cpu().numpy(),
-              ops.linear_split(xd, ops.split_planes(Wd), tile=0).cpu().numpy()):
+    for y, lvl in ((ops.linear_bx(xd, ops.wfrag_pack(Wd), N, bm=64).cpu().numpy(), FP32_LEVEL),
+                   (ops.linear_bx(xd, ops.wfrag_pack(Wd), N, bm=64, products=3).cpu().numpy(),
+                    THREE_PRODUCT_LEVEL),
+                   (ops.linear_split(xd, ops.split_planes(Wd), tile=0).cpu().numpy(), FP32_LEVEL)):
         for r in bad:
             assert np.isnan(y[r]).all(), r
-        assert np.abs(y[clean] - ref).max() / np.abs(ref).max() < FP32_LEVEL
+        assert np.abs(y[clean] - ref).max() / np.abs(ref).max() < lvl
     y32 = ops.linear(xd, Wd).cpu().numpy()  # the fp32 kernel, for contrast
     assert np.isfinite(y32[7]).all() and not np.isfinite(y32[3]).any()
 
