@@ -10,13 +10,14 @@ Also reported on the same JSON line:
   roofline      the dominant kernel's achieved fp32 FLOP/s (HIP events around graph
                 replays of its launches under continuous load, on the replay stream)
                 vs the 157.3 TFLOP/s fp32 matrix peak (for a split-operand kernel,
-                which forms each fp32 product from three (projections, the
-                estimator's default) or six (attention) bf16 MFMA products, also
+                which forms each fp32 product from three bf16 MFMA products (the
+                estimator's default; six in its fp32-GEMM-level mode), also
                 the bf16 MFMA flops executed vs the 2.5 PFLOP/s dense bf16 peak, as
                 bf16_pipe), and its HBM traffic per launch from the committed
                 rocprofv3 FETCH_SIZE / WRITE_SIZE summary;
-  six_products  the same timed steps with the block projections on the six-product
-                split (fp32-GEMM error level; lx_dit_set_products(dit, 6));
+  six_products  the same timed steps with the block projections and attention on
+                the six-product split (fp32-GEMM error level;
+                lx_dit_set_products(dit, 6));
   kernels       per-kernel-class timings of one step's launches (same method), each
                 class on the kernel the estimator runs for it;
   fused_ops     achieved HBM GB/s of every fused op at the configs' shapes, with
@@ -42,10 +43,9 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0
 MFMA_F32_PEAK_TFLOPS = 157.3
 MFMA_BF16_PEAK_TFLOPS = 2500.0
-# bf16 MFMA products per fp32 product: the estimator's projections (its default,
-# lx_dit.cpp `products`) and the split-operand attention
+# bf16 MFMA products per fp32 product in the estimator's split-operand
+# projections and attention (its default, lx_dit.cpp `products`)
 DIT_PRODUCTS = 3
-ATTN_PRODUCTS = 6
 
 
 def parse():
@@ -277,8 +277,10 @@ def gemm_kernels(torch, ops, T, dev):
         "gemm_ff0_gelu": (proj(xd, w1, b1, gelu, ff), 2 * M * F * D, 1),
         "gemm_ff2_gated": (proj(xf, w2, bd, gated, hv), 2 * M * D * F, 1),
         "attention": ((lambda: ops.attention(qv[..., :D], qv[..., D:2 * D], qv[..., 2 * D:], 16,
-                                             out=att), "attn_bx_kernel / attn_flash_kernel",
-                       None, None),
+                                             out=att, products=DIT_PRODUCTS),
+                       f"attn_bx_kernel ({DIT_PRODUCTS} products) / attn_flash_kernel", None,
+                       lambda: ops.attention(qv[..., :D], qv[..., D:2 * D], qv[..., 2 * D:], 16,
+                                             out=att, products=6)),
                       4 * B * 16 * T * T * 64, 1),
     }
     # hipBLASLt (torch.mm, fp32) on the same plain-GEMM shapes, as a library reference point
@@ -860,7 +862,7 @@ def main():
     if dom["kernel"].startswith(("gemm_bx_kernel", "attn_bx_kernel")):
         # the same work as executed: bf16 MFMA products per fp32 product, against
         # the dense bf16 peak
-        npr = DIT_PRODUCTS if dom["kernel"].startswith("gemm_bx_kernel") else ATTN_PRODUCTS
+        npr = DIT_PRODUCTS
         bf = npr * dom["tflops"]
         roofline["bf16_pipe"] = {"achieved": round(bf, 3), "peak": MFMA_BF16_PEAK_TFLOPS,
                                  "frac": round(bf / MFMA_BF16_PEAK_TFLOPS, 4),
@@ -911,8 +913,8 @@ def main():
         "products": DIT_PRODUCTS,
         "six_products": {"ms_per_step": round(six_ms_per_step, 4),
                          "value": round(T / (six_ms_per_step * 1e-3), 1),
-                         "note": "same steps, block projections as six bf16 products per "
-                                 "fp32 product (fp32-GEMM error level)"},
+                         "note": "same steps, block projections and attention as six bf16 "
+                                 "products per fp32 product (fp32-GEMM error level)"},
         "kernels": {k: {kk: (round(vv, 2) if kk != "kernel" else vv)
                         for kk, vv in v.items() if kk in
                         ("avg_us", "tflops", "hipblaslt_us", "kernel", "fp32_kernel_us", "gbs",

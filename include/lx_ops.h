@@ -290,6 +290,14 @@ int lx_attention_f32(const float* q, int ldq, const float* k, int ldk, const flo
                      int ldv, float* o, int ldo, int B, int Tq, int Tk, int n_heads,
                      int n_kv_heads, int head_dim, float scale, int causal, int q_offset,
                      hipStream_t stream);
+/* lx_attention_f32 with the split-operand kernel's product count: 6 (as
+ * lx_attention_f32) or 3 (two bf16 parts per operand, three products: about
+ * half the matrix-core work; the grids that run the fp32 kernel ignore it).
+ * The estimator calls it with its lx_dit_set_products setting. */
+int lx_attention_np_f32(const float* q, int ldq, const float* k, int ldk, const float* v,
+                        int ldv, float* o, int ldo, int B, int Tq, int Tk, int n_heads,
+                        int n_kv_heads, int head_dim, float scale, int causal, int q_offset,
+                        int products, hipStream_t stream);
 
 /* Causal grouped conv1d + Mish (one CausalConvPositionEmbedding half):
  *   y[b,t,oc] = mish(bias[oc] + sum_{k<K, ic<C/G} w[oc, ic, k] *
@@ -369,13 +377,15 @@ typedef struct lx_dit_capture {
 } lx_dit_capture;
 int lx_dit_set_capture(lx_dit* dit, const lx_dit_capture* cap);
 
-/* Arithmetic of the block projections (q|k|v, out, FF0, FF2) on the
- * fragment-order split-operand GEMM (lx_linear_bx): products = 3 (the default:
- * two bf16 parts per operand, a0 b0 + a0 b1 + a1 b0; max relative error about
- * 5e-6 per projection at B = 2, T = 500) or 6 (three parts, i + j <= 2: about
- * 1.3e-6, the level of an fp32 GEMM, at 1.4-1.55x the projection time).
- * Attention keeps its six-product split either way.  No counterpart in the
- * reference, whose ggml projections are fp32 SGEMM (src/flow/ops.cpp:20-26). */
+/* Arithmetic of the block projections (q|k|v, out, FF0, FF2, on the
+ * fragment-order split-operand GEMM lx_linear_bx) and of attention
+ * (lx_attention_np_f32): products = 3 (the default: two bf16 parts per
+ * operand, a0 b0 + a0 b1 + a1 b0; max relative error about 5e-6 per projection
+ * at B = 2, T = 500) or 6 (three parts, i + j <= 2: about 1.3e-6, the level of
+ * an fp32 GEMM; projections 1.4-1.55x and attention 1.3-1.65x the time).  After
+ * 22 blocks at T = 500 the estimator output is within 1.2e-6 (3) and 4.8e-7 (6)
+ * of the oracle.  No counterpart in the reference, whose ggml projections are
+ * fp32 SGEMM (src/flow/ops.cpp:20-26). */
 int lx_dit_set_products(lx_dit* dit, int products);
 
 /* Full CFM Euler solve with classifier-free guidance, device resident

@@ -156,6 +156,9 @@ SIGNATURES = [
     ("lx_attention_f32", C.c_int,
      [fp, C.c_int, fp, C.c_int, fp, C.c_int, fp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
       C.c_int, C.c_int, C.c_float, C.c_int, C.c_int, stream_t]),
+    ("lx_attention_np_f32", C.c_int,
+     [fp, C.c_int, fp, C.c_int, fp, C.c_int, fp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
+      C.c_int, C.c_int, C.c_float, C.c_int, C.c_int, C.c_int, stream_t]),
     ("lx_conv_pos_mish_f32", C.c_int,
      [fp, fp, fp, fp, fp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, stream_t]),
     ("lx_conv_pack_weight_f32", C.c_int, [fp, fp, C.c_int, C.c_int, C.c_int, stream_t]),

@@ -507,8 +507,16 @@ __device__ __forceinline__ void split3(floatx8 v, bf16x8& x0, bf16x8& x1, bf16x8
   x2 = __builtin_convertvector(r - bf16x8_to_f32(x1), bf16x8);
 }
 
-// acc += sum of the six split products a_i b_j, i + j <= 2 (smallest first)
-__device__ __forceinline__ floatx16 mfma_split6(const bf16x8* a, const bf16x8* b, floatx16 acc) {
+// acc += sum of the NP split products (smallest first): six a_i b_j with
+// i + j <= 2 of three-part splits, or three (a1 b0 + a0 b1 + a0 b0) of
+// two-part splits
+template <int NP>
+__device__ __forceinline__ floatx16 mfma_split(const bf16x8* a, const bf16x8* b, floatx16 acc) {
+  if (NP == 3) {
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], b[0], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[1], acc, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[0], acc, 0, 0, 0);
+  }
   acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[2], b[0], acc, 0, 0, 0);
   acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], b[1], acc, 0, 0, 0);
   acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[2], acc, 0, 0, 0);
@@ -517,13 +525,15 @@ __device__ __forceinline__ floatx16 mfma_split6(const bf16x8* a, const bf16x8* b
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[0], acc, 0, 0, 0);
 }
 
-// LDS of the split kernel, two buffers each of K planes [3][KT keys][kKP]
-// and V^T planes [3][64 channels][KT + 8] (bf16); the merge reuses it.
+// LDS of the split kernel, two buffers each of K planes [NPL][KT keys][kKP]
+// and V^T planes [NPL][64 channels][KT + 8] (bf16; NPL = 3 parts for six
+// products, 2 for three); the merge reuses it.
 constexpr int kKP = kHD + 8;  // bf16 per K plane row (144 bytes: conflict-free 16-byte reads)
-template <int QS, int KS>
+template <int QS, int KS, int NP = 6>
 constexpr size_t bx_lds() {
   constexpr int KT = 32 * KS;
-  constexpr size_t planes = (size_t)2 * 2 * 3 * (KT * kKP + kHD * (KT + 8));
+  constexpr int NPL = NP == 6 ? 3 : 2;
+  constexpr size_t planes = (size_t)2 * 2 * NPL * (KT * kKP + kHD * (KT + 8));
   constexpr size_t merge = KS == 2 ? (size_t)QS * 2 * 18 * 64 * 4
                                    : (size_t)(QS * (KS - 1) * 64 * 34 + QS * 32 * kLD) * 4;
   return planes > merge ? planes : merge;
@@ -541,7 +551,7 @@ __device__ __forceinline__ int vt_pos(int k) {
 // beside the PV MFMAs.  K and V rotate through two LDS buffers each: K of
 // tile t + 2 replaces K of tile t (its scores were formed in iteration t - 1),
 // V of tile t + 1 replaces V of tile t - 1, so one barrier per tile suffices.
-template <int QS, int KS, bool BUF>
+template <int QS, int KS, bool BUF, int NP>
 __global__ __launch_bounds__(64 * QS * KS) void attn_bx_kernel(
     const float* __restrict__ q, int ldq, const float* __restrict__ k, int ldk,
     const float* __restrict__ v, int ldv, float* __restrict__ o, int ldo, int Tq, int Tk,
@@ -552,13 +562,14 @@ __global__ __launch_bounds__(64 * QS * KS) void attn_bx_kernel(
   constexpr int LPT = KT * 16 / NT;  // K float4 per thread per tile
   constexpr int LPV = LPT / 2;       // V key pairs (two float4) per thread per tile
   constexpr int VP = KT + 8;         // bf16 per V^T plane row
-  constexpr int KBUF = 3 * KT * kKP;  // bf16 per K buffer
-  constexpr int VBUF = 3 * kHD * VP;  // bf16 per V buffer
+  constexpr int NPL = NP == 6 ? 3 : 2;  // bf16 parts per operand
+  constexpr int KBUF = NPL * KT * kKP;  // bf16 per K buffer
+  constexpr int VBUF = NPL * kHD * VP;  // bf16 per V buffer
   static_assert(LPT * NT == KT * 16 && LPV * 2 == LPT, "operand tile must split evenly");
-  static_assert(bx_lds<QS, KS>() <= 160 * 1024, "LDS of one CU");
+  static_assert(bx_lds<QS, KS, NP>() <= 160 * 1024, "LDS of one CU");
   extern __shared__ __attribute__((aligned(16))) float lds[];
-  __bf16* Kp = reinterpret_cast<__bf16*>(lds);  // [2][3][KT][kKP]
-  __bf16* Vt = Kp + 2 * KBUF;                    // [2][3][64][VP]
+  __bf16* Kp = reinterpret_cast<__bf16*>(lds);  // [2][NPL][KT][kKP]
+  __bf16* Vt = Kp + 2 * KBUF;                    // [2][NPL][64][VP]
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int qs = wave % QS, ks = wave / QS;
@@ -655,9 +666,9 @@ __global__ __launch_bounds__(64 * QS * KS) void attn_bx_kernel(
       const int idx = tid + NT * j;
       const int row = idx >> 4, c = (idx & 15) * 4;
       bf16x4 x[3];
-      split3(rk[j], x[0], x[1], x[2]);
+      split3(rk[j], x[0], x[1], x[2]);  // (the third part is dead code with two)
 #pragma unroll
-      for (int p = 0; p < 3; ++p)
+      for (int p = 0; p < NPL; ++p)
         *reinterpret_cast<bf16x4*>(dst + (p * KT + row) * kKP + c) = x[p];
     }
   };
@@ -673,7 +684,7 @@ __global__ __launch_bounds__(64 * QS * KS) void attn_bx_kernel(
       split3(rv[j][0], x0[0], x0[1], x0[2]);
       split3(rv[j][1], x1[0], x1[1], x1[2]);
 #pragma unroll
-      for (int p = 0; p < 3; ++p)
+      for (int p = 0; p < NPL; ++p)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           bf16x2 pair;
@@ -693,9 +704,9 @@ __global__ __launch_bounds__(64 * QS * KS) void attn_bx_kernel(
     for (int st = 0; st < 4; ++st) {
       bf16x8 ka[3];
 #pragma unroll
-      for (int p = 0; p < 3; ++p)
+      for (int p = 0; p < NPL; ++p)
         ka[p] = *reinterpret_cast<const bf16x8*>(kfrag + buf * KBUF + p * KT * kKP + st * 16);
-      s = mfma_split6(ka, qb[st], s);
+      s = mfma_split<NP>(ka, qb[st], s);
     }
     return s;
   };
@@ -775,12 +786,12 @@ __global__ __launch_bounds__(64 * QS * KS) void attn_bx_kernel(
         split3(pv, pb[0], pb[1], pb[2]);
         bf16x8 va[3], vc[3];
 #pragma unroll
-        for (int p = 0; p < 3; ++p) {
+        for (int p = 0; p < NPL; ++p) {
           va[p] = *reinterpret_cast<const bf16x8*>(vb + p * kHD * VP + u * 16);
           vc[p] = *reinterpret_cast<const bf16x8*>(vb + (p * kHD + 32) * VP + u * 16);
         }
-        o0 = mfma_split6(va, pb, o0);
-        o1 = mfma_split6(vc, pb, o1);
+        o0 = mfma_split<NP>(va, pb, o0);
+        o1 = mfma_split<NP>(vc, pb, o1);
       }
     }
     if (ld_k) stage_k(t & 1);
@@ -836,12 +847,12 @@ __global__ __launch_bounds__(64 * QS * KS) void attn_bx_kernel(
     for (int u = 0; u < 2; ++u) {
       bf16x8 va[3], vc[3];
 #pragma unroll
-      for (int p = 0; p < 3; ++p) {
+      for (int p = 0; p < NPL; ++p) {
         va[p] = *reinterpret_cast<const bf16x8*>(vb + p * kHD * VP + u * 16);
         vc[p] = *reinterpret_cast<const bf16x8*>(vb + (p * kHD + 32) * VP + u * 16);
       }
-      o0 = mfma_split6(va, pb[u], o0);
-      o1 = mfma_split6(vc, pb[u], o1);
+      o0 = mfma_split<NP>(va, pb[u], o0);
+      o1 = mfma_split<NP>(vc, pb[u], o1);
     }
     stage_k(t & 1);
     stage_v((t + 1) & 1);
@@ -883,7 +894,7 @@ __global__ __launch_bounds__(64 * QS * KS) void attn_bx_kernel(
     // in part order (part 0's terms first) and store it straight from the
     // registers: register i of lane (r, h) holds channels (i/4)*8 + h*4 +
     // i%4 of query r, four consecutive channels per float4.
-    static_assert(QS * 2 * 18 * 64 * 4 <= bx_lds<QS, KS>(), "exchange space");
+    static_assert(QS * 2 * 18 * 64 * 4 <= bx_lds<QS, KS, NP>(), "exchange space");
     float* pub = lds + (qs * 2 + ks) * (18 * 64);
     const floatx16& give = ks == 0 ? o1 : o0;
 #pragma unroll
@@ -976,14 +987,10 @@ __global__ __launch_bounds__(64 * QS * KS) void attn_bx_kernel(
 }
 
 }  // namespace
-}  // namespace lx
-
-using namespace lx;
-
-extern "C" int lx_attention_f32(const float* q, int ldq, const float* k, int ldk,
-                                const float* v, int ldv, float* o, int ldo, int B, int Tq,
-                                int Tk, int n_heads, int n_kv_heads, int head_dim, float scale,
-                                int causal, int q_offset, hipStream_t stream) {
+int attention(const float* q, int ldq, const float* k, int ldk, const float* v, int ldv, float* o,
+              int ldo, int B, int Tq, int Tk, int n_heads, int n_kv_heads, int head_dim,
+              float scale, int causal, int q_offset, int products, hipStream_t stream) {
+  LX_REQUIRE(products == 3 || products == 6, "attention: %d products (3 or 6)", products);
   LX_REQUIRE(q && k && v && o, "attention: null pointer");
   LX_REQUIRE(B > 0 && Tq > 0 && Tk > 0 && n_heads > 0 && n_kv_heads > 0,
              "attention: bad shape");
@@ -1029,11 +1036,20 @@ extern "C" int lx_attention_f32(const float* q, int ldq, const float* k, int ldk
   // grid of several rounds (T = 1500: 181 vs 170 us) and the small grids stay
   // on the fp32 kernel, whose 70 KB (or single-buffered) LDS lets two
   // workgroups share a CU.
+  // With three products (two bf16 parts per operand) the same split and
+  // layouts apply.
   const bool split = layout == 2 || (layout == 1 && wg64 <= 256);
+  const bool np3 = products == 3;
   auto pick = [&]() {
+    if (split && np3) {
+      if (layout == 2)
+        return buf ? attn_bx_kernel<4, 2, true, 3> : attn_bx_kernel<4, 2, false, 3>;
+      return buf ? attn_bx_kernel<2, 2, true, 3> : attn_bx_kernel<2, 2, false, 3>;
+    }
     if (split) {
-      if (layout == 2) return buf ? attn_bx_kernel<4, 2, true> : attn_bx_kernel<4, 2, false>;
-      return buf ? attn_bx_kernel<2, 2, true> : attn_bx_kernel<2, 2, false>;
+      if (layout == 2)
+        return buf ? attn_bx_kernel<4, 2, true, 6> : attn_bx_kernel<4, 2, false, 6>;
+      return buf ? attn_bx_kernel<2, 2, true, 6> : attn_bx_kernel<2, 2, false, 6>;
     }
     if (layout == 0)
       return buf ? attn_flash_kernel<1, 4, false, true> : attn_flash_kernel<1, 4, false, false>;
@@ -1042,10 +1058,12 @@ extern "C" int lx_attention_f32(const float* q, int ldq, const float* k, int ldk
   auto kern = pick();
   const int qt = layout == 0 ? 32 : layout == 1 ? 64 : 128;
   const int threads = layout == 2 ? 512 : 256;
-  const size_t lds = split ? (layout == 2 ? bx_lds<4, 2>() : bx_lds<2, 2>())
-                           : (layout == 0 ? flash_lds<1, 4, false>() : flash_lds<2, 2, true>());
-  const int variant = split ? 2 + (layout == 2) : layout;
-  static LdsLimit once[4][2];  // [kernel variant][buf]
+  const size_t lds =
+      split ? (np3 ? (layout == 2 ? bx_lds<4, 2, 3>() : bx_lds<2, 2, 3>())
+                   : (layout == 2 ? bx_lds<4, 2, 6>() : bx_lds<2, 2, 6>()))
+            : (layout == 0 ? flash_lds<1, 4, false>() : flash_lds<2, 2, true>());
+  const int variant = split ? 2 + (layout == 2) + 2 * np3 : layout;
+  static LdsLimit once[6][2];  // [kernel variant][buf]
   const int rc = raise_lds_limit((const void*)kern, lds, once[variant][buf], "attention");
   if (rc) return rc;
   const long nwg = (long)((Tq + qt - 1) / qt) * n_heads * B;
@@ -1053,4 +1071,24 @@ extern "C" int lx_attention_f32(const float* q, int ldq, const float* k, int ldk
   hipLaunchKernelGGL(kern, dim3((unsigned)nwg), dim3(threads), lds, stream, q, ldq, k, ldk, v, ldv,
                      o, ldo, Tq, Tk, n_heads, rep, scale * log2e, causal, q_offset);
   return check_launch("attn_flash_kernel");
+}
+
+}  // namespace lx
+
+using namespace lx;
+
+extern "C" int lx_attention_f32(const float* q, int ldq, const float* k, int ldk,
+                                const float* v, int ldv, float* o, int ldo, int B, int Tq,
+                                int Tk, int n_heads, int n_kv_heads, int head_dim, float scale,
+                                int causal, int q_offset, hipStream_t stream) {
+  return attention(q, ldq, k, ldk, v, ldv, o, ldo, B, Tq, Tk, n_heads, n_kv_heads, head_dim,
+                   scale, causal, q_offset, 6, stream);
+}
+
+extern "C" int lx_attention_np_f32(const float* q, int ldq, const float* k, int ldk,
+                                   const float* v, int ldv, float* o, int ldo, int B, int Tq,
+                                   int Tk, int n_heads, int n_kv_heads, int head_dim, float scale,
+                                   int causal, int q_offset, int products, hipStream_t stream) {
+  return attention(q, ldq, k, ldk, v, ldv, o, ldo, B, Tq, Tk, n_heads, n_kv_heads, head_dim,
+                   scale, causal, q_offset, products, stream);
 }

@@ -241,9 +241,9 @@ int forward_core(lx_dit* m, const float* x, long x_bstride, const float* mu, con
     rope.rope_sections = 2;
     rope.rope_base = kRopeBase;
     LX_TRY(proj(m->xn, D, wf0, w0, m->qkv_b[i], m->qkv, 3 * D, 3 * D, D, &rope));
-    LX_TRY(lx_attention_f32(m->qkv, 3 * D, m->qkv + D, 3 * D, m->qkv + 2 * D, 3 * D, m->att, D, B,
-                            T, T, m->heads, m->heads, m->hd, 1.0f / std::sqrt((float)m->hd), 0, 0,
-                            s));
+    LX_TRY(attention(m->qkv, 3 * D, m->qkv + D, 3 * D, m->qkv + 2 * D, 3 * D, m->att, D, B, T,
+                     T, m->heads, m->heads, m->hd, 1.0f / std::sqrt((float)m->hd), 0, 0,
+                     m->products, s));
     LX_TRY(proj_gated(m->att, D, wf1, w1, m->out_b[i], gate_msa, D));
 
     LX_TRY(adaln(shift_mlp, scale_mlp, m->xn));

@@ -133,6 +133,11 @@ int splitk_qkv_rope_cache(const float* ws, int splits, int M, const float* bias,
 // ---- split-operand GEMM with W in fragment order (lx_gemm_bx.hip) ----
 // lx_linear_bx_f32 (arguments and outputs as declared in lx_ops.h).
 int linear_bx(const lx_linear_bx& g, hipStream_t stream);
+// lx_attention_f32 with the split-operand kernel's product count (3 or 6; the
+// fp32 kernel, which small grids run, ignores it).
+int attention(const float* q, int ldq, const float* k, int ldk, const float* v, int ldv, float* o,
+              int ldo, int B, int Tq, int Tk, int n_heads, int n_kv_heads, int head_dim,
+              float scale, int causal, int q_offset, int products, hipStream_t stream);
 // W (N, K) -> fragment order (3 * N * K bf16); N % 32 == 0, K % 16 == 0.
 int wfrag_pack(const float* W, void* Wf, int N, int K, hipStream_t stream);
 

@@ -257,18 +257,19 @@ def bx_scratch(device, bm=128, max_tiles=4096):
 
 
 def attention(q, k, v, n_heads, n_kv_heads=None, scale=None, causal=False, q_offset=0,
-              out=None, head_dim=64):
+              out=None, head_dim=64, products=6):
     """softmax(scale q k^T) v per head; q (B, Tq, *), k/v (B, Tk, *) with heads packed from
-    column 0 (row strides may exceed the head span).  src/flow/dit.cpp:34-51."""
+    column 0 (row strides may exceed the head span); products: the split-operand kernel's
+    bf16 products per fp32 product (6 or 3).  src/flow/dit.cpp:34-51."""
     n_kv_heads = n_kv_heads or n_heads
     B, Tq = q.shape[0], q.shape[1]
     Tk = k.shape[1]
     scale = scale if scale is not None else head_dim ** -0.5
     if out is None:
         out = torch.empty(B, Tq, n_heads * head_dim, device=q.device, dtype=torch.float32)
-    check(lib.lx_attention_f32(_p(q), q.stride(1), _p(k), k.stride(1), _p(v), v.stride(1),
-                               _p(out), out.stride(1), B, Tq, Tk, n_heads, n_kv_heads, head_dim,
-                               scale, int(causal), q_offset, stream()))
+    check(lib.lx_attention_np_f32(_p(q), q.stride(1), _p(k), k.stride(1), _p(v), v.stride(1),
+                                  _p(out), out.stride(1), B, Tq, Tk, n_heads, n_kv_heads,
+                                  head_dim, scale, int(causal), q_offset, products, stream()))
     return out
 
 

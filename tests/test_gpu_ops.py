@@ -3,7 +3,8 @@ inputs, at the configs' shapes (B=2, T=500 / 3000, D=1024; Qwen2 L=256 / 1).
 
 Bars: embedding gather bit-exact; fp32 ops max|gpu - oracle| / max|oracle| below
 1e-4 (the per-op tolerance of the target); GEMMs and attention below 1e-4 as
-well (fp32 MFMA, no reduced precision).
+well (fp32 matrix cores, or bf16 ones on two- or three-part splits of the fp32
+operands, with the error levels their own tests state).
 """
 import numpy as np
 import pytest
@@ -417,18 +418,23 @@ def test_attention_dit(gpu, ops, B, T):
     assert orc.rel_err(o, ref) < TOL
 
 
+@pytest.mark.parametrize("products", [6, 3])
 @pytest.mark.parametrize("T", [500, 1000, 1500])
-def test_attention_fp32_level_error(gpu, ops, T):
+def test_attention_fp32_level_error(gpu, ops, T, products):
     """T = 500 (64-query layout, one round) and T = 1000 (128-query layout) run the
-    split-operand kernel, which forms Q K^T and P V from three-part bf16 splits of
-    the fp32 operands; T = 1500 runs the fp32 kernel.  Against a float64
-    softmax(q k^T) v both stay at fp32 level, the maximum error below 2e-6 of the
-    output's largest magnitude (measured: split kernel 1.0e-6 at T = 500 and 8.9e-7
-    at T = 1000, fp32 kernel 1.1e-6 at T = 1500)."""
+    split-operand kernel, which forms Q K^T and P V from bf16 splits of the fp32
+    operands; T = 1500 runs the fp32 kernel.  Against a float64 softmax(q k^T) v
+    with N(0, 1) q and k (scores of std 1): six products (three-part splits) stay
+    at fp32 level, the maximum error below 2e-6 of the output's largest magnitude
+    (measured: 1.0e-6 at T = 500, 8.9e-7 at T = 1000, fp32 kernel 1.1e-6 at
+    T = 1500); three products (two-part splits) below 4e-5 (measured 1.5e-5 and
+    1.8e-5: a score error of about 2^-17 of sum |q_i k_i| moves each probability
+    by that much times ln 2)."""
     B, D = 2, 1024
     qkv = rnd((B, T, 3 * D), 21)
     qd = dev(qkv, gpu)
-    o = ops.attention(qd[..., :D], qd[..., D:2 * D], qd[..., 2 * D:], 16).double().cpu()
+    o = ops.attention(qd[..., :D], qd[..., D:2 * D], qd[..., 2 * D:], 16,
+                      products=products).double().cpu()
     x = torch.from_numpy(qkv).double()
     worst = 0.0
     for hh in (0, 5, 15):
@@ -437,8 +443,8 @@ def test_attention_fp32_level_error(gpu, ops, T):
         vh = x[:, :, 2 * D + hh * 64:2 * D + hh * 64 + 64]
         ref = torch.softmax(qh @ kh.transpose(1, 2), dim=-1) @ vh
         worst = max(worst, float((o[:, :, c] - ref).abs().max() / ref.abs().max()))
-    announce(f"attention T={T} max error vs float64: {worst:.2e}")
-    assert worst < 2e-6
+    announce(f"attention T={T} products={products} max error vs float64: {worst:.2e}")
+    assert worst < (2e-6 if products == 6 or T == 1500 else 4e-5)
 
 
 @pytest.mark.parametrize("Tq", [64, 2500, 2048])
