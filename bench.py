@@ -662,7 +662,8 @@ def counter_probe(torch, ops, launches=20):
         ops.linear_bx(ff, f2, D, out=part, out_kind=ops.LX_BX_OUT_PARTIAL, bm=64, slices=2,
                       products=DIT_PRODUCTS)
     for _ in range(launches):
-        ops.attention(q3[..., :D], q3[..., D:2 * D], q3[..., 2 * D:], 16, 16, out=att)
+        ops.attention(q3[..., :D], q3[..., D:2 * D], q3[..., 2 * D:], 16, 16, out=att,
+                      products=DIT_PRODUCTS)
     torch.cuda.synchronize()
     print(f"counter probe: {launches} x QKV, FF0, out, FF2 GEMMs and attention (B={B} T={T})",
           flush=True)

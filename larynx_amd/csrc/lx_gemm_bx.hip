@@ -38,16 +38,26 @@ constexpr int kBxWaves = 4;
 constexpr int kBxThreads = 64 * kBxWaves;
 constexpr int kBxBN = 32 * kBxWaves;  // columns per workgroup
 constexpr int kBxBK = 32;             // k per slab: two 16-wide MFMA k steps
-constexpr int kBxBufs = 4;            // A slab buffers
+constexpr int kBxBufs = 4;            // A slab buffers (six products)
 
 // NP products per element pair: 6 (three parts each, i + j <= 2) or 3 (two
 // parts each: a0 b0 + a0 b1 + a1 b0); NP / 2 + 1 bf16 planes per operand.
+#ifndef LX_BX_PD3
+#define LX_BX_PD3 4
+#endif
+#ifndef LX_BX_NG3
+#define LX_BX_NG3 2
+#endif
 template <int BMB, int NP>
 struct BxCfg {
   static constexpr int BM = 32 * BMB;
   static constexpr int NPL = NP == 6 ? 3 : 2;
+  // pipeline depth: PD slab buffers and W register sets, NG A staging sets
+  static constexpr int PD = NP == 6 ? kBxBufs : LX_BX_PD3;
+  static constexpr int NG = NP == 6 ? 2 : LX_BX_NG3;
+  static_assert(PD % NG == 0 && PD >= NG + 2 && PD % 2 == 0, "pipeline depth");
   static constexpr int ABUF = NPL * BM * kBxBK;  // bf16 per A slab buffer (NPL planes)
-  static constexpr size_t lds_k = (size_t)kBxBufs * ABUF * 2;
+  static constexpr size_t lds_k = (size_t)PD * ABUF * 2;
   static constexpr size_t lds_c = (size_t)BM * (kBxBN + 4) * 4;
   static constexpr size_t lds = lds_k > lds_c ? lds_k : lds_c;
 };
@@ -225,70 +235,83 @@ gemm_bx_kernel(BxArgs a, EpiArgs ep) {
               as_bf16x8(wv[NP == 6 ? kPw6[q] : kPw3[q]]), acc[i], 0, 0, 0);
     };
     // Registers: A fragments of the two k steps (fa0, fa1); the W fragments of
-    // four slabs (slab s in set s % 4: k step 0's three planes, then k step
-    // 1's); two A staging sets (gy for even slabs, gx for odd ones).  LDS: four
-    // slab buffers (slab s in buffer s % 4).  Prefetch distances: W three
-    // slabs, A two slabs from load to LDS store and three from store to use,
-    // so a load has about two slabs of MFMAs (2-3 us) to arrive.
+    // PD slabs (slab s in set s % PD: k step 0's planes, then k step 1's); NG A
+    // staging sets (slab s uses set s % NG).  LDS: PD slab buffers (slab s in
+    // buffer s % PD).  At slab s the A tile of slab s + PD - 1 is split into
+    // LDS (from the staging set, loaded NG slabs earlier) and the A tile of
+    // slab s + PD - 1 + NG is loaded into it; the W fragments of slab s + PD - 1
+    // are loaded into the set slab s - 1 has finished with.  Latency cover:
+    // A NG slabs of MFMAs, W PD - 1.  Both product counts run PD = 4, NG = 2:
+    // with three products (half the MFMAs per slab) the deeper PD = 6, NG = 3
+    // fits the registers but measured slower (T = 500 FF0 20.5 -> 21.3 us,
+    // Euler step 2.82 -> 2.86 ms), so the loads are not waiting on latency.
+    constexpr int PD = Cfg::PD, NG = Cfg::NG;
     uintx4_t fa0[BMB][3], fa1[BMB][3];
-    uintx4_t wv0[6], wv1[6], wv2[6], wv3[6];
-    floatx4 gx[LA], gy[LA];
-    auto load_ws = [&](uintx4_t* wv, int s) {
-      load_w(wv, s, 0);
-      load_w(wv + 3, s, 1);
+    uintx4_t wv[PD][6];
+    floatx4 gst[NG][LA];
+    auto load_ws = [&](uintx4_t* w, int s) {
+      load_w(w, s, 0);
+      load_w(w + 3, s, 1);
     };
     // Every prefetch is unconditional (indices clamped to the last slab; the
     // surplus slabs go to buffers nobody reads), so each body issues its
-    // global loads in one fixed order: at the top of slab s the loads in
-    // flight are A(s + 3), W(s + 1), A(s + 4), W(s + 2), oldest first.  The
-    // prologue ends in that same order, so the waits the compiler derives
+    // global loads in one fixed order: slab j issues A(j + PD - 1 + NG), then
+    // W(j + PD - 1).  The prologue first loads and stores A(0 .. PD - 2) and
+    // loads W(0 .. PD - 2 - NG), then issues the loads of the virtual slabs
+    // j = -NG .. -1 in that same order, so the waits the compiler derives
     // (from the merge of both paths into the loop) never stall on a recent
-    // load; it issues slabs 0-2 together (one memory latency).
+    // load.
     const int last = nk - 1;
     {
-      floatx4 gz[LA];
-      load_a(gx, 0);
-      load_a(gy, min(1, last));
-      load_a(gz, min(2, last));
-      load_ws(wv0, 0);
-      store_a(gx, 0);
-      store_a(gy, 1);
-      store_a(gz, 2);
-      load_a(gy, min(3, last));
-      load_ws(wv1, min(1, last));
-      load_a(gx, min(4, last));
-      load_ws(wv2, min(2, last));
+      floatx4 pre[PD - 1][LA];  // A(0 .. PD - 2) in flight together: one memory latency
+#pragma unroll
+      for (int i = 0; i < PD - 1; ++i) load_a(pre[i], min(i, last));
+#pragma unroll
+      for (int i = 0; i <= PD - 2 - NG; ++i) load_ws(wv[i], min(i, last));
+#pragma unroll
+      for (int i = 0; i < PD - 1; ++i) store_a(pre[i], i);
+#pragma unroll
+      for (int j = -NG; j < 0; ++j) {
+        load_a(gst[(j + NG) % NG], min(j + PD - 1 + NG, last));
+        load_ws(wv[(j + PD - 1 + PD) % PD], min(j + PD - 1, last));
+      }
     }
     __syncthreads();
     read_a(fa0, 0, 0);
     // Slab s.  k step 0: its MFMAs, beside them the fragment reads of k step
-    // 1, the staging of slab s + 3 (into slab s - 1's buffer) and the loads of
-    // slab s + 5 (into the staging set just stored).  Then the barrier (k step
-    // 1's fragments and slab s + 3 are in LDS; every wave is past its reads of
-    // slab s - 1's buffer).  k step 1: its MFMAs, beside them the next slab's
-    // k step 0 fragment reads and the W of slab s + 3 (into slab s - 1's
-    // register set).  The group barriers interleave one memory instruction per
-    // MFMA so that the matrix pipe keeps issuing while they go out.
+    // 1, the staging of slab s + PD - 1 (into slab s - 1's buffer) and the loads
+    // of slab s + PD - 1 + NG (into the staging set just stored).  Then the
+    // barrier (k step 1's fragments and slab s + PD - 1 are in LDS; every wave
+    // is past its reads of slab s - 1's buffer).  k step 1: its MFMAs, beside
+    // them the next slab's k step 0 fragment reads and the W of slab s + PD - 1
+    // (into slab s - 1's register set).  The group barriers interleave one
+    // memory instruction per MFMA so that the matrix pipe keeps issuing while
+    // they go out.
     constexpr int NM = NP * BMB;           // MFMAs per k step
     constexpr int NR = NPL * BMB;          // fragment reads per k step
     constexpr int NW = NPL * LA;           // staging LDS stores
-    auto body = [&](int s, int b, uintx4_t* wc, uintx4_t* wn, floatx4* g) {
+    // i = s % PD (a compile-time constant in every call)
+    auto body = [&](int s, int i) {
+      const int b = i;
+      uintx4_t* wc = wv[i];
+      uintx4_t* wn = wv[(i + PD - 1) % PD];
+      floatx4* g = gst[i % NG];
       read_a(fa1, b, 1);
-      store_a(g, (b + 3) & 3);
-      load_a(g, min(s + 5, last));
+      store_a(g, (b + PD - 1) % PD);
+      load_a(g, min(s + PD - 1 + NG, last));
       mul(fa0, wc);
 #pragma unroll
-      for (int i = 0; i < NR; ++i) {
+      for (int k = 0; k < NR; ++k) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
       }
 #pragma unroll
-      for (int i = 0; i < NW; ++i) {
+      for (int k = 0; k < NW; ++k) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // DS write
       }
 #pragma unroll
-      for (int i = 0; i < LA; ++i) {
+      for (int k = 0; k < LA; ++k) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read (A)
       }
@@ -296,16 +319,16 @@ gemm_bx_kernel(BxArgs a, EpiArgs ep) {
       __builtin_amdgcn_sched_barrier(0);  // k step 1's MFMAs stay below the barrier
       __syncthreads();
       __builtin_amdgcn_sched_barrier(0);
-      read_a(fa0, (b + 1) & 3, 0);
-      load_ws(wn, min(s + 3, last));
+      read_a(fa0, (b + 1) % PD, 0);
+      load_ws(wn, min(s + PD - 1, last));
       mul(fa1, wc + 3);
 #pragma unroll
-      for (int i = 0; i < NR; ++i) {
+      for (int k = 0; k < NR; ++k) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
       }
 #pragma unroll
-      for (int i = 0; i < 2 * NPL; ++i) {
+      for (int k = 0; k < 2 * NPL; ++k) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
         __builtin_amdgcn_sched_group_barrier(0x020, 1, 1);  // VMEM read (W)
       }
@@ -313,15 +336,17 @@ gemm_bx_kernel(BxArgs a, EpiArgs ep) {
       __builtin_amdgcn_sched_barrier(0);
     };
     int s = 0;
-    for (; s + 4 <= nk; s += 4) {
-      body(s, 0, wv0, wv3, gy);
-      body(s + 1, 1, wv1, wv0, gx);
-      body(s + 2, 2, wv2, wv1, gy);
-      body(s + 3, 3, wv3, wv2, gx);
+    for (; s + PD <= nk; s += PD) {
+#pragma unroll
+      for (int i = 0; i < PD; ++i) body(s + i, i);
     }
-    if (s < nk) {  // nk % 4 == 2
-      body(s, 0, wv0, wv3, gy);
-      body(s + 1, 1, wv1, wv0, gx);
+    // nk is even: the rest is an even number of slabs below PD
+#pragma unroll
+    for (int i = 0; i + 2 < PD; i += 2) {
+      if (s + i < nk) {
+        body(s + i, i);
+        body(s + i + 1, i + 1);
+      }
     }
     __syncthreads();
 
@@ -611,7 +636,10 @@ int linear_bx(const lx_linear_bx& g, hipStream_t stream) {
     // every CU gets the same number of slab pairs whatever the tile count.
     const int tiles = a.tiles_m * a.tiles_n;
     const long units = (long)tiles * (g.K / (2 * kBxBK));
-    const int G = (int)std::min<long>(device_cus(), units);
+#ifndef LX_BX_SK_SLOTS64
+#define LX_BX_SK_SLOTS64 1
+#endif
+    const int G = (int)std::min<long>(device_cus() * (g.bm == 64 ? LX_BX_SK_SLOTS64 : 1), units);
     const size_t need = (size_t)2 * G * g.bm * kBxBN;
     if (tiles <= g.n_counters && need <= g.ws_floats && need * 4 < (1u << 31)) {
       a.streamk = 1;
