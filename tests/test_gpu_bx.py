@@ -244,10 +244,12 @@ def test_split_operand_nonfinite_inputs(gpu, ops):
     qkv[0, 10, 3 * 64 + 5] = np.nan         # q of batch 0, query 10, head 3
     qkv[1, 20, D + 5 * 64 + 7] = np.inf     # k of batch 1, key 20, head 5
     qd = dev(qkv, gpu)
-    o = ops.attention(qd[..., :D], qd[..., D:2 * D], qd[..., 2 * D:], 16).cpu().numpy()
     hit = np.zeros((B, T, 16), bool)
     hit[0, 10, 3] = True
     hit[1, :, 5] = True
-    oh = o.reshape(B, T, 16, 64)
-    assert np.isnan(oh[hit]).all()
-    assert np.isfinite(oh[~hit]).all()
+    for products in (6, 3):
+        o = ops.attention(qd[..., :D], qd[..., D:2 * D], qd[..., 2 * D:], 16,
+                          products=products).cpu().numpy()
+        oh = o.reshape(B, T, 16, 64)
+        assert np.isnan(oh[hit]).all(), products
+        assert np.isfinite(oh[~hit]).all(), products
