@@ -1036,10 +1036,12 @@ int attention(const float* q, int ldq, const float* k, int ldk, const float* v, 
   // grid of several rounds (T = 1500: 181 vs 170 us) and the small grids stay
   // on the fp32 kernel, whose 70 KB (or single-buffered) LDS lets two
   // workgroups share a CU.
-  // With three products (two bf16 parts per operand) the same split and
-  // layouts apply.
-  const bool split = layout == 2 || (layout == 1 && wg64 <= 256);
+  // With three products (two bf16 parts per operand) the split kernel's K/V
+  // planes take 72 KB (64-query layout), so two of its workgroups share a CU
+  // and it also runs the 64-query grids of several rounds (T = 1500: 157 ->
+  // 99 us; T = 2500: 416 -> 263 us against the fp32 kernel).
   const bool np3 = products == 3;
+  const bool split = layout == 2 || (layout == 1 && (wg64 <= 256 || np3));
   auto pick = [&]() {
     if (split && np3) {
       if (layout == 2)

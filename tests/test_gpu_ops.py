@@ -406,14 +406,19 @@ def test_linear_split_rejects_bad_arguments(gpu, ops):
         ops.linear_split(x[:, :48], planes[:, :, :48], tile=1)  # K = 48 not a multiple of 32
 
 
+@pytest.mark.parametrize("products", [6, 3])
 @pytest.mark.parametrize("B,T", [(2, 500), (2, 45), (1, 1), (2, 3000), (2, 1000), (2, 1020),
-                                 (1, 2000), (2, 1500)])
-def test_attention_dit(gpu, ops, B, T):
-    announce(f"attention dit B={B} T={T}")
+                                 (1, 2000), (2, 1500), (1, 2500)])
+def test_attention_dit(gpu, ops, B, T, products):
+    """Every layout: 32-query workgroups (T = 45, 1), 64-query grids of one round
+    (T = 500) and of several (T = 1500, 2500; the fp32 kernel with six products, the
+    split-operand kernel with three), 128-query grids (T = 1000, 2000, 3000)."""
+    announce(f"attention dit B={B} T={T} products={products}")
     D = 1024
     qkv = rnd((B, T, 3 * D), 1)
     qd = dev(qkv, gpu)
-    o = ops.attention(qd[..., :D], qd[..., D:2 * D], qd[..., 2 * D:], 16).cpu().numpy()
+    o = ops.attention(qd[..., :D], qd[..., D:2 * D], qd[..., 2 * D:], 16,
+                      products=products).cpu().numpy()
     ref = orc.attention(qkv[..., :D], qkv[..., D:2 * D], qkv[..., 2 * D:], 16)
     assert orc.rel_err(o, ref) < TOL
 
@@ -423,13 +428,14 @@ def test_attention_dit(gpu, ops, B, T):
 def test_attention_fp32_level_error(gpu, ops, T, products):
     """T = 500 (64-query layout, one round) and T = 1000 (128-query layout) run the
     split-operand kernel, which forms Q K^T and P V from bf16 splits of the fp32
-    operands; T = 1500 runs the fp32 kernel.  Against a float64 softmax(q k^T) v
-    with N(0, 1) q and k (scores of std 1): six products (three-part splits) stay
-    at fp32 level, the maximum error below 2e-6 of the output's largest magnitude
-    (measured: 1.0e-6 at T = 500, 8.9e-7 at T = 1000, fp32 kernel 1.1e-6 at
-    T = 1500); three products (two-part splits) below 4e-5 (measured 1.5e-5 and
-    1.8e-5: a score error of about 2^-17 of sum |q_i k_i| moves each probability
-    by that much times ln 2)."""
+    operands; T = 1500 (64-query layout, two rounds) runs the fp32 kernel with six
+    products and the split-operand kernel with three.  Against a float64
+    softmax(q k^T) v with N(0, 1) q and k (scores of std 1): six products
+    (three-part splits) stay at fp32 level, the maximum error below 2e-6 of the
+    output's largest magnitude (measured: 1.0e-6 at T = 500, 8.9e-7 at T = 1000,
+    fp32 kernel 1.1e-6 at T = 1500); three products (two-part splits) below 4e-5
+    (measured 1.5e-5 and 1.8e-5: a score error of about 2^-17 of sum |q_i k_i|
+    moves each probability by that much times ln 2)."""
     B, D = 2, 1024
     qkv = rnd((B, T, 3 * D), 21)
     qd = dev(qkv, gpu)
@@ -444,22 +450,23 @@ def test_attention_fp32_level_error(gpu, ops, T, products):
         ref = torch.softmax(qh @ kh.transpose(1, 2), dim=-1) @ vh
         worst = max(worst, float((o[:, :, c] - ref).abs().max() / ref.abs().max()))
     announce(f"attention T={T} products={products} max error vs float64: {worst:.2e}")
-    assert worst < (2e-6 if products == 6 or T == 1500 else 4e-5)
+    assert worst < (2e-6 if products == 6 else 4e-5)
 
 
-@pytest.mark.parametrize("Tq", [64, 2500, 2048])
-def test_attention_kv_past_2gib(gpu, ops, Tq):
+@pytest.mark.parametrize("Tq,products", [(64, 6), (2500, 6), (2048, 6), (2500, 3)])
+def test_attention_kv_past_2gib(gpu, ops, Tq, products):
     """K and V rows of a fused (180000, 3072) buffer (2.2 GB, row stride 3072): byte
-    offsets pass 2^31, so every layout (Tq = 64: 32-query workgroups; 2500: 64-query;
-    2048: 128-query) loads K/V through 64-bit addresses with keys clamped into range.
+    offsets pass 2^31, so every layout (Tq = 64: 32-query workgroups; 2500: 64-query,
+    the fp32 kernel with six products and the split-operand kernel with three; 2048:
+    128-query) loads K/V through 64-bit addresses with keys clamped into range.
     Sampled queries are checked against a float64 softmax(q k^T) v computed with torch."""
-    announce(f"attention Tq={Tq} Tk=180000 (64-bit K/V addressing)")
+    announce(f"attention Tq={Tq} Tk=180000 products={products} (64-bit K/V addressing)")
     Tk, H, D = 180000, 16, 1024
     g = torch.Generator(device=gpu).manual_seed(6)
     q = torch.randn(1, Tq, D, device=gpu, generator=g)
     kv = torch.randn(1, Tk, 3 * D, device=gpu, generator=g)
     k, v = kv[..., :D], kv[..., 2 * D:]
-    o = ops.attention(q, k, v, H)
+    o = ops.attention(q, k, v, H, products=products)
     sel = [0, 1, Tq // 2, Tq - 1]
     for h in (0, 7, 15):
         c = slice(h * 64, h * 64 + 64)
@@ -486,17 +493,18 @@ def test_attention_wide_layout_gqa(gpu, ops, causal):
     assert orc.rel_err(o, ref) < TOL
 
 
-@pytest.mark.parametrize("B,T", [(2, 1000), (1, 2000)])
-def test_attention_wide_layout_causal(gpu, ops, B, T):
+@pytest.mark.parametrize("B,T,products", [(2, 1000, 6), (1, 2000, 6), (1, 1500, 3)])
+def test_attention_wide_layout_causal(gpu, ops, B, T, products):
     """Causal masking through the 128-query layout (grids of a whole number of
-    workgroups per CU), with a query offset on the second case."""
-    announce(f"attention wide causal B={B} T={T}")
+    workgroups per CU) and, with three products, the split-operand kernel's 64-query
+    grid of several rounds, with a query offset where B = 1."""
+    announce(f"attention wide causal B={B} T={T} products={products}")
     D = 1024
     off = 0 if B == 2 else 48
     q = rnd((B, T, D), 11)
     k, v = rnd((B, T + off, D), 12), rnd((B, T + off, D), 13)
     o = ops.attention(dev(q, gpu), dev(k, gpu), dev(v, gpu), 16, causal=True,
-                      q_offset=off).cpu().numpy()
+                      q_offset=off, products=products).cpu().numpy()
     ref = orc.attention(q, k, v, 16, causal=True, q_offset=off)
     assert orc.rel_err(o, ref) < TOL
 
