@@ -317,6 +317,21 @@ int lx_conv_pos_mish_f32(const float* x, const float* wp, const float* bias,
 int lx_conv_pack_weight_f32(const float* w, float* wp, int C, int G, int K,
                             hipStream_t stream);
 
+/* lx_conv_pos_mish_f32 as fp32 arithmetic on the bf16 matrix cores: the
+ * operand splits and product counts of lx_linear_bx (products 3 or 6), the
+ * input window split once per workgroup, the weight `wf` in MFMA fragment
+ * order written by lx_conv_frag_pack_f32 (3 * C * 64 * K bf16, 16-byte
+ * aligned).  Same arguments, shapes and result otherwise (error of the
+ * products as lx_linear_bx's).  Replaces the same nodes as
+ * lx_conv_pos_mish_f32 (src/flow/dit.cpp:113-122); the estimator runs it with
+ * its lx_dit_set_products setting. */
+int lx_conv_pos_mish_bx_f32(const float* x, const void* wf, const float* bias,
+                            const float* resid, float* y, int B, int T, int C, int G, int K,
+                            int products, hipStream_t stream);
+/* Packs a torch Conv1d weight w (C, 64, K) (C/G = 64, K <= 32) into the
+ * fragment order read above (done once at load). */
+int lx_conv_frag_pack_f32(const float* w, void* wf, int C, int G, int K, hipStream_t stream);
+
 /* ------------------------------------------------------------------------ */
 /* DiT estimator and CFM Euler loop (host C++ over the ops above)            */
 /* ------------------------------------------------------------------------ */

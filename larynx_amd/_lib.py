@@ -162,6 +162,10 @@ SIGNATURES = [
     ("lx_conv_pos_mish_f32", C.c_int,
      [fp, fp, fp, fp, fp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, stream_t]),
     ("lx_conv_pack_weight_f32", C.c_int, [fp, fp, C.c_int, C.c_int, C.c_int, stream_t]),
+    ("lx_conv_pos_mish_bx_f32", C.c_int,
+     [fp, C.c_void_p, fp, fp, fp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
+      stream_t]),
+    ("lx_conv_frag_pack_f32", C.c_int, [fp, C.c_void_p, C.c_int, C.c_int, C.c_int, stream_t]),
     ("lx_dit_create", C.c_int,
      [C.POINTER(DitWeights), C.c_int, C.c_int, C.POINTER(C.c_void_p)]),
     ("lx_dit_destroy", None, [C.c_void_p]),

@@ -51,7 +51,9 @@ struct lx_dit {
   // packed weights
   float *tm0_w, *tm0_b, *tm2_w, *tm2_b;
   float *in_w, *in_b;
-  float *conv1_wp, *conv1_b, *conv2_wp, *conv2_b;
+  // conv_pos weights in MFMA fragment order (conv_frag_pack: 3 * D * 64 * K bf16)
+  void *conv1_wf, *conv2_wf;
+  float *conv1_b, *conv2_b;
   float *ada_w, *ada_b;                 // (NA, D), (NA)
   // Block projections: with `frag` the weights are kept only in MFMA
   // fragment order (wfrag_pack: three bf16 parts, 3 * N * K bf16) for the
@@ -126,18 +128,19 @@ int forward_core(lx_dit* m, const float* x, long x_bstride, const float* mu, con
   // InputEmbedding: proj(concat[x, cond, mu, spks]) + conv_pos_embed.
   LX_TRY(dit_pack_input(x, x_bstride, cond, mu, spks, cfg, m->A0, B, T, mel, s));
   LX_TRY(lx_linear_f32(m->A0, 4 * mel, m->in_w, m->in_b, m->xe, D, rows, D, 4 * mel, nullptr, s));
-  LX_TRY(conv_pos_mish_packed(m->xe, m->conv1_wp, m->conv1_b, nullptr, m->c1, B, T, D, kConvG,
-                              kConvK, s));
+  // conv_pos on the split-operand conv with the estimator's product count.
+  LX_TRY(conv_pos_mish_bx(m->xe, m->conv1_wf, m->conv1_b, nullptr, m->c1, B, T, D, kConvG, kConvK,
+                          m->products, s));
   // h = xe + mish(conv2(c1)); c1 doubles as the conv_pos capture source below.
-  LX_TRY(conv_pos_mish_packed(m->c1, m->conv2_wp, m->conv2_b, m->xe, m->h, B, T, D, kConvG, kConvK,
-                              s));
+  LX_TRY(conv_pos_mish_bx(m->c1, m->conv2_wf, m->conv2_b, m->xe, m->h, B, T, D, kConvG, kConvK,
+                          m->products, s));
   if (m->cap.input_proj)
     (void)hipMemcpyAsync(m->cap.input_proj, m->xe, sizeof(float) * rows * D,
                          hipMemcpyDeviceToDevice, s);
   if (m->cap.conv_pos) {
     // conv_pos = h - xe is not recomputed; re-run conv2 without the residual.
-    LX_TRY(conv_pos_mish_packed(m->c1, m->conv2_wp, m->conv2_b, nullptr, m->xn, B, T, D, kConvG,
-                                kConvK, s));
+    LX_TRY(conv_pos_mish_bx(m->c1, m->conv2_wf, m->conv2_b, nullptr, m->xn, B, T, D, kConvG,
+                            kConvK, m->products, s));
     (void)hipMemcpyAsync(m->cap.conv_pos, m->xn, sizeof(float) * rows * D,
                          hipMemcpyDeviceToDevice, s);
   }
@@ -321,10 +324,11 @@ extern "C" int lx_dit_create(const lx_dit_weights* w, int B, int max_T, lx_dit**
   m->tm2_b = A(D);
   m->in_w = A((size_t)D * 4 * mel);
   m->in_b = A(D);
-  m->conv1_wp = A((size_t)D * 64 * kConvK);
+  m->conv1_wf = a.alloc<unsigned short>((size_t)3 * D * 64 * kConvK);
   m->conv1_b = A(D);
-  m->conv2_wp = A((size_t)D * 64 * kConvK);
+  m->conv2_wf = a.alloc<unsigned short>((size_t)3 * D * 64 * kConvK);
   m->conv2_b = A(D);
+  ok = ok && m->conv1_wf && m->conv2_wf;
   m->ada_w = A((size_t)m->NA * D);
   m->ada_b = A(m->NA);
   const size_t rows = (size_t)B * max_T;
@@ -414,8 +418,8 @@ extern "C" int lx_dit_create(const lx_dit_weights* w, int B, int max_T, lx_dit**
   C(m->conv1_b, w->conv_pos_1_b, D);
   C(m->conv2_b, w->conv_pos_2_b, D);
   if (rc == LX_OK) rc = (w->conv_pos_1_w && w->conv_pos_2_w) ? LX_OK : LX_ERR_ARG;
-  if (rc == LX_OK) rc = conv_weight_pack(w->conv_pos_1_w, m->conv1_wp, D, kConvG, kConvK, s);
-  if (rc == LX_OK) rc = conv_weight_pack(w->conv_pos_2_w, m->conv2_wp, D, kConvG, kConvK, s);
+  if (rc == LX_OK) rc = conv_frag_pack(w->conv_pos_1_w, m->conv1_wf, D, kConvG, kConvK, s);
+  if (rc == LX_OK) rc = conv_frag_pack(w->conv_pos_2_w, m->conv2_wf, D, kConvG, kConvK, s);
   for (int i = 0; i < depth && rc == LX_OK; ++i) {
     const lx_dit_block_weights& bw = w->blocks[i];
     C(m->ada_w + (size_t)i * 6 * D * D, bw.attn_norm_w, (size_t)6 * D * D);

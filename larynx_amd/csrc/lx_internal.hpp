@@ -226,6 +226,12 @@ int conv_kmajor_pack(const float* w, int OC, int IC, int K, float* wp, hipStream
 // (synchronous), so the weight file's device copy can be released.
 int qwen2_own_tables(lx_qwen2* m);
 
+// Conv weight (C, 64, K) -> MFMA fragment order (lx_conv_frag_pack_f32), and the
+// split-operand grouped conv + Mish on it (lx_conv_pos_mish_bx_f32).
+int conv_frag_pack(const float* w, void* wf, int C, int G, int K, hipStream_t stream);
+int conv_pos_mish_bx(const float* x, const void* wf, const float* bias, const float* resid,
+                     float* y, int B, int T, int C, int G, int K, int products,
+                     hipStream_t stream);
 // Grouped conv + Mish with tap-major packed weights (lx_conv_pos_mish_f32).
 int conv_pos_mish_packed(const float* x, const float* wp, const float* bias, const float* resid,
                          float* y, int B, int T, int C, int G, int K, hipStream_t stream);

@@ -17,7 +17,7 @@ from ._lib import (LX_BX_OUT_F32, LX_BX_OUT_PARTIAL, LX_EPI_GATED_RESID,
 __all__ = [
     "stream", "ada_ln", "adaln_resid", "adaln_emb", "rope_partial", "gelu_tanh", "gated_residual",
     "timestep_embed", "time_mlp", "rms_norm", "rope_full", "swiglu", "embed_gather", "linear",
-    "attention", "conv_pos_mish", "conv_pack_weight", "Epilogue", "split_planes",
+    "attention", "conv_pos_mish", "conv_pack_weight", "conv_frag_pack", "conv_pos_mish_bx", "Epilogue", "split_planes",
     "linear_split", "wfrag_pack", "linear_bx", "bx_scratch",
     "LX_EPI_NONE", "LX_EPI_GELU_TANH", "LX_EPI_GATED_RESID", "LX_EPI_ROPE_PARTIAL",
     "LX_EPI_RESID", "LX_EPI_SWIGLU_PAIRED", "LX_BX_OUT_F32", "LX_BX_OUT_PARTIAL",
@@ -288,4 +288,23 @@ def conv_pos_mish(x, wp, bias, resid=None, groups=16, kernel=31):
     y = torch.empty_like(x)
     check(lib.lx_conv_pos_mish_f32(_p(x), _p(wp), _p(bias), _p(resid), _p(y), B, T, Cc, groups,
                                    kernel, stream()))
+    return y
+
+
+def conv_frag_pack(w, groups=16):
+    """torch Conv1d weight (C, 64, K) -> MFMA fragment order (3 * C * 64 * K bf16) for
+    conv_pos_mish_bx."""
+    Cc, cg, K = w.shape
+    wf = torch.empty(3 * Cc * cg * K, device=w.device, dtype=torch.bfloat16)
+    check(lib.lx_conv_frag_pack_f32(_p(w), wf.data_ptr(), Cc, groups, K, stream()))
+    return wf
+
+
+def conv_pos_mish_bx(x, wf, bias, resid=None, groups=16, kernel=31, products=3):
+    """conv_pos_mish as fp32 arithmetic on the bf16 matrix cores (split operands, 3 or 6
+    products per fp32 product); wf = conv_frag_pack(w).  src/flow/dit.cpp:113-122."""
+    B, T, Cc = x.shape
+    y = torch.empty_like(x)
+    check(lib.lx_conv_pos_mish_bx_f32(_p(x), wf.data_ptr(), _p(bias), _p(resid), _p(y), B, T, Cc,
+                                      groups, kernel, products, stream()))
     return y

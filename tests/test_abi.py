@@ -64,6 +64,9 @@ def test_argument_errors_need_no_device():
     assert lib.lx_linear_f32(fake, 6, fake, None, fake, 6, 8, 8, 6, None, None) == LX_ERR_ARG
     assert lib.lx_conv_pos_mish_f32(fake, fake, fake, None, fake, 1, 8, 1024, 8, 31,
                                     None) == LX_ERR_ARG  # 128 channels per group
+    assert lib.lx_conv_pos_mish_bx_f32(fake, fake, fake, None, fake, 1, 8, 1024, 16, 31, 4,
+                                       None) == LX_ERR_ARG  # products 3 or 6
+    assert lib.lx_conv_frag_pack_f32(fake, fake, 1024, 16, 33, None) == LX_ERR_ARG
     # fragment-order GEMM: N not a multiple of 128, an empty last K slice (18
     # steps of 64 as 7 slices of 3), a tile height other than 64 / 128, a
     # product count other than 3 / 6

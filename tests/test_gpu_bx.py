@@ -217,7 +217,8 @@ def test_split_operand_nonfinite_inputs(gpu, ops):
     fp32 kernel gives +-inf or a finite product; every other output is
     unaffected.  GEMM: the rows of A holding such an element.  Attention: the
     query row of such a q element, and every query of the (batch, head) whose
-    keys hold one."""
+    keys hold one.  conv_pos: the channels of its group at the frames whose
+    causal window holds it."""
     announce("split-operand kernels: non-finite inputs")
     M, N, K = 1000, 1024, 1024
     x = rnd((M, K), 40)
@@ -253,3 +254,20 @@ def test_split_operand_nonfinite_inputs(gpu, ops):
         oh = o.reshape(B, T, 16, 64)
         assert np.isnan(oh[hit]).all(), products
         assert np.isfinite(oh[~hit]).all(), products
+
+    # conv_pos: an infinite input element reaches the 64 outputs of its group at
+    # the K frames whose causal window holds it
+    T, Kc = 100, 31
+    xc = rnd((1, T, D), 43)
+    wc, bc = rnd((D, 64, Kc), 44, 0.03), rnd((D,), 45, 0.03)
+    xc[0, 10, 3 * 64 + 5] = np.inf
+    hitc = np.zeros((1, T, D), bool)
+    hitc[0, 10:10 + Kc, 3 * 64:4 * 64] = True
+    x0 = xc.copy()
+    x0[0, 10, 3 * 64 + 5] = 0.0
+    refc = orc.conv_pos_mish(x0, wc, bc)
+    wf = ops.conv_frag_pack(dev(wc, gpu))
+    for products in (6, 3):
+        yc = ops.conv_pos_mish_bx(dev(xc, gpu), wf, dev(bc, gpu), products=products).cpu().numpy()
+        assert np.isnan(yc[hitc]).all(), products
+        assert orc.rel_err(yc[~hitc], refc[~hitc]) < TOL, products

@@ -586,3 +586,120 @@ def test_conv_pos_mish_kernel_sizes(gpu, ops, T, K):
     wp = ops.conv_pack_weight(dev(w, gpu))
     y = ops.conv_pos_mish(dev(x, gpu), wp, dev(b, gpu), dev(r, gpu), kernel=K).cpu().numpy()
     assert orc.rel_err(y, orc.conv_pos_mish(x, w, b, r)) < TOL
+
+
+def unpack_conv_frag(wf, C, K):
+    """w (C, 64, K) rebuilt on the host from conv_frag_pack's order: part p of
+    w[64 g + 32 ob + l % 32, 16 ks + (l // 32) * 8 + j, k] at
+    ((((g * K + k) * 2 + ob) * 4 + ks) * 3 + p) * 512 + l * 8 + j."""
+    G = C // 64
+    u = wf.view(torch.int16).cpu().numpy().astype(np.int32).astype(np.uint32) << 16
+    f = u.view(np.float32).reshape(G, K, 2, 4, 3, 2, 32, 8)  # g, k, ob, ks, part, h, r, j
+    tot = (f[:, :, :, :, 0].astype(np.float64) + f[:, :, :, :, 1]) + f[:, :, :, :, 2]
+    return tot.transpose(0, 2, 5, 3, 4, 6, 1).reshape(C, 64, K)
+
+
+def test_conv_frag_pack_layout_and_parts_exact(gpu, ops):
+    """The fragment order places every tap weight where the MFMA B operand expects
+    it, and its three bf16 parts sum back to the fp32 weight exactly."""
+    announce("conv_frag_pack layout")
+    C, K = 128, 5
+    w = rnd((C, 64, K), 9, 0.05)
+    wf = ops.conv_frag_pack(dev(w, gpu), groups=C // 64)
+    assert wf.numel() == 3 * C * 64 * K
+    assert np.array_equal(unpack_conv_frag(wf, C, K), w.astype(np.float64))
+
+
+@pytest.mark.parametrize("products", [3, 6])
+@pytest.mark.parametrize("B,T", [(2, 500), (2, 50), (1, 1), (2, 3000)])
+def test_conv_pos_mish_bx(gpu, ops, B, T, products):
+    """The split-operand conv_pos (the estimator's) against the oracle, with and
+    without the residual, ragged last frame tiles (T = 500, 50, 1, 3000)."""
+    announce(f"conv_pos_bx B={B} T={T} products={products}")
+    Cc = 1024
+    x, r = rnd((B, T, Cc), 1), rnd((B, T, Cc), 4)
+    w, b = rnd((Cc, 64, 31), 2, 0.03), rnd((Cc,), 3, 0.03)
+    wf = ops.conv_frag_pack(dev(w, gpu))
+    y = ops.conv_pos_mish_bx(dev(x, gpu), wf, dev(b, gpu), dev(r, gpu),
+                             products=products).cpu().numpy()
+    assert orc.rel_err(y, orc.conv_pos_mish(x, w, b, r)) < TOL
+    y0 = ops.conv_pos_mish_bx(dev(x, gpu), wf, dev(b, gpu), products=products).cpu().numpy()
+    assert orc.rel_err(y0, orc.conv_pos_mish(x, w, b)) < TOL
+
+
+@pytest.mark.parametrize("T,K", [(50, 1), (50, 2), (50, 32), (130, 17), (2100, 5)])
+def test_conv_pos_mish_bx_kernel_sizes(gpu, ops, T, K):
+    """Tap counts other than the model's 31: the four tap groups take ceil(K / 4)
+    taps each (K = 1 and 2 leave groups without taps, K = 17 a short last group)."""
+    announce(f"conv_pos_bx B=1 T={T} K={K}")
+    Cc = 1024
+    x, r = rnd((1, T, Cc), 5), rnd((1, T, Cc), 6)
+    w, b = rnd((Cc, 64, K), 7, 0.03), rnd((Cc,), 8, 0.03)
+    wf = ops.conv_frag_pack(dev(w, gpu))
+    y = ops.conv_pos_mish_bx(dev(x, gpu), wf, dev(b, gpu), dev(r, gpu), kernel=K,
+                             products=3).cpu().numpy()
+    assert orc.rel_err(y, orc.conv_pos_mish(x, w, b, r)) < TOL
+
+
+@pytest.mark.parametrize("products", [3, 6])
+def test_conv_pos_mish_bx_error_level(gpu, ops, products):
+    """Against the oracle (float64 sums) at T = 500 with N(0, 1) inputs: six
+    products stay at the fp32 level (below 4e-6 of the output's largest
+    magnitude, the bound of the split-operand GEMM), three below 2e-5."""
+    announce(f"conv_pos_bx error level products={products}")
+    B, T, Cc = 2, 500, 1024
+    x = rnd((B, T, Cc), 11)
+    w, b = rnd((Cc, 64, 31), 12, 0.03), rnd((Cc,), 13, 0.03)
+    wf = ops.conv_frag_pack(dev(w, gpu))
+    y = ops.conv_pos_mish_bx(dev(x, gpu), wf, dev(b, gpu), products=products).cpu().numpy()
+    err = orc.rel_err(y, orc.conv_pos_mish(x, w, b))
+    announce(f"conv_pos_bx products={products} error {err:.2e}")
+    assert err < (4e-6 if products == 6 else 2e-5), err
+
+
+def test_conv_pos_mish_bx_rejects_bad_arguments(gpu, ops):
+    from larynx_amd import LxError
+    announce("conv_pos_bx bad arguments")
+    x = torch.zeros(1, 8, 1024, device=gpu)
+    b = torch.zeros(1024, device=gpu)
+    wf = ops.conv_frag_pack(torch.zeros(1024, 64, 31, device=gpu))
+    with pytest.raises(LxError):
+        ops.conv_pos_mish_bx(x, wf, b, products=4)
+    with pytest.raises(LxError):  # 128 channels per group
+        ops.conv_pos_mish_bx(x, wf, b, groups=8)
+    with pytest.raises(LxError):
+        ops.conv_pos_mish_bx(x, wf, b, kernel=33)
+    with pytest.raises(LxError):
+        ops.conv_frag_pack(torch.zeros(1024, 64, 33, device=gpu))
+
+
+@pytest.mark.parametrize("split", [False, True])
+def test_mish_elementwise_through_conv(gpu, ops, split):
+    """Mish (the conv epilogue, x n / (n + 2) with n = e^x (e^x + 2)) element by
+    element over [-100, 100] and around its branch at 20: a one-tap conv whose
+    weight is the identity within each group passes x through exactly (fp32
+    kernel; six-product split, whose three parts sum to x), so y = mish(x),
+    checked against float64 x tanh(softplus(x)) within 1e-5 relative (outputs
+    below 1e-30 in magnitude, x < -70, within 1e-35 absolute: a flushed subnormal
+    e^x is allowed there)."""
+    announce(f"mish elementwise split={split}")
+    Cc = 1024
+    vals = np.concatenate([np.linspace(-100, 100, 64 * Cc - 16, dtype=np.float32),
+                           np.float32([0, -0.0, 1e-30, -1e-30, 19.999998, 20, 20.000002, 9,
+                                       9.02, 30, 44.5, 88, -87, -88.7, -89, -104])])
+    x = vals.reshape(1, 64, Cc)
+    w = np.zeros((Cc, 64, 1), np.float32)
+    w[np.arange(Cc), np.arange(Cc) % 64, 0] = 1.0
+    b = np.zeros(Cc, np.float32)
+    if split:
+        y = ops.conv_pos_mish_bx(dev(x, gpu), ops.conv_frag_pack(dev(w, gpu)), dev(b, gpu),
+                                 kernel=1, products=6)
+    else:
+        y = ops.conv_pos_mish(dev(x, gpu), ops.conv_pack_weight(dev(w, gpu)), dev(b, gpu),
+                              kernel=1)
+    y = y.cpu().numpy().astype(np.float64).ravel()
+    xd = vals.astype(np.float64)
+    ref = xd * np.tanh(np.logaddexp(0.0, xd))
+    err = np.abs(y - ref) / np.maximum(np.abs(ref), 1e-30)
+    assert np.all(np.isfinite(y))
+    assert err.max() < 1e-5, (err.max(), xd[err.argmax()])
