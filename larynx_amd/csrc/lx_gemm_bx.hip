@@ -433,7 +433,11 @@ gemm_bx_kernel(BxArgs a, EpiArgs ep) {
     const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
     constexpr bool PRE = BMB == 4;
     float4 eg[SLOTS], ey[SLOTS];
-    int epos[SLOTS];
+    // Rotary epilogue: only tiles that hold rotated columns read positions.
+    bool rot = false;
+    if (EPI == LX_EPI_ROPE_PARTIAL)
+      for (int k = 0; k < ep.sections; ++k)
+        rot |= n0 < k * ep.section + ep.rot_dim && n0 + kBxBN > k * ep.section;
 #pragma unroll
     for (int j = 0; j < SLOTS; ++j) {
       if (!PRE) break;
@@ -441,14 +445,12 @@ gemm_bx_kernel(BxArgs a, EpiArgs ep) {
       const int row = idx / (kBxBN / 4), c = (idx % (kBxBN / 4)) * 4;
       const int m = min(m0 + row, a.M - 1), n = n0 + c;
       eg[j] = ey[j] = z4;
-      epos[j] = 0;
       if (OUT == BX_OUT_F32) {
         if (EPI == LX_EPI_GATED_RESID)
           eg[j] = *reinterpret_cast<const float4*>(ep.gate + (long)(m / ep.rows_per_batch) *
                                                                  ep.gate_stride + n);
         if (EPI == LX_EPI_GATED_RESID || EPI == LX_EPI_RESID)
           ey[j] = *reinterpret_cast<const float4*>(a.Y + (long)m * a.ldy + n);
-        if (EPI == LX_EPI_ROPE_PARTIAL) epos[j] = ep.pos[m % ep.rows_per_batch];
       }
     }
     constexpr int LDC = kBxBN + 4;
@@ -466,25 +468,28 @@ gemm_bx_kernel(BxArgs a, EpiArgs ep) {
     // loop, past the register budget of the 64-row tiles.
     int etid = tid;
     asm volatile("" : "+v"(etid));
+    // A thread's slots share their 4 columns (kBxThreads is a multiple of the
+    // 32 float4 per row): the bias is one float4, loaded once before the first
+    // store (reloaded after each store to Y, it waited for a round trip).
+    const int ec = (etid % (kBxBN / 4)) * 4;
+    const float4 eb = a.bias ? *reinterpret_cast<const float4*>(a.bias + n0 + ec) : z4;
 #pragma unroll
     for (int j = 0; j < SLOTS; ++j) {
       const int idx = etid + j * kBxThreads;
-      const int row = idx / (kBxBN / 4), c = (idx % (kBxBN / 4)) * 4;
-      const int m = m0 + row, n = n0 + c;
+      const int row = idx / (kBxBN / 4);
+      const int m = m0 + row, n = n0 + ec;
       if (m >= a.M) continue;
-      const float4 v = *reinterpret_cast<const float4*>(Cs + row * LDC + c);
-      const float4 eb = a.bias ? *reinterpret_cast<const float4*>(a.bias + n) : z4;
+      const float4 v = *reinterpret_cast<const float4*>(Cs + row * LDC + ec);
       if (!PRE) {
         eg[j] = ey[j] = z4;
-        epos[j] = 0;
         if (EPI == LX_EPI_GATED_RESID)
           eg[j] = *reinterpret_cast<const float4*>(ep.gate + (long)(m / ep.rows_per_batch) *
                                                                  ep.gate_stride + n);
         if (EPI == LX_EPI_GATED_RESID || EPI == LX_EPI_RESID)
           ey[j] = *reinterpret_cast<const float4*>(a.Y + (long)m * a.ldy + n);
-        if (EPI == LX_EPI_ROPE_PARTIAL) epos[j] = ep.pos[m % ep.rows_per_batch];
       }
-      epilogue4v<EPI>(a.Y, (int)a.ldy, m, n, v, eb, eg[j], ey[j], epos[j], ep);
+      const int posm = rot ? ep.pos[m % ep.rows_per_batch] : 0;
+      epilogue4v<EPI>(a.Y, (int)a.ldy, m, n, v, eb, eg[j], ey[j], posm, ep);
     }
   }
 }

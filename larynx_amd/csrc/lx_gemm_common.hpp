@@ -23,7 +23,7 @@ typedef unsigned uintx2_t __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ void rotate_pair(float& x0, float& x1, float ang) {
   float s, c;
-  sincosf(ang, &s, &c);
+  rope_sincos(ang, &s, &c);
   float a = x0 * c - x1 * s;
   float b = x1 * c + x0 * s;
   x0 = a;
