@@ -119,12 +119,16 @@ def splitk_slices(M, N, K, target_wgs=512, max_slices=8):
 
 def in_step_matrix(records, ops):
     """Average in-step duration of the T=500 step's matrix kernels (64-row tiles,
-    the estimator's product count) from activity records of whole steps; the
-    out and FF2 projections share one kernel (the partial-product output)."""
+    the estimator's product count; with three products the activations arrive
+    as two-part packed rows and FF0 writes its output packed) from activity
+    records of whole steps; the out and FF2 projections share one kernel (the
+    partial-product output)."""
+    ap = ", 1" if DIT_PRODUCTS == 3 else ""
+    ff0_out = ops.LX_BX_OUT_PACKED if DIT_PRODUCTS == 3 else ops.LX_BX_OUT_F32
     pats = {
-        "gemm_qkv_rope": f"gemm_bx_kernel<{ops.LX_EPI_ROPE_PARTIAL}, 2, 0, {DIT_PRODUCTS}>",
-        "gemm_ff0_gelu": f"gemm_bx_kernel<{ops.LX_EPI_GELU_TANH}, 2, 0, {DIT_PRODUCTS}>",
-        "gemm_out_ff2_partial": f"gemm_bx_kernel<{ops.LX_EPI_NONE}, 2, 1, {DIT_PRODUCTS}>",
+        "gemm_qkv_rope": f"gemm_bx_kernel<{ops.LX_EPI_ROPE_PARTIAL}, 2, 0, {DIT_PRODUCTS}{ap}>",
+        "gemm_ff0_gelu": f"gemm_bx_kernel<{ops.LX_EPI_GELU_TANH}, 2, {ff0_out}, {DIT_PRODUCTS}{ap}>",
+        "gemm_out_ff2_partial": f"gemm_bx_kernel<{ops.LX_EPI_NONE}, 2, 1, {DIT_PRODUCTS}{ap}>",
         "attention": f"attn_bx_kernel<2, 2, true, {DIT_PRODUCTS}>",
     }
     out = {}
@@ -143,6 +147,18 @@ def prefill_bx_slices(rows, N, K):
     most = min(9, steps, max(1, 256 // tiles))
     per = -(-steps // most)
     return -(-steps // per)
+
+
+def pack2(torch, x):
+    """Two-part packed rows of an fp32 (M, K) tensor, built with torch: each
+    aligned group of four values as the four bf16(x) then the four
+    bf16(x - bf16(x)) (round to nearest even), in the group's 16 bytes -- the
+    operand linear_bx reads with a_packed."""
+    M, K = x.shape
+    x0 = x.to(torch.bfloat16)
+    x1 = (x - x0.float()).to(torch.bfloat16)
+    both = torch.stack([x0.view(M, K // 4, 4), x1.view(M, K // 4, 4)], dim=2)
+    return both.reshape(M, 2 * K).view(torch.float32).contiguous()
 
 
 def event_time_ms(fn, n, torch):
@@ -274,27 +290,36 @@ def gemm_kernels(torch, ops, T, dev):
     qv = qkv.view(B, T, 3 * D)
     hv = h.view(M, D)
 
-    def proj(x, W, b, ep, y):
+    def proj(x, W, b, ep, y, pack_out=False):
         N = W.shape[0]
         wf = ops.wfrag_pack(W)
         kind, sl = dit_projection_plan(M, N)
         fp32 = (lambda: ops.linear(x, W, b, ep, out=y))
+        xp = pack2(torch, x)
 
         def bx(products):
+            # with three products the estimator passes its activations as
+            # two-part packed rows (and FF0 writes its output that way)
+            pk = products == 3
+            a = xp if pk else x
             if kind == "partial":
-                return lambda: ops.linear_bx(x, wf, N, out=part, out_kind=ops.LX_BX_OUT_PARTIAL,
-                                             bm=64, slices=sl, products=products)
-            return lambda: ops.linear_bx(x, wf, N, b, ep, out=y, bm=64, products=products)
+                return lambda: ops.linear_bx(a, wf, N, out=part, out_kind=ops.LX_BX_OUT_PARTIAL,
+                                             bm=64, slices=sl, products=products, a_packed=pk)
+            ok = ops.LX_BX_OUT_PACKED if pk and pack_out else ops.LX_BX_OUT_F32
+            return lambda: ops.linear_bx(a, wf, N, b, ep, out=y, out_kind=ok, bm=64,
+                                         products=products, a_packed=pk)
         kern = (f"gemm_bx_kernel 64x128, {DIT_PRODUCTS} products"
+                + (", packed activations" if DIT_PRODUCTS == 3 else "")
                 + (f", {sl} K slices (sum folded into adaln_resid)" if kind == "partial" else ""))
         return bx(DIT_PRODUCTS), kern, fp32, bx(6)
     cases = {
         "gemm_qkv_rope": (proj(xd, wq, bq, rope, qkv), 2 * M * 3 * D * D, 1),
         "gemm_out_gated": (proj(xd, wo, bd, gated, hv), 2 * M * D * D, 1),
-        "gemm_ff0_gelu": (proj(xd, w1, b1, gelu, ff), 2 * M * F * D, 1),
+        "gemm_ff0_gelu": (proj(xd, w1, b1, gelu, ff, pack_out=True), 2 * M * F * D, 1),
         "gemm_ff2_gated": (proj(xf, w2, bd, gated, hv), 2 * M * D * F, 1),
         "attention": ((lambda: ops.attention(qv[..., :D], qv[..., D:2 * D], qv[..., 2 * D:], 16,
-                                             out=att, products=DIT_PRODUCTS),
+                                             out=att, products=DIT_PRODUCTS,
+                                             out_packed=DIT_PRODUCTS == 3),
                        f"attn_bx_kernel ({DIT_PRODUCTS} products) / attn_flash_kernel", None,
                        lambda: ops.attention(qv[..., :D], qv[..., D:2 * D], qv[..., 2 * D:], 16,
                                              out=att, products=6)),
@@ -324,7 +349,8 @@ def gemm_kernels(torch, ops, T, dev):
     # folds the previous projection's two K slices into h first
     if dit_projection_plan(M, D)[0] == "partial":
         ms = steady_launch_ms(lambda: ops.adaln_resid(h, part, bd, gate, emb[:, :D],
-                                                      emb[:, D:2 * D], out=xn), torch)
+                                                      emb[:, D:2 * D], out=xn,
+                                                      packed=DIT_PRODUCTS == 3), torch)
         nbytes = 5 * M * D * 4 + 4 * B * D * 4
         kern = "adaln_resid_kernel (2 K slices + bias, gated residual, LayerNorm)"
     else:
@@ -667,20 +693,27 @@ def counter_probe(torch, ops, launches=20):
     w2 = torch.randn(D, F, device=dev, generator=g) * 0.02
     fq, f0, fo, f2 = (ops.wfrag_pack(w) for w in (wq, w0, wo, w2))
     part = torch.empty(2, M, D, device=dev)
+    # as the estimator runs them: with three products the activations arrive
+    # as two-part packed rows and FF0 / attention write theirs packed
+    pk = DIT_PRODUCTS == 3
+    xa = pack2(torch, xd) if pk else xd
+    ff0_out = ops.LX_BX_OUT_PACKED if pk else ops.LX_BX_OUT_F32
     torch.cuda.synchronize()
     for _ in range(launches):
-        ops.linear_bx(xd, fq, 3 * D, bq, rope, out=qkv, bm=64, products=DIT_PRODUCTS)
+        ops.linear_bx(xa, fq, 3 * D, bq, rope, out=qkv, bm=64, products=DIT_PRODUCTS,
+                      a_packed=pk)
     for _ in range(launches):
-        ops.linear_bx(xd, f0, F, b0, gelu, out=ff, bm=64, products=DIT_PRODUCTS)
+        ops.linear_bx(xa, f0, F, b0, gelu, out=ff, out_kind=ff0_out, bm=64,
+                      products=DIT_PRODUCTS, a_packed=pk)
     for _ in range(launches):
-        ops.linear_bx(xd, fo, D, out=part, out_kind=ops.LX_BX_OUT_PARTIAL, bm=64, slices=2,
-                      products=DIT_PRODUCTS)
+        ops.linear_bx(xa, fo, D, out=part, out_kind=ops.LX_BX_OUT_PARTIAL, bm=64, slices=2,
+                      products=DIT_PRODUCTS, a_packed=pk)
     for _ in range(launches):
         ops.linear_bx(ff, f2, D, out=part, out_kind=ops.LX_BX_OUT_PARTIAL, bm=64, slices=2,
-                      products=DIT_PRODUCTS)
+                      products=DIT_PRODUCTS, a_packed=pk)
     for _ in range(launches):
         ops.attention(q3[..., :D], q3[..., D:2 * D], q3[..., 2 * D:], 16, 16, out=att,
-                      products=DIT_PRODUCTS)
+                      products=DIT_PRODUCTS, out_packed=pk)
     torch.cuda.synchronize()
     print(f"counter probe: {launches} x QKV, FF0, out, FF2 GEMMs and attention (B={B} T={T})",
           flush=True)
@@ -730,9 +763,12 @@ def traffic_probe(torch, ops, launches=20):
     src = torch.randn(COPY_PROBE_BYTES // 4, device=dev, generator=g)
     dst = torch.empty_like(src)
     fq = ops.wfrag_pack(wq)
+    pk = DIT_PRODUCTS == 3  # the estimator's packed activations
+    xa = pack2(torch, xd) if pk else xd
     torch.cuda.synchronize()
     for _ in range(launches):
-        ops.linear_bx(xd, fq, 3 * D, bq, rope, out=qkv, bm=64, products=DIT_PRODUCTS)
+        ops.linear_bx(xa, fq, 3 * D, bq, rope, out=qkv, bm=64, products=DIT_PRODUCTS,
+                      a_packed=pk)
     torch.cuda.synchronize()
     for _ in range(launches):
         dst.copy_(src)

@@ -76,6 +76,14 @@ int lx_adaln_resid_f32(float* h, const float* partials, int splits, long partial
                        const float* bias, const float* gate, long gate_stride,
                        const float* shift, const float* scale, long mod_stride, float* y,
                        int B, int T, int D, float eps, hipStream_t stream);
+/* The same with y written as two-part packed rows (lx_linear_bx's a_packed
+ * operand; bit-identical products to the fp32 y it packs): how the estimator
+ * feeds its three-product QKV and FF0 projections.  No counterpart in the
+ * reference (its activations stay fp32). */
+int lx_adaln_resid_packed_f32(float* h, const float* partials, int splits, long partial_stride,
+                              const float* bias, const float* gate, long gate_stride,
+                              const float* shift, const float* scale, long mod_stride, void* y,
+                              int B, int T, int D, float eps, hipStream_t stream);
 
 /* AdaLN modulation embedding (GEMV over the batch rows):
  *   emb[b, :] = W @ silu(c[b, :]) + bias,   W: (n_out, D) row-major.
@@ -249,10 +257,19 @@ int lx_linear_split_f32(const float* x, int ldx, const void* planes, const float
  * (x0 + x1, 16 significant bits each) and the three products a0 b0 + a0 b1 +
  * a1 b0: half the matrix-core work and two thirds of the W traffic, each
  * product within about 2^-16 of a * b (the packed weight is the same).
+ * Two-part packed rows (three products, bm 64; no stream-K): an fp32 row
+ * packed as 16 bytes per aligned group of four values x, the four bf16(x) and
+ * then the four bf16(x - bf16(x)) -- the same bytes, addresses and row stride
+ * as the fp32 row.  a_packed = 1: A holds such rows (the GEMM does not split
+ * it again; results are bit-identical to the fp32 A it was packed from).
+ * out = LX_BX_OUT_PACKED: Y receives the fp32 epilogue's result (no epilogue
+ * or GELU) as packed rows, for the next such GEMM.  The estimator passes its
+ * activations this way with three products (lx_adaln_resid_packed_f32,
+ * lx_attention_np_f32's out_packed).
  * Replaces linear() = ggml_mul_mat + ggml_add (src/flow/ops.cpp:20-26) with the
  * node its epilogue absorbs; the fragment-ordered weight has no counterpart
  * in the reference (its weights stay fp32). */
-enum { LX_BX_OUT_F32 = 0, LX_BX_OUT_PARTIAL = 1 };
+enum { LX_BX_OUT_F32 = 0, LX_BX_OUT_PARTIAL = 1, LX_BX_OUT_PACKED = 2 };
 typedef struct lx_linear_bx {
   const float* A;
   long lda;
@@ -270,6 +287,7 @@ typedef struct lx_linear_bx {
   unsigned* counters;
   int n_counters;
   int products;
+  int a_packed;
 } lx_linear_bx;
 int lx_wfrag_pack_f32(const float* W, void* Wf, int N, int K, hipStream_t stream);
 int lx_linear_bx_f32(const lx_linear_bx* g, hipStream_t stream);
@@ -293,11 +311,15 @@ int lx_attention_f32(const float* q, int ldq, const float* k, int ldk, const flo
 /* lx_attention_f32 with the split-operand kernel's product count: 6 (as
  * lx_attention_f32) or 3 (two bf16 parts per operand, three products: about
  * half the matrix-core work; the grids that run the fp32 kernel ignore it).
- * The estimator calls it with its lx_dit_set_products setting. */
+ * out_packed != 0: o receives two-part packed rows (lx_linear_bx's a_packed
+ * operand) instead of fp32.  The estimator calls it with its
+ * lx_dit_set_products setting and, with three products, packed output for
+ * its out projection. */
 int lx_attention_np_f32(const float* q, int ldq, const float* k, int ldk, const float* v,
                         int ldv, float* o, int ldo, int B, int Tq, int Tk, int n_heads,
                         int n_kv_heads, int head_dim, float scale, int causal, int q_offset,
-                        int products, hipStream_t stream);
+                        int products, int out_packed,
+                        hipStream_t stream);
 
 /* Causal grouped conv1d + Mish (one CausalConvPositionEmbedding half):
  *   y[b,t,oc] = mish(bias[oc] + sum_{k<K, ic<C/G} w[oc, ic, k] *

@@ -28,6 +28,7 @@ LX_EPI_SWIGLU_PAIRED = 5
 
 LX_BX_OUT_F32 = 0
 LX_BX_OUT_PARTIAL = 1
+LX_BX_OUT_PACKED = 2
 
 fp = C.c_void_p  # device pointer
 ip = C.c_void_p
@@ -61,6 +62,7 @@ class LinearBx(C.Structure):
         ("slice_stride", C.c_long), ("M", C.c_int), ("N", C.c_int), ("K", C.c_int),
         ("bm", C.c_int), ("slices", C.c_int), ("ws", fp), ("ws_floats", C.c_size_t),
         ("counters", C.c_void_p), ("n_counters", C.c_int), ("products", C.c_int),
+        ("a_packed", C.c_int),
     ]
 
 
@@ -129,6 +131,9 @@ SIGNATURES = [
     ("lx_adaln_resid_f32", C.c_int,
      [fp, fp, C.c_int, C.c_long, fp, fp, C.c_long, fp, fp, C.c_long, fp, C.c_int, C.c_int,
       C.c_int, C.c_float, stream_t]),
+    ("lx_adaln_resid_packed_f32", C.c_int,
+     [fp, fp, C.c_int, C.c_long, fp, fp, C.c_long, fp, fp, C.c_long, fp, C.c_int, C.c_int,
+      C.c_int, C.c_float, stream_t]),
     ("lx_adaln_emb_f32", C.c_int, [fp, fp, fp, fp, C.c_int, C.c_int, C.c_int, stream_t]),
     ("lx_rope_partial_interleaved_f32", C.c_int,
      [fp, fp, ip, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, stream_t]),
@@ -158,7 +163,7 @@ SIGNATURES = [
       C.c_int, C.c_int, C.c_float, C.c_int, C.c_int, stream_t]),
     ("lx_attention_np_f32", C.c_int,
      [fp, C.c_int, fp, C.c_int, fp, C.c_int, fp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
-      C.c_int, C.c_int, C.c_float, C.c_int, C.c_int, C.c_int, stream_t]),
+      C.c_int, C.c_int, C.c_float, C.c_int, C.c_int, C.c_int, C.c_int, stream_t]),
     ("lx_conv_pos_mish_f32", C.c_int,
      [fp, fp, fp, fp, fp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, stream_t]),
     ("lx_conv_pack_weight_f32", C.c_int, [fp, fp, C.c_int, C.c_int, C.c_int, stream_t]),

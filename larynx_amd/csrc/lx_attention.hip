@@ -17,6 +17,7 @@
 #include <type_traits>
 
 #include "lx_common.hpp"
+#include "lx_gemm_common.hpp"
 
 namespace lx {
 namespace {
@@ -44,11 +45,20 @@ constexpr size_t flash_lds() {
   return (size_t)2 * (DB ? 2 : 1) * 32 * KS * kLD * sizeof(float);
 }
 
+// Four output channels: fp32, or (opk) a two-part packed group for the
+// three-product GEMM that consumes the attention output.
+__device__ __forceinline__ void store_o4(float* p, floatx4 w, int opk) {
+  if (opk)
+    *reinterpret_cast<uintx4_t*>(p) = pack2_bf16(w);
+  else
+    *reinterpret_cast<floatx4*>(p) = w;
+}
+
 template <int QS, int KS, bool DB, bool BUF>
 __global__ __launch_bounds__(64 * QS * KS) void attn_flash_kernel(
     const float* __restrict__ q, int ldq, const float* __restrict__ k, int ldk,
     const float* __restrict__ v, int ldv, float* __restrict__ o, int ldo, int Tq, int Tk,
-    int n_heads, int rep, float qscale, int causal, int q_offset) {
+    int n_heads, int rep, float qscale, int causal, int q_offset, int opk) {
   constexpr int kQT = 32 * QS;   // queries per workgroup
   constexpr int KT = 32 * KS;    // keys per LDS tile
   constexpr int NT = 64 * QS * KS;   // threads
@@ -376,7 +386,7 @@ __global__ __launch_bounds__(64 * QS * KS) void attn_flash_kernel(
           const float mine = keep[i] * a_s, other = part[i * 64 + lane] * a_o;
           w[e] = (ks == 0 ? mine + other : other + mine) * inv;
         }
-        *reinterpret_cast<floatx4*>(orow + g * 8) = w;
+        store_o4(orow + g * 8, w, opk);
       }
     }
     return;
@@ -435,8 +445,8 @@ __global__ __launch_bounds__(64 * QS * KS) void attn_flash_kernel(
     const int qi = qt0 + row;
     if (qi < Tq) {
       const float* src = otile + (row >> 5) * (32 * kLD) + (row & 31) * kLD + c;
-      *reinterpret_cast<floatx4*>(o + ((long)b * Tq + qi) * ldo + head * kHD + c) =
-          *reinterpret_cast<const floatx4*>(src);
+      store_o4(o + ((long)b * Tq + qi) * ldo + head * kHD + c,
+               *reinterpret_cast<const floatx4*>(src), opk);
     }
   }
 }
@@ -555,7 +565,7 @@ template <int QS, int KS, bool BUF, int NP>
 __global__ __launch_bounds__(64 * QS * KS) void attn_bx_kernel(
     const float* __restrict__ q, int ldq, const float* __restrict__ k, int ldk,
     const float* __restrict__ v, int ldv, float* __restrict__ o, int ldo, int Tq, int Tk,
-    int n_heads, int rep, float qscale, int causal, int q_offset) {
+    int n_heads, int rep, float qscale, int causal, int q_offset, int opk) {
   constexpr int kQT = 32 * QS;
   constexpr int KT = 32 * KS;
   constexpr int NT = 64 * QS * KS;
@@ -921,7 +931,7 @@ __global__ __launch_bounds__(64 * QS * KS) void attn_bx_kernel(
           const float mine = keep[i] * a_s, other = part[i * 64 + lane] * a_o;
           w[e] = (ks == 0 ? mine + other : other + mine) * inv;
         }
-        *reinterpret_cast<floatx4*>(orow + g * 8) = w;
+        store_o4(orow + g * 8, w, opk);
       }
     }
     return;
@@ -980,8 +990,8 @@ __global__ __launch_bounds__(64 * QS * KS) void attn_bx_kernel(
     const int qi = qt0 + row;
     if (qi < Tq) {
       const float* src = otile + (row >> 5) * (32 * kLD) + (row & 31) * kLD + c;
-      *reinterpret_cast<floatx4*>(o + ((long)b * Tq + qi) * ldo + head * kHD + c) =
-          *reinterpret_cast<const floatx4*>(src);
+      store_o4(o + ((long)b * Tq + qi) * ldo + head * kHD + c,
+               *reinterpret_cast<const floatx4*>(src), opk);
     }
   }
 }
@@ -989,7 +999,8 @@ __global__ __launch_bounds__(64 * QS * KS) void attn_bx_kernel(
 }  // namespace
 int attention(const float* q, int ldq, const float* k, int ldk, const float* v, int ldv, float* o,
               int ldo, int B, int Tq, int Tk, int n_heads, int n_kv_heads, int head_dim,
-              float scale, int causal, int q_offset, int products, hipStream_t stream) {
+              float scale, int causal, int q_offset, int products, int out_packed,
+              hipStream_t stream) {
   LX_REQUIRE(products == 3 || products == 6, "attention: %d products (3 or 6)", products);
   LX_REQUIRE(q && k && v && o, "attention: null pointer");
   LX_REQUIRE(B > 0 && Tq > 0 && Tk > 0 && n_heads > 0 && n_kv_heads > 0,
@@ -1071,7 +1082,8 @@ int attention(const float* q, int ldq, const float* k, int ldk, const float* v, 
   const long nwg = (long)((Tq + qt - 1) / qt) * n_heads * B;
   LX_REQUIRE(nwg < (1L << 31), "attention: %ld workgroups exceed the grid limit", nwg);
   hipLaunchKernelGGL(kern, dim3((unsigned)nwg), dim3(threads), lds, stream, q, ldq, k, ldk, v, ldv,
-                     o, ldo, Tq, Tk, n_heads, rep, scale * log2e, causal, q_offset);
+                     o, ldo, Tq, Tk, n_heads, rep, scale * log2e, causal, q_offset,
+                     out_packed ? 1 : 0);
   return check_launch("attn_flash_kernel");
 }
 
@@ -1084,13 +1096,14 @@ extern "C" int lx_attention_f32(const float* q, int ldq, const float* k, int ldk
                                 int Tk, int n_heads, int n_kv_heads, int head_dim, float scale,
                                 int causal, int q_offset, hipStream_t stream) {
   return attention(q, ldq, k, ldk, v, ldv, o, ldo, B, Tq, Tk, n_heads, n_kv_heads, head_dim,
-                   scale, causal, q_offset, 6, stream);
+                   scale, causal, q_offset, 6, 0, stream);
 }
 
 extern "C" int lx_attention_np_f32(const float* q, int ldq, const float* k, int ldk,
                                    const float* v, int ldv, float* o, int ldo, int B, int Tq,
                                    int Tk, int n_heads, int n_kv_heads, int head_dim, float scale,
-                                   int causal, int q_offset, int products, hipStream_t stream) {
+                                   int causal, int q_offset, int products, int out_packed,
+                                   hipStream_t stream) {
   return attention(q, ldq, k, ldk, v, ldv, o, ldo, B, Tq, Tk, n_heads, n_kv_heads, head_dim,
-                   scale, causal, q_offset, products, stream);
+                   scale, causal, q_offset, products, out_packed, stream);
 }

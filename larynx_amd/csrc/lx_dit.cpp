@@ -160,22 +160,33 @@ int forward_core(lx_dit* m, const float* x, long x_bstride, const float* mu, con
   } pend;
   bool pending = false;
   const bool partial = m->frag && rows <= kPartialRows && D % 128 == 0 && m->F % 128 == 0;
-  auto adaln = [&](const float* shift, const float* scale, float* y) -> int {
-    if (!pending) return lx_adaln_modulate_f32(m->h, shift, scale, NA, y, B, T, D, kLnEps, s);
+  // With three products the block's activations (the modulated LayerNorms'
+  // output, attention's output, FF0's GELU output) pass to the projections
+  // that read them as two-part packed rows: each producer splits its output
+  // once, with the roundings the GEMM would apply (bit-identical results),
+  // instead of every column tile of the consumer splitting it again.
+  const bool pk = m->frag && m->products == 3;
+  auto adaln = [&](const float* shift, const float* scale, float* y, bool packed) -> int {
+    if (!pending && !packed)
+      return lx_adaln_modulate_f32(m->h, shift, scale, NA, y, B, T, D, kLnEps, s);
+    const int S = pending ? 2 : 0;
     pending = false;
-    return lx_adaln_resid_f32(m->h, m->Rws, 2, (long)rows * D, pend.bias, pend.gate, NA, shift,
-                              scale, NA, y, B, T, D, kLnEps, s);
+    return adaln_resid(m->h, S ? m->Rws : nullptr, S, (long)rows * D, S ? pend.bias : nullptr,
+                       S ? pend.gate : nullptr, NA, shift, scale, NA, y, B, T, D, kLnEps,
+                       packed ? 1 : 0, s);
   };
   auto proj = [&](const float* x, int ldx, const void* Wf, const float* W, const float* bias,
-                  float* y, int ldy, int N, int K, const lx_epilogue* epi) -> int {
+                  float* y, int ldy, int N, int K, const lx_epilogue* epi,
+                  bool pack_out = false) -> int {
     if (!m->frag) return lx_linear_f32(x, ldx, W, bias, y, ldy, rows, N, K, epi, s);
     lx_linear_bx g{};
+    g.a_packed = pk ? 1 : 0;
     g.A = x;
     g.lda = ldx;
     g.Wf = Wf;
     g.bias = bias;
     g.epi = epi;
-    g.out = LX_BX_OUT_F32;
+    g.out = pack_out && pk ? LX_BX_OUT_PACKED : LX_BX_OUT_F32;
     g.Y = y;
     g.ldy = ldy;
     g.M = rows;
@@ -198,6 +209,7 @@ int forward_core(lx_dit* m, const float* x, long x_bstride, const float* mu, con
       return proj(x, ldx, Wf, W, bias, m->h, D, D, K, &gated);
     }
     lx_linear_bx g{};
+    g.a_packed = pk ? 1 : 0;
     g.A = x;
     g.lda = ldx;
     g.Wf = Wf;
@@ -234,7 +246,7 @@ int forward_core(lx_dit* m, const float* x, long x_bstride, const float* mu, con
     const float* w2 = m->frag ? nullptr : m->ff0_w[i];
     const float* w3 = m->frag ? nullptr : m->ff2_w[i];
 
-    LX_TRY(adaln(shift_msa, scale_msa, m->xn));
+    LX_TRY(adaln(shift_msa, scale_msa, m->xn, pk));
     lx_epilogue rope{};
     rope.kind = LX_EPI_ROPE_PARTIAL;
     rope.rows_per_batch = T;
@@ -246,13 +258,13 @@ int forward_core(lx_dit* m, const float* x, long x_bstride, const float* mu, con
     LX_TRY(proj(m->xn, D, wf0, w0, m->qkv_b[i], m->qkv, 3 * D, 3 * D, D, &rope));
     LX_TRY(attention(m->qkv, 3 * D, m->qkv + D, 3 * D, m->qkv + 2 * D, 3 * D, m->att, D, B, T,
                      T, m->heads, m->heads, m->hd, 1.0f / std::sqrt((float)m->hd), 0, 0,
-                     m->products, s));
+                     m->products, pk ? 1 : 0, s));
     LX_TRY(proj_gated(m->att, D, wf1, w1, m->out_b[i], gate_msa, D));
 
-    LX_TRY(adaln(shift_mlp, scale_mlp, m->xn));
+    LX_TRY(adaln(shift_mlp, scale_mlp, m->xn, pk));
     lx_epilogue gelu{};
     gelu.kind = LX_EPI_GELU_TANH;
-    LX_TRY(proj(m->xn, D, wf2, w2, m->ff0_b[i], m->ff, m->F, m->F, D, &gelu));
+    LX_TRY(proj(m->xn, D, wf2, w2, m->ff0_b[i], m->ff, m->F, m->F, D, &gelu, /*pack_out*/ true));
     LX_TRY(proj_gated(m->ff, m->F, wf3, w3, m->ff2_b[i], gate_mlp, m->F));
     if (m->cap.blocks) {
       if (pending) {  // the block's output: fold the FF2 slices into h now
@@ -266,7 +278,7 @@ int forward_core(lx_dit* m, const float* x, long x_bstride, const float* mu, con
   }
   // norm_out (AdaLayerNormZero_Final): chunk order scale, shift (src/flow/dit.cpp:134-135).
   const float* ef = emb + (long)m->depth * 6 * D;
-  LX_TRY(adaln(/*shift*/ ef + D, /*scale*/ ef, m->xn));
+  LX_TRY(adaln(/*shift*/ ef + D, /*scale*/ ef, m->xn, /*packed*/ false));
   if (m->cap.norm_out)
     (void)hipMemcpyAsync(m->cap.norm_out, m->xn, sizeof(float) * rows * D, hipMemcpyDeviceToDevice,
                          s);

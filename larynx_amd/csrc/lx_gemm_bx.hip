@@ -78,11 +78,11 @@ struct BxArgs {
   unsigned* counters;   // stream-K arrival counts, one per tile, zero between launches
 };
 
-enum { BX_OUT_F32 = LX_BX_OUT_F32, BX_OUT_PARTIAL = LX_BX_OUT_PARTIAL };
+enum { BX_OUT_F32 = LX_BX_OUT_F32, BX_OUT_PARTIAL = LX_BX_OUT_PARTIAL, BX_OUT_PACKED = LX_BX_OUT_PACKED };
 
-// Fragments are held as 32-bit vectors and reinterpreted as bf16 only at the
-// MFMA (loop-carried bf16 vectors are otherwise rebuilt element by element).
-typedef unsigned uintx4_t __attribute__((ext_vector_type(4)));
+// Fragments are held as 32-bit vectors (uintx4_t) and reinterpreted as bf16
+// only at the MFMA (loop-carried bf16 vectors are otherwise rebuilt element by
+// element).
 __device__ __forceinline__ sbf16x8 as_bf16x8(uintx4_t v) { return __builtin_bit_cast(sbf16x8, v); }
 
 // Three bf16 parts of four fp32 values.
@@ -112,7 +112,10 @@ __device__ __forceinline__ int bx_owner(long p, long U, int G) {
 #ifndef LX_BX_WAVES64
 #define LX_BX_WAVES64 2
 #endif
-template <int EPI, int BMB, int OUT, int NP>
+// AP: A holds two-part packed rows (pack2_bf16; three products): the staging
+// stores its parts without splitting them.  OUT = BX_OUT_PACKED: the fp32
+// epilogue's result is stored as packed rows for the next such GEMM.
+template <int EPI, int BMB, int OUT, int NP, int AP = 0>
 __global__ __launch_bounds__(kBxThreads) __attribute__((amdgpu_waves_per_eu(
     BMB == 2 ? LX_BX_WAVES64 : 1, BMB == 2 ? LX_BX_WAVES64 : 1))) void
 gemm_bx_kernel(BxArgs a, EpiArgs ep) {
@@ -196,7 +199,14 @@ gemm_bx_kernel(BxArgs a, EpiArgs ep) {
 #pragma unroll
       for (int i = 0; i < LA; ++i) {
         bf16x4_t x0, x1, x2;
-        split3(g[i], x0, x1, x2);  // (x2 is dead code with two planes)
+        if (AP) {  // already split by the producer
+          const uintx4_t u = __builtin_bit_cast(uintx4_t, g[i]);
+          x0 = __builtin_bit_cast(bf16x4_t, uintx2_t{u[0], u[1]});
+          x1 = __builtin_bit_cast(bf16x4_t, uintx2_t{u[2], u[3]});
+          x2 = x1;
+        } else {
+          split3(g[i], x0, x1, x2);  // (x2 is dead code with two planes)
+        }
         *reinterpret_cast<bf16x4_t*>(base + sa[i]) = x0;
         *reinterpret_cast<bf16x4_t*>(base + BM * kBxBK + sa[i]) = x1;
         if (NPL == 3) *reinterpret_cast<bf16x4_t*>(base + 2 * BM * kBxBK + sa[i]) = x2;
@@ -445,7 +455,7 @@ gemm_bx_kernel(BxArgs a, EpiArgs ep) {
       const int row = idx / (kBxBN / 4), c = (idx % (kBxBN / 4)) * 4;
       const int m = min(m0 + row, a.M - 1), n = n0 + c;
       eg[j] = ey[j] = z4;
-      if (OUT == BX_OUT_F32) {
+      if (OUT != BX_OUT_PARTIAL) {
         if (EPI == LX_EPI_GATED_RESID)
           eg[j] = *reinterpret_cast<const float4*>(ep.gate + (long)(m / ep.rows_per_batch) *
                                                                  ep.gate_stride + n);
@@ -489,7 +499,7 @@ gemm_bx_kernel(BxArgs a, EpiArgs ep) {
           ey[j] = *reinterpret_cast<const float4*>(a.Y + (long)m * a.ldy + n);
       }
       const int posm = rot ? ep.pos[m % ep.rows_per_batch] : 0;
-      epilogue4v<EPI>(a.Y, (int)a.ldy, m, n, v, eb, eg[j], ey[j], posm, ep);
+      epilogue4v<EPI, OUT == BX_OUT_PACKED>(a.Y, (int)a.ldy, m, n, v, eb, eg[j], ey[j], posm, ep);
     }
   }
 }
@@ -536,9 +546,9 @@ int device_cus() {
   return cus[dev];
 }
 
-template <int EPI, int BMB, int OUT, int NP>
+template <int EPI, int BMB, int OUT, int NP, int AP>
 int launch_bx(const BxArgs& a, const EpiArgs& ep, hipStream_t stream) {
-  auto kern = gemm_bx_kernel<EPI, BMB, OUT, NP>;
+  auto kern = gemm_bx_kernel<EPI, BMB, OUT, NP, AP>;
   static LdsLimit once;
   const size_t lds = BxCfg<BMB, NP>::lds;
   int rc = raise_lds_limit((const void*)kern, lds, once, "linear_bx");
@@ -548,18 +558,28 @@ int launch_bx(const BxArgs& a, const EpiArgs& ep, hipStream_t stream) {
   return check_launch("gemm_bx_kernel");
 }
 
-template <int BMB, int NP>
+// Packed operands (AP = 1, BX_OUT_PACKED) exist for three products on 64-row
+// tiles only (the host checks this).
+template <int BMB, int NP, int AP = 0>
 int dispatch_bx(const BxArgs& a, int out, const EpiArgs& ep, hipStream_t s) {
-  if (out == BX_OUT_PARTIAL) return launch_bx<LX_EPI_NONE, BMB, BX_OUT_PARTIAL, NP>(a, ep, s);
+  if (out == BX_OUT_PARTIAL) return launch_bx<LX_EPI_NONE, BMB, BX_OUT_PARTIAL, NP, AP>(a, ep, s);
+  if constexpr (BMB == 2 && NP == 3) {
+    if (out == BX_OUT_PACKED) {
+      if (ep.kind == LX_EPI_GELU_TANH)
+        return launch_bx<LX_EPI_GELU_TANH, BMB, BX_OUT_PACKED, NP, AP>(a, ep, s);
+      return launch_bx<LX_EPI_NONE, BMB, BX_OUT_PACKED, NP, AP>(a, ep, s);
+    }
+  }
   switch (ep.kind) {
-    case LX_EPI_NONE: return launch_bx<LX_EPI_NONE, BMB, BX_OUT_F32, NP>(a, ep, s);
-    case LX_EPI_GELU_TANH: return launch_bx<LX_EPI_GELU_TANH, BMB, BX_OUT_F32, NP>(a, ep, s);
-    case LX_EPI_GATED_RESID: return launch_bx<LX_EPI_GATED_RESID, BMB, BX_OUT_F32, NP>(a, ep, s);
+    case LX_EPI_NONE: return launch_bx<LX_EPI_NONE, BMB, BX_OUT_F32, NP, AP>(a, ep, s);
+    case LX_EPI_GELU_TANH: return launch_bx<LX_EPI_GELU_TANH, BMB, BX_OUT_F32, NP, AP>(a, ep, s);
+    case LX_EPI_GATED_RESID:
+      return launch_bx<LX_EPI_GATED_RESID, BMB, BX_OUT_F32, NP, AP>(a, ep, s);
     case LX_EPI_ROPE_PARTIAL:
-      return launch_bx<LX_EPI_ROPE_PARTIAL, BMB, BX_OUT_F32, NP>(a, ep, s);
-    case LX_EPI_RESID: return launch_bx<LX_EPI_RESID, BMB, BX_OUT_F32, NP>(a, ep, s);
+      return launch_bx<LX_EPI_ROPE_PARTIAL, BMB, BX_OUT_F32, NP, AP>(a, ep, s);
+    case LX_EPI_RESID: return launch_bx<LX_EPI_RESID, BMB, BX_OUT_F32, NP, AP>(a, ep, s);
     case LX_EPI_SWIGLU_PAIRED:
-      return launch_bx<LX_EPI_SWIGLU_PAIRED, BMB, BX_OUT_F32, NP>(a, ep, s);
+      return launch_bx<LX_EPI_SWIGLU_PAIRED, BMB, BX_OUT_F32, NP, AP>(a, ep, s);
     default: break;
   }
   set_error("linear_bx: epilogue kind %d not available", ep.kind);
@@ -589,8 +609,12 @@ int linear_bx(const lx_linear_bx& g, hipStream_t stream) {
              "linear_bx: lda=%ld (K=%d), A must stay below 2 GiB", g.lda, g.K);
   LX_REQUIRE(((uintptr_t)g.A | (uintptr_t)g.Wf) % 16 == 0,
              "linear_bx: operands must be 16-byte aligned");
-  LX_REQUIRE(g.out == BX_OUT_F32 || g.out == BX_OUT_PARTIAL, "linear_bx: unknown output %d",
-             g.out);
+  LX_REQUIRE(g.out == BX_OUT_F32 || g.out == BX_OUT_PARTIAL || g.out == BX_OUT_PACKED,
+             "linear_bx: unknown output %d", g.out);
+  LX_REQUIRE(g.a_packed == 0 || g.a_packed == 1, "linear_bx: a_packed=%d must be 0 or 1",
+             g.a_packed);
+  LX_REQUIRE((!g.a_packed && g.out != BX_OUT_PACKED) || (g.products == 3 && g.bm == 64),
+             "linear_bx: packed operands need three products and 64-row tiles");
   const int slices = g.slices < 1 ? 1 : g.slices;
   int kslice = g.K;
   if (slices > 1) {
@@ -609,6 +633,8 @@ int linear_bx(const lx_linear_bx& g, hipStream_t stream) {
     LX_REQUIRE(g.Y && g.ldy >= g.N && (slices == 1 || g.slice_stride >= (long)g.M * g.ldy),
                "linear_bx: bad partial output");
   } else {
+    LX_REQUIRE(g.out != BX_OUT_PACKED || ep.kind == LX_EPI_NONE || ep.kind == LX_EPI_GELU_TANH,
+               "linear_bx: the packed output takes no epilogue but GELU (kind %d)", ep.kind);
     LX_REQUIRE(g.Y && g.ldy >= (ep.kind == LX_EPI_SWIGLU_PAIRED ? g.N / 2 : g.N) &&
                    g.ldy < (1L << 31),
                "linear_bx: bad output");
@@ -636,7 +662,7 @@ int linear_bx(const lx_linear_bx& g, hipStream_t stream) {
   a.ws = nullptr;
   a.ws_bytes = 0;
   a.counters = nullptr;
-  if (g.ws && g.counters && g.out != BX_OUT_PARTIAL) {
+  if (g.ws && g.counters && g.out == BX_OUT_F32 && !g.a_packed) {
     // Stream-K over one workgroup per CU (at most one per slab pair of work):
     // every CU gets the same number of slab pairs whatever the tile count.
     const int tiles = a.tiles_m * a.tiles_n;
@@ -654,6 +680,7 @@ int linear_bx(const lx_linear_bx& g, hipStream_t stream) {
       a.counters = g.counters;
     }
   }
+  if (g.a_packed) return dispatch_bx<2, 3, 1>(a, g.out, ep, stream);
   if (g.products == 3)
     return g.bm == 128 ? dispatch_bx<4, 3>(a, g.out, ep, stream)
                        : dispatch_bx<2, 3>(a, g.out, ep, stream);

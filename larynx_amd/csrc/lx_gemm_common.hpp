@@ -20,6 +20,24 @@ struct EpiArgs {
 
 typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
 typedef unsigned uintx2_t __attribute__((ext_vector_type(2)));
+typedef unsigned uintx4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ floatx4 bf16x4_back(bf16x4_t h);
+
+// Two-part packed rows (the A operand of the three-product split-operand GEMM,
+// written once by its producer): each aligned group of four fp32 values x as
+// 16 bytes, the four leading parts bf16(x), then the four remainders
+// bf16(x - bf16(x)) -- the same roundings as the GEMM's own split, in the
+// bytes the fp32 group would occupy.  Contraction is off here: fused with the
+// producer's last multiply (GELU's x * r, attention's sum * 1/l) the remainder
+// would be taken from the unrounded product, not from the fp32 value.
+__device__ __forceinline__ uintx4_t pack2_bf16(floatx4 v) {
+#pragma clang fp contract(off)
+  const bf16x4_t x0 = __builtin_convertvector(v, bf16x4_t);
+  const bf16x4_t x1 = __builtin_convertvector(v - bf16x4_back(x0), bf16x4_t);
+  const uintx2_t u0 = __builtin_bit_cast(uintx2_t, x0), u1 = __builtin_bit_cast(uintx2_t, x1);
+  return uintx4_t{u0[0], u0[1], u1[0], u1[1]};
+}
 
 __device__ __forceinline__ void rotate_pair(float& x0, float& x1, float ang) {
   float s, c;
@@ -32,8 +50,9 @@ __device__ __forceinline__ void rotate_pair(float& x0, float& x1, float ang) {
 
 // float4 epilogue of 4 columns n..n+3 (all < N) of row m with its operands
 // already loaded: b = bias[n..n+3], g = gate row segment, yo = the residual.
-// Same per-component operations as epilogue4.
-template <int EPI>
+// Same per-component operations as epilogue4.  PK: the result is stored as a
+// two-part packed group (pack2_bf16) instead of four floats.
+template <int EPI, bool PK = false>
 __device__ __forceinline__ void epilogue4v(float* Y, int ldy, int m, int n, float4 v, float4 b,
                                            float4 g, float4 yo, int posm, const EpiArgs& ep) {
   float vv[4] = {v.x + b.x, v.y + b.y, v.z + b.z, v.w + b.w};
@@ -62,7 +81,10 @@ __device__ __forceinline__ void epilogue4v(float* Y, int ldy, int m, int n, floa
     o = make_float4(yo.x + vv[0] * g.x, yo.y + vv[1] * g.y, yo.z + vv[2] * g.z, yo.w + vv[3] * g.w);
   else if (EPI == LX_EPI_RESID)
     o = make_float4(yo.x + vv[0], yo.y + vv[1], yo.z + vv[2], yo.w + vv[3]);
-  *reinterpret_cast<float4*>(Y + (long)m * ldy + n) = o;
+  if (PK)
+    *reinterpret_cast<uintx4_t*>(Y + (long)m * ldy + n) = pack2_bf16(floatx4{o.x, o.y, o.z, o.w});
+  else
+    *reinterpret_cast<float4*>(Y + (long)m * ldy + n) = o;
 }
 
 typedef __bf16 sbf16x8 __attribute__((ext_vector_type(8)));

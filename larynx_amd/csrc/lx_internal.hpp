@@ -130,6 +130,13 @@ int splitk_qkv_rope_cache(const float* ws, int splits, int M, const float* bias,
                           int n_kv_heads, const int* pos, const float* inv_freq, float* q_out,
                           int ldq, float* k_cache, float* v_cache, int row0, hipStream_t stream);
 
+// lx_adaln_resid_f32, with y as two-part packed rows when out_packed
+// (lx_adaln_resid_packed_f32).
+int adaln_resid(float* h, const float* partials, int splits, long partial_stride,
+                const float* bias, const float* gate, long gate_stride, const float* shift,
+                const float* scale, long mod_stride, float* y, int B, int T, int D, float eps,
+                int out_packed, hipStream_t stream);
+
 // ---- split-operand GEMM with W in fragment order (lx_gemm_bx.hip) ----
 // lx_linear_bx_f32 (arguments and outputs as declared in lx_ops.h).
 int linear_bx(const lx_linear_bx& g, hipStream_t stream);
@@ -137,7 +144,8 @@ int linear_bx(const lx_linear_bx& g, hipStream_t stream);
 // fp32 kernel, which small grids run, ignores it).
 int attention(const float* q, int ldq, const float* k, int ldk, const float* v, int ldv, float* o,
               int ldo, int B, int Tq, int Tk, int n_heads, int n_kv_heads, int head_dim,
-              float scale, int causal, int q_offset, int products, hipStream_t stream);
+              float scale, int causal, int q_offset, int products, int out_packed,
+              hipStream_t stream);
 // W (N, K) -> fragment order (3 * N * K bf16); N % 32 == 0, K % 16 == 0.
 int wfrag_pack(const float* W, void* Wf, int N, int K, hipStream_t stream);
 

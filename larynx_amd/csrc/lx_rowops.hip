@@ -7,6 +7,7 @@
 // The (1 + scale) / shift vectors of the block's batch are staged in LDS once
 // per workgroup.
 #include "lx_common.hpp"
+#include "lx_gemm_common.hpp"
 
 namespace lx {
 namespace {
@@ -98,7 +99,7 @@ __global__ __launch_bounds__(kRowsPerBlock * kWave) void adaln_resid_kernel(
     float* h, const float* P, int S, long pstride, const float* __restrict__ bias,
     const float* __restrict__ gate, long gate_stride, const float* __restrict__ shift,
     const float* __restrict__ scale, long mod_stride, float* y, int rows, int T, int D,
-    float eps) {
+    float eps, int pk) {
   extern __shared__ float smem[];
   const int D4 = D >> 2;
   const int row0 = blockIdx.x * kRowsPerBlock;
@@ -198,7 +199,10 @@ __global__ __launch_bounds__(kRowsPerBlock * kWave) void adaln_resid_kernel(
       o.y = ((v[j].y - mean) * rstd) * m.y + sh.y;
       o.z = ((v[j].z - mean) * rstd) * m.z + sh.z;
       o.w = ((v[j].w - mean) * rstd) * m.w + sh.w;
-      yr[i] = o;
+      if (pk)  // two-part packed row for the three-product GEMM
+        reinterpret_cast<uintx4_t*>(yr)[i] = pack2_bf16(floatx4{o.x, o.y, o.z, o.w});
+      else
+        yr[i] = o;
     }
   }
 }
@@ -280,11 +284,11 @@ extern "C" int lx_adaln_modulate_f32(const float* x, const float* shift, const f
   return check_launch("adaln_kernel");
 }
 
-extern "C" int lx_adaln_resid_f32(float* h, const float* partials, int splits,
-                                  long partial_stride, const float* bias, const float* gate,
-                                  long gate_stride, const float* shift, const float* scale,
-                                  long mod_stride, float* y, int B, int T, int D, float eps,
-                                  hipStream_t stream) {
+namespace lx {
+int adaln_resid(float* h, const float* partials, int splits, long partial_stride,
+                const float* bias, const float* gate, long gate_stride, const float* shift,
+                const float* scale, long mod_stride, float* y, int B, int T, int D, float eps,
+                int out_packed, hipStream_t stream) {
   LX_REQUIRE(h && shift && scale, "adaln_resid: null pointer");
   LX_REQUIRE(B > 0 && T > 0 && D > 0, "adaln_resid: bad shape B=%d T=%d D=%d", B, T, D);
   LX_REQUIRE(D % 4 == 0 && D <= 16 * 256, "adaln_resid: D=%d must be a multiple of 4, <= 4096",
@@ -311,7 +315,7 @@ extern "C" int lx_adaln_resid_f32(float* h, const float* partials, int splits,
 #define LX_AR(NVV, SM)                                                                          \
   hipLaunchKernelGGL((adaln_resid_kernel<NVV, SM>), dim3(nblk), dim3(kRowsPerBlock * kWave), lds,     \
                      stream, h, partials, splits, partial_stride, bias, gate, gate_stride, shift, \
-                     scale, mod_stride, y, rows, T, D, eps)
+                     scale, mod_stride, y, rows, T, D, eps, out_packed ? 1 : 0)
   if (nv <= 4)
     LX_AR(4, 4);
   else if (nv <= 8)
@@ -320,6 +324,27 @@ extern "C" int lx_adaln_resid_f32(float* h, const float* partials, int splits,
     LX_AR(16, 0);  // splits == 0 here
 #undef LX_AR
   return check_launch("adaln_resid_kernel");
+}
+}  // namespace lx
+
+extern "C" int lx_adaln_resid_f32(float* h, const float* partials, int splits,
+                                  long partial_stride, const float* bias, const float* gate,
+                                  long gate_stride, const float* shift, const float* scale,
+                                  long mod_stride, float* y, int B, int T, int D, float eps,
+                                  hipStream_t stream) {
+  return adaln_resid(h, partials, splits, partial_stride, bias, gate, gate_stride, shift, scale,
+                     mod_stride, y, B, T, D, eps, 0, stream);
+}
+
+extern "C" int lx_adaln_resid_packed_f32(float* h, const float* partials, int splits,
+                                         long partial_stride, const float* bias,
+                                         const float* gate, long gate_stride,
+                                         const float* shift, const float* scale,
+                                         long mod_stride, void* y, int B, int T, int D, float eps,
+                                         hipStream_t stream) {
+  LX_REQUIRE(y, "adaln_resid_packed: null output");
+  return adaln_resid(h, partials, splits, partial_stride, bias, gate, gate_stride, shift, scale,
+                     mod_stride, static_cast<float*>(y), B, T, D, eps, 1, stream);
 }
 
 extern "C" int lx_rmsnorm_f32(const float* x, const float* w, float* y, int rows, int D,

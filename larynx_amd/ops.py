@@ -10,17 +10,18 @@ import ctypes as C
 
 import torch
 
-from ._lib import (LX_BX_OUT_F32, LX_BX_OUT_PARTIAL, LX_EPI_GATED_RESID,
+from ._lib import (LX_BX_OUT_F32, LX_BX_OUT_PACKED, LX_BX_OUT_PARTIAL, LX_EPI_GATED_RESID,
                    LX_EPI_GELU_TANH, LX_EPI_NONE, LX_EPI_RESID, LX_EPI_ROPE_PARTIAL,
                    LX_EPI_SWIGLU_PAIRED, Epilogue, LinearBx, check, lib)
 
 __all__ = [
     "stream", "ada_ln", "adaln_resid", "adaln_emb", "rope_partial", "gelu_tanh", "gated_residual",
     "timestep_embed", "time_mlp", "rms_norm", "rope_full", "swiglu", "embed_gather", "linear",
-    "attention", "conv_pos_mish", "conv_pack_weight", "conv_frag_pack", "conv_pos_mish_bx", "Epilogue", "split_planes",
-    "linear_split", "wfrag_pack", "linear_bx", "bx_scratch",
+    "attention", "conv_pos_mish", "conv_pack_weight", "conv_frag_pack", "conv_pos_mish_bx",
+    "Epilogue", "split_planes", "linear_split", "wfrag_pack", "linear_bx", "bx_scratch",
     "LX_EPI_NONE", "LX_EPI_GELU_TANH", "LX_EPI_GATED_RESID", "LX_EPI_ROPE_PARTIAL",
     "LX_EPI_RESID", "LX_EPI_SWIGLU_PAIRED", "LX_BX_OUT_F32", "LX_BX_OUT_PARTIAL",
+    "LX_BX_OUT_PACKED",
 ]
 
 
@@ -55,20 +56,21 @@ def ada_ln(x, scale, shift, eps=1e-6, out=None):
     return y
 
 
-def adaln_resid(h, partials, bias, gate, shift, scale, out=None, eps=1e-6):
+def adaln_resid(h, partials, bias, gate, shift, scale, out=None, eps=1e-6, packed=False):
     """h += gate * (sum of the K-slice partials (S, B*T, D) + bias), in place; then,
     unless out is False, LN(h) * (1 + scale) + shift into out (B, T, D).
-    gate/shift/scale: (B, D) views (row stride = their stride(0)).
+    gate/shift/scale: (B, D) views (row stride = their stride(0)).  packed: out
+    receives two-part packed rows (linear_bx's a_packed operand) in its fp32 bytes.
     src/flow/dit.cpp:71,77 + src/flow/ops.cpp:94-104."""
     B, T, D = h.shape
     S = 0 if partials is None else partials.shape[0]
     y = None
     if out is not False:
         y = torch.empty_like(h) if out is None else out
-    check(lib.lx_adaln_resid_f32(_p(h), _p(partials), S,
-                                 partials.stride(0) if S else 0, _p(bias), _p(gate),
-                                 gate.stride(0) if gate is not None else 0, _p(shift), _p(scale),
-                                 shift.stride(0), _p(y), B, T, D, eps, stream()))
+    fn = lib.lx_adaln_resid_packed_f32 if packed else lib.lx_adaln_resid_f32
+    check(fn(_p(h), _p(partials), S, partials.stride(0) if S else 0, _p(bias), _p(gate),
+             gate.stride(0) if gate is not None else 0, _p(shift), _p(scale), shift.stride(0),
+             _p(y), B, T, D, eps, stream()))
     return y
 
 
@@ -214,12 +216,13 @@ def wfrag_pack(W):
 
 
 def linear_bx(a, wf, N, b=None, epilogue=None, out=None, out_kind=LX_BX_OUT_F32, bm=128,
-              slices=1, scratch=None, products=6):
+              slices=1, scratch=None, products=6, a_packed=False):
     """epi(a @ W^T + b) with fp32 arithmetic on the bf16 matrix cores, W given as
     wfrag_pack(W) (N rows), a fp32 (M, K).  out_kind LX_BX_OUT_F32: (M, N) (out= the
     residual stream for residual epilogues); LX_BX_OUT_PARTIAL: (slices, M, N) raw
-    K-slice products.  scratch = bx_scratch(): the launch runs stream-K over the
-    CUs.  src/flow/ops.cpp:20-26."""
+    K-slice products; LX_BX_OUT_PACKED: (M, N) as two-part packed rows.  a_packed: a
+    holds two-part packed rows (three products, bm 64).  scratch = bx_scratch(): the
+    launch runs stream-K over the CUs.  src/flow/ops.cpp:20-26."""
     M, K = a.shape
     g = LinearBx()
     g.A, g.lda = a.data_ptr(), a.stride(0)
@@ -229,6 +232,7 @@ def linear_bx(a, wf, N, b=None, epilogue=None, out=None, out_kind=LX_BX_OUT_F32,
         g.epi = C.pointer(epilogue)
     g.out = out_kind
     g.M, g.N, g.K, g.bm, g.slices, g.products = M, N, K, bm, slices, products
+    g.a_packed = int(a_packed)
     if out_kind == LX_BX_OUT_PARTIAL:
         if out is None:
             out = torch.empty(slices, M, N, device=a.device, dtype=torch.float32)
@@ -257,10 +261,11 @@ def bx_scratch(device, bm=128, max_tiles=4096):
 
 
 def attention(q, k, v, n_heads, n_kv_heads=None, scale=None, causal=False, q_offset=0,
-              out=None, head_dim=64, products=6):
+              out=None, head_dim=64, products=6, out_packed=False):
     """softmax(scale q k^T) v per head; q (B, Tq, *), k/v (B, Tk, *) with heads packed from
     column 0 (row strides may exceed the head span); products: the split-operand kernel's
-    bf16 products per fp32 product (6 or 3).  src/flow/dit.cpp:34-51."""
+    bf16 products per fp32 product (6 or 3); out_packed: the output as two-part packed
+    rows (linear_bx's a_packed operand).  src/flow/dit.cpp:34-51."""
     n_kv_heads = n_kv_heads or n_heads
     B, Tq = q.shape[0], q.shape[1]
     Tk = k.shape[1]
@@ -269,7 +274,8 @@ def attention(q, k, v, n_heads, n_kv_heads=None, scale=None, causal=False, q_off
         out = torch.empty(B, Tq, n_heads * head_dim, device=q.device, dtype=torch.float32)
     check(lib.lx_attention_np_f32(_p(q), q.stride(1), _p(k), k.stride(1), _p(v), v.stride(1),
                                   _p(out), out.stride(1), B, Tq, Tk, n_heads, n_kv_heads,
-                                  head_dim, scale, int(causal), q_offset, products, stream()))
+                                  head_dim, scale, int(causal), q_offset, products,
+                                  int(out_packed), stream()))
     return out
 
 

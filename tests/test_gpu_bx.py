@@ -37,6 +37,31 @@ def ops(gpu):
     return o
 
 
+def bf16_rne(f):
+    """bfloat16 bits of float32 values, rounded to nearest even (finite inputs)."""
+    u = np.ascontiguousarray(f, np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def pack2_np(x):
+    """Two-part packed rows on the host: each aligned group of four fp32 values as
+    the four bf16(x) then the four bf16(x - bf16(x)), in the group's 16 bytes."""
+    x = np.ascontiguousarray(x, np.float32)
+    h0 = bf16_rne(x)
+    x0 = (h0.astype(np.uint32) << 16).view(np.float32)
+    h1 = bf16_rne(x - x0)
+    sh = x.shape[:-1] + (x.shape[-1] // 4, 1, 4)
+    both = np.concatenate([h0.reshape(sh), h1.reshape(sh)], axis=-2)
+    return np.ascontiguousarray(both).reshape(x.shape[:-1] + (2 * x.shape[-1],)).view(np.float32)
+
+
+def same_bits(a, b):
+    a = a.cpu().numpy() if isinstance(a, torch.Tensor) else a
+    b = b.cpu().numpy() if isinstance(b, torch.Tensor) else b
+    return np.array_equal(np.ascontiguousarray(a).view(np.uint32),
+                          np.ascontiguousarray(b).view(np.uint32))
+
+
 def unpack_wfrag(wf, N, K):
     """W rebuilt on the host from its fragment order: part p of W[nb*32 + l % 32,
     ks*16 + (l // 32)*8 + j] sits at ((nb*(K/16) + ks)*3 + p)*512 + l*8 + j."""
@@ -170,6 +195,13 @@ def test_linear_bx_rejects_bad_arguments(gpu, ops):
         ops.linear_bx(x, wf, 128, slices=2)
     with pytest.raises(LxError):
         ops.linear_bx(x[:, :96], ops.wfrag_pack(torch.zeros(128, 96, device=gpu)), 128)
+    with pytest.raises(LxError):  # packed operands: three products, 64-row tiles
+        ops.linear_bx(x, wf, 128, bm=64, products=6, a_packed=True)
+    with pytest.raises(LxError):
+        ops.linear_bx(x, wf, 128, bm=128, products=3, a_packed=True)
+    with pytest.raises(LxError):  # the packed output takes no epilogue but GELU
+        ops.linear_bx(x, wf, 128, epilogue=ops.Epilogue(kind=ops.LX_EPI_SWIGLU_PAIRED),
+                      out_kind=ops.LX_BX_OUT_PACKED, bm=64, products=3)
 
 
 @pytest.mark.parametrize("B,T,S", [(2, 500, 2), (2, 500, 0), (2, 24, 4), (2, 3, 1), (1, 7, 2)])
@@ -271,3 +303,74 @@ def test_split_operand_nonfinite_inputs(gpu, ops):
         yc = ops.conv_pos_mish_bx(dev(xc, gpu), wf, dev(bc, gpu), products=products).cpu().numpy()
         assert np.isnan(yc[hitc]).all(), products
         assert orc.rel_err(yc[~hitc], refc[~hitc]) < TOL, products
+
+
+@pytest.mark.parametrize("M", [1000, 45])
+def test_linear_bx_packed_operands_bit_identical(gpu, ops, M):
+    """A given as two-part packed rows (the roundings the GEMM applies itself)
+    gives bit-identical results to the fp32 A it packs, for every epilogue the
+    estimator uses and for K-slice partials; the packed output (none / GELU) is
+    the packing of the fp32 output."""
+    announce(f"linear_bx packed operands M={M}")
+    D, F = 1024, 2048
+    T = max(1, M // 2)
+    x = rnd((M, D), 50)
+    xd, xp = dev(x, gpu), dev(pack2_np(x), gpu)
+    W, b = rnd((3 * D, D), 51, 0.03), rnd((3 * D,), 52)
+    pos = torch.arange(T, dtype=torch.int32, device=gpu)
+    gate = dev(rnd((M // T + 1, D), 53, 0.3), gpu)
+    h = dev(rnd((M, D), 54), gpu)
+    cases = {
+        "rope": (ops.Epilogue(kind=ops.LX_EPI_ROPE_PARTIAL, rows_per_batch=T, pos=pos.data_ptr(),
+                              rot_dim=64, rope_section=D, rope_sections=2, rope_base=10000.0),
+                 3 * D),
+        "gelu": (ops.Epilogue(kind=ops.LX_EPI_GELU_TANH), F),
+        "none": (None, D),
+        "gated": (ops.Epilogue(kind=ops.LX_EPI_GATED_RESID, rows_per_batch=T,
+                               gate=gate.data_ptr(), gate_stride=D), D),
+    }
+    for name, (ep, N) in cases.items():
+        wf = ops.wfrag_pack(dev(W[:N], gpu))
+        bd = dev(b[:N], gpu)
+        outs = []
+        for a, packed in ((xd, False), (xp, True)):
+            out = h.clone() if name == "gated" else None
+            outs.append(ops.linear_bx(a, wf, N, bd, ep, out=out, bm=64, products=3,
+                                      a_packed=packed))
+        assert same_bits(outs[0], outs[1]), name
+        if name in ("gelu", "none"):
+            yp = ops.linear_bx(xp, wf, N, bd, ep, out_kind=ops.LX_BX_OUT_PACKED, bm=64,
+                               products=3, a_packed=True)
+            assert same_bits(yp, pack2_np(outs[0].cpu().numpy())), name
+    wf = ops.wfrag_pack(dev(W[:D], gpu))
+    P = [ops.linear_bx(a, wf, D, out_kind=ops.LX_BX_OUT_PARTIAL, slices=2, bm=64, products=3,
+                       a_packed=packed) for a, packed in ((xd, False), (xp, True))]
+    assert same_bits(P[0], P[1])
+
+
+def test_packed_producers_match_host_packing(gpu, ops):
+    """The producers' packed outputs are the host packing of their fp32 outputs:
+    the modulated LayerNorm with folded K slices, and attention on the
+    split-operand layouts (T = 500, 1000) and the fp32 kernel's small grid
+    (T = 24), with three and six products."""
+    announce("packed producers")
+    B, T, D = 2, 500, 1024
+    h = rnd((B, T, D), 60)
+    parts = rnd((2, B * T, D), 61, 0.1)
+    emb = rnd((B, 6 * D), 62, 0.3)
+    ed = dev(emb, gpu)
+    args = (dev(parts, gpu), dev(rnd((D,), 63), gpu), ed[:, 2 * D:3 * D], ed[:, :D],
+            ed[:, D:2 * D])
+    y = ops.adaln_resid(dev(h, gpu), *args)
+    yp = ops.adaln_resid(dev(h, gpu), *args, packed=True)
+    assert same_bits(yp, pack2_np(y.cpu().numpy()))
+    y0 = ops.adaln_resid(dev(h, gpu), None, None, None, ed[:, :D], ed[:, D:2 * D])
+    y0p = ops.adaln_resid(dev(h, gpu), None, None, None, ed[:, :D], ed[:, D:2 * D], packed=True)
+    assert same_bits(y0p, pack2_np(y0.cpu().numpy()))
+    for Tq in (500, 1000, 24):
+        qkv = dev(rnd((B, Tq, 3 * D), 64), gpu)
+        q, k, v = qkv[..., :D], qkv[..., D:2 * D], qkv[..., 2 * D:]
+        for products in (3, 6):
+            o = ops.attention(q, k, v, 16, products=products)
+            op = ops.attention(q, k, v, 16, products=products, out_packed=True)
+            assert same_bits(op, pack2_np(o.cpu().numpy())), (Tq, products)
