@@ -257,7 +257,8 @@ int lx_linear_split_f32(const float* x, int ldx, const void* planes, const float
  * (x0 + x1, 16 significant bits each) and the three products a0 b0 + a0 b1 +
  * a1 b0: half the matrix-core work and two thirds of the W traffic, each
  * product within about 2^-16 of a * b (the packed weight is the same).
- * Two-part packed rows (three products, bm 64; no stream-K): an fp32 row
+ * Two-part packed rows (three products; the packed output on bm 64; no
+ * stream-K): an fp32 row
  * packed as 16 bytes per aligned group of four values x, the four bf16(x) and
  * then the four bf16(x - bf16(x)) -- the same bytes, addresses and row stride
  * as the fp32 row.  a_packed = 1: A holds such rows (the GEMM does not split

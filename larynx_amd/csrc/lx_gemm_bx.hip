@@ -558,8 +558,8 @@ int launch_bx(const BxArgs& a, const EpiArgs& ep, hipStream_t stream) {
   return check_launch("gemm_bx_kernel");
 }
 
-// Packed operands (AP = 1, BX_OUT_PACKED) exist for three products on 64-row
-// tiles only (the host checks this).
+// Packed operands exist for three products (AP = 1 on 64- and 128-row tiles,
+// BX_OUT_PACKED on 64-row tiles; the host checks this).
 template <int BMB, int NP, int AP = 0>
 int dispatch_bx(const BxArgs& a, int out, const EpiArgs& ep, hipStream_t s) {
   if (out == BX_OUT_PARTIAL) return launch_bx<LX_EPI_NONE, BMB, BX_OUT_PARTIAL, NP, AP>(a, ep, s);
@@ -613,8 +613,9 @@ int linear_bx(const lx_linear_bx& g, hipStream_t stream) {
              "linear_bx: unknown output %d", g.out);
   LX_REQUIRE(g.a_packed == 0 || g.a_packed == 1, "linear_bx: a_packed=%d must be 0 or 1",
              g.a_packed);
-  LX_REQUIRE((!g.a_packed && g.out != BX_OUT_PACKED) || (g.products == 3 && g.bm == 64),
-             "linear_bx: packed operands need three products and 64-row tiles");
+  LX_REQUIRE((!g.a_packed || g.products == 3) && (g.out != BX_OUT_PACKED ||
+                                                   (g.products == 3 && g.bm == 64)),
+             "linear_bx: packed operands need three products (the packed output 64-row tiles)");
   const int slices = g.slices < 1 ? 1 : g.slices;
   int kslice = g.K;
   if (slices > 1) {
@@ -680,7 +681,9 @@ int linear_bx(const lx_linear_bx& g, hipStream_t stream) {
       a.counters = g.counters;
     }
   }
-  if (g.a_packed) return dispatch_bx<2, 3, 1>(a, g.out, ep, stream);
+  if (g.a_packed)
+    return g.bm == 128 ? dispatch_bx<4, 3, 1>(a, g.out, ep, stream)
+                       : dispatch_bx<2, 3, 1>(a, g.out, ep, stream);
   if (g.products == 3)
     return g.bm == 128 ? dispatch_bx<4, 3>(a, g.out, ep, stream)
                        : dispatch_bx<2, 3>(a, g.out, ep, stream);

@@ -121,7 +121,8 @@ size_t split_tail_ws_floats(int M, int N, int K, int* tail_tiles);
 // x[m, :] += sum_s ws[s][m, :] (+ bias); then, if norm_w, hn[m, :] =
 // RMSNorm(x[m, :]) * norm_w (the next sub-layer's input norm).  Rows of N floats.
 int splitk_resid_rmsnorm(const float* ws, int splits, int M, int N, const float* bias, float* x,
-                         const float* norm_w, float eps, float* hn, hipStream_t stream);
+                         const float* norm_w, float eps, float* hn, hipStream_t stream,
+                         int out_packed = 0);
 // v = sum_s ws[s][m, :] + bias over the fused q|k|v row (n_heads + 2 n_kv_heads
 // heads of 64); NEOX rotary at position pos[m] on the q and k heads; q ->
 // q_out[m, 0:n_heads*64] (row stride ldq), k / v -> k_cache / v_cache row

@@ -138,7 +138,7 @@ size_t splitk_ws_floats(int max_ctx, int H, int QKV, int I, int* tails) {
 // q|k|v, o_proj or down_proj as K-slice partial products into m->ws; returns the
 // slice count through *splits.
 int prefill_partials(lx_qwen2* m, const float* x, int ldx, const void* wf, const float* w,
-                     int rows, int N, int K, int* splits, hipStream_t s) {
+                     int rows, int N, int K, int* splits, hipStream_t s, bool x_packed = false) {
   if (m->frag) {
     const int sl = prefill_bx_slices(rows, N, K);
     lx_linear_bx g{};
@@ -155,6 +155,7 @@ int prefill_partials(lx_qwen2* m, const float* x, int ldx, const void* wf, const
     g.bm = 64;
     g.slices = sl;
     g.products = m->products;
+    g.a_packed = x_packed ? 1 : 0;
     *splits = sl;
     return linear_bx(g, s);
   }
@@ -173,17 +174,26 @@ int prefill_partials(lx_qwen2* m, const float* x, int ldx, const void* wf, const
 //   down_proj: K-slice partials, then residual + next_norm.
 // Every projection runs on the fragment-order split-operand GEMM when the
 // geometry allows (m->frag: N multiples of 128, K of 64), else on the fp32 GEMMs.
-int prefill_layer(lx_qwen2* m, Layer& L, int rows, const float* next_norm, hipStream_t s) {
+// With three products on the fragment-order GEMM, the GEMM inputs written by
+// this layer's kernels (attention's output, the RMSNorm outputs) are two-part
+// packed rows (bit-identical products, no split per column tile); hn_packed:
+// m->hn arrives packed (written by the previous layer), pack_next: write the
+// next norm packed (not the final norm, which the fp32 logits GEMM reads).
+int prefill_layer(lx_qwen2* m, Layer& L, int rows, const float* next_norm, hipStream_t s,
+                  bool hn_packed, bool pack_next) {
   const int H = m->H, KV = m->KV, QKV = m->QKV;
+  const bool pk = m->frag && m->products == 3;
   int sp = 0;
-  LX_TRY(prefill_partials(m, m->hn, H, L.qkv_wf, L.qkv_w, rows, QKV, H, &sp, s));
+  LX_TRY(prefill_partials(m, m->hn, H, L.qkv_wf, L.qkv_w, rows, QKV, H, &sp, s, pk && hn_packed));
   LX_TRY(splitk_qkv_rope_cache(m->ws, sp, rows, L.qkv_b, m->NH, m->NKV, m->pos, m->rope_tab,
                                m->qkv, QKV, L.k_cache, L.v_cache, 0, s));
   const float scale = 1.0f / std::sqrt((float)m->HD);
-  LX_TRY(lx_attention_f32(m->qkv, QKV, L.k_cache, KV, L.v_cache, KV, m->att, H, 1, rows, rows,
-                          m->NH, m->NKV, m->HD, scale, /*causal*/ 1, /*q_offset*/ 0, s));
-  LX_TRY(prefill_partials(m, m->att, H, L.o_wf, L.o_w, rows, H, H, &sp, s));
-  LX_TRY(splitk_resid_rmsnorm(m->ws, sp, rows, H, nullptr, m->x, L.post_norm, m->eps, m->hn, s));
+  LX_TRY(attention(m->qkv, QKV, L.k_cache, KV, L.v_cache, KV, m->att, H, 1, rows, rows, m->NH,
+                   m->NKV, m->HD, scale, /*causal*/ 1, /*q_offset*/ 0, /*products*/ 6,
+                   /*out_packed*/ pk ? 1 : 0, s));
+  LX_TRY(prefill_partials(m, m->att, H, L.o_wf, L.o_w, rows, H, H, &sp, s, pk));
+  LX_TRY(splitk_resid_rmsnorm(m->ws, sp, rows, H, nullptr, m->x, L.post_norm, m->eps, m->hn, s,
+                              pk));
   lx_epilogue swiglu{};
   swiglu.kind = LX_EPI_SWIGLU_PAIRED;
   if (m->frag) {
@@ -191,6 +201,7 @@ int prefill_layer(lx_qwen2* m, Layer& L, int rows, const float* next_norm, hipSt
     // (L = 256: 152 tiles, 33 vs 35 us), else 64-row tiles (L = 1024: 95 vs 116 us)
     lx_linear_bx g{};
     g.A = m->hn;
+    g.a_packed = pk ? 1 : 0;
     g.lda = H;
     g.Wf = L.gu_wf;
     g.epi = &swiglu;
@@ -209,7 +220,8 @@ int prefill_layer(lx_qwen2* m, Layer& L, int rows, const float* next_norm, hipSt
                              &swiglu, m->ws, m->ws_floats, m->arrivals, m->n_arrivals, s));
   }
   LX_TRY(prefill_partials(m, m->act, m->I, L.down_wf, L.down_w, rows, H, m->I, &sp, s));
-  return splitk_resid_rmsnorm(m->ws, sp, rows, H, nullptr, m->x, next_norm, m->eps, m->hn, s);
+  return splitk_resid_rmsnorm(m->ws, sp, rows, H, nullptr, m->x, next_norm, m->eps, m->hn, s,
+                              pk && pack_next);
 }
 
 // One decode layer (src/llm/llm.cpp:254-289): RMSNorm + QKV + rotary + cache
@@ -547,7 +559,8 @@ extern "C" int lx_qwen2_prefill(lx_qwen2* m, const float* lm_input, int L, float
   LX_TRY(lx_rmsnorm_f32(m->x, m->layers[0].in_norm, m->hn, L, H, m->eps, s));
   for (int l = 0; l < m->NL; ++l) {
     const float* next_norm = l + 1 < m->NL ? m->layers[l + 1].in_norm : m->final_norm;
-    LX_TRY(prefill_layer(m, m->layers[l], L, next_norm, s));
+    LX_TRY(prefill_layer(m, m->layers[l], L, next_norm, s, /*hn_packed*/ l > 0,
+                         /*pack_next*/ l + 1 < m->NL));
     if (hidden)
       (void)hipMemcpyAsync(hidden + (size_t)l * L * H, m->x, sizeof(float) * (size_t)L * H,
                            hipMemcpyDeviceToDevice, s);

@@ -8,6 +8,7 @@
 //     (src/llm/ops.cpp:21-30) and the KV cache append (llm.cpp:200-204).
 // The K slices are summed in a fixed order, so results are reproducible.
 #include "lx_common.hpp"
+#include "lx_gemm_common.hpp"
 #include "lx_internal.hpp"
 
 namespace lx {
@@ -51,7 +52,7 @@ __global__ __launch_bounds__(256) void resid_rmsnorm_kernel(const float* __restr
                                                             int splits, int M, int N,
                                                             const float* __restrict__ bias,
                                                             float* x, const float* __restrict__ w,
-                                                            float eps, float* hn) {
+                                                            float eps, float* hn, int pk) {
   __shared__ float red[4];
   const int row = blockIdx.x, t = threadIdx.x;
   const int N4 = N >> 2;
@@ -96,7 +97,10 @@ __global__ __launch_bounds__(256) void resid_rmsnorm_kernel(const float* __restr
       o.y = (v[j].y * r) * g.y;
       o.z = (v[j].z * r) * g.z;
       o.w = (v[j].w * r) * g.w;
-      hr[i] = o;
+      if (pk)  // two-part packed row for the three-product GEMM
+        reinterpret_cast<uintx4_t*>(hr)[i] = pack2_bf16(floatx4{o.x, o.y, o.z, o.w});
+      else
+        hr[i] = o;
     }
   }
 }
@@ -155,20 +159,21 @@ __global__ __launch_bounds__(256) void qkv_rope_cache_kernel(
 }  // namespace
 
 int splitk_resid_rmsnorm(const float* ws, int splits, int M, int N, const float* bias, float* x,
-                         const float* norm_w, float eps, float* hn, hipStream_t stream) {
+                         const float* norm_w, float eps, float* hn, hipStream_t stream,
+                         int out_packed) {
   LX_REQUIRE(ws && x && M > 0 && N > 0 && N % 4 == 0 && splits >= 1 && splits <= kMaxSplits &&
                  (!norm_w || hn),
              "splitk_resid_rmsnorm: bad args");
   const int nv = (N / 4 + 255) / 256;
   if (nv <= 1)
     hipLaunchKernelGGL(resid_rmsnorm_kernel<1>, dim3(M), dim3(256), 0, stream, ws, splits, M, N,
-                       bias, x, norm_w, eps, hn);
+                       bias, x, norm_w, eps, hn, out_packed ? 1 : 0);
   else if (nv <= 2)
     hipLaunchKernelGGL(resid_rmsnorm_kernel<2>, dim3(M), dim3(256), 0, stream, ws, splits, M, N,
-                       bias, x, norm_w, eps, hn);
+                       bias, x, norm_w, eps, hn, out_packed ? 1 : 0);
   else if (nv <= 4)
     hipLaunchKernelGGL(resid_rmsnorm_kernel<4>, dim3(M), dim3(256), 0, stream, ws, splits, M, N,
-                       bias, x, norm_w, eps, hn);
+                       bias, x, norm_w, eps, hn, out_packed ? 1 : 0);
   else {
     set_error("splitk_resid_rmsnorm: N=%d too wide", N);
     return LX_ERR_ARG;

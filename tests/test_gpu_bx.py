@@ -195,10 +195,10 @@ def test_linear_bx_rejects_bad_arguments(gpu, ops):
         ops.linear_bx(x, wf, 128, slices=2)
     with pytest.raises(LxError):
         ops.linear_bx(x[:, :96], ops.wfrag_pack(torch.zeros(128, 96, device=gpu)), 128)
-    with pytest.raises(LxError):  # packed operands: three products, 64-row tiles
+    with pytest.raises(LxError):  # packed operands: three products
         ops.linear_bx(x, wf, 128, bm=64, products=6, a_packed=True)
-    with pytest.raises(LxError):
-        ops.linear_bx(x, wf, 128, bm=128, products=3, a_packed=True)
+    with pytest.raises(LxError):  # the packed output: 64-row tiles
+        ops.linear_bx(x, wf, 128, out_kind=ops.LX_BX_OUT_PACKED, bm=128, products=3)
     with pytest.raises(LxError):  # the packed output takes no epilogue but GELU
         ops.linear_bx(x, wf, 128, epilogue=ops.Epilogue(kind=ops.LX_EPI_SWIGLU_PAIRED),
                       out_kind=ops.LX_BX_OUT_PACKED, bm=64, products=3)
@@ -346,6 +346,12 @@ def test_linear_bx_packed_operands_bit_identical(gpu, ops, M):
     P = [ops.linear_bx(a, wf, D, out_kind=ops.LX_BX_OUT_PARTIAL, slices=2, bm=64, products=3,
                        a_packed=packed) for a, packed in ((xd, False), (xp, True))]
     assert same_bits(P[0], P[1])
+    # 128-row tiles (the Qwen2 prefill's gate/up) read packed rows too
+    wf2 = ops.wfrag_pack(dev(W[:2 * D], gpu))
+    sw = ops.Epilogue(kind=ops.LX_EPI_SWIGLU_PAIRED)
+    Y = [ops.linear_bx(a, wf2, 2 * D, dev(b[:2 * D], gpu), sw, bm=128, products=3,
+                       a_packed=packed) for a, packed in ((xd, False), (xp, True))]
+    assert same_bits(Y[0], Y[1])
 
 
 def test_packed_producers_match_host_packing(gpu, ops):
