@@ -126,10 +126,11 @@ def in_step_matrix(records, ops):
     ap = ", 1" if DIT_PRODUCTS == 3 else ""
     ff0_out = ops.LX_BX_OUT_PACKED if DIT_PRODUCTS == 3 else ops.LX_BX_OUT_F32
     pats = {
-        "gemm_qkv_rope": f"gemm_bx_kernel<{ops.LX_EPI_ROPE_PARTIAL}, 2, 0, {DIT_PRODUCTS}{ap}>",
+        "gemm_qkv_rope": f"gemm_bx_kernel<{ops.LX_EPI_ROPE_PARTIAL}, 2, {ff0_out}, {DIT_PRODUCTS}{ap}>",
         "gemm_ff0_gelu": f"gemm_bx_kernel<{ops.LX_EPI_GELU_TANH}, 2, {ff0_out}, {DIT_PRODUCTS}{ap}>",
         "gemm_out_ff2_partial": f"gemm_bx_kernel<{ops.LX_EPI_NONE}, 2, 1, {DIT_PRODUCTS}{ap}>",
-        "attention": f"attn_bx_kernel<2, 2, true, {DIT_PRODUCTS}>",
+        "attention": f"attn_bx_kernel<2, 2, true, {DIT_PRODUCTS}"
+                     + (", true>" if DIT_PRODUCTS == 3 else ">"),
     }
     out = {}
     for k, pat in pats.items():
@@ -290,7 +291,7 @@ def gemm_kernels(torch, ops, T, dev):
     qv = qkv.view(B, T, 3 * D)
     hv = h.view(M, D)
 
-    def proj(x, W, b, ep, y, pack_out=False):
+    def proj(x, W, b, ep, y, pack_out=False, pack_from=0):
         N = W.shape[0]
         wf = ops.wfrag_pack(W)
         kind, sl = dit_projection_plan(M, N)
@@ -306,20 +307,24 @@ def gemm_kernels(torch, ops, T, dev):
                 return lambda: ops.linear_bx(a, wf, N, out=part, out_kind=ops.LX_BX_OUT_PARTIAL,
                                              bm=64, slices=sl, products=products, a_packed=pk)
             ok = ops.LX_BX_OUT_PACKED if pk and pack_out else ops.LX_BX_OUT_F32
+            pf = pack_from if pk and pack_out else 0
             return lambda: ops.linear_bx(a, wf, N, b, ep, out=y, out_kind=ok, bm=64,
-                                         products=products, a_packed=pk)
+                                         products=products, a_packed=pk, pack_from=pf)
         kern = (f"gemm_bx_kernel 64x128, {DIT_PRODUCTS} products"
                 + (", packed activations" if DIT_PRODUCTS == 3 else "")
                 + (f", {sl} K slices (sum folded into adaln_resid)" if kind == "partial" else ""))
         return bx(DIT_PRODUCTS), kern, fp32, bx(6)
     cases = {
-        "gemm_qkv_rope": (proj(xd, wq, bq, rope, qkv), 2 * M * 3 * D * D, 1),
+        # q fp32, k and v packed for the split attention (T = 500's layout)
+        "gemm_qkv_rope": (proj(xd, wq, bq, rope, qkv, pack_out=True, pack_from=D),
+                          2 * M * 3 * D * D, 1),
         "gemm_out_gated": (proj(xd, wo, bd, gated, hv), 2 * M * D * D, 1),
         "gemm_ff0_gelu": (proj(xd, w1, b1, gelu, ff, pack_out=True), 2 * M * F * D, 1),
         "gemm_ff2_gated": (proj(xf, w2, bd, gated, hv), 2 * M * D * F, 1),
         "attention": ((lambda: ops.attention(qv[..., :D], qv[..., D:2 * D], qv[..., 2 * D:], 16,
                                              out=att, products=DIT_PRODUCTS,
-                                             out_packed=DIT_PRODUCTS == 3),
+                                             out_packed=DIT_PRODUCTS == 3,
+                                             kv_packed=DIT_PRODUCTS == 3),
                        f"attn_bx_kernel ({DIT_PRODUCTS} products) / attn_flash_kernel", None,
                        lambda: ops.attention(qv[..., :D], qv[..., D:2 * D], qv[..., 2 * D:], 16,
                                              out=att, products=6)),
@@ -700,8 +705,8 @@ def counter_probe(torch, ops, launches=20):
     ff0_out = ops.LX_BX_OUT_PACKED if pk else ops.LX_BX_OUT_F32
     torch.cuda.synchronize()
     for _ in range(launches):
-        ops.linear_bx(xa, fq, 3 * D, bq, rope, out=qkv, bm=64, products=DIT_PRODUCTS,
-                      a_packed=pk)
+        ops.linear_bx(xa, fq, 3 * D, bq, rope, out=qkv, out_kind=ff0_out, bm=64,
+                      products=DIT_PRODUCTS, a_packed=pk, pack_from=D if pk else 0)
     for _ in range(launches):
         ops.linear_bx(xa, f0, F, b0, gelu, out=ff, out_kind=ff0_out, bm=64,
                       products=DIT_PRODUCTS, a_packed=pk)
@@ -713,7 +718,7 @@ def counter_probe(torch, ops, launches=20):
                       products=DIT_PRODUCTS, a_packed=pk)
     for _ in range(launches):
         ops.attention(q3[..., :D], q3[..., D:2 * D], q3[..., 2 * D:], 16, 16, out=att,
-                      products=DIT_PRODUCTS, out_packed=pk)
+                      products=DIT_PRODUCTS, out_packed=pk, kv_packed=pk)
     torch.cuda.synchronize()
     print(f"counter probe: {launches} x QKV, FF0, out, FF2 GEMMs and attention (B={B} T={T})",
           flush=True)
@@ -768,7 +773,8 @@ def traffic_probe(torch, ops, launches=20):
     torch.cuda.synchronize()
     for _ in range(launches):
         ops.linear_bx(xa, fq, 3 * D, bq, rope, out=qkv, bm=64, products=DIT_PRODUCTS,
-                      a_packed=pk)
+                      a_packed=pk, pack_from=D if pk else 0,
+                      out_kind=ops.LX_BX_OUT_PACKED if pk else ops.LX_BX_OUT_F32)
     torch.cuda.synchronize()
     for _ in range(launches):
         dst.copy_(src)

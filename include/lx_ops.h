@@ -263,10 +263,12 @@ int lx_linear_split_f32(const float* x, int ldx, const void* planes, const float
  * then the four bf16(x - bf16(x)) -- the same bytes, addresses and row stride
  * as the fp32 row.  a_packed = 1: A holds such rows (the GEMM does not split
  * it again; results are bit-identical to the fp32 A it was packed from).
- * out = LX_BX_OUT_PACKED: Y receives the fp32 epilogue's result (no epilogue
- * or GELU) as packed rows, for the next such GEMM.  The estimator passes its
- * activations this way with three products (lx_adaln_resid_packed_f32,
- * lx_attention_np_f32's out_packed).
+ * out = LX_BX_OUT_PACKED: Y receives the fp32 epilogue's result (no epilogue,
+ * GELU or rotary) as packed rows from column pack_from on (a multiple of 4;
+ * the columns before it stay fp32), for the next such GEMM or the
+ * three-product attention (K and V).  The estimator passes its activations
+ * this way with three products (lx_adaln_resid_packed_f32,
+ * lx_attention_np_f32's out_packed and kv_packed).
  * Replaces linear() = ggml_mul_mat + ggml_add (src/flow/ops.cpp:20-26) with the
  * node its epilogue absorbs; the fragment-ordered weight has no counterpart
  * in the reference (its weights stay fp32). */
@@ -289,6 +291,7 @@ typedef struct lx_linear_bx {
   int n_counters;
   int products;
   int a_packed;
+  int pack_from;
 } lx_linear_bx;
 int lx_wfrag_pack_f32(const float* W, void* Wf, int N, int K, hipStream_t stream);
 int lx_linear_bx_f32(const lx_linear_bx* g, hipStream_t stream);
@@ -313,13 +316,17 @@ int lx_attention_f32(const float* q, int ldq, const float* k, int ldk, const flo
  * lx_attention_f32) or 3 (two bf16 parts per operand, three products: about
  * half the matrix-core work; the grids that run the fp32 kernel ignore it).
  * out_packed != 0: o receives two-part packed rows (lx_linear_bx's a_packed
- * operand) instead of fp32.  The estimator calls it with its
- * lx_dit_set_products setting and, with three products, packed output for
- * its out projection. */
+ * operand) instead of fp32.  kv_packed != 0: k and v are two-part packed rows
+ * (lx_linear_bx's LX_BX_OUT_PACKED), for three products on the layouts of the
+ * split kernel (64-query grids of at least 256 workgroups, 128-query grids of
+ * whole rounds); other shapes return an error.  The estimator calls it with
+ * its lx_dit_set_products setting and, with three products, packed K/V from
+ * its QKV projection where they apply and packed output for its out
+ * projection. */
 int lx_attention_np_f32(const float* q, int ldq, const float* k, int ldk, const float* v,
                         int ldv, float* o, int ldo, int B, int Tq, int Tk, int n_heads,
                         int n_kv_heads, int head_dim, float scale, int causal, int q_offset,
-                        int products, int out_packed,
+                        int products, int out_packed, int kv_packed,
                         hipStream_t stream);
 
 /* Causal grouped conv1d + Mish (one CausalConvPositionEmbedding half):

@@ -62,7 +62,7 @@ class LinearBx(C.Structure):
         ("slice_stride", C.c_long), ("M", C.c_int), ("N", C.c_int), ("K", C.c_int),
         ("bm", C.c_int), ("slices", C.c_int), ("ws", fp), ("ws_floats", C.c_size_t),
         ("counters", C.c_void_p), ("n_counters", C.c_int), ("products", C.c_int),
-        ("a_packed", C.c_int),
+        ("a_packed", C.c_int), ("pack_from", C.c_int),
     ]
 
 
@@ -163,7 +163,7 @@ SIGNATURES = [
       C.c_int, C.c_int, C.c_float, C.c_int, C.c_int, stream_t]),
     ("lx_attention_np_f32", C.c_int,
      [fp, C.c_int, fp, C.c_int, fp, C.c_int, fp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
-      C.c_int, C.c_int, C.c_float, C.c_int, C.c_int, C.c_int, C.c_int, stream_t]),
+      C.c_int, C.c_int, C.c_float, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, stream_t]),
     ("lx_conv_pos_mish_f32", C.c_int,
      [fp, fp, fp, fp, fp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, stream_t]),
     ("lx_conv_pack_weight_f32", C.c_int, [fp, fp, C.c_int, C.c_int, C.c_int, stream_t]),

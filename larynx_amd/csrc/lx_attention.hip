@@ -510,6 +510,13 @@ __device__ __forceinline__ void split3(floatx4 v, bf16x4& x0, bf16x4& x1, bf16x4
   x1 = __builtin_convertvector(r, bf16x4);
   x2 = __builtin_convertvector(r - bf16x4_to_f32(x1), bf16x4);
 }
+// The two bf16 parts of a packed group (pack2_bf16) loaded as 16 bytes.
+__device__ __forceinline__ void unpack2(floatx4 v, bf16x4* x) {
+  const uintx4 u = __builtin_bit_cast(uintx4, v);
+  x[0] = __builtin_bit_cast(bf16x4, uintx2{u[0], u[1]});
+  x[1] = __builtin_bit_cast(bf16x4, uintx2{u[2], u[3]});
+  x[2] = x[1];
+}
 __device__ __forceinline__ void split3(floatx8 v, bf16x8& x0, bf16x8& x1, bf16x8& x2) {
   x0 = __builtin_convertvector(v, bf16x8);
   const floatx8 r = v - bf16x8_to_f32(x0);
@@ -561,7 +568,9 @@ __device__ __forceinline__ int vt_pos(int k) {
 // beside the PV MFMAs.  K and V rotate through two LDS buffers each: K of
 // tile t + 2 replaces K of tile t (its scores were formed in iteration t - 1),
 // V of tile t + 1 replaces V of tile t - 1, so one barrier per tile suffices.
-template <int QS, int KS, bool BUF, int NP>
+// KVP: K and V arrive as two-part packed rows (their producer split them
+// once; three products), so staging stores the parts without splitting.
+template <int QS, int KS, bool BUF, int NP, bool KVP = false>
 __global__ __launch_bounds__(64 * QS * KS) void attn_bx_kernel(
     const float* __restrict__ q, int ldq, const float* __restrict__ k, int ldk,
     const float* __restrict__ v, int ldv, float* __restrict__ o, int ldo, int Tq, int Tk,
@@ -676,7 +685,10 @@ __global__ __launch_bounds__(64 * QS * KS) void attn_bx_kernel(
       const int idx = tid + NT * j;
       const int row = idx >> 4, c = (idx & 15) * 4;
       bf16x4 x[3];
-      split3(rk[j], x[0], x[1], x[2]);  // (the third part is dead code with two)
+      if constexpr (KVP)
+        unpack2(rk[j], x);
+      else
+        split3(rk[j], x[0], x[1], x[2]);  // (the third part is dead code with two)
 #pragma unroll
       for (int p = 0; p < NPL; ++p)
         *reinterpret_cast<bf16x4*>(dst + (p * KT + row) * kKP + c) = x[p];
@@ -691,8 +703,13 @@ __global__ __launch_bounds__(64 * QS * KS) void attn_bx_kernel(
       v_map(idx, pr, c);
       const int pos = vt_pos(2 * pr);
       bf16x4 x0[3], x1[3];
-      split3(rv[j][0], x0[0], x0[1], x0[2]);
-      split3(rv[j][1], x1[0], x1[1], x1[2]);
+      if constexpr (KVP) {
+        unpack2(rv[j][0], x0);
+        unpack2(rv[j][1], x1);
+      } else {
+        split3(rv[j][0], x0[0], x0[1], x0[2]);
+        split3(rv[j][1], x1[0], x1[1], x1[2]);
+      }
 #pragma unroll
       for (int p = 0; p < NPL; ++p)
 #pragma unroll
@@ -997,10 +1014,26 @@ __global__ __launch_bounds__(64 * QS * KS) void attn_bx_kernel(
 }
 
 }  // namespace
+// Layout of a launch: 0 small grids (32-query workgroups), 1 64-query, 2
+// 128-query; and whether the split-operand kernel runs it (see attention()).
+static int attention_layout(int B, int Tq, int n_heads, int products, bool* split) {
+  const long wg64 = (long)((Tq + 63) / 64) * n_heads * B;
+  const long wg128 = (long)((Tq + 127) / 128) * n_heads * B;
+  const int layout = wg64 < 256 ? 0 : (wg128 % 256 == 0 ? 2 : 1);  // small / 64-query / wide
+  *split = layout == 2 || (layout == 1 && (wg64 <= 256 || products == 3));
+  return layout;
+}
+
+bool attention_takes_packed_kv(int B, int Tq, int n_heads, int products) {
+  bool split = false;
+  attention_layout(B, Tq, n_heads, products, &split);
+  return split && products == 3;
+}
+
 int attention(const float* q, int ldq, const float* k, int ldk, const float* v, int ldv, float* o,
               int ldo, int B, int Tq, int Tk, int n_heads, int n_kv_heads, int head_dim,
               float scale, int causal, int q_offset, int products, int out_packed,
-              hipStream_t stream) {
+              hipStream_t stream, int kv_packed) {
   LX_REQUIRE(products == 3 || products == 6, "attention: %d products (3 or 6)", products);
   LX_REQUIRE(q && k && v && o, "attention: null pointer");
   LX_REQUIRE(B > 0 && Tq > 0 && Tk > 0 && n_heads > 0 && n_kv_heads > 0,
@@ -1037,9 +1070,8 @@ int attention(const float* q, int ldq, const float* k, int ldk, const float* v, 
   // 75.9 -> 73.8).  Grids that
   // leave a partial round (T = 1500: 384 workgroups; 2500: 640) run slower
   // than the 64-query layout and keep it.
-  const long wg64 = (long)((Tq + 63) / 64) * n_heads * B;
-  const long wg128 = (long)((Tq + 127) / 128) * n_heads * B;
-  const int layout = wg64 < 256 ? 0 : (wg128 % 256 == 0 ? 2 : 1);  // small / 64-query / wide
+  bool split = false;
+  const int layout = attention_layout(B, Tq, n_heads, products, &split);
   // The split-operand kernel (attn_bx_kernel) runs the 128-query layout and
   // the 64-query layout when its grid fits the CUs in one round (T = 500: 23.6
   // vs 26.2 us; T = 1000: 59.7 vs 81.2; T = 2000: 210 vs 275; T = 3000: 450
@@ -1052,8 +1084,15 @@ int attention(const float* q, int ldq, const float* k, int ldk, const float* v, 
   // and it also runs the 64-query grids of several rounds (T = 1500: 157 ->
   // 99 us; T = 2500: 416 -> 263 us against the fp32 kernel).
   const bool np3 = products == 3;
-  const bool split = layout == 2 || (layout == 1 && (wg64 <= 256 || np3));
+  // K / V as packed rows: the three-product split kernel only.
+  LX_REQUIRE(!kv_packed || (split && np3),
+             "attention: packed K/V need the three-product split kernel (B=%d Tq=%d)", B, Tq);
   auto pick = [&]() {
+    if (split && np3 && kv_packed) {
+      if (layout == 2)
+        return buf ? attn_bx_kernel<4, 2, true, 3, true> : attn_bx_kernel<4, 2, false, 3, true>;
+      return buf ? attn_bx_kernel<2, 2, true, 3, true> : attn_bx_kernel<2, 2, false, 3, true>;
+    }
     if (split && np3) {
       if (layout == 2)
         return buf ? attn_bx_kernel<4, 2, true, 3> : attn_bx_kernel<4, 2, false, 3>;
@@ -1075,8 +1114,8 @@ int attention(const float* q, int ldq, const float* k, int ldk, const float* v, 
       split ? (np3 ? (layout == 2 ? bx_lds<4, 2, 3>() : bx_lds<2, 2, 3>())
                    : (layout == 2 ? bx_lds<4, 2, 6>() : bx_lds<2, 2, 6>()))
             : (layout == 0 ? flash_lds<1, 4, false>() : flash_lds<2, 2, true>());
-  const int variant = split ? 2 + (layout == 2) + 2 * np3 : layout;
-  static LdsLimit once[6][2];  // [kernel variant][buf]
+  const int variant = split ? 2 + (layout == 2) + 2 * np3 + 2 * (kv_packed != 0) : layout;
+  static LdsLimit once[8][2];  // [kernel variant][buf]
   const int rc = raise_lds_limit((const void*)kern, lds, once[variant][buf], "attention");
   if (rc) return rc;
   const long nwg = (long)((Tq + qt - 1) / qt) * n_heads * B;
@@ -1096,14 +1135,14 @@ extern "C" int lx_attention_f32(const float* q, int ldq, const float* k, int ldk
                                 int Tk, int n_heads, int n_kv_heads, int head_dim, float scale,
                                 int causal, int q_offset, hipStream_t stream) {
   return attention(q, ldq, k, ldk, v, ldv, o, ldo, B, Tq, Tk, n_heads, n_kv_heads, head_dim,
-                   scale, causal, q_offset, 6, 0, stream);
+                   scale, causal, q_offset, 6, 0, stream, 0);
 }
 
 extern "C" int lx_attention_np_f32(const float* q, int ldq, const float* k, int ldk,
                                    const float* v, int ldv, float* o, int ldo, int B, int Tq,
                                    int Tk, int n_heads, int n_kv_heads, int head_dim, float scale,
                                    int causal, int q_offset, int products, int out_packed,
-                                   hipStream_t stream) {
+                                   int kv_packed, hipStream_t stream) {
   return attention(q, ldq, k, ldk, v, ldv, o, ldo, B, Tq, Tk, n_heads, n_kv_heads, head_dim,
-                   scale, causal, q_offset, products, out_packed, stream);
+                   scale, causal, q_offset, products, out_packed, stream, kv_packed);
 }

@@ -175,12 +175,17 @@ int forward_core(lx_dit* m, const float* x, long x_bstride, const float* mu, con
                        S ? pend.gate : nullptr, NA, shift, scale, NA, y, B, T, D, kLnEps,
                        packed ? 1 : 0, s);
   };
+  // K and V leave the QKV projection packed too where attention runs on the
+  // three-product split kernel (it then stages them without splitting; q
+  // stays fp32: attention scales it before its own split).
+  const bool pk_kv = pk && attention_takes_packed_kv(B, T, m->heads, 3);
   auto proj = [&](const float* x, int ldx, const void* Wf, const float* W, const float* bias,
                   float* y, int ldy, int N, int K, const lx_epilogue* epi,
-                  bool pack_out = false) -> int {
+                  bool pack_out = false, int pack_from = 0) -> int {
     if (!m->frag) return lx_linear_f32(x, ldx, W, bias, y, ldy, rows, N, K, epi, s);
     lx_linear_bx g{};
     g.a_packed = pk ? 1 : 0;
+    g.pack_from = pack_out && pk ? pack_from : 0;
     g.A = x;
     g.lda = ldx;
     g.Wf = Wf;
@@ -255,10 +260,11 @@ int forward_core(lx_dit* m, const float* x, long x_bstride, const float* mu, con
     rope.rope_section = D;   // q occupies columns [0, D), k [D, 2D)
     rope.rope_sections = 2;
     rope.rope_base = kRopeBase;
-    LX_TRY(proj(m->xn, D, wf0, w0, m->qkv_b[i], m->qkv, 3 * D, 3 * D, D, &rope));
+    LX_TRY(proj(m->xn, D, wf0, w0, m->qkv_b[i], m->qkv, 3 * D, 3 * D, D, &rope, pk_kv,
+                /*pack_from*/ D));
     LX_TRY(attention(m->qkv, 3 * D, m->qkv + D, 3 * D, m->qkv + 2 * D, 3 * D, m->att, D, B, T,
                      T, m->heads, m->heads, m->hd, 1.0f / std::sqrt((float)m->hd), 0, 0,
-                     m->products, pk ? 1 : 0, s));
+                     m->products, pk ? 1 : 0, s, pk_kv ? 1 : 0));
     LX_TRY(proj_gated(m->att, D, wf1, w1, m->out_b[i], gate_msa, D));
 
     LX_TRY(adaln(shift_mlp, scale_mlp, m->xn, pk));

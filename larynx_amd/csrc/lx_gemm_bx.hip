@@ -567,6 +567,8 @@ int dispatch_bx(const BxArgs& a, int out, const EpiArgs& ep, hipStream_t s) {
     if (out == BX_OUT_PACKED) {
       if (ep.kind == LX_EPI_GELU_TANH)
         return launch_bx<LX_EPI_GELU_TANH, BMB, BX_OUT_PACKED, NP, AP>(a, ep, s);
+      if (ep.kind == LX_EPI_ROPE_PARTIAL)
+        return launch_bx<LX_EPI_ROPE_PARTIAL, BMB, BX_OUT_PACKED, NP, AP>(a, ep, s);
       return launch_bx<LX_EPI_NONE, BMB, BX_OUT_PACKED, NP, AP>(a, ep, s);
     }
   }
@@ -634,8 +636,13 @@ int linear_bx(const lx_linear_bx& g, hipStream_t stream) {
     LX_REQUIRE(g.Y && g.ldy >= g.N && (slices == 1 || g.slice_stride >= (long)g.M * g.ldy),
                "linear_bx: bad partial output");
   } else {
-    LX_REQUIRE(g.out != BX_OUT_PACKED || ep.kind == LX_EPI_NONE || ep.kind == LX_EPI_GELU_TANH,
-               "linear_bx: the packed output takes no epilogue but GELU (kind %d)", ep.kind);
+    LX_REQUIRE(g.out != BX_OUT_PACKED || ep.kind == LX_EPI_NONE || ep.kind == LX_EPI_GELU_TANH ||
+                   ep.kind == LX_EPI_ROPE_PARTIAL,
+               "linear_bx: the packed output takes no epilogue, GELU or rotary (kind %d)",
+               ep.kind);
+    LX_REQUIRE(g.pack_from >= 0 && g.pack_from % 4 == 0 && (g.pack_from == 0 || g.out == BX_OUT_PACKED),
+               "linear_bx: pack_from=%d must be a multiple of 4 (packed output)", g.pack_from);
+    ep.pack_from = g.pack_from;
     LX_REQUIRE(g.Y && g.ldy >= (ep.kind == LX_EPI_SWIGLU_PAIRED ? g.N / 2 : g.N) &&
                    g.ldy < (1L << 31),
                "linear_bx: bad output");

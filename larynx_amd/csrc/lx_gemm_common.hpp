@@ -9,7 +9,8 @@ namespace lx {
 
 struct EpiArgs {
   int kind;
-  int vec;  // y, bias, gate rows 16-byte aligned: float4 epilogue path
+  int vec;        // y, bias, gate rows 16-byte aligned: float4 epilogue path
+  int pack_from;  // packed output: columns below it stay fp32
   int rows_per_batch;
   const float* gate;
   long gate_stride;
@@ -51,7 +52,8 @@ __device__ __forceinline__ void rotate_pair(float& x0, float& x1, float ang) {
 // float4 epilogue of 4 columns n..n+3 (all < N) of row m with its operands
 // already loaded: b = bias[n..n+3], g = gate row segment, yo = the residual.
 // Same per-component operations as epilogue4.  PK: the result is stored as a
-// two-part packed group (pack2_bf16) instead of four floats.
+// two-part packed group (pack2_bf16) instead of four floats from column
+// ep.pack_from on.
 template <int EPI, bool PK = false>
 __device__ __forceinline__ void epilogue4v(float* Y, int ldy, int m, int n, float4 v, float4 b,
                                            float4 g, float4 yo, int posm, const EpiArgs& ep) {
@@ -81,7 +83,7 @@ __device__ __forceinline__ void epilogue4v(float* Y, int ldy, int m, int n, floa
     o = make_float4(yo.x + vv[0] * g.x, yo.y + vv[1] * g.y, yo.z + vv[2] * g.z, yo.w + vv[3] * g.w);
   else if (EPI == LX_EPI_RESID)
     o = make_float4(yo.x + vv[0], yo.y + vv[1], yo.z + vv[2], yo.w + vv[3]);
-  if (PK)
+  if (PK && n >= ep.pack_from)
     *reinterpret_cast<uintx4_t*>(Y + (long)m * ldy + n) = pack2_bf16(floatx4{o.x, o.y, o.z, o.w});
   else
     *reinterpret_cast<float4*>(Y + (long)m * ldy + n) = o;

@@ -146,7 +146,10 @@ int linear_bx(const lx_linear_bx& g, hipStream_t stream);
 int attention(const float* q, int ldq, const float* k, int ldk, const float* v, int ldv, float* o,
               int ldo, int B, int Tq, int Tk, int n_heads, int n_kv_heads, int head_dim,
               float scale, int causal, int q_offset, int products, int out_packed,
-              hipStream_t stream);
+              hipStream_t stream, int kv_packed = 0);
+// Whether attention() runs this shape on the three-product split kernel, the
+// one that reads K and V as two-part packed rows (kv_packed).
+bool attention_takes_packed_kv(int B, int Tq, int n_heads, int products);
 // W (N, K) -> fragment order (3 * N * K bf16); N % 32 == 0, K % 16 == 0.
 int wfrag_pack(const float* W, void* Wf, int N, int K, hipStream_t stream);
 

@@ -216,7 +216,7 @@ def wfrag_pack(W):
 
 
 def linear_bx(a, wf, N, b=None, epilogue=None, out=None, out_kind=LX_BX_OUT_F32, bm=128,
-              slices=1, scratch=None, products=6, a_packed=False):
+              slices=1, scratch=None, products=6, a_packed=False, pack_from=0):
     """epi(a @ W^T + b) with fp32 arithmetic on the bf16 matrix cores, W given as
     wfrag_pack(W) (N rows), a fp32 (M, K).  out_kind LX_BX_OUT_F32: (M, N) (out= the
     residual stream for residual epilogues); LX_BX_OUT_PARTIAL: (slices, M, N) raw
@@ -233,6 +233,7 @@ def linear_bx(a, wf, N, b=None, epilogue=None, out=None, out_kind=LX_BX_OUT_F32,
     g.out = out_kind
     g.M, g.N, g.K, g.bm, g.slices, g.products = M, N, K, bm, slices, products
     g.a_packed = int(a_packed)
+    g.pack_from = pack_from
     if out_kind == LX_BX_OUT_PARTIAL:
         if out is None:
             out = torch.empty(slices, M, N, device=a.device, dtype=torch.float32)
@@ -261,11 +262,12 @@ def bx_scratch(device, bm=128, max_tiles=4096):
 
 
 def attention(q, k, v, n_heads, n_kv_heads=None, scale=None, causal=False, q_offset=0,
-              out=None, head_dim=64, products=6, out_packed=False):
+              out=None, head_dim=64, products=6, out_packed=False, kv_packed=False):
     """softmax(scale q k^T) v per head; q (B, Tq, *), k/v (B, Tk, *) with heads packed from
     column 0 (row strides may exceed the head span); products: the split-operand kernel's
     bf16 products per fp32 product (6 or 3); out_packed: the output as two-part packed
-    rows (linear_bx's a_packed operand).  src/flow/dit.cpp:34-51."""
+    rows (linear_bx's a_packed operand); kv_packed: k and v given as packed rows (three
+    products, the split kernel's layouts).  src/flow/dit.cpp:34-51."""
     n_kv_heads = n_kv_heads or n_heads
     B, Tq = q.shape[0], q.shape[1]
     Tk = k.shape[1]
@@ -275,7 +277,7 @@ def attention(q, k, v, n_heads, n_kv_heads=None, scale=None, causal=False, q_off
     check(lib.lx_attention_np_f32(_p(q), q.stride(1), _p(k), k.stride(1), _p(v), v.stride(1),
                                   _p(out), out.stride(1), B, Tq, Tk, n_heads, n_kv_heads,
                                   head_dim, scale, int(causal), q_offset, products,
-                                  int(out_packed), stream()))
+                                  int(out_packed), int(kv_packed), stream()))
     return out
 
 

@@ -380,3 +380,36 @@ def test_packed_producers_match_host_packing(gpu, ops):
             o = ops.attention(q, k, v, 16, products=products)
             op = ops.attention(q, k, v, 16, products=products, out_packed=True)
             assert same_bits(op, pack2_np(o.cpu().numpy())), (Tq, products)
+
+
+def test_packed_kv_into_attention_bit_identical(gpu, ops):
+    """The QKV projection with its rotary epilogue writes q fp32 and k, v as packed
+    rows (pack_from = D); attention reading them packed (three products, the split
+    kernel's layouts: T = 500 and 1500 on 64-query workgroups, 1000 on 128-query)
+    gives bit-identical output to attention on the fp32 q, k, v; the fp32 kernel's
+    small grids refuse packed K/V."""
+    from larynx_amd import LxError
+    announce("packed K/V into attention")
+    B, D = 2, 1024
+    for T in (500, 1500, 1000):
+        M = B * T
+        x = dev(rnd((M, D), 70), gpu)
+        wf = ops.wfrag_pack(dev(rnd((3 * D, D), 71, 0.03), gpu))
+        bq = dev(rnd((3 * D,), 72), gpu)
+        pos = torch.arange(T, dtype=torch.int32, device=gpu)
+        rope = ops.Epilogue(kind=ops.LX_EPI_ROPE_PARTIAL, rows_per_batch=T, pos=pos.data_ptr(),
+                            rot_dim=64, rope_section=D, rope_sections=2, rope_base=10000.0)
+        y = ops.linear_bx(x, wf, 3 * D, bq, rope, bm=64, products=3)
+        yp = ops.linear_bx(x, wf, 3 * D, bq, rope, out_kind=ops.LX_BX_OUT_PACKED, bm=64,
+                           products=3, pack_from=D)
+        yc = y.cpu().numpy()
+        assert same_bits(yp[:, :D], yc[:, :D])
+        assert same_bits(yp[:, D:], pack2_np(yc[:, D:]))
+        q3, p3 = y.view(B, T, 3 * D), yp.view(B, T, 3 * D)
+        o = ops.attention(q3[..., :D], q3[..., D:2 * D], q3[..., 2 * D:], 16, products=3)
+        op = ops.attention(p3[..., :D], p3[..., D:2 * D], p3[..., 2 * D:], 16, products=3,
+                           kv_packed=True)
+        assert same_bits(o, op), T
+    q = torch.zeros(2, 24, D, device=gpu)
+    with pytest.raises(LxError):
+        ops.attention(q, q, q, 16, products=3, kv_packed=True)
