@@ -893,13 +893,17 @@ def main():
     rec = profiled_kernels(torch, lambda: [step(i) for i in range(3)])
     rows, D, mel = 2 * T, 1024, 80
     p_slices = splitk_slices(rows, mel, D)
+    # every modulated LayerNorm of the step runs as adaln_resid_kernel: the first
+    # (block 0's) without slices, the other 2 * depth fold the previous
+    # projection's two K slices into h first
+    ln_plain = 2 * rows * D * 4 + 2 * 2 * D * 4
+    ln_fold = 5 * rows * D * 4 + 4 * 2 * D * 4
     in_path = {
-        "adaln_in_step": kernel_gbs(rec, "adaln_kernel", 2 * rows * D * 4 + 2 * 2 * D * 4,
-                                    f"modulated LayerNorm before QKV / FF0, B=2 T={T}"),
         "adaln_resid_in_step": kernel_gbs(
-            rec, "adaln_resid_kernel", 5 * rows * D * 4 + 4 * 2 * D * 4,
-            f"the out / FF2 projection's two K slices + bias into h (gated residual), then "
-            f"the modulated LayerNorm, B=2 T={T}"),
+            rec, "adaln_resid_kernel", [ln_plain] + [ln_fold] * (2 * cfg.depth),
+            f"the modulated LayerNorms of a step (B=2 T={T}): the first on h alone, the "
+            f"other {2 * cfg.depth} after the out / FF2 projection's two K slices + bias into h "
+            f"(gated residual)"),
         "euler_in_step": kernel_gbs(rec, "euler_kernel",
                                     p_slices * rows * mel * 4 + 2 * mel * T * 4 + mel * 4,
                                     f"{p_slices} proj_out K slices + bias summed, CFG "
