@@ -604,24 +604,18 @@ __global__ __launch_bounds__(64 * QS * KS) void attn_bx_kernel(
   const int qt0 = qtile * kQT;
   const int q0 = qt0 + qs * 32;
 
-  // Q^T operand, split: qb[s][p] holds part p of Q[q0 + r][s*16 + h*8 + j] *
-  // scale * log2(e), j = 0..7.
-  bf16x8 qb[4][3];
+  // Q rows of this lane (scaled and split below, once the first K/V tiles'
+  // loads are in flight behind them)
+  floatx4 qraw[8];
   {
     const float* qrow = q + ((long)b * Tq + min(q0 + r, Tq - 1)) * ldq + head * kHD + h * 8;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      const floatx4 lo4 = *reinterpret_cast<const floatx4*>(qrow + s * 16) * qscale;
-      const floatx4 hi4 = *reinterpret_cast<const floatx4*>(qrow + s * 16 + 4) * qscale;
-      floatx8 x;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        x[e] = lo4[e];
-        x[4 + e] = hi4[e];
-      }
-      split3(x, qb[s][0], qb[s][1], qb[s][2]);
+      qraw[2 * s] = *reinterpret_cast<const floatx4*>(qrow + s * 16);
+      qraw[2 * s + 1] = *reinterpret_cast<const floatx4*>(qrow + s * 16 + 4);
     }
   }
+  bf16x8 qb[4][3];
   const int my_q = q_offset + q0 + r;
   const int kend = causal ? min(Tk, q_offset + min(qt0 + kQT - 1, Tq - 1) + 1) : Tk;
   const int ntiles = (kend + KT - 1) / KT;
@@ -636,19 +630,20 @@ __global__ __launch_bounds__(64 * QS * KS) void attn_bx_kernel(
   const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
       (void*)vbase, (short)0, BUF ? (int)(((long)(Tk - 1) * ldv + kHD) * 4) : 0, 0x00020000);
   floatx4 rk[LPT], rv[LPV][2];
-  auto gload_k = [&](int t) {
+  auto gload_k_to = [&](int t, floatx4* dst) {
 #pragma unroll
     for (int j = 0; j < LPT; ++j) {
       const int idx = tid + NT * j;
       const int row = idx >> 4, c = (idx & 15) * 4;
       if (BUF) {
-        rk[j] = __builtin_amdgcn_raw_buffer_load_b128(krs, (row * ldk + c) * 4, t * KT * ldk * 4, 0);
+        dst[j] = __builtin_amdgcn_raw_buffer_load_b128(krs, (row * ldk + c) * 4, t * KT * ldk * 4, 0);
       } else {
         const int key = min(t * KT + row, Tk - 1);
-        rk[j] = *reinterpret_cast<const floatx4*>(kbase + (long)key * ldk + c);
+        dst[j] = *reinterpret_cast<const floatx4*>(kbase + (long)key * ldk + c);
       }
     }
   };
+  auto gload_k = [&](int t) { gload_k_to(t, rk); };
   // V key pair pr, channels c..c+3 of step idx: a wave's 64 steps cover 16
   // consecutive pairs x 16 channels, so its V^T stores (rows c+e, 16 key
   // pairs per row, rows 4 apart) fall on 64 distinct LDS banks.
@@ -678,7 +673,7 @@ __global__ __launch_bounds__(64 * QS * KS) void attn_bx_kernel(
     }
   };
   // split a loaded tile and store its parts into LDS buffer `buf`
-  auto stage_k = [&](int buf) {
+  auto stage_k_from = [&](int buf, const floatx4* src) {
     __bf16* dst = Kp + buf * KBUF;
 #pragma unroll
     for (int j = 0; j < LPT; ++j) {
@@ -686,14 +681,15 @@ __global__ __launch_bounds__(64 * QS * KS) void attn_bx_kernel(
       const int row = idx >> 4, c = (idx & 15) * 4;
       bf16x4 x[3];
       if constexpr (KVP)
-        unpack2(rk[j], x);
+        unpack2(src[j], x);
       else
-        split3(rk[j], x[0], x[1], x[2]);  // (the third part is dead code with two)
+        split3(src[j], x[0], x[1], x[2]);  // (the third part is dead code with two)
 #pragma unroll
       for (int p = 0; p < NPL; ++p)
         *reinterpret_cast<bf16x4*>(dst + (p * KT + row) * kKP + c) = x[p];
     }
   };
+  auto stage_k = [&](int buf) { stage_k_from(buf, rk); };
   auto stage_v = [&](int buf) {
     __bf16* dst = Vt + buf * VBUF;
 #pragma unroll
@@ -747,15 +743,32 @@ __global__ __launch_bounds__(64 * QS * KS) void attn_bx_kernel(
   float m_run = -INFINITY, l_run = 0.0f;
   const __bf16* vfrag = Vt + r * VP + ks * 32 + h * 8;
 
+  // Prologue: Q, K and V of tile 0 and K of tile 1 are requested together (one
+  // memory round trip), then Q is split while the tiles are in flight.
+  // Tile 1's loads are clamped into range (or zero-filled by the buffer
+  // descriptor) when there is no tile 1; no later iteration reads its buffer.
   if (ntiles > 0) {
+    floatx4 rk1[LPT];
     gload_k(0);
     gload_v(0);
+    gload_k_to(1, rk1);
+    // Q^T operand, split: qb[s][p] holds part p of Q[q0 + r][s*16 + h*8 + j] *
+    // scale * log2(e), j = 0..7.
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const floatx4 lo4 = qraw[2 * s] * qscale;
+      const floatx4 hi4 = qraw[2 * s + 1] * qscale;
+      floatx8 x;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        x[e] = lo4[e];
+        x[4 + e] = hi4[e];
+      }
+      split3(x, qb[s][0], qb[s][1], qb[s][2]);
+    }
     stage_k(0);
     stage_v(0);
-  }
-  if (ntiles > 1) {
-    gload_k(1);
-    stage_k(1);
+    stage_k_from(1, rk1);
   }
   __syncthreads();
   // iteration t: s_in holds the scores of tile t, s_out receives tile t + 1's

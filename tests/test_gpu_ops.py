@@ -32,7 +32,7 @@ def ops(gpu):
 
 
 # --- a1 / a2 ---------------------------------------------------------------------
-@pytest.mark.parametrize("B,T", [(2, 500), (2, 3000), (2, 24), (2, 3), (1, 1), (4, 7)])
+@pytest.mark.parametrize("B,T", [(2, 500), (2, 3000), (3, 1999), (2, 24), (2, 3), (1, 1), (4, 7)])
 def test_adaln(gpu, ops, B, T):
     announce(f"adaln B={B} T={T}")
     D = 1024
