@@ -254,6 +254,14 @@ def dit_projection_plan(rows, N):
     return "direct", 1
 
 
+def split_tail_fits(rows, N, cus):
+    """Whether lx_linear_bx's split tail engages for a 64-row-tile launch (the
+    estimator asks for it on the QKV projection): tile count between CUs and
+    2 CUs with (tiles - CUs) * S = CUs for S = 2 or 4."""
+    tiles = -(-rows // 64) * (N // 128)
+    return any(cus < tiles and (tiles - cus) * s == cus for s in (2, 4))
+
+
 def gemm_kernels(torch, ops, T, dev):
     """Per-class timings of one estimator block's launches at the step's shapes,
     each class on the kernel and plan the estimator runs for it (the split-operand
@@ -291,12 +299,16 @@ def gemm_kernels(torch, ops, T, dev):
     qv = qkv.view(B, T, 3 * D)
     hv = h.view(M, D)
 
-    def proj(x, W, b, ep, y, pack_out=False, pack_from=0):
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    scr = ops.bx_scratch(dev, bm=64)
+
+    def proj(x, W, b, ep, y, pack_out=False, pack_from=0, split_tail=False):
         N = W.shape[0]
         wf = ops.wfrag_pack(W)
         kind, sl = dit_projection_plan(M, N)
         fp32 = (lambda: ops.linear(x, W, b, ep, out=y))
         xp = pack2(torch, x)
+        st = dict(scratch=scr, split_tail=True) if split_tail else {}
 
         def bx(products):
             # with three products the estimator passes its activations as
@@ -309,14 +321,16 @@ def gemm_kernels(torch, ops, T, dev):
             ok = ops.LX_BX_OUT_PACKED if pk and pack_out else ops.LX_BX_OUT_F32
             pf = pack_from if pk and pack_out else 0
             return lambda: ops.linear_bx(a, wf, N, b, ep, out=y, out_kind=ok, bm=64,
-                                         products=products, a_packed=pk, pack_from=pf)
+                                         products=products, a_packed=pk, pack_from=pf, **st)
         kern = (f"gemm_bx_kernel 64x128, {DIT_PRODUCTS} products"
                 + (", packed activations" if DIT_PRODUCTS == 3 else "")
-                + (f", {sl} K slices (sum folded into adaln_resid)" if kind == "partial" else ""))
+                + (f", {sl} K slices (sum folded into adaln_resid)" if kind == "partial" else "")
+                + (", split tail" if split_tail and split_tail_fits(M, N, cus) else ""))
         return bx(DIT_PRODUCTS), kern, fp32, bx(6)
     cases = {
         # q fp32, k and v packed for the split attention (T = 500's layout)
-        "gemm_qkv_rope": (proj(xd, wq, bq, rope, qkv, pack_out=True, pack_from=D),
+        "gemm_qkv_rope": (proj(xd, wq, bq, rope, qkv, pack_out=True, pack_from=D,
+                               split_tail=True),
                           2 * M * 3 * D * D, 1),
         "gemm_out_gated": (proj(xd, wo, bd, gated, hv), 2 * M * D * D, 1),
         "gemm_ff0_gelu": (proj(xd, w1, b1, gelu, ff, pack_out=True), 2 * M * F * D, 1),
@@ -703,10 +717,12 @@ def counter_probe(torch, ops, launches=20):
     pk = DIT_PRODUCTS == 3
     xa = pack2(torch, xd) if pk else xd
     ff0_out = ops.LX_BX_OUT_PACKED if pk else ops.LX_BX_OUT_F32
+    scr = ops.bx_scratch(dev, bm=64)  # the QKV projection's split tail, as in the step
     torch.cuda.synchronize()
     for _ in range(launches):
         ops.linear_bx(xa, fq, 3 * D, bq, rope, out=qkv, out_kind=ff0_out, bm=64,
-                      products=DIT_PRODUCTS, a_packed=pk, pack_from=D if pk else 0)
+                      products=DIT_PRODUCTS, a_packed=pk, pack_from=D if pk else 0,
+                      scratch=scr, split_tail=True)
     for _ in range(launches):
         ops.linear_bx(xa, f0, F, b0, gelu, out=ff, out_kind=ff0_out, bm=64,
                       products=DIT_PRODUCTS, a_packed=pk)
@@ -770,11 +786,13 @@ def traffic_probe(torch, ops, launches=20):
     fq = ops.wfrag_pack(wq)
     pk = DIT_PRODUCTS == 3  # the estimator's packed activations
     xa = pack2(torch, xd) if pk else xd
+    scr = ops.bx_scratch(dev, bm=64)  # the split tail, as in the step
     torch.cuda.synchronize()
     for _ in range(launches):
         ops.linear_bx(xa, fq, 3 * D, bq, rope, out=qkv, bm=64, products=DIT_PRODUCTS,
                       a_packed=pk, pack_from=D if pk else 0,
-                      out_kind=ops.LX_BX_OUT_PACKED if pk else ops.LX_BX_OUT_F32)
+                      out_kind=ops.LX_BX_OUT_PACKED if pk else ops.LX_BX_OUT_F32,
+                      scratch=scr, split_tail=True)
     torch.cuda.synchronize()
     for _ in range(launches):
         dst.copy_(src)

@@ -62,7 +62,7 @@ class LinearBx(C.Structure):
         ("slice_stride", C.c_long), ("M", C.c_int), ("N", C.c_int), ("K", C.c_int),
         ("bm", C.c_int), ("slices", C.c_int), ("ws", fp), ("ws_floats", C.c_size_t),
         ("counters", C.c_void_p), ("n_counters", C.c_int), ("products", C.c_int),
-        ("a_packed", C.c_int), ("pack_from", C.c_int),
+        ("a_packed", C.c_int), ("pack_from", C.c_int), ("split_tail", C.c_int),
     ]
 
 

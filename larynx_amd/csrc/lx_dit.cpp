@@ -73,6 +73,13 @@ struct lx_dit {
   float *A0, *xe, *c1, *h, *xn, *qkv, *att, *ff, *P;
   float* Pws;          // split-K slices of proj_out (kProjSplitMax x rows x mel)
   float* Rws;          // K slices of the out / FF2 projections (2 x kPartialRows x D)
+  // The QKV projection's split tail (lx_linear_bx.split_tail): partial tiles of
+  // the split workgroups (CUs x 64 x 128 floats) and one arrival count per tile
+  // (zeroed here, left zeroed by every launch).
+  float* qkv_ws = nullptr;
+  size_t qkv_ws_floats = 0;
+  unsigned* qkv_cnt = nullptr;
+  int qkv_ncnt = 0;
   int proj_splits = 1; // slices of the last forward's proj_out
   long proj_slice = 0; // floats between slices
   int* pos;
@@ -181,9 +188,16 @@ int forward_core(lx_dit* m, const float* x, long x_bstride, const float* mu, con
   const bool pk_kv = pk && attention_takes_packed_kv(B, T, m->heads, 3);
   auto proj = [&](const float* x, int ldx, const void* Wf, const float* W, const float* bias,
                   float* y, int ldy, int N, int K, const lx_epilogue* epi,
-                  bool pack_out = false, int pack_from = 0) -> int {
+                  bool pack_out = false, int pack_from = 0, bool split_tail = false) -> int {
     if (!m->frag) return lx_linear_f32(x, ldx, W, bias, y, ldy, rows, N, K, epi, s);
     lx_linear_bx g{};
+    if (split_tail && m->qkv_ws) {
+      g.split_tail = 1;
+      g.ws = m->qkv_ws;
+      g.ws_floats = m->qkv_ws_floats;
+      g.counters = m->qkv_cnt;
+      g.n_counters = m->qkv_ncnt;
+    }
     g.a_packed = pk ? 1 : 0;
     g.pack_from = pack_out && pk ? pack_from : 0;
     g.A = x;
@@ -260,8 +274,10 @@ int forward_core(lx_dit* m, const float* x, long x_bstride, const float* mu, con
     rope.rope_section = D;   // q occupies columns [0, D), k [D, 2D)
     rope.rope_sections = 2;
     rope.rope_base = kRopeBase;
+    // QKV: 384 tiles at B * T = 1000, 1.5 per CU; the split tail runs 256 whole
+    // and 128 in two k ranges, so every CU gets the same work.
     LX_TRY(proj(m->xn, D, wf0, w0, m->qkv_b[i], m->qkv, 3 * D, 3 * D, D, &rope, pk_kv,
-                /*pack_from*/ D));
+                /*pack_from*/ D, /*split_tail*/ true));
     LX_TRY(attention(m->qkv, 3 * D, m->qkv + D, 3 * D, m->qkv + 2 * D, 3 * D, m->att, D, B, T,
                      T, m->heads, m->heads, m->hd, 1.0f / std::sqrt((float)m->hd), 0, 0,
                      m->products, pk ? 1 : 0, s, pk_kv ? 1 : 0));
@@ -389,6 +405,18 @@ extern "C" int lx_dit_create(const lx_dit_weights* w, int B, int max_T, lx_dit**
   m->P = A(rows * mel);
   m->Pws = A(rows * mel * kProjSplitMax);
   m->Rws = m->frag ? A((size_t)2 * std::min<size_t>(rows, kPartialRows) * D) : nullptr;
+  if (m->frag) {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+        cus > 0) {
+      m->qkv_ws_floats = (size_t)cus * 64 * 128;
+      m->qkv_ws = A(m->qkv_ws_floats);
+      m->qkv_ncnt = (int)((rows + 63) / 64) * (3 * D / 128);
+      m->qkv_cnt = a.alloc<unsigned>(m->qkv_ncnt);
+      ok = ok && m->qkv_cnt;
+    }
+  }
   m->pos = a.alloc<int>(max_T);
   ok = ok && m->pos;
   if (!ok) {
@@ -472,6 +500,9 @@ extern "C" int lx_dit_create(const lx_dit_weights* w, int B, int max_T, lx_dit**
   C(m->proj_w, w->proj_out_w, (size_t)mel * D);
   C(m->proj_b, w->proj_out_b, mel);
   if (rc == LX_OK) rc = iota_i32(m->pos, max_T, s);
+  if (rc == LX_OK && m->qkv_cnt &&
+      hipMemsetAsync(m->qkv_cnt, 0, sizeof(unsigned) * m->qkv_ncnt, s) != hipSuccess)
+    rc = LX_ERR_LAUNCH;
   if (rc == LX_OK && hipStreamSynchronize(s) != hipSuccess) {
     set_error("dit_create: weight packing failed");
     rc = LX_ERR_LAUNCH;

@@ -71,11 +71,14 @@ struct BxArgs {
   long ldy;
   long slice_stride;
   int M, N, K, kslice, tiles_m, tiles_n, slices;
-  int streamk;          // 1: stream-K over `grid` workgroups (ws and counters set)
+  int streamk;          // 1: stream-K over `grid` workgroups; 2: split tail (ws and counters set)
   int grid;
-  float* ws;            // stream-K partial tiles: 2 per workgroup, BM * 128 floats each
+  float* ws;            // partial tiles: stream-K 2 per workgroup, split tail 1 per split
+                        // workgroup, BM * 128 floats each
   int ws_bytes;
-  unsigned* counters;   // stream-K arrival counts, one per tile, zero between launches
+  unsigned* counters;   // arrival counts, one per tile, zero between launches
+  int split_full;       // split tail: tiles [0, split_full) run whole, one workgroup each;
+  int split_s;          // every later tile runs as split_s workgroups of consecutive k ranges
 };
 
 enum { BX_OUT_F32 = LX_BX_OUT_F32, BX_OUT_PARTIAL = LX_BX_OUT_PARTIAL, BX_OUT_PACKED = LX_BX_OUT_PACKED };
@@ -145,8 +148,27 @@ gemm_bx_kernel(BxArgs a, EpiArgs ep) {
   // slice may hold fewer); stream-K (one slice): an equal share of all of them
   const int tile_pairs =
       min(npt, a.K / (2 * kBxBK) - (w / (a.tiles_m * a.tiles_n)) * npt);
-  const long u0 = a.streamk ? (long)w * U / G : (long)w * npt;
-  const long u1 = a.streamk ? (long)(w + 1) * U / G : u0 + tile_pairs;
+  long u0 = a.streamk == 1 ? (long)w * U / G : (long)w * npt;
+  long u1 = a.streamk == 1 ? (long)(w + 1) * U / G : u0 + tile_pairs;
+  // Split tail (one slice): each XCD's first split_full / 8 workgroups take
+  // whole tiles, its next ones the k ranges of the later tiles (split_s per
+  // tile, consecutive), so the dispatcher's first round puts one whole tile
+  // and, in the second, one part of a split tile on every CU.  sid numbers
+  // the split workgroups (their partial tile slot).
+  int sid = -1;
+  if (a.streamk == 2) {
+    const int x = blockIdx.x & 7, i = blockIdx.x >> 3;
+    const int fx = a.split_full >> 3, sx = (G - a.split_full) >> 3;
+    if (i < fx) {
+      u0 = (long)(x * fx + i) * npt;
+      u1 = u0 + npt;
+    } else {
+      sid = x * sx + (i - fx);
+      const int t = a.split_full + sid / a.split_s, p = sid % a.split_s;
+      u0 = (long)t * npt + p * npt / a.split_s;
+      u1 = (long)t * npt + (p + 1) * npt / a.split_s;
+    }
+  }
   constexpr int SLAB_BYTES = kBxBK * 4;  // A bytes per row per slab
   // A fragments: row block i, plane p, k step st of a slab buffer
   const int aoff = fr * kBxBK;
@@ -166,7 +188,7 @@ gemm_bx_kernel(BxArgs a, EpiArgs ep) {
     const long uend = min(u1, (long)(t + 1) * npt);
     const int q1 = (int)(uend - (long)t * npt);
     u = uend;
-    const int slot = first_seg ? 2 * w : 2 * w + 1;
+    const int slot = a.streamk == 2 ? sid : first_seg ? 2 * w : 2 * w + 1;
     if (!first_seg) __syncthreads();  // the last segment's epilogue is done with the LDS
     first_seg = false;
     const int mt = t % a.tiles_m;
@@ -388,7 +410,11 @@ gemm_bx_kernel(BxArgs a, EpiArgs ep) {
         }
       __builtin_amdgcn_s_waitcnt(0);  // the stores are performed before the count
       const long tu0 = (long)t * npt;
-      const int cf = bx_owner(tu0, U, G), cl = bx_owner(tu0 + npt - 1, U, G);
+      // the tile's contributors, in k order: stream-K workgroups cf..cl, or
+      // split workgroups (sid) cf..cl
+      const int cf = a.streamk == 2 ? (t - a.split_full) * a.split_s : bx_owner(tu0, U, G);
+      const int cl = a.streamk == 2 ? cf + a.split_s - 1 : bx_owner(tu0 + npt - 1, U, G);
+      const int own = a.streamk == 2 ? sid : w;
       __syncthreads();
       if (tid == 0)
         s_last = __hip_atomic_fetch_add(a.counters + t, 1u, __ATOMIC_RELAXED,
@@ -399,13 +425,14 @@ gemm_bx_kernel(BxArgs a, EpiArgs ep) {
       // two contributors' loads in flight at a time.
       floatx16 tot[BMB];
       auto part = [&](floatx16* pv, int c) {
-        if (c == w) {
+        if (c == own) {
 #pragma unroll
           for (int i = 0; i < BMB; ++i) pv[i] = acc[i];
           return;
         }
         // c's first segment starts inside this tile, else this tile is its last
-        const int cs = (long)c * U / G >= tu0 ? 2 * c : 2 * c + 1;
+        // (a split workgroup has one slot)
+        const int cs = a.streamk == 2 ? c : (long)c * U / G >= tu0 ? 2 * c : 2 * c + 1;
         const int cb = cs * (BM * kBxBN) * 4 + ((wave * BMB) * 4 * 64 + lane) * 16;
 #pragma unroll
         for (int i = 0; i < BMB; ++i)
@@ -670,7 +697,32 @@ int linear_bx(const lx_linear_bx& g, hipStream_t stream) {
   a.ws = nullptr;
   a.ws_bytes = 0;
   a.counters = nullptr;
-  if (g.ws && g.counters && g.out == BX_OUT_F32 && !g.a_packed) {
+  a.split_full = 0;
+  a.split_s = 0;
+  LX_REQUIRE(g.split_tail == 0 || g.split_tail == 1, "linear_bx: split_tail=%d must be 0 or 1",
+             g.split_tail);
+  if (g.split_tail && g.ws && g.counters && slices == 1) {
+    // whole tiles on the first round of CUs, the rest split along K onto the
+    // second (only where that gives every CU the same work)
+    const int cus = device_cus();
+    const int tiles = a.tiles_m * a.tiles_n;
+    const int npt = g.K / (2 * kBxBK);
+    int S = 0;
+    for (int sp : {2, 4})
+      if (tiles > cus && (long)(tiles - cus) * sp == cus && npt >= sp) S = sp;
+    const int G = cus + (tiles - cus) * S;
+    const size_t need = (size_t)(G - cus) * g.bm * kBxBN;
+    if (S && cus % 8 == 0 && (G - cus) % 8 == 0 && tiles <= g.n_counters &&
+        need <= g.ws_floats && need * 4 < (1u << 31)) {
+      a.streamk = 2;
+      a.grid = G;
+      a.split_full = cus;
+      a.split_s = S;
+      a.ws = g.ws;
+      a.ws_bytes = (int)(need * 4);
+      a.counters = g.counters;
+    }
+  } else if (g.ws && g.counters && g.out == BX_OUT_F32 && !g.a_packed) {
     // Stream-K over one workgroup per CU (at most one per slab pair of work):
     // every CU gets the same number of slab pairs whatever the tile count.
     const int tiles = a.tiles_m * a.tiles_n;

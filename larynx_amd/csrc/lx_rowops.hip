@@ -54,6 +54,8 @@ __global__ __launch_bounds__(kRowsPerBlock * kWave) void adaln_kernel(
   // Issue this wave's first row loads first so their latency overlaps the
   // modulation staging below.
   float4 v[NV], nv[NV];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) nv[j] = make_float4(0.f, 0.f, 0.f, 0.f);  // read by the last copy
   load_row(v, row0 + wave);
   const int b_first = row0 / T;
   const int nb = (rend - 1) / T - b_first + 1;
@@ -153,6 +155,14 @@ __global__ __launch_bounds__(kRowsPerBlock * kWave) void adaln_resid_kernel(
   constexpr int PS = SMAX > 0 ? SMAX : 1;
   float4 v[NV], pv[PS][NV];
   float4 nv[PF ? NV : 1], npv[PF ? PS : 1][PF ? NV : 1];
+  if constexpr (PF) {  // read by the copy after a wave's last row
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      nv[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (int sl = 0; sl < PS; ++sl) npv[sl][j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
   load_row(v, pv, min(row0 + wave, rows - 1));
   const int b_first = row0 / T;
   const int nb = (rend - 1) / T - b_first + 1;

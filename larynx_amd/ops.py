@@ -216,13 +216,14 @@ def wfrag_pack(W):
 
 
 def linear_bx(a, wf, N, b=None, epilogue=None, out=None, out_kind=LX_BX_OUT_F32, bm=128,
-              slices=1, scratch=None, products=6, a_packed=False, pack_from=0):
+              slices=1, scratch=None, products=6, a_packed=False, pack_from=0, split_tail=False):
     """epi(a @ W^T + b) with fp32 arithmetic on the bf16 matrix cores, W given as
     wfrag_pack(W) (N rows), a fp32 (M, K).  out_kind LX_BX_OUT_F32: (M, N) (out= the
     residual stream for residual epilogues); LX_BX_OUT_PARTIAL: (slices, M, N) raw
     K-slice products; LX_BX_OUT_PACKED: (M, N) as two-part packed rows.  a_packed: a
     holds two-part packed rows (three products, bm 64).  scratch = bx_scratch(): the
-    launch runs stream-K over the CUs.  src/flow/ops.cpp:20-26."""
+    launch runs stream-K over the CUs, or with split_tail the tiles past one per CU
+    split along K (when the tile count allows).  src/flow/ops.cpp:20-26."""
     M, K = a.shape
     g = LinearBx()
     g.A, g.lda = a.data_ptr(), a.stride(0)
@@ -234,6 +235,7 @@ def linear_bx(a, wf, N, b=None, epilogue=None, out=None, out_kind=LX_BX_OUT_F32,
     g.M, g.N, g.K, g.bm, g.slices, g.products = M, N, K, bm, slices, products
     g.a_packed = int(a_packed)
     g.pack_from = pack_from
+    g.split_tail = int(split_tail)
     if out_kind == LX_BX_OUT_PARTIAL:
         if out is None:
             out = torch.empty(slices, M, N, device=a.device, dtype=torch.float32)

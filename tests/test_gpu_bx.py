@@ -179,6 +179,53 @@ def test_linear_bx_streamk_is_deterministic(gpu, ops):
         assert torch.equal(ops.linear_bx(x, wf, 3072, scratch=scr), y0)
 
 
+@pytest.mark.parametrize("N,S", [(3072, 2), (2560, 4)])
+def test_linear_bx_split_tail(gpu, ops, N, S):
+    """Split tail at B*T = 1000 (16 row tiles of 64): N = 3072 gives 384 tiles, 256
+    run whole and 128 as two k ranges each; N = 2560 gives 320, 256 whole and 64 as
+    four.  In the QKV form (packed A, rotary epilogue, fp32 or packed k / v output):
+    the whole tiles (columns below 2048) are bit-identical to the data-parallel
+    launch, the split ones sum their parts in k order (within the per-op bar of the
+    oracle, bit-identical over repeated calls), and the arrival counts are left at
+    zero."""
+    announce(f"linear_bx split tail N={N} S={S}")
+    M, D, T = 1000, 1024, 500
+    x, W, b = rnd((M, D), 60), rnd((N, D), 61, 0.03), rnd((N,), 62)
+    xp, wf, bd = dev(pack2_np(x), gpu), ops.wfrag_pack(dev(W, gpu)), dev(b, gpu)
+    pos = torch.arange(T, dtype=torch.int32, device=gpu)
+    ep = ops.Epilogue(kind=ops.LX_EPI_ROPE_PARTIAL, rows_per_batch=T, pos=pos.data_ptr(),
+                      rot_dim=64, rope_section=D, rope_sections=2, rope_base=10000.0)
+    scr = ops.bx_scratch(gpu, bm=64)
+    kw = dict(bm=64, products=3, a_packed=True)
+    y_dp = ops.linear_bx(xp, wf, N, bd, ep, **kw)
+    y_st = ops.linear_bx(xp, wf, N, bd, ep, scratch=scr, split_tail=True, **kw)
+    assert same_bits(y_st[:, :2048], y_dp[:, :2048])
+    assert not same_bits(y_st[:, 2048:], y_dp[:, 2048:])  # the split tiles summed their parts
+    ref = orc.linear(x, W, b).reshape(2, T, N)
+    p = np.arange(T, dtype=np.int32)
+    q = orc.rope_partial(np.ascontiguousarray(ref[..., :D]), p)
+    k = orc.rope_partial(np.ascontiguousarray(ref[..., D:2 * D]), p)
+    ref = np.concatenate([q, k, ref[..., 2 * D:]], -1).reshape(M, N)
+    assert orc.rel_err(y_st.cpu().numpy(), ref) < TOL
+    assert orc.rel_err(y_dp.cpu().numpy(), ref) < TOL
+    for _ in range(3):
+        assert torch.equal(ops.linear_bx(xp, wf, N, bd, ep, scratch=scr, split_tail=True, **kw),
+                           y_st)
+    pk = dict(out_kind=ops.LX_BX_OUT_PACKED, pack_from=D, **kw)
+    yp_dp = ops.linear_bx(xp, wf, N, bd, ep, **pk)
+    yp_st = ops.linear_bx(xp, wf, N, bd, ep, scratch=scr, split_tail=True, **pk)
+    assert same_bits(yp_st[:, :2048], yp_dp[:, :2048])
+    assert same_bits(yp_st, pack2_np_from(y_st.cpu().numpy(), D))
+    assert int(scr[1].abs().sum()) == 0
+
+
+def pack2_np_from(y, c0):
+    """Columns [c0, ...) of fp32 rows as two-part packed groups, the rest unchanged."""
+    out = np.array(y, np.float32, copy=True)
+    out[:, c0:] = pack2_np(np.ascontiguousarray(y[:, c0:]))
+    return out
+
+
 def test_linear_bx_rejects_bad_arguments(gpu, ops):
     from larynx_amd import LxError
     announce("linear_bx bad arguments")
