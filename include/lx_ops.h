@@ -253,14 +253,14 @@ int lx_linear_split_f32(const float* x, int ldx, const void* planes, const float
  * workgroups is summed by the last to finish, in k order (deterministic, no
  * waiting).  Calls sharing one ws / counters pair must not overlap.
  * split_tail = 1 with ws and counters (one slice; any output and operand form):
- * when the tile count T lies between CUs and 2 * CUs with (T - CUs) * S = CUs
- * for S = 2 or 4, CUs tiles run whole and each of the other T - CUs runs as S
- * workgroups over consecutive k ranges, so every CU holds one whole tile and
- * one part of a split one (at B*T = 1000 the 384 QKV tiles: 256 whole, 128
- * split in two).  The last part of a split tile to finish sums the parts'
- * products in k order and applies the epilogue (deterministic, no waiting).
- * ws needs CUs * bm * 128 floats, counters one per tile; other shapes run as
- * without scratch.
+ * when the tile count T lies between CUs and 2 * CUs, CUs tiles run whole and
+ * each of the other T - CUs runs as S workgroups over consecutive k ranges (S
+ * the largest of 2..8 with (T - CUs) * S <= CUs, a multiple of 8, and at most
+ * K / 64 ranges), so every CU holds one whole tile and at most one part of a
+ * split one (at B*T = 1000 the 384 QKV tiles: 256 whole, 128 split in two).
+ * The last part of a split tile to finish sums the parts' products in k order
+ * and applies the epilogue (deterministic, no waiting).  ws needs CUs * bm *
+ * 128 floats, counters one per tile; other shapes run as without scratch.
  * products: 6 (or 0) forms each element pair as the six products of the
  * three-part splits (fp32-level error, the default); 3 uses two-part splits
  * (x0 + x1, 16 significant bits each) and the three products a0 b0 + a0 b1 +

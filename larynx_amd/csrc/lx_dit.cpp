@@ -406,16 +406,11 @@ extern "C" int lx_dit_create(const lx_dit_weights* w, int B, int max_T, lx_dit**
   m->Pws = A(rows * mel * kProjSplitMax);
   m->Rws = m->frag ? A((size_t)2 * std::min<size_t>(rows, kPartialRows) * D) : nullptr;
   if (m->frag) {
-    int dev = 0, cus = 0;
-    if (hipGetDevice(&dev) == hipSuccess &&
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
-        cus > 0) {
-      m->qkv_ws_floats = (size_t)cus * 64 * 128;
-      m->qkv_ws = A(m->qkv_ws_floats);
-      m->qkv_ncnt = (int)((rows + 63) / 64) * (3 * D / 128);
-      m->qkv_cnt = a.alloc<unsigned>(m->qkv_ncnt);
-      ok = ok && m->qkv_cnt;
-    }
+    m->qkv_ws_floats = bx_split_ws_floats(64);
+    m->qkv_ws = A(m->qkv_ws_floats);
+    m->qkv_ncnt = (int)((rows + 63) / 64) * (3 * D / 128);
+    m->qkv_cnt = a.alloc<unsigned>(m->qkv_ncnt);
+    ok = ok && m->qkv_cnt;
   }
   m->pos = a.alloc<int>(max_T);
   ok = ok && m->pos;

@@ -617,6 +617,20 @@ int dispatch_bx(const BxArgs& a, int out, const EpiArgs& ep, hipStream_t s) {
 
 }  // namespace
 
+int bx_split_parts(int M, int N, int K, int bm) {
+  // S: the most parts per split tile (at most 8, at most K / 64) with the split
+  // workgroups filling at most the CUs' second round in whole XCD shares
+  const int cus = device_cus();
+  const int tiles = ((M + bm - 1) / bm) * (N / kBxBN);
+  const int npt = K / (2 * kBxBK);
+  if (cus % 8 || tiles <= cus || tiles >= 2 * cus) return 0;
+  for (int sp = std::min(8, cus / (tiles - cus)); sp >= 2; --sp)
+    if ((tiles - cus) * sp % 8 == 0 && npt >= sp) return sp;
+  return 0;
+}
+
+size_t bx_split_ws_floats(int bm) { return (size_t)device_cus() * bm * kBxBN; }
+
 int wfrag_pack(const float* W, void* Wf, int N, int K, hipStream_t stream) {
   LX_REQUIRE(W && Wf && N > 0 && K > 0 && N % 32 == 0 && K % 16 == 0,
              "wfrag_pack: bad shape N=%d K=%d", N, K);
@@ -703,17 +717,13 @@ int linear_bx(const lx_linear_bx& g, hipStream_t stream) {
              g.split_tail);
   if (g.split_tail && g.ws && g.counters && slices == 1) {
     // whole tiles on the first round of CUs, the rest split along K onto the
-    // second (only where that gives every CU the same work)
+    // second, so that no CU holds two whole tiles
     const int cus = device_cus();
     const int tiles = a.tiles_m * a.tiles_n;
-    const int npt = g.K / (2 * kBxBK);
-    int S = 0;
-    for (int sp : {2, 4})
-      if (tiles > cus && (long)(tiles - cus) * sp == cus && npt >= sp) S = sp;
+    const int S = bx_split_parts(g.M, g.N, g.K, g.bm);
     const int G = cus + (tiles - cus) * S;
     const size_t need = (size_t)(G - cus) * g.bm * kBxBN;
-    if (S && cus % 8 == 0 && (G - cus) % 8 == 0 && tiles <= g.n_counters &&
-        need <= g.ws_floats && need * 4 < (1u << 31)) {
+    if (S && tiles <= g.n_counters && need <= g.ws_floats && need * 4 < (1u << 31)) {
       a.streamk = 2;
       a.grid = G;
       a.split_full = cus;

@@ -141,6 +141,10 @@ int adaln_resid(float* h, const float* partials, int splits, long partial_stride
 // ---- split-operand GEMM with W in fragment order (lx_gemm_bx.hip) ----
 // lx_linear_bx_f32 (arguments and outputs as declared in lx_ops.h).
 int linear_bx(const lx_linear_bx& g, hipStream_t stream);
+// Parts per split tile of lx_linear_bx's split tail for an (M, N, K) launch on
+// bm-row tiles (0: the split tail does not apply), and the ws it needs.
+int bx_split_parts(int M, int N, int K, int bm);
+size_t bx_split_ws_floats(int bm);
 // lx_attention_f32 with the split-operand kernel's product count (3 or 6; the
 // fp32 kernel, which small grids run, ignores it).
 int attention(const float* q, int ldq, const float* k, int ldk, const float* v, int ldv, float* o,

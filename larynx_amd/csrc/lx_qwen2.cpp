@@ -197,9 +197,19 @@ int prefill_layer(lx_qwen2* m, Layer& L, int rows, const float* next_norm, hipSt
   lx_epilogue swiglu{};
   swiglu.kind = LX_EPI_SWIGLU_PAIRED;
   if (m->frag) {
-    // gate/up + SwiGLU: 128-row tiles while they fit one round over the CUs
-    // (L = 256: 152 tiles, 33 vs 35 us), else 64-row tiles (L = 1024: 95 vs 116 us)
+    // gate/up + SwiGLU: 64-row tiles with the split tail where it applies (L =
+    // 256: 304 tiles, 256 whole and 48 in five k ranges; 24.3 vs 25.3 us on
+    // 128-row tiles with cold weights), else 128-row tiles while they fit one
+    // round over the CUs, else 64-row tiles (L = 1024: 95 vs 116 us)
+    const bool split = bx_split_parts(rows, 2 * m->I, H, 64) > 0;
     lx_linear_bx g{};
+    if (split) {
+      g.split_tail = 1;
+      g.ws = m->ws;
+      g.ws_floats = m->ws_floats;
+      g.counters = m->arrivals;
+      g.n_counters = m->n_arrivals;
+    }
     g.A = m->hn;
     g.a_packed = pk ? 1 : 0;
     g.lda = H;
@@ -211,7 +221,7 @@ int prefill_layer(lx_qwen2* m, Layer& L, int rows, const float* next_norm, hipSt
     g.M = rows;
     g.N = 2 * m->I;
     g.K = H;
-    g.bm = (long)((rows + 127) / 128) * (2 * m->I / 128) <= 256 ? 128 : 64;
+    g.bm = split ? 64 : (long)((rows + 127) / 128) * (2 * m->I / 128) <= 256 ? 128 : 64;
     g.slices = 1;
     g.products = m->products;
     LX_TRY(linear_bx(g, s));
@@ -415,9 +425,11 @@ extern "C" int lx_qwen2_create(const lx_qwen2_weights* w, int max_ctx, lx_qwen2*
   m->att = A(rows * H);
   m->act = A(rows * I);
   int tails = 0;
-  m->ws_floats = splitk_ws_floats(max_ctx, H, QKV, I, &tails);
+  m->ws_floats = std::max(splitk_ws_floats(max_ctx, H, QKV, I, &tails), bx_split_ws_floats(64));
   m->ws = A(m->ws_floats);
-  m->n_arrivals = tails > 0 ? tails : 1;
+  // counters of the fp32 split tail, and one per tile of the gate/up split tail
+  // (fewer than 2 x CUs tiles where it applies)
+  m->n_arrivals = std::max(tails, 1024);
   m->arrivals = a.alloc<unsigned>(m->n_arrivals);
   ok = ok && m->arrivals;
   m->max_splits = dec_attention_splits(max_ctx);
