@@ -302,7 +302,7 @@ def gemm_kernels(torch, ops, T, dev):
     cus = torch.cuda.get_device_properties(dev).multi_processor_count
     scr = ops.bx_scratch(dev, bm=64)
 
-    def proj(x, W, b, ep, y, pack_out=False, pack_from=0, split_tail=False):
+    def proj(x, W, b, ep, y, pack_out=False, pack_from=0, split_tail=True):
         N = W.shape[0]
         wf = ops.wfrag_pack(W)
         kind, sl = dit_projection_plan(M, N)
@@ -329,8 +329,7 @@ def gemm_kernels(torch, ops, T, dev):
         return bx(DIT_PRODUCTS), kern, fp32, bx(6)
     cases = {
         # q fp32, k and v packed for the split attention (T = 500's layout)
-        "gemm_qkv_rope": (proj(xd, wq, bq, rope, qkv, pack_out=True, pack_from=D,
-                               split_tail=True),
+        "gemm_qkv_rope": (proj(xd, wq, bq, rope, qkv, pack_out=True, pack_from=D),
                           2 * M * 3 * D * D, 1),
         "gemm_out_gated": (proj(xd, wo, bd, gated, hv), 2 * M * D * D, 1),
         "gemm_ff0_gelu": (proj(xd, w1, b1, gelu, ff, pack_out=True), 2 * M * F * D, 1),

@@ -73,9 +73,9 @@ struct lx_dit {
   float *A0, *xe, *c1, *h, *xn, *qkv, *att, *ff, *P;
   float* Pws;          // split-K slices of proj_out (kProjSplitMax x rows x mel)
   float* Rws;          // K slices of the out / FF2 projections (2 x kPartialRows x D)
-  // The QKV projection's split tail (lx_linear_bx.split_tail): partial tiles of
+  // The projections' split tail (lx_linear_bx.split_tail): partial tiles of
   // the split workgroups (CUs x 64 x 128 floats) and one arrival count per tile
-  // (zeroed here, left zeroed by every launch).
+  // of the widest projection (zeroed here, left zeroed by every launch).
   float* qkv_ws = nullptr;
   size_t qkv_ws_floats = 0;
   unsigned* qkv_cnt = nullptr;
@@ -186,12 +186,15 @@ int forward_core(lx_dit* m, const float* x, long x_bstride, const float* mu, con
   // three-product split kernel (it then stages them without splitting; q
   // stays fp32: attention scales it before its own split).
   const bool pk_kv = pk && attention_takes_packed_kv(B, T, m->heads, 3);
+  // Every projection on the fragment-order GEMM asks for the split tail: it
+  // applies where the launch's tiles number between one and two per CU (T = 500:
+  // the QKV projection's 384 tiles run 256 whole and 128 in two k ranges).
   auto proj = [&](const float* x, int ldx, const void* Wf, const float* W, const float* bias,
                   float* y, int ldy, int N, int K, const lx_epilogue* epi,
-                  bool pack_out = false, int pack_from = 0, bool split_tail = false) -> int {
+                  bool pack_out = false, int pack_from = 0) -> int {
     if (!m->frag) return lx_linear_f32(x, ldx, W, bias, y, ldy, rows, N, K, epi, s);
     lx_linear_bx g{};
-    if (split_tail && m->qkv_ws) {
+    if (m->qkv_ws) {
       g.split_tail = 1;
       g.ws = m->qkv_ws;
       g.ws_floats = m->qkv_ws_floats;
@@ -274,10 +277,8 @@ int forward_core(lx_dit* m, const float* x, long x_bstride, const float* mu, con
     rope.rope_section = D;   // q occupies columns [0, D), k [D, 2D)
     rope.rope_sections = 2;
     rope.rope_base = kRopeBase;
-    // QKV: 384 tiles at B * T = 1000, 1.5 per CU; the split tail runs 256 whole
-    // and 128 in two k ranges, so every CU gets the same work.
     LX_TRY(proj(m->xn, D, wf0, w0, m->qkv_b[i], m->qkv, 3 * D, 3 * D, D, &rope, pk_kv,
-                /*pack_from*/ D, /*split_tail*/ true));
+                /*pack_from*/ D));
     LX_TRY(attention(m->qkv, 3 * D, m->qkv + D, 3 * D, m->qkv + 2 * D, 3 * D, m->att, D, B, T,
                      T, m->heads, m->heads, m->hd, 1.0f / std::sqrt((float)m->hd), 0, 0,
                      m->products, pk ? 1 : 0, s, pk_kv ? 1 : 0));
@@ -408,7 +409,7 @@ extern "C" int lx_dit_create(const lx_dit_weights* w, int B, int max_T, lx_dit**
   if (m->frag) {
     m->qkv_ws_floats = bx_split_ws_floats(64);
     m->qkv_ws = A(m->qkv_ws_floats);
-    m->qkv_ncnt = (int)((rows + 63) / 64) * (3 * D / 128);
+    m->qkv_ncnt = (int)((rows + 63) / 64) * (std::max(3 * D, F) / 128);
     m->qkv_cnt = a.alloc<unsigned>(m->qkv_ncnt);
     ok = ok && m->qkv_cnt;
   }

@@ -200,13 +200,13 @@ def test_dit_T3000_two_blocks_vs_oracle(gpu):
     assert orc.rel_err(dphi.cpu().numpy(), ref) < 1e-4
 
 
-@pytest.mark.parametrize("T", [1000, 2000])
+@pytest.mark.parametrize("T", [1000, 2000, 750])
 def test_dit_two_blocks_split_gemm_vs_oracle(gpu, T):
     """Every block projection (QKV + rotary, out and FF2 with the gated
-    residual, FF0 + GELU) runs the split-operand bf16 GEMM, whose tiles fill
-    whole rounds of the CUs: at B=2, T=2000 (4000 rows) all on 128 x 128 tiles;
-    at T=1000 (2000 rows) QKV, out and FF2 on 128 x 64 and FF0 on 128 x 128.
-    The result matches the oracle at the per-op tolerance."""
+    residual, FF0 + GELU) runs the split-operand bf16 GEMM on 64 x 128 tiles
+    with the gated residual in the out / FF2 epilogues (more than 1024 rows);
+    at T=750 (1500 rows) FF0's 384 tiles take the split tail (256 whole, 128 in
+    two k ranges).  The result matches the oracle at the per-op tolerance."""
     from larynx_amd.flow import DiTConfig, DiTEstimator, dit_param_shapes
     announce(f"dit T={T} depth=2 split GEMMs vs oracle")
     cfg = DiTConfig(depth=2)
