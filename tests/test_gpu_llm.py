@@ -204,8 +204,9 @@ def test_decode_crosses_split_classes(gpu, qwen, max_ctx, n0):
 def test_prefill_ragged_lengths(gpu, qwen, L):
     """Prefill at lengths that leave partial 64-row tiles and change the
     split-K plan (1 row: one tile per column band; 300 rows: five bands).  At
-    200 rows the gate/up launch splits its tail tiles over K (4 row bands x 152
-    column tiles = 512 whole + 96 sliced), with the last row band partial."""
+    200 and 300 rows the gate/up launch runs the split tail on 64-row tiles (4
+    row bands x 76 column tiles = 256 whole + 48 in five k ranges; 5 x 76 = 256
+    whole + 124 in two), with the last row band partial."""
     cfg, params, _, lm = qwen
     announce(f"qwen2 prefill L={L}")
     lm_in = torch.from_numpy(orc.normal((L, cfg.hidden), 300 + L, 1, 0.5)).to(gpu)
@@ -225,9 +226,10 @@ def test_prefill_ragged_lengths(gpu, qwen, L):
 
 
 def test_prefill_split_tail_is_deterministic(gpu, qwen):
-    """The gate/up launch at L=256 sums the K slices of its tail tiles in slice
-    order whichever slice arrives last: two prefills of the same input give
-    bit-identical hidden states, logits and caches."""
+    """The gate/up launch at L=256 (split tail: 256 whole tiles, 48 in five k
+    ranges) sums the parts of its split tiles in k order whichever part arrives
+    last: two prefills of the same input give bit-identical hidden states,
+    logits and caches."""
     cfg, params, _, lm = qwen
     announce("qwen2 prefill L=256 twice (split tail determinism)")
     lm_in = torch.from_numpy(orc.normal((256, cfg.hidden), 4040, 1, 0.5)).to(gpu)
