@@ -252,7 +252,8 @@ int lx_linear_split_f32(const float* x, int ldx, const void* planes, const float
  * takes an equal share of the tiles' k range; a tile shared by several
  * workgroups is summed by the last to finish, in k order (deterministic, no
  * waiting).  Calls sharing one ws / counters pair must not overlap.
- * split_tail = 1 with ws and counters (one slice; any output and operand form):
+ * split_tail = 1 with ws and counters (one slice; the fp32 or packed output, any
+ * operand form):
  * when the tile count T lies between CUs and 2 * CUs, CUs tiles run whole and
  * each of the other T - CUs runs as S workgroups over consecutive k ranges (S
  * the largest of 2..8 with (T - CUs) * S <= CUs, a multiple of 8, and at most

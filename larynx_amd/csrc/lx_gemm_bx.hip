@@ -715,7 +715,7 @@ int linear_bx(const lx_linear_bx& g, hipStream_t stream) {
   a.split_s = 0;
   LX_REQUIRE(g.split_tail == 0 || g.split_tail == 1, "linear_bx: split_tail=%d must be 0 or 1",
              g.split_tail);
-  if (g.split_tail && g.ws && g.counters && slices == 1) {
+  if (g.split_tail && g.ws && g.counters && slices == 1 && g.out != BX_OUT_PARTIAL) {
     // whole tiles on the first round of CUs, the rest split along K onto the
     // second, so that no CU holds two whole tiles
     const int cus = device_cus();

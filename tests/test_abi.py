@@ -84,6 +84,9 @@ def test_argument_errors_need_no_device():
     g.bm, g.products = 64, 4
     assert lib.lx_linear_bx_f32(C.byref(g), None) == LX_ERR_ARG
     assert b"products" in lib.lx_last_error()
+    g.products, g.split_tail = 3, 2  # split_tail is a 0 / 1 switch
+    assert lib.lx_linear_bx_f32(C.byref(g), None) == LX_ERR_ARG
+    assert b"split_tail" in lib.lx_last_error()
     # the folded residual takes at most four partial slices
     assert lib.lx_adaln_resid_f32(fake, fake, 5, 1 << 20, None, fake, 1024, fake, fake, 1024,
                                   fake, 2, 8, 1024, 1e-6, None) == LX_ERR_ARG

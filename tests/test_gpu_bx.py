@@ -216,6 +216,12 @@ def test_linear_bx_split_tail(gpu, ops, N, S):
     yp_st = ops.linear_bx(xp, wf, N, bd, ep, scratch=scr, split_tail=True, **pk)
     assert same_bits(yp_st[:, :2048], yp_dp[:, :2048])
     assert same_bits(yp_st, pack2_np_from(y_st.cpu().numpy(), D))
+    # raw partial products have no epilogue to finish a split tile: the same launch
+    # as without scratch
+    Pd = ops.linear_bx(xp, wf, N, out_kind=ops.LX_BX_OUT_PARTIAL, **kw)
+    Ps = ops.linear_bx(xp, wf, N, out_kind=ops.LX_BX_OUT_PARTIAL, scratch=scr, split_tail=True,
+                       **kw)
+    assert same_bits(Ps, Pd)
     assert int(scr[1].abs().sum()) == 0
 
 
