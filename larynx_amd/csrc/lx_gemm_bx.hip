@@ -153,7 +153,7 @@ gemm_bx_kernel(BxArgs a, EpiArgs ep) {
   // Split tail (one slice): each XCD's first split_full / 8 workgroups take
   // whole tiles, its next ones the k ranges of the later tiles (split_s per
   // tile, consecutive), so the dispatcher's first round puts one whole tile
-  // and, in the second, one part of a split tile on every CU.  sid numbers
+  // and its second at most one part of a split tile on every CU.  sid numbers
   // the split workgroups (their partial tile slot).
   int sid = -1;
   if (a.streamk == 2) {
