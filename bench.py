@@ -818,7 +818,7 @@ def main():
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (requested --gpus {args.gpus}); the DiT path "
               "shards by CFG row / heads across GPUs by design but no multi-GPU figure is "
-              "produced by this build.", file=sys.stderr)
+              "produced.", file=sys.stderr)
         sys.exit(2)
     import torch
     if not torch.cuda.is_available():
@@ -942,8 +942,8 @@ def main():
                         key=lambda kv: kv[1]["avg_us"] * kv[1]["per_block"])
     dom_us = dom["avg_us"]
     dom_tflops = dom["flop"] / (dom_us * 1e-6) / 1e12
-    # MFMA utilisation as the survey defines it: the GEMM's fp32 flops per
-    # second against the 157.3 TFLOP/s fp32 matrix peak, whatever pipe runs it
+    # MFMA utilisation: the GEMM's fp32 flops per second against the 157.3
+    # TFLOP/s fp32 matrix peak, whatever pipe runs it
     roofline = {"kernel": dom_name, "impl": dom["kernel"], "bound": "mfma",
                 "achieved": round(dom_tflops, 3), "peak": MFMA_F32_PEAK_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(dom_tflops / MFMA_F32_PEAK_TFLOPS, 4),

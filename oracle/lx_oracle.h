@@ -3,7 +3,7 @@
  *
  * TEST INFRASTRUCTURE ONLY.  This is a plain-C restatement of the reference's
  * algorithms (Larynx src/flow/ and src/llm/ sources, with the PyTorch
- * semantics of tests/flow_reference.py), used as the checker for the HIP
+ * semantics of tests/flow_reference.py), used as the test oracle for the HIP
  * library and, in bench.py, as the timed CPU baseline.  It is never linked
  * into or called by the product path (larynx_amd/liblxops.so).
  *

@@ -1,7 +1,7 @@
 """ctypes front end of the CPU oracle (liblxoracle.so).
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
-cpu_baseline leg of bench.py, as the checker / CPU baseline.  Never used by the
+cpu_baseline leg of bench.py, as the test oracle / CPU baseline.  Never used by the
 product path.  Arrays are numpy float32 (C-contiguous).
 """
 import ctypes as C

@@ -4,7 +4,7 @@
 // include/larynx/llm/llm.h:16-104 (host std::vector inputs and outputs, bool
 // returns with the message on stderr), with the ggml backend replaced by the
 // lx_flow / lx_qwen2 objects.  Built into tests/cxx/libdropin.so and driven by
-// tests/test_gpu_dropin_cxx.py; INTEGRATION.md shows the same code inline.
+// tests/test_gpu_dropin_cxx.py.
 #pragma once
 
 #include <cstdint>
